@@ -1,0 +1,231 @@
+"""ctypes view of include/deltanet_core.h and thin launchers over torch tensors.
+
+The structs below mirror the C header field for field. Torch supplies device
+memory and the current HIP stream; every computation runs in
+libdeltanet_core.so. There is no fallback: a missing library raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from pathlib import Path
+
+import torch
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = _HERE / "libdeltanet_core.so"
+
+DN_F32, DN_BF16 = 0, 1
+DN_ALGO_AUTO, DN_ALGO_GENERIC, DN_ALGO_MFMA = 0, 1, 2
+
+STATUS = {
+    0: "DN_OK",
+    -1: "DN_ERR_SEQUENCE",
+    -2: "DN_ERR_SHAPE",
+    -3: "DN_ERR_GATE_WIDTH",
+    -4: "DN_ERR_CHUNK_LEN",
+    -5: "DN_ERR_NONFINITE",
+    -6: "DN_ERR_NULL",
+    -7: "DN_ERR_DTYPE",
+    -8: "DN_ERR_WORKSPACE",
+    -9: "DN_ERR_UNSUPPORTED",
+    -10: "DN_ERR_HIP",
+}
+
+EXPORTS = [
+    "dn_chunk_fwd", "dn_chunk_bwd", "dn_step", "dn_chunk_fwd_workspace_bytes",
+    "dn_chunk_bwd_workspace_bytes", "dn_chunk_fwd_algo", "dn_chunk_bwd_algo",
+    "dn_last_error", "dn_version",
+]
+
+_i64, _i32, _f64, _vp, _sz = (ctypes.c_int64, ctypes.c_int32, ctypes.c_double,
+                              ctypes.c_void_p, ctypes.c_size_t)
+
+
+class ChunkFwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i64), ("sequence", _i64), ("nheads", _i64), ("head_k_dim", _i64),
+        ("head_v_dim", _i64), ("erase_width", _i64), ("write_width", _i64),
+        ("decay_width", _i64), ("has_gate", _i32), ("chunk_len", _i32), ("scale", _f64),
+        ("qkv_dtype", _i32), ("y_dtype", _i32), ("algo", _i32), ("check_finite", _i32),
+        ("q", _vp), ("k", _vp), ("v", _vp), ("erase", _vp), ("write", _vp), ("g", _vp),
+        ("state_in", _vp), ("y", _vp), ("state_out", _vp), ("workspace", _vp),
+        ("workspace_bytes", _sz),
+    ]
+
+
+class ChunkBwdArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i64), ("sequence", _i64), ("nheads", _i64), ("head_k_dim", _i64),
+        ("head_v_dim", _i64), ("erase_width", _i64), ("write_width", _i64),
+        ("decay_width", _i64), ("has_gate", _i32), ("chunk_len", _i32), ("scale", _f64),
+        ("qkv_dtype", _i32), ("grad_dtype", _i32), ("algo", _i32), ("check_finite", _i32),
+        ("d_y", _vp), ("d_state_final", _vp), ("q", _vp), ("k", _vp), ("v", _vp),
+        ("erase", _vp), ("write", _vp), ("g", _vp), ("state_in", _vp), ("d_q", _vp),
+        ("d_k", _vp), ("d_v", _vp), ("d_erase", _vp), ("d_write", _vp), ("d_g", _vp),
+        ("d_state", _vp), ("workspace", _vp), ("workspace_bytes", _sz),
+    ]
+
+
+class StepArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i64), ("nheads", _i64), ("head_k_dim", _i64), ("head_v_dim", _i64),
+        ("erase_width", _i64), ("write_width", _i64), ("decay_width", _i64),
+        ("has_gate", _i32), ("scale", _f64), ("qkv_dtype", _i32), ("y_dtype", _i32),
+        ("check_finite", _i32),
+        ("q", _vp), ("k", _vp), ("v", _vp), ("erase", _vp), ("write", _vp), ("g", _vp),
+        ("state_in", _vp), ("y", _vp), ("state_out", _vp),
+    ]
+
+
+_LIB = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libdeltanet_core.so (built by __graft_entry__.build())."""
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python -c 'import __graft_entry__ as g; "
+                "g.build()'` — there is no CPU fallback for the delta-rule core")
+        L = ctypes.CDLL(str(LIB_PATH))
+        L.dn_chunk_fwd.argtypes = [ctypes.POINTER(ChunkFwdArgs), _vp]
+        L.dn_chunk_fwd.restype = ctypes.c_int
+        L.dn_chunk_bwd.argtypes = [ctypes.POINTER(ChunkBwdArgs), _vp]
+        L.dn_chunk_bwd.restype = ctypes.c_int
+        L.dn_step.argtypes = [ctypes.POINTER(StepArgs), _vp]
+        L.dn_step.restype = ctypes.c_int
+        L.dn_chunk_fwd_workspace_bytes.argtypes = [ctypes.POINTER(ChunkFwdArgs)]
+        L.dn_chunk_fwd_workspace_bytes.restype = _sz
+        L.dn_chunk_bwd_workspace_bytes.argtypes = [ctypes.POINTER(ChunkBwdArgs)]
+        L.dn_chunk_bwd_workspace_bytes.restype = _sz
+        L.dn_chunk_fwd_algo.argtypes = [ctypes.POINTER(ChunkFwdArgs)]
+        L.dn_chunk_fwd_algo.restype = ctypes.c_int
+        L.dn_chunk_bwd_algo.argtypes = [ctypes.POINTER(ChunkBwdArgs)]
+        L.dn_chunk_bwd_algo.restype = ctypes.c_int
+        L.dn_last_error.restype = ctypes.c_char_p
+        L.dn_version.restype = ctypes.c_char_p
+        _LIB = L
+    return _LIB
+
+
+class DeltaError(ValueError):
+    """A failed check of the core; carries the dn_status code."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"{STATUS.get(code, code)}: {message}")
+        self.code = code
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        raise DeltaError(rc, lib().dn_last_error().decode())
+
+
+def dtype_tag(t: torch.dtype) -> int:
+    if t == torch.float32:
+        return DN_F32
+    if t == torch.bfloat16:
+        return DN_BF16
+    raise DeltaError(-7, f"unsupported dtype {t}; use float32 or bfloat16")
+
+
+def ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_handle():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def nan_scale(scale):
+    return float("nan") if scale is None else float(scale)
+
+
+def chunk_fwd_args(q, k, v, erase, write, g, state, y, state_out, chunk_len, scale,
+                   algo=DN_ALGO_AUTO, check_finite=False, workspace=None):
+    B, S, H, K = q.shape
+    V = v.shape[3]
+    a = ChunkFwdArgs()
+    a.batch, a.sequence, a.nheads, a.head_k_dim, a.head_v_dim = B, S, H, K, V
+    a.erase_width, a.write_width = erase.shape[3], write.shape[3]
+    a.decay_width = 0 if g is None else g.shape[3]
+    a.has_gate = 0 if g is None else 1
+    a.chunk_len = int(chunk_len)
+    a.scale = nan_scale(scale)
+    a.qkv_dtype = dtype_tag(q.dtype)
+    a.y_dtype = dtype_tag(y.dtype)
+    a.algo = int(algo)
+    a.check_finite = int(bool(check_finite))
+    a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    a.erase, a.write = erase.data_ptr(), write.data_ptr()
+    a.g = None if g is None else g.data_ptr()
+    a.state_in, a.y, a.state_out = state.data_ptr(), y.data_ptr(), state_out.data_ptr()
+    if workspace is not None:
+        a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel()
+    return a
+
+
+def run_chunk_fwd(args: ChunkFwdArgs) -> None:
+    check(lib().dn_chunk_fwd(ctypes.byref(args), stream_handle()))
+
+
+def step_args(q, k, v, erase, write, g, state, y, state_out, scale, check_finite=False):
+    B, H, K = q.shape
+    V = v.shape[2]
+    a = StepArgs()
+    a.batch, a.nheads, a.head_k_dim, a.head_v_dim = B, H, K, V
+    a.erase_width, a.write_width = erase.shape[2], write.shape[2]
+    a.decay_width = 0 if g is None else g.shape[2]
+    a.has_gate = 0 if g is None else 1
+    a.scale = nan_scale(scale)
+    a.qkv_dtype = dtype_tag(q.dtype)
+    a.y_dtype = dtype_tag(y.dtype)
+    a.check_finite = int(bool(check_finite))
+    a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    a.erase, a.write = erase.data_ptr(), write.data_ptr()
+    a.g = None if g is None else g.data_ptr()
+    a.state_in, a.y, a.state_out = state.data_ptr(), y.data_ptr(), state_out.data_ptr()
+    return a
+
+
+def run_step(args: StepArgs) -> None:
+    check(lib().dn_step(ctypes.byref(args), stream_handle()))
+
+
+def chunk_bwd_args(dy, dstate, q, k, v, erase, write, g, state, grads, chunk_len, scale,
+                   algo=DN_ALGO_AUTO, check_finite=False, workspace=None):
+    dq, dk, dv, de, dw, dg, ds = grads
+    B, S, H, K = q.shape
+    V = v.shape[3]
+    a = ChunkBwdArgs()
+    a.batch, a.sequence, a.nheads, a.head_k_dim, a.head_v_dim = B, S, H, K, V
+    a.erase_width, a.write_width = erase.shape[3], write.shape[3]
+    a.decay_width = 0 if g is None else g.shape[3]
+    a.has_gate = 0 if g is None else 1
+    a.chunk_len = int(chunk_len)
+    a.scale = nan_scale(scale)
+    a.qkv_dtype = dtype_tag(q.dtype)
+    a.grad_dtype = dtype_tag(dy.dtype)
+    a.algo = int(algo)
+    a.check_finite = int(bool(check_finite))
+    a.d_y = dy.data_ptr()
+    a.d_state_final = None if dstate is None else dstate.data_ptr()
+    a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    a.erase, a.write = erase.data_ptr(), write.data_ptr()
+    a.g = None if g is None else g.data_ptr()
+    a.state_in = state.data_ptr()
+    a.d_q, a.d_k, a.d_v = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+    a.d_erase, a.d_write = de.data_ptr(), dw.data_ptr()
+    a.d_g = None if dg is None else dg.data_ptr()
+    a.d_state = ds.data_ptr()
+    if workspace is not None:
+        a.workspace, a.workspace_bytes = workspace.data_ptr(), workspace.numel()
+    return a
+
+
+def run_chunk_bwd(args: ChunkBwdArgs) -> None:
+    check(lib().dn_chunk_bwd(ctypes.byref(args), stream_handle()))

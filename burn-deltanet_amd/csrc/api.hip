@@ -1,0 +1,360 @@
+// The C ABI (include/deltanet_core.h): argument checks that mirror the
+// reference's assertions, workspace management and kernel dispatch.
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "dn_common.hpp"
+
+namespace dn {
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(DN_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Library-managed workspace: grow-only, one buffer per device, freed at exit.
+struct Pool {
+  std::mutex mu;
+  std::vector<void*> ptr;
+  std::vector<size_t> size;
+  ~Pool() {
+    for (void* p : ptr)
+      if (p) (void)hipFree(p);
+  }
+};
+Pool g_pool;
+
+hipError_t pool_get(size_t bytes, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(g_pool.mu);
+  if (size_t(dev) >= g_pool.ptr.size()) {
+    g_pool.ptr.resize(size_t(dev) + 1, nullptr);
+    g_pool.size.resize(size_t(dev) + 1, 0);
+  }
+  if (g_pool.size[size_t(dev)] < bytes) {
+    // Callers on this device may still be using the old buffer on their
+    // streams; drain the device before it is replaced.
+    if (g_pool.ptr[size_t(dev)]) {
+      if ((e = hipDeviceSynchronize()) != hipSuccess) return e;
+      (void)hipFree(g_pool.ptr[size_t(dev)]);
+      g_pool.ptr[size_t(dev)] = nullptr;
+      g_pool.size[size_t(dev)] = 0;
+    }
+    void* p = nullptr;
+    if ((e = hipMalloc(&p, bytes)) != hipSuccess) return e;
+    g_pool.ptr[size_t(dev)] = p;
+    g_pool.size[size_t(dev)] = bytes;
+  }
+  *out = g_pool.ptr[size_t(dev)];
+  return hipSuccess;
+}
+
+bool valid_dtype(int t) { return t == DN_F32 || t == DN_BF16; }
+
+// The reference's shape/gate checks (path.rs:177-208, recurrent.rs:51-54).
+int check_common(int64_t batch, int64_t sequence, int64_t nheads, int64_t K, int64_t V,
+                 int64_t ew, int64_t ww, int64_t dw, int32_t has_gate) {
+  if (sequence < 1) return fail(DN_ERR_SEQUENCE, "sequence length must be at least 1");
+  if (batch < 1 || nheads < 1 || K < 1 || V < 1)
+    return fail(DN_ERR_SHAPE, "batch, nheads, head_k_dim and head_v_dim must be at least 1");
+  if (batch * sequence * nheads * (K > V ? K : V) >= (int64_t(1) << 40))
+    return fail(DN_ERR_SHAPE, "tensor too large");
+  if (!(ew == 1 || ew == K))
+    return fail(DN_ERR_GATE_WIDTH, "erase gate: last axis must be 1 or " + std::to_string(K) +
+                                       ", got " + std::to_string(ew));
+  if (!(ww == 1 || ww == V))
+    return fail(DN_ERR_GATE_WIDTH, "write gate: last axis must be 1 or " + std::to_string(V) +
+                                       ", got " + std::to_string(ww));
+  if (has_gate && !(dw == 1 || dw == K))
+    return fail(DN_ERR_GATE_WIDTH, "forget gate: last axis must be 1 or " + std::to_string(K) +
+                                       ", got " + std::to_string(dw));
+  return DN_OK;
+}
+
+float resolve_scale(double scale, int64_t K) {
+  return std::isnan(scale) ? float(1.0 / std::sqrt(double(K))) : float(scale);
+}
+
+Dims make_dims(int64_t B, int64_t S, int64_t H, int64_t K, int64_t V, int64_t ew, int64_t ww,
+               int64_t dw, int32_t has_gate, int32_t L, double scale) {
+  Dims d;
+  d.B = int(B);
+  d.S = int(S);
+  d.H = int(H);
+  d.K = int(K);
+  d.V = int(V);
+  d.ew = int(ew);
+  d.ww = int(ww);
+  d.dw = has_gate ? int(dw) : 0;
+  d.L = L;
+  d.N = int((S + L - 1) / L);
+  d.scale = resolve_scale(scale, K);
+  return d;
+}
+
+// NaN/Inf guard over a list of (pointer, count, dtype); synchronises.
+struct Guarded {
+  const void* p;
+  size_t n;
+  int dtype;
+};
+
+// One device int per device for the guard flag, allocated on first use.
+hipError_t guard_flag(int** out) {
+  static std::mutex mu;
+  static std::vector<int*> flags;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  if (size_t(dev) >= flags.size()) flags.resize(size_t(dev) + 1, nullptr);
+  if (!flags[size_t(dev)]) {
+    void* p = nullptr;
+    if ((e = hipMalloc(&p, sizeof(int))) != hipSuccess) return e;
+    flags[size_t(dev)] = static_cast<int*>(p);
+  }
+  *out = flags[size_t(dev)];
+  return hipSuccess;
+}
+
+int nonfinite_check(const std::vector<Guarded>& list, hipStream_t stream, const char* when) {
+  int* flag = nullptr;
+  hipError_t e = guard_flag(&flag);
+  if (e != hipSuccess) return hip_fail(e, "guard flag allocation");
+  int host = 0;
+  if ((e = hipMemcpyAsync(flag, &host, sizeof(int), hipMemcpyHostToDevice, stream)) !=
+      hipSuccess)
+    return hip_fail(e, "guard flag upload");
+  for (const Guarded& g : list)
+    if (g.p && g.n)
+      if ((e = launch_nonfinite_scan(g.p, g.n, g.dtype, flag, stream)) != hipSuccess)
+        return hip_fail(e, "nonfinite scan launch");
+  if ((e = hipMemcpyAsync(&host, flag, sizeof(int), hipMemcpyDeviceToHost, stream)) !=
+      hipSuccess)
+    return hip_fail(e, "guard flag readback");
+  if ((e = hipStreamSynchronize(stream)) != hipSuccess) return hip_fail(e, "guard sync");
+  if (host) return fail(DN_ERR_NONFINITE, std::string("NaN or Inf found in the ") + when);
+  return DN_OK;
+}
+
+int check_fwd(const dn_chunk_fwd_args* a) {
+  if (!a) return fail(DN_ERR_NULL, "args is NULL");
+  if (int rc = check_common(a->batch, a->sequence, a->nheads, a->head_k_dim, a->head_v_dim,
+                            a->erase_width, a->write_width, a->decay_width, a->has_gate))
+    return rc;
+  if (a->chunk_len < 1) return fail(DN_ERR_CHUNK_LEN, "chunk_len must be at least 1");
+  if (!valid_dtype(a->qkv_dtype) || !valid_dtype(a->y_dtype))
+    return fail(DN_ERR_DTYPE, "dtype must be DN_F32 or DN_BF16");
+  if (!a->q || !a->k || !a->v || !a->erase || !a->write || !a->state_in || !a->y ||
+      !a->state_out || (a->has_gate && !a->g))
+    return fail(DN_ERR_NULL, "a required tensor pointer is NULL");
+  return DN_OK;
+}
+
+int check_bwd(const dn_chunk_bwd_args* a) {
+  if (!a) return fail(DN_ERR_NULL, "args is NULL");
+  if (int rc = check_common(a->batch, a->sequence, a->nheads, a->head_k_dim, a->head_v_dim,
+                            a->erase_width, a->write_width, a->decay_width, a->has_gate))
+    return rc;
+  if (a->chunk_len < 1) return fail(DN_ERR_CHUNK_LEN, "chunk_len must be at least 1");
+  if (!valid_dtype(a->qkv_dtype) || !valid_dtype(a->grad_dtype))
+    return fail(DN_ERR_DTYPE, "dtype must be DN_F32 or DN_BF16");
+  if (!a->d_y || !a->q || !a->k || !a->v || !a->erase || !a->write || !a->state_in ||
+      !a->d_q || !a->d_k || !a->d_v || !a->d_erase || !a->d_write || !a->d_state ||
+      (a->has_gate && (!a->g || !a->d_g)))
+    return fail(DN_ERR_NULL, "a required tensor pointer is NULL");
+  return DN_OK;
+}
+
+int fwd_algo(const dn_chunk_fwd_args* a, const Dims& d) {
+  if (a->algo == DN_ALGO_GENERIC) return DN_ALGO_GENERIC;
+  const bool fits = mfma_fwd_supported(d, a->qkv_dtype, a->y_dtype);
+  if (a->algo == DN_ALGO_MFMA) return fits ? DN_ALGO_MFMA : DN_ERR_UNSUPPORTED;
+  return fits ? DN_ALGO_MFMA : DN_ALGO_GENERIC;
+}
+
+}  // namespace
+}  // namespace dn
+
+using namespace dn;
+
+extern "C" {
+
+const char* dn_last_error(void) { return g_last_error.c_str(); }
+
+const char* dn_version(void) { return "deltanet-mi355x 0.1.0 (gfx950)"; }
+
+int dn_chunk_fwd_algo(const dn_chunk_fwd_args* a) {
+  if (int rc = check_fwd(a)) return rc;
+  Dims d = make_dims(a->batch, a->sequence, a->nheads, a->head_k_dim, a->head_v_dim,
+                     a->erase_width, a->write_width, a->decay_width, a->has_gate, a->chunk_len,
+                     a->scale);
+  return fwd_algo(a, d);
+}
+
+size_t dn_chunk_fwd_workspace_bytes(const dn_chunk_fwd_args* a) {
+  if (check_fwd(a)) return 0;
+  Dims d = make_dims(a->batch, a->sequence, a->nheads, a->head_k_dim, a->head_v_dim,
+                     a->erase_width, a->write_width, a->decay_width, a->has_gate, a->chunk_len,
+                     a->scale);
+  const int algo = fwd_algo(a, d);
+  if (algo == DN_ALGO_MFMA) return mfma_fwd_workspace(d);
+  if (algo == DN_ALGO_GENERIC) return generic_fwd_workspace(d);
+  return 0;
+}
+
+int dn_chunk_fwd(const dn_chunk_fwd_args* a, hipStream_t stream) {
+  g_last_error.clear();
+  if (int rc = check_fwd(a)) return rc;
+  Dims d = make_dims(a->batch, a->sequence, a->nheads, a->head_k_dim, a->head_v_dim,
+                     a->erase_width, a->write_width, a->decay_width, a->has_gate, a->chunk_len,
+                     a->scale);
+  const int algo = fwd_algo(a, d);
+  if (algo < 0)
+    return fail(DN_ERR_UNSUPPORTED, "DN_ALGO_MFMA does not cover this shape/dtype");
+  const size_t need = algo == DN_ALGO_MFMA ? mfma_fwd_workspace(d) : generic_fwd_workspace(d);
+  void* ws = a->workspace;
+  if (ws) {
+    if (a->workspace_bytes < need)
+      return fail(DN_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) +
+                                        " bytes");
+  } else if (need) {
+    hipError_t e = pool_get(need, &ws);
+    if (e != hipSuccess) return hip_fail(e, "workspace allocation");
+  }
+  const size_t nq = size_t(d.B) * d.S * d.H, ns = size_t(d.B) * d.H * d.K * d.V;
+  if (a->check_finite) {
+    std::vector<Guarded> in = {{a->q, nq * d.K, a->qkv_dtype},
+                               {a->k, nq * d.K, a->qkv_dtype},
+                               {a->v, nq * d.V, a->qkv_dtype},
+                               {a->erase, nq * d.ew, DN_F32},
+                               {a->write, nq * d.ww, DN_F32},
+                               {a->has_gate ? a->g : nullptr, nq * d.dw, DN_F32},
+                               {a->state_in, ns, DN_F32}};
+    if (int rc = nonfinite_check(in, stream, "inputs")) return rc;
+  }
+  hipError_t e;
+  if (algo == DN_ALGO_MFMA)
+    e = mfma_fwd(d, a->y_dtype, a->q, a->k, a->v, a->erase, a->write,
+                 a->has_gate ? a->g : nullptr, a->state_in, a->y, a->state_out, ws, stream);
+  else
+    e = generic_fwd(d, a->qkv_dtype, a->y_dtype, a->q, a->k, a->v, a->erase, a->write,
+                    a->has_gate ? a->g : nullptr, a->state_in, a->y, a->state_out, ws, stream);
+  if (e != hipSuccess) return hip_fail(e, "dn_chunk_fwd launch");
+  if (a->check_finite) {
+    std::vector<Guarded> out = {{a->y, nq * d.V, a->y_dtype}, {a->state_out, ns, DN_F32}};
+    if (int rc = nonfinite_check(out, stream, "outputs")) return rc;
+  }
+  return DN_OK;
+}
+
+int dn_chunk_bwd_algo(const dn_chunk_bwd_args* a) {
+  if (int rc = check_bwd(a)) return rc;
+  if (a->algo == DN_ALGO_MFMA) return DN_ERR_UNSUPPORTED;
+  return DN_ALGO_GENERIC;
+}
+
+size_t dn_chunk_bwd_workspace_bytes(const dn_chunk_bwd_args* a) {
+  if (check_bwd(a)) return 0;
+  Dims d = make_dims(a->batch, a->sequence, a->nheads, a->head_k_dim, a->head_v_dim,
+                     a->erase_width, a->write_width, a->decay_width, a->has_gate, a->chunk_len,
+                     a->scale);
+  return generic_bwd_workspace(d);
+}
+
+int dn_chunk_bwd(const dn_chunk_bwd_args* a, hipStream_t stream) {
+  g_last_error.clear();
+  if (int rc = check_bwd(a)) return rc;
+  if (a->algo == DN_ALGO_MFMA)
+    return fail(DN_ERR_UNSUPPORTED, "the backward has no DN_ALGO_MFMA path yet");
+  Dims d = make_dims(a->batch, a->sequence, a->nheads, a->head_k_dim, a->head_v_dim,
+                     a->erase_width, a->write_width, a->decay_width, a->has_gate, a->chunk_len,
+                     a->scale);
+  const size_t need = generic_bwd_workspace(d);
+  void* ws = a->workspace;
+  if (ws) {
+    if (a->workspace_bytes < need)
+      return fail(DN_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) +
+                                        " bytes");
+  } else {
+    hipError_t e = pool_get(need, &ws);
+    if (e != hipSuccess) return hip_fail(e, "workspace allocation");
+  }
+  const size_t nq = size_t(d.B) * d.S * d.H, ns = size_t(d.B) * d.H * d.K * d.V;
+  if (a->check_finite) {
+    std::vector<Guarded> in = {{a->d_y, nq * d.V, a->grad_dtype},
+                               {a->d_state_final, ns, DN_F32},
+                               {a->q, nq * d.K, a->qkv_dtype},
+                               {a->k, nq * d.K, a->qkv_dtype},
+                               {a->v, nq * d.V, a->qkv_dtype},
+                               {a->erase, nq * d.ew, DN_F32},
+                               {a->write, nq * d.ww, DN_F32},
+                               {a->has_gate ? a->g : nullptr, nq * d.dw, DN_F32},
+                               {a->state_in, ns, DN_F32}};
+    if (int rc = nonfinite_check(in, stream, "inputs")) return rc;
+  }
+  hipError_t e = generic_bwd(d, a->qkv_dtype, a->grad_dtype, a->d_y, a->d_state_final, a->q,
+                             a->k, a->v, a->erase, a->write, a->has_gate ? a->g : nullptr,
+                             a->state_in, a->d_q, a->d_k, a->d_v, a->d_erase, a->d_write,
+                             a->has_gate ? a->d_g : nullptr, a->d_state, ws, stream);
+  if (e != hipSuccess) return hip_fail(e, "dn_chunk_bwd launch");
+  if (a->check_finite) {
+    std::vector<Guarded> out = {{a->d_q, nq * d.K, a->grad_dtype},
+                                {a->d_k, nq * d.K, a->grad_dtype},
+                                {a->d_v, nq * d.V, a->grad_dtype},
+                                {a->d_erase, nq * d.ew, DN_F32},
+                                {a->d_write, nq * d.ww, DN_F32},
+                                {a->has_gate ? a->d_g : nullptr, nq * d.dw, DN_F32},
+                                {a->d_state, ns, DN_F32}};
+    if (int rc = nonfinite_check(out, stream, "outputs")) return rc;
+  }
+  return DN_OK;
+}
+
+int dn_step(const dn_step_args* a, hipStream_t stream) {
+  g_last_error.clear();
+  if (!a) return fail(DN_ERR_NULL, "args is NULL");
+  if (int rc = check_common(a->batch, 1, a->nheads, a->head_k_dim, a->head_v_dim,
+                            a->erase_width, a->write_width, a->decay_width, a->has_gate))
+    return rc;
+  if (!valid_dtype(a->qkv_dtype) || !valid_dtype(a->y_dtype))
+    return fail(DN_ERR_DTYPE, "dtype must be DN_F32 or DN_BF16");
+  if (!a->q || !a->k || !a->v || !a->erase || !a->write || !a->state_in || !a->y ||
+      !a->state_out || (a->has_gate && !a->g))
+    return fail(DN_ERR_NULL, "a required tensor pointer is NULL");
+  const size_t nh = size_t(a->batch) * a->nheads, ns = nh * a->head_k_dim * a->head_v_dim;
+  if (a->check_finite) {
+    std::vector<Guarded> in = {{a->q, nh * a->head_k_dim, a->qkv_dtype},
+                               {a->k, nh * a->head_k_dim, a->qkv_dtype},
+                               {a->v, nh * a->head_v_dim, a->qkv_dtype},
+                               {a->erase, nh * a->erase_width, DN_F32},
+                               {a->write, nh * a->write_width, DN_F32},
+                               {a->has_gate ? a->g : nullptr, nh * a->decay_width, DN_F32},
+                               {a->state_in, ns, DN_F32}};
+    if (int rc = nonfinite_check(in, stream, "inputs")) return rc;
+  }
+  hipError_t e = launch_step(*a, resolve_scale(a->scale, a->head_k_dim), stream);
+  if (e != hipSuccess) return hip_fail(e, "dn_step launch");
+  if (a->check_finite) {
+    std::vector<Guarded> out = {{a->y, nh * a->head_v_dim, a->y_dtype},
+                                {a->state_out, ns, DN_F32}};
+    if (int rc = nonfinite_check(out, stream, "outputs")) return rc;
+  }
+  return DN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,97 @@
+// Shared device/host helpers of the delta-rule core (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstddef>
+
+#include "deltanet_core.h"
+
+namespace dn {
+
+// ---------------------------------------------------------------------------
+// bf16 as raw bits: the inputs are plain 16-bit buffers; arithmetic is fp32.
+// ---------------------------------------------------------------------------
+
+struct bf16 {
+  uint16_t bits;
+};
+
+__host__ __device__ inline float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(uint32_t(b) << 16);
+}
+
+// Round to nearest even (NaN stays NaN).
+__host__ __device__ inline uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return uint16_t((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+
+template <class T>
+__device__ inline float ld(const T* p, size_t i);
+template <>
+__device__ inline float ld<float>(const float* p, size_t i) {
+  return p[i];
+}
+template <>
+__device__ inline float ld<bf16>(const bf16* p, size_t i) {
+  return bf16_to_f32(p[i].bits);
+}
+
+template <class T>
+__device__ inline void st(T* p, size_t i, float v);
+template <>
+__device__ inline void st<float>(float* p, size_t i, float v) {
+  p[i] = v;
+}
+template <>
+__device__ inline void st<bf16>(bf16* p, size_t i, float v) {
+  p[i].bits = f32_to_bf16(v);
+}
+
+// ---------------------------------------------------------------------------
+// Problem dimensions shared by the chunk kernels.
+// ---------------------------------------------------------------------------
+
+struct Dims {
+  int B, S, H, K, V;
+  int ew, ww, dw;  // gate widths; dw = 0 when ungated
+  int L, N;        // chunk_len, nchunks = ceil(S / L)
+  float scale;
+};
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// Launch helpers (defined in the per-path translation units).
+hipError_t launch_step(const dn_step_args& a, float scale, hipStream_t stream);
+
+struct GenericFwdPlan {
+  size_t ws_bytes;
+};
+size_t generic_fwd_workspace(const Dims& d);
+hipError_t generic_fwd(const Dims& d, int qkv_dtype, int y_dtype, const void* q, const void* k,
+                       const void* v, const float* erase, const float* write, const float* g,
+                       const float* state_in, void* y, float* state_out, void* ws,
+                       hipStream_t stream);
+size_t generic_bwd_workspace(const Dims& d);
+hipError_t generic_bwd(const Dims& d, int qkv_dtype, int grad_dtype, const void* dy,
+                       const float* dstate_final, const void* q, const void* k, const void* v,
+                       const float* erase, const float* write, const float* g,
+                       const float* state_in, void* dq, void* dk, void* dv, float* derase,
+                       float* dwrite, float* dg, float* dstate, void* ws, hipStream_t stream);
+
+bool mfma_fwd_supported(const Dims& d, int qkv_dtype, int y_dtype);
+size_t mfma_fwd_workspace(const Dims& d);
+hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, const void* v,
+                    const float* erase, const float* write, const float* g,
+                    const float* state_in, void* y, float* state_out, void* ws,
+                    hipStream_t stream);
+
+// NaN/Inf guard: sets *flag (device int) to 1 if any element is not finite.
+hipError_t launch_nonfinite_scan(const void* p, size_t n, int dtype, int* flag,
+                                 hipStream_t stream);
+
+}  // namespace dn

@@ -1,0 +1,247 @@
+// dn_step: one delta-rule tick (src/delta/recurrent.rs:41-99) as a single
+// read-modify-write pass over the fp32 state.
+//
+// The reference evaluates S⁻ = α⊙S, r = S⁻ᵀ(k⊙erase), u = v⊙write − r,
+// S = S⁻ + k uᵀ, y = Sᵀ(scale·q) as separate tensor ops, each a pass over
+// [batch, nheads, K, V]. Here both reductions come from one read of S:
+//     y = Sᵀq' = S⁻ᵀq' + u (kᵀq'),
+// so each element of S is read once and written once — the HBM roofline of
+// the step is 2·4·K·V bytes per head plus the token's vectors.
+//
+// Work split: one workgroup of 256 lanes per (column tile of 64, head, batch).
+// Lane t owns columns 4·(t mod 16) … +3 of the tile and rows (t div 16) + 16·r,
+// holding its slice of S in registers between the read and the write.
+
+#include "dn_common.hpp"
+
+namespace dn {
+namespace {
+
+struct StepParams {
+  int B, H, K, V, ew, ww, dw;
+  float scale;
+  const void *q, *k, *v;
+  const float *erase, *write, *g;
+  const float* s_in;
+  void* y;
+  float* s_out;
+};
+
+constexpr int kTileV = 64;
+constexpr int kThreads = 256;
+constexpr int kRowGroups = kThreads / (kTileV / 4);  // 16
+
+__device__ inline float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+  return x;
+}
+
+template <class TQ, class TY, int RPT, bool VEC4>
+__global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
+  const int tile = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x;
+  const int cg = tid & 15, rg = tid >> 4;
+  const int K = p.K, V = p.V;
+  const int j0 = tile * kTileV + 4 * cg;
+  const size_t bh = size_t(b) * p.H + h;
+
+  extern __shared__ float lds[];
+  float* s_k = lds;            // k
+  float* s_ke = s_k + K;       // k ⊙ erase
+  float* s_q = s_ke + K;       // scale · q
+  float* s_a = s_q + K;        // exp(g) per key row
+  float* red_r = s_a + K;      // [16][64]
+  float* red_q = red_r + kRowGroups * kTileV;
+  float* s_u = red_q + kRowGroups * kTileV;  // [64]
+  float* s_kq = s_u + kTileV;                // [1]
+
+  const TQ* q = static_cast<const TQ*>(p.q) + bh * K;
+  const TQ* k = static_cast<const TQ*>(p.k) + bh * K;
+  for (int i = tid; i < K; i += kThreads) {
+    const float ki = ld(k, i);
+    s_k[i] = ki;
+    s_ke[i] = ki * p.erase[bh * p.ew + (p.ew == 1 ? 0 : i)];
+    s_q[i] = p.scale * ld(q, i);
+    s_a[i] = p.dw ? expf(p.g[bh * p.dw + (p.dw == 1 ? 0 : i)]) : 1.0f;
+  }
+  __syncthreads();
+  if (tid < 64) {
+    float acc = 0.f;
+    for (int i = tid; i < K; i += 64) acc += s_k[i] * s_q[i];
+    acc = wave_sum(acc);
+    if (tid == 0) s_kq[0] = acc;
+  }
+
+  // Read S once; decay it; both partial reductions.
+  const float* sin = p.s_in + bh * size_t(K) * V;
+  float s[RPT][4];
+  float pr[4] = {0.f, 0.f, 0.f, 0.f}, pq[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg + kRowGroups * r;
+    if (i < K) {
+      const float* row = sin + size_t(i) * V + j0;
+      if (VEC4 && j0 + 3 < V) {
+        const float4 x = *reinterpret_cast<const float4*>(row);
+        s[r][0] = x.x;
+        s[r][1] = x.y;
+        s[r][2] = x.z;
+        s[r][3] = x.w;
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) s[r][c] = (j0 + c < V) ? row[c] : 0.f;
+      }
+      const float a = s_a[i], ke = s_ke[i], qq = s_q[i];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        s[r][c] *= a;
+        pr[c] += s[r][c] * ke;
+        pq[c] += s[r][c] * qq;
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    red_r[rg * kTileV + 4 * cg + c] = pr[c];
+    red_q[rg * kTileV + 4 * cg + c] = pq[c];
+  }
+  __syncthreads();
+
+  // u = v ⊙ write − r;  y = S⁻ᵀq' + u (kᵀq').
+  if (tid < kTileV) {
+    const int j = tile * kTileV + tid;
+    float rr = 0.f, qs = 0.f;
+#pragma unroll
+    for (int x = 0; x < kRowGroups; ++x) {
+      rr += red_r[x * kTileV + tid];
+      qs += red_q[x * kTileV + tid];
+    }
+    float u = 0.f;
+    if (j < V) {
+      const TQ* v = static_cast<const TQ*>(p.v) + bh * V;
+      u = ld(v, j) * p.write[bh * p.ww + (p.ww == 1 ? 0 : j)] - rr;
+      st(static_cast<TY*>(p.y), bh * V + j, qs + u * s_kq[0]);
+    }
+    s_u[tid] = u;
+  }
+  __syncthreads();
+
+  // S = S⁻ + k uᵀ, written once.
+  float* sout = p.s_out + bh * size_t(K) * V;
+  float u4[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) u4[c] = s_u[4 * cg + c];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg + kRowGroups * r;
+    if (i < K) {
+      const float ki = s_k[i];
+      float* row = sout + size_t(i) * V + j0;
+      if (VEC4 && j0 + 3 < V) {
+        float4 x;
+        x.x = s[r][0] + ki * u4[0];
+        x.y = s[r][1] + ki * u4[1];
+        x.z = s[r][2] + ki * u4[2];
+        x.w = s[r][3] + ki * u4[3];
+        *reinterpret_cast<float4*>(row) = x;
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          if (j0 + c < V) row[c] = s[r][c] + ki * u4[c];
+      }
+    }
+  }
+}
+
+// Fallback for head_k_dim > 512: one workgroup per (head, batch), two passes
+// over S (one lane per column).
+template <class TQ, class TY>
+__global__ __launch_bounds__(kThreads) void step_wide_kernel(StepParams p) {
+  const int h = blockIdx.y, b = blockIdx.z;
+  const size_t bh = size_t(b) * p.H + h;
+  const int K = p.K, V = p.V;
+  const TQ* q = static_cast<const TQ*>(p.q) + bh * K;
+  const TQ* k = static_cast<const TQ*>(p.k) + bh * K;
+  const TQ* v = static_cast<const TQ*>(p.v) + bh * V;
+  const float* sin = p.s_in + bh * size_t(K) * V;
+  float* sout = p.s_out + bh * size_t(K) * V;
+  for (int j = threadIdx.x; j < V; j += kThreads) {
+    float rr = 0.f, qs = 0.f, kq = 0.f;
+    for (int i = 0; i < K; ++i) {
+      const float a = p.dw ? expf(p.g[bh * p.dw + (p.dw == 1 ? 0 : i)]) : 1.0f;
+      const float sv = sin[size_t(i) * V + j] * a;
+      const float ki = ld(k, i);
+      rr += sv * ki * p.erase[bh * p.ew + (p.ew == 1 ? 0 : i)];
+      const float qi = p.scale * ld(q, i);
+      qs += sv * qi;
+      kq += ki * qi;
+    }
+    const float u = ld(v, j) * p.write[bh * p.ww + (p.ww == 1 ? 0 : j)] - rr;
+    st(static_cast<TY*>(p.y), bh * V + j, qs + u * kq);
+    for (int i = 0; i < K; ++i) {
+      const float a = p.dw ? expf(p.g[bh * p.dw + (p.dw == 1 ? 0 : i)]) : 1.0f;
+      sout[size_t(i) * V + j] = sin[size_t(i) * V + j] * a + ld(k, i) * u;
+    }
+  }
+}
+
+template <class TQ, class TY>
+hipError_t launch_typed(const StepParams& p, hipStream_t stream) {
+  const bool vec4 = (p.V % 4) == 0 &&
+                    ((reinterpret_cast<uintptr_t>(p.s_in) | reinterpret_cast<uintptr_t>(p.s_out)) %
+                     16) == 0;
+  const int rpt_needed = (p.K + kRowGroups - 1) / kRowGroups;
+  dim3 grid((p.V + kTileV - 1) / kTileV, p.H, p.B);
+  const size_t lds = sizeof(float) * (4 * size_t(p.K) + 2 * kRowGroups * kTileV + kTileV + 1);
+#define DN_STEP_LAUNCH(RPT)                                                                   \
+  do {                                                                                        \
+    if (vec4)                                                                                 \
+      hipLaunchKernelGGL((step_tile_kernel<TQ, TY, RPT, true>), grid, dim3(kThreads), lds,   \
+                         stream, p);                                                          \
+    else                                                                                      \
+      hipLaunchKernelGGL((step_tile_kernel<TQ, TY, RPT, false>), grid, dim3(kThreads), lds,  \
+                         stream, p);                                                          \
+    return hipGetLastError();                                                                 \
+  } while (0)
+  if (rpt_needed <= 1) DN_STEP_LAUNCH(1);
+  if (rpt_needed <= 2) DN_STEP_LAUNCH(2);
+  if (rpt_needed <= 4) DN_STEP_LAUNCH(4);
+  if (rpt_needed <= 8) DN_STEP_LAUNCH(8);
+  if (rpt_needed <= 16) DN_STEP_LAUNCH(16);
+  if (rpt_needed <= 32) DN_STEP_LAUNCH(32);
+#undef DN_STEP_LAUNCH
+  hipLaunchKernelGGL((step_wide_kernel<TQ, TY>), dim3(1, p.H, p.B), dim3(kThreads), 0, stream,
+                     p);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_step(const dn_step_args& a, float scale, hipStream_t stream) {
+  StepParams p;
+  p.B = int(a.batch);
+  p.H = int(a.nheads);
+  p.K = int(a.head_k_dim);
+  p.V = int(a.head_v_dim);
+  p.ew = int(a.erase_width);
+  p.ww = int(a.write_width);
+  p.dw = a.has_gate ? int(a.decay_width) : 0;
+  p.scale = scale;
+  p.q = a.q;
+  p.k = a.k;
+  p.v = a.v;
+  p.erase = a.erase;
+  p.write = a.write;
+  p.g = a.g;
+  p.s_in = a.state_in;
+  p.y = a.y;
+  p.s_out = a.state_out;
+  const bool qb = a.qkv_dtype == DN_BF16, yb = a.y_dtype == DN_BF16;
+  if (qb && yb) return launch_typed<bf16, bf16>(p, stream);
+  if (qb) return launch_typed<bf16, float>(p, stream);
+  if (yb) return launch_typed<float, bf16>(p, stream);
+  return launch_typed<float, float>(p, stream);
+}
+
+}  // namespace dn

@@ -1,0 +1,172 @@
+/* deltanet_core.h — C ABI of the MI355X (gfx950) delta-rule core.
+ *
+ * Drop-in boundary for burn-deltanet's delta-rule core (Rust crate
+ * `burn-deltanet` v0.14.0). Three entry points replace the reference's three
+ * interfaces on the hot path:
+ *
+ *   dn_chunk_fwd  ← DeltaChunkBackendExt::delta_chunk_recalculated
+ *                   (src/delta/chunk_recalculated/chunk_recalculated.rs:86-151;
+ *                    reached through DeltaInput::run, src/delta/path.rs:215-231)
+ *   dn_step       ← delta_step (src/delta/recurrent.rs:41-99)
+ *   dn_chunk_bwd  ← combined_backward
+ *                   (src/delta/chunk_recalculated/combined_backward.rs:72-189,
+ *                    called from the autodiff node, backward.rs:82-170)
+ *
+ * Conventions (src/delta/path.rs:120-141). All tensors are dense row-major
+ * device buffers in the reference's axis order:
+ *   q, k      [batch, sequence, nheads, head_k_dim]      dtype qkv_dtype
+ *   v         [batch, sequence, nheads, head_v_dim]      dtype qkv_dtype
+ *   erase     [batch, sequence, nheads, erase_width]     float32, width 1 | head_k_dim
+ *   write     [batch, sequence, nheads, write_width]     float32, width 1 | head_v_dim
+ *   g         [batch, sequence, nheads, decay_width]     float32, width 1 | head_k_dim,
+ *             log forget gate g = log α ≤ 0; read only when has_gate != 0
+ *   state     [batch, nheads, head_k_dim, head_v_dim]    float32
+ *   y         [batch, sequence, nheads, head_v_dim]      dtype y_dtype
+ * For dn_step the `sequence` axis is absent ([batch, nheads, ·]).
+ * q and k arrive L2-normalised and unscaled; `scale` is applied to q inside
+ * (NaN selects 1/sqrt(head_k_dim), path.rs:161-165). The core applies exp(g)
+ * and nothing else to the gates.
+ *
+ * The reference is functional; here outputs are written to caller buffers.
+ * state_out may alias state_in (an in-place update of the state). No other
+ * output may alias an input.
+ *
+ * Every call is asynchronous on `stream` (NULL = the default stream) unless
+ * check_finite is set, which synchronises to read the NaN/Inf guard back.
+ * Return value: DN_OK or a negative dn_status; dn_last_error() gives the text
+ * of the reference's assertion that the status mirrors.
+ */
+#ifndef DELTANET_CORE_H
+#define DELTANET_CORE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  DN_F32 = 0,
+  DN_BF16 = 1,
+} dn_dtype;
+
+/* Which kernels run dn_chunk_fwd / dn_chunk_bwd. AUTO picks the MFMA path
+ * whenever the shape and dtypes allow it. */
+typedef enum {
+  DN_ALGO_AUTO = 0,
+  DN_ALGO_GENERIC = 1, /* fp32 arithmetic, any shape */
+  DN_ALGO_MFMA = 2,    /* bf16 MFMA tiles; DN_ERR_UNSUPPORTED if the shape does not fit */
+} dn_algo;
+
+typedef enum {
+  DN_OK = 0,
+  DN_ERR_SEQUENCE = -1,    /* "sequence length must be at least 1" (path.rs:179) */
+  DN_ERR_SHAPE = -2,       /* a dimension < 1, or shapes that disagree (path.rs:180-185,
+                              recurrent.rs:51-54) */
+  DN_ERR_GATE_WIDTH = -3,  /* "{gate}: last axis must be 1 or {full}" (path.rs:187-197) */
+  DN_ERR_CHUNK_LEN = -4,   /* "chunk_len must be at least 1" (path.rs:219) */
+  DN_ERR_NONFINITE = -5,   /* NaN/Inf guard on inputs or outputs (sanity, path.rs:198-207) */
+  DN_ERR_NULL = -6,        /* a required pointer is NULL */
+  DN_ERR_DTYPE = -7,       /* unknown dtype tag */
+  DN_ERR_WORKSPACE = -8,   /* caller workspace smaller than dn_*_workspace_bytes() */
+  DN_ERR_UNSUPPORTED = -9, /* DN_ALGO_MFMA requested for a shape it does not cover */
+  DN_ERR_HIP = -10,        /* a HIP runtime call failed */
+} dn_status;
+
+/* DeltaChunkBackendExt::delta_chunk_recalculated (chunk_recalculated.rs:115-151). */
+typedef struct {
+  int64_t batch, sequence, nheads, head_k_dim, head_v_dim;
+  int64_t erase_width, write_width, decay_width; /* decay_width ignored when !has_gate */
+  int32_t has_gate;
+  int32_t chunk_len;     /* tokens per chunk, >= 1; the reference default is 64 */
+  double scale;          /* NaN => 1/sqrt(head_k_dim) */
+  int32_t qkv_dtype;     /* dn_dtype of q, k, v */
+  int32_t y_dtype;       /* dn_dtype of y */
+  int32_t algo;          /* dn_algo */
+  int32_t check_finite;  /* nonzero: NaN/Inf guard on inputs and outputs (synchronises) */
+  const void *q, *k, *v;
+  const float *erase, *write, *g;
+  const float *state_in;
+  void *y;
+  float *state_out;
+  void *workspace;         /* NULL => library-managed workspace */
+  size_t workspace_bytes;
+} dn_chunk_fwd_args;
+
+/* combined_backward (combined_backward.rs:72-189). Same leaves as the forward,
+ * plus the two incoming cotangents; writes the seven gradients. d_erase,
+ * d_write and d_g are reduced to their gate's own width (forward.rs:106-112);
+ * d_g is the gradient with respect to g = log α. */
+typedef struct {
+  int64_t batch, sequence, nheads, head_k_dim, head_v_dim;
+  int64_t erase_width, write_width, decay_width;
+  int32_t has_gate;
+  int32_t chunk_len;
+  double scale;
+  int32_t qkv_dtype;     /* dtype of q, k, v */
+  int32_t grad_dtype;    /* dtype of d_y and of d_q, d_k, d_v */
+  int32_t algo;
+  int32_t check_finite;
+  const void *d_y;               /* [batch, sequence, nheads, head_v_dim] */
+  const float *d_state_final;    /* [batch, nheads, head_k_dim, head_v_dim]; NULL = zeros */
+  const void *q, *k, *v;
+  const float *erase, *write, *g;
+  const float *state_in;
+  void *d_q, *d_k, *d_v;
+  float *d_erase, *d_write, *d_g; /* d_g may be NULL when !has_gate */
+  float *d_state;
+  void *workspace;
+  size_t workspace_bytes;
+} dn_chunk_bwd_args;
+
+/* delta_step (recurrent.rs:41-99): one tick for all heads. */
+typedef struct {
+  int64_t batch, nheads, head_k_dim, head_v_dim;
+  int64_t erase_width, write_width, decay_width;
+  int32_t has_gate;
+  double scale;          /* NaN => 1/sqrt(head_k_dim) */
+  int32_t qkv_dtype;
+  int32_t y_dtype;
+  int32_t check_finite;
+  const void *q, *k, *v;        /* [batch, nheads, head_k_dim | head_v_dim] */
+  const float *erase, *write, *g;
+  const float *state_in;        /* [batch, nheads, head_k_dim, head_v_dim] */
+  void *y;                      /* [batch, nheads, head_v_dim] */
+  float *state_out;             /* may alias state_in */
+} dn_step_args;
+
+/* Replaces DeltaChunkBackendExt::delta_chunk_recalculated
+ * (src/delta/chunk_recalculated/chunk_recalculated.rs:110-151). */
+int dn_chunk_fwd(const dn_chunk_fwd_args *args, hipStream_t stream);
+
+/* Replaces combined_backward
+ * (src/delta/chunk_recalculated/combined_backward.rs:72-84). */
+int dn_chunk_bwd(const dn_chunk_bwd_args *args, hipStream_t stream);
+
+/* Replaces delta_step (src/delta/recurrent.rs:41-50). */
+int dn_step(const dn_step_args *args, hipStream_t stream);
+
+/* Bytes of device workspace dn_chunk_fwd / dn_chunk_bwd need for these
+ * arguments (0 on invalid arguments). Has no counterpart in the reference,
+ * whose tensors are allocated by Burn; it lets a caller own the memory. */
+size_t dn_chunk_fwd_workspace_bytes(const dn_chunk_fwd_args *args);
+size_t dn_chunk_bwd_workspace_bytes(const dn_chunk_bwd_args *args);
+
+/* Which algorithm AUTO would pick (DN_ALGO_GENERIC or DN_ALGO_MFMA). */
+int dn_chunk_fwd_algo(const dn_chunk_fwd_args *args);
+int dn_chunk_bwd_algo(const dn_chunk_bwd_args *args);
+
+/* Text of the last error on this thread (empty string if none). */
+const char *dn_last_error(void);
+
+/* Library version string. */
+const char *dn_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DELTANET_CORE_H */

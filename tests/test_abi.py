@@ -1,0 +1,128 @@
+"""The C ABI without a GPU: the library loads, exports every symbol that
+include/deltanet_core.h declares, and rejects invalid arguments with the
+status codes that mirror the reference's assertions (path.rs:177-231,
+recurrent.rs:51-54) before touching the device."""
+
+import ctypes
+import re
+
+import pytest
+import torch
+
+from conftest import ROOT, load_package
+
+pkg = load_package()
+abi = pkg.abi
+
+
+def header_symbols():
+    text = (ROOT / "include" / "deltanet_core.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char \*)\s*(dn_\w+)\s*\(", text,
+                                 re.M)))
+
+
+def test_header_declares_the_three_entry_points():
+    syms = header_symbols()
+    for name in ["dn_chunk_fwd", "dn_chunk_bwd", "dn_step"]:
+        assert name in syms
+    assert sorted(abi.EXPORTS) == syms
+
+
+def test_library_exports_every_declared_symbol():
+    lib = abi.lib()
+    for name in header_symbols():
+        assert hasattr(lib, name), name
+    assert b"gfx950" in lib.dn_version()
+
+
+def fwd_args(**over):
+    a = abi.ChunkFwdArgs()
+    a.batch, a.sequence, a.nheads, a.head_k_dim, a.head_v_dim = 1, 8, 1, 4, 6
+    a.erase_width, a.write_width, a.decay_width = 1, 1, 1
+    a.has_gate, a.chunk_len, a.scale = 1, 64, float("nan")
+    a.qkv_dtype = a.y_dtype = abi.DN_F32
+    fake = 0x1000  # never dereferenced: every case below fails its checks first
+    for f in ["q", "k", "v", "erase", "write", "g", "state_in", "y", "state_out"]:
+        setattr(a, f, fake)
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(sequence=0), -1, "sequence length must be at least 1"),
+    (dict(batch=0), -2, "at least 1"),
+    (dict(erase_width=3), -3, "erase gate: last axis must be 1 or 4, got 3"),
+    (dict(write_width=5), -3, "write gate: last axis must be 1 or 6, got 5"),
+    (dict(decay_width=2), -3, "forget gate: last axis must be 1 or 4, got 2"),
+    (dict(chunk_len=0), -4, "chunk_len must be at least 1"),
+    (dict(qkv_dtype=7), -7, "dtype"),
+    (dict(q=None), -6, "NULL"),
+])
+def test_chunk_fwd_rejects_invalid_arguments(over, code, msg):
+    lib = abi.lib()
+    a = fwd_args(**over)
+    rc = lib.dn_chunk_fwd(ctypes.byref(a), None)
+    assert rc == code
+    assert msg in lib.dn_last_error().decode()
+    assert lib.dn_chunk_fwd_workspace_bytes(ctypes.byref(a)) == 0
+
+
+def test_ungated_call_ignores_the_gate_width():
+    """has_gate = 0 is the reference's placeholder gate (chunk_recalculated.rs:50-56):
+    its width is never checked."""
+    a = fwd_args(has_gate=0, decay_width=2, g=None, chunk_len=0)
+    assert abi.lib().dn_chunk_fwd(ctypes.byref(a), None) == -4
+
+
+def test_step_rejects_invalid_arguments():
+    lib = abi.lib()
+    a = abi.StepArgs()
+    a.batch, a.nheads, a.head_k_dim, a.head_v_dim = 1, 1, 4, 6
+    a.erase_width, a.write_width, a.decay_width, a.has_gate = 2, 1, 0, 0
+    a.scale = 1.0
+    assert lib.dn_step(ctypes.byref(a), None) == -3
+    a.erase_width = 1
+    assert lib.dn_step(ctypes.byref(a), None) == -6  # null pointers
+
+
+def test_bwd_rejects_missing_d_g():
+    lib = abi.lib()
+    a = abi.ChunkBwdArgs()
+    a.batch, a.sequence, a.nheads, a.head_k_dim, a.head_v_dim = 1, 4, 1, 4, 4
+    a.erase_width = a.write_width = a.decay_width = 1
+    a.has_gate, a.chunk_len, a.scale = 1, 4, float("nan")
+    for f in ["d_y", "q", "k", "v", "erase", "write", "g", "state_in", "d_q", "d_k", "d_v",
+              "d_erase", "d_write", "d_state"]:
+        setattr(a, f, 0x1000)
+    assert lib.dn_chunk_bwd(ctypes.byref(a), None) == -6
+    a.algo = abi.DN_ALGO_MFMA
+    a.d_g = 0x1000
+    assert lib.dn_chunk_bwd_algo(ctypes.byref(a)) == -9
+
+
+def test_host_mirror_sanity_mirrors_the_reference_asserts():
+    """DeltaInput::sanity (path.rs:177-208) raises before any device work."""
+    z = lambda *s: torch.zeros(*s)
+    good = dict(q_bshk=z(1, 3, 2, 4), k_bshk=z(1, 3, 2, 4), v_bshv=z(1, 3, 2, 6),
+                erase_bshK=z(1, 3, 2, 1), write_bshV=z(1, 3, 2, 1), g_bshK=None,
+                state_bhkv=z(1, 2, 4, 6))
+    pkg.DeltaInput(**good).sanity()
+    with pytest.raises(pkg.DeltaError, match="erase gate: last axis must be 1 or 4, got 3"):
+        pkg.DeltaInput(**{**good, "erase_bshK": z(1, 3, 2, 3)}).sanity()
+    with pytest.raises(pkg.DeltaError, match="forget gate"):
+        pkg.DeltaInput(**{**good, "g_bshK": z(1, 3, 2, 2)}).sanity()
+    with pytest.raises(pkg.DeltaError, match="state"):
+        pkg.DeltaInput(**{**good, "state_bhkv": z(1, 2, 6, 4)}).sanity()
+    with pytest.raises(pkg.DeltaError, match="sequence length"):
+        pkg.DeltaInput(**{**good, "q_bshk": z(1, 0, 2, 4)}).sanity()
+    with pytest.raises(pkg.DeltaError, match="chunk_len must be at least 1"):
+        pkg.DeltaInput(**good).run(pkg.DeltaPath.with_chunk_len(0))
+
+
+def test_delta_path_mirrors_the_reference():
+    P = pkg.DeltaPath
+    assert P.default() == P.chunk() == P("chunk_recalculated")
+    assert P.default().resolved_chunk_len() == 64
+    assert P.recurrent().resolved_chunk_len() == 1
+    assert P.with_chunk_len(16).resolved_chunk_len() == 16
