@@ -1,0 +1,283 @@
+#!/usr/bin/env python3
+"""Benchmark of the delta-rule core on one MI355X.
+
+Headline (BASELINE.json metric "chunk fwd tokens/s + decode step µs (GDN H16
+dk128) at 1 GPU; % roofline"):
+
+* value  = chunkwise forward throughput on BASELINE config 2 (Gated DeltaNet
+  prefill: B=8, H=16, T=4096, dk=128, dv=256, chunk 64; bf16 q/k/v, fp32 β/g
+  and state, bf16 y). One step = one dn_chunk_fwd over the whole batch, inputs
+  already resident in HBM.
+* decode = config 3 (batch 256, H16, dk128, dv256, fp32 state ≈ 537 MB):
+  µs per dn_step over consecutive steps, and its HBM roofline.
+* roofline = the dominant kernel of the forward, timed with HIP events on its
+  own stream by the library's profiler (dn_profile_*), against algorithmic
+  bytes per launch (DESIGN.md lists the per-unit figures).
+* cpu_baseline = the CPU oracle (a C++ restatement of the reference algorithm,
+  incl. its 24·L³ ladder) on a bounded sample of config 2, all host threads.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 3]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+METRIC = "chunk fwd tokens/s + decode step µs (GDN H16 dk128) at 1 GPU; % roofline"
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+
+
+def load_package():
+    sys.path.insert(0, str(ROOT))
+    import __graft_entry__ as ge
+    return ge.load_package()
+
+
+def gdn_inputs(torch, B, T, H, K, V, g_scale, seed, qkv_dtype, device):
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    def l2(x):
+        return x / torch.sqrt((x * x).sum(-1, keepdim=True) + 1e-6)
+    q = l2(torch.randn((B, T, H, K), generator=gen, device=device)).to(qkv_dtype)
+    k = l2(torch.randn((B, T, H, K), generator=gen, device=device)).to(qkv_dtype)
+    v = torch.randn((B, T, H, V), generator=gen, device=device).to(qkv_dtype)
+    beta = torch.sigmoid(torch.randn((B, T, H, 1), generator=gen, device=device))
+    g = -torch.nn.functional.softplus(torch.randn((B, T, H, 1), generator=gen,
+                                                  device=device)) * g_scale
+    return q, k, v, beta, g
+
+
+def bench_chunk_fwd(torch, pkg, steps, warmup, algo):
+    B, T, H, K, V, L = 8, 4096, 16, 128, 256, 64
+    dev = torch.device("cuda:0")
+    q, k, v, beta, g = gdn_inputs(torch, B, T, H, K, V, 0.05, 20260828, torch.bfloat16, dev)
+    s0 = torch.zeros((B, H, K, V), dtype=torch.float32, device=dev)
+    y = torch.empty((B, T, H, V), dtype=torch.bfloat16, device=dev)
+    s1 = torch.empty_like(s0)
+    abi = pkg.abi
+    args = abi.chunk_fwd_args(q, k, v, beta, beta, g, s0, y, s1, L, None, algo=algo)
+    ws_bytes = abi.lib().dn_chunk_fwd_workspace_bytes(args)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
+    chosen = abi.lib().dn_chunk_fwd_algo(args)
+    run = lambda: abi.run_chunk_fwd(args)
+    for _ in range(warmup):
+        run()
+    torch.cuda.synchronize()
+    abi.profile_enable(True)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record()
+    for _ in range(steps):
+        run()
+    stop.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    prof = abi.profile_read()
+    abi.profile_enable(False)
+    ms = start.elapsed_time(stop) / steps
+    tokens = B * T
+    G = B * (T // L) * H
+    # Algorithmic bytes per launch of each forward kernel.
+    qk = 2 * B * T * H * K * 2          # q and k, bf16
+    vb = B * T * H * V * 2              # v, bf16
+    yb = B * T * H * V * 2              # y, bf16
+    gates = 2 * B * T * H * 4           # β and g, fp32
+    st = B * H * K * V * 4              # one fp32 state
+    tri = 3 * G * L * L * 2             # T (hi, lo) and attn, bf16
+    gcb = G * L * 4                     # in-chunk cumulative gate, fp32
+    kernel_bytes = {
+        "dn_mfma_intra": qk + gates + tri + gcb,
+        "dn_mfma_scan": qk + vb + yb + 2 * gates + tri + gcb + 2 * st,
+    }
+    flops_unit = 6 * L * L * K + 4 * L * L * V + 6 * L * K * V + L ** 3 / 3
+    path_bytes = qk + vb + yb + gates + 2 * st
+    return dict(ms=ms, wall_ms=wall * 1e3 / steps, tokens=tokens, prof=prof,
+                kernel_bytes=kernel_bytes, path_bytes=path_bytes,
+                path_flops=G * flops_unit, algo=chosen, ws_bytes=ws_bytes)
+
+
+def bench_decode(torch, pkg, steps, warmup):
+    B, H, K, V = 256, 16, 128, 256
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20260829)
+    S = torch.randn((B, H, K, V), generator=gen, device=dev) * 0.02
+    n_tok = steps  # one distinct token per timed step: a steps-token sequence
+    l2 = lambda x: x / torch.sqrt((x * x).sum(-1, keepdim=True) + 1e-6)
+    q = l2(torch.randn((n_tok, B, H, K), generator=gen, device=dev))
+    k = l2(torch.randn((n_tok, B, H, K), generator=gen, device=dev))
+    v = torch.randn((n_tok, B, H, V), generator=gen, device=dev)
+    beta = torch.sigmoid(torch.randn((n_tok, B, H, 1), generator=gen, device=dev))
+    g = -torch.nn.functional.softplus(torch.randn((n_tok, B, H, 1), generator=gen,
+                                                  device=dev)) * 0.05
+    y = torch.empty((B, H, V), dtype=torch.float32, device=dev)
+    abi = pkg.abi
+    argv = [abi.step_args(q[t], k[t], v[t], beta[t], beta[t], g[t], S, y, S, None)
+            for t in range(n_tok)]
+    lib = abi.lib()
+    import ctypes
+    stream = abi.stream_handle()
+    refs = [ctypes.byref(a) for a in argv]
+    def run(t):
+        rc = lib.dn_step(refs[t % n_tok], stream)
+        if rc:
+            abi.check(rc)
+    for t in range(warmup):
+        run(t)
+    torch.cuda.synchronize()
+    abi.profile_enable(True)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for t in range(steps):
+        run(t)
+    stop.record()
+    torch.cuda.synchronize()
+    prof = abi.profile_read()
+    abi.profile_enable(False)
+    us = start.elapsed_time(stop) * 1e3 / steps
+    step_bytes = 2 * B * H * K * V * 4 + B * H * (2 * K + 2 * V + 2) * 4
+    name = "dn_step_tile"
+    k_us = prof[name][0] * 1e3 / prof[name][1] if name in prof else us
+    return dict(us=us, kernel_us=k_us, bytes=step_bytes, prof=prof)
+
+
+def cpu_baseline(torch):
+    """The oracle on the whole config-2 workload (B=8, H=16, T=4096: 32768
+    tokens), fp32, all available host threads (OMP_NUM_THREADS)."""
+    import numpy as np
+    sys.path.insert(0, str(ROOT))
+    from oracle import oracle as O
+    B, T, H, K, V, L = 8, 4096, 16, 128, 256, 64
+    rng = np.random.default_rng(20260828)
+    l2 = lambda x: x / np.sqrt((x * x).sum(-1, keepdims=True) + 1e-6)
+    q = l2(rng.standard_normal((B, T, H, K), dtype=np.float32))
+    k = l2(rng.standard_normal((B, T, H, K), dtype=np.float32))
+    v = rng.standard_normal((B, T, H, V), dtype=np.float32)
+    beta = (1 / (1 + np.exp(-rng.standard_normal((B, T, H, 1))))).astype(np.float32)
+    g = (-np.log1p(np.exp(rng.standard_normal((B, T, H, 1)))) * 0.05).astype(np.float32)
+    s0 = np.zeros((B, H, K, V), np.float32)
+    threads = O.max_threads()
+    O.chunk_fwd(q[:, :64], k[:, :64], v[:, :64], beta[:, :64], beta[:, :64], g[:, :64], s0,
+                chunk_len=L, dtype=np.float32)
+    t0 = time.perf_counter()
+    O.chunk_fwd(q, k, v, beta, beta, g, s0, chunk_len=L, dtype=np.float32)
+    dt = time.perf_counter() - t0
+    return dict(value=B * T / dt, unit="tokens/s", cores=threads, kind="port",
+                sample=f"full config 2 (B=8 H=16 T=4096 dk=128 dv=256, 32768 tokens), "
+                       f"fp32, {threads} OpenMP threads, {dt:.2f} s")
+
+
+def traffic_from_profiles(kernel):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
+    path = ROOT / "profiles" / "traffic.json"
+    if not path.exists():
+        return None
+    try:
+        data = json.loads(path.read_text())
+        return data.get(kernel, {}).get("bytes_per_launch")
+    except (ValueError, OSError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--decode-steps", type=int, default=1000)
+    ap.add_argument("--algo", choices=["auto", "generic", "mfma"], default="auto")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-decode", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one GPU only: the delta-rule core shards over (batch, "
+              "head) with no communication (DESIGN.md), and this build runs no "
+              "multi-GPU path. Use --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    pkg = load_package()
+    algo = {"auto": 0, "generic": 1, "mfma": 2}[args.algo]
+    print(f"[bench] chunk forward: config 2, {args.warmup} warmup + {args.steps} steps",
+          file=sys.stderr, flush=True)
+    fw = bench_chunk_fwd(torch, pkg, args.steps, args.warmup, algo)
+    tok_s = fw["tokens"] / (fw["ms"] / 1e3)
+    prof = fw["prof"]
+    dom = max(prof, key=lambda n: prof[n][0]) if prof else None
+    roof = None
+    if dom:
+        avg_s = prof[dom][0] / prof[dom][1] / 1e3
+        nbytes = fw["kernel_bytes"].get(dom)
+        if nbytes:
+            ach = nbytes / avg_s / 1e9
+            roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1),
+                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                    "traffic": traffic_from_profiles(dom),
+                    "avg_launch_us": round(avg_s * 1e6, 2),
+                    "algorithmic_bytes": nbytes}
+    per_kernel = {n: {"avg_us": round(v[0] / v[1] * 1e3, 2), "launches": v[1]}
+                  for n, v in prof.items()}
+    print(f"[bench] forward {fw['ms']:.3f} ms/step, {tok_s:.3e} tokens/s, kernels "
+          f"{per_kernel}", file=sys.stderr, flush=True)
+
+    decode = None
+    if not args.no_decode:
+        print(f"[bench] decode: config 3, {args.decode_steps} steps", file=sys.stderr,
+              flush=True)
+        dc = bench_decode(torch, pkg, args.decode_steps, 10)
+        gbs = dc["bytes"] / (dc["kernel_us"] * 1e-6) / 1e9
+        decode = {"us_per_step": round(dc["us"], 2), "kernel_us": round(dc["kernel_us"], 2),
+                  "steps": args.decode_steps, "bytes_per_step": dc["bytes"],
+                  "achieved_GBs": round(gbs, 1), "peak_GBs": HBM_PEAK_GBS,
+                  "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        print(f"[bench] decode {decode}", file=sys.stderr, flush=True)
+
+    cpu = None
+    if not args.no_cpu:
+        print("[bench] cpu baseline (oracle)", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(torch)
+        cpu["value"] = round(cpu["value"], 1)
+
+    path_gbs = fw["path_bytes"] / (fw["ms"] / 1e3) / 1e9
+    out = {
+        "metric": METRIC,
+        "value": round(tok_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(fw["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "config 2: Gated DeltaNet chunkwise prefill (core forward)",
+                   "batch": 8, "seq_len": 4096, "nheads": 16, "head_k_dim": 128,
+                   "head_v_dim": 256, "chunk_len": 64, "qkv": "bf16", "state": "fp32",
+                   "y": "bf16", "algo": {1: "generic", 2: "mfma"}.get(fw["algo"], fw["algo"])},
+        "roofline": roof,
+        "path_roofline": {"bound": "hbm", "achieved": round(path_gbs, 1),
+                          "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                          "frac": round(path_gbs / HBM_PEAK_GBS, 4),
+                          "algorithmic_bytes": fw["path_bytes"],
+                          "mfma_TFLOPs": round(fw["path_flops"] / (fw["ms"] / 1e3) / 1e12, 2)},
+        "kernels": per_kernel,
+        "decode": decode,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -37,7 +37,7 @@ STATUS = {
 EXPORTS = [
     "dn_chunk_fwd", "dn_chunk_bwd", "dn_step", "dn_chunk_fwd_workspace_bytes",
     "dn_chunk_bwd_workspace_bytes", "dn_chunk_fwd_algo", "dn_chunk_bwd_algo",
-    "dn_last_error", "dn_version",
+    "dn_last_error", "dn_version", "dn_profile_enable", "dn_profile_read",
 ]
 
 _i64, _i32, _f64, _vp, _sz = (ctypes.c_int64, ctypes.c_int32, ctypes.c_double,
@@ -106,6 +106,12 @@ def lib() -> ctypes.CDLL:
         L.dn_chunk_fwd_algo.restype = ctypes.c_int
         L.dn_chunk_bwd_algo.argtypes = [ctypes.POINTER(ChunkBwdArgs)]
         L.dn_chunk_bwd_algo.restype = ctypes.c_int
+        L.dn_profile_enable.argtypes = [ctypes.c_int]
+        L.dn_profile_enable.restype = ctypes.c_int
+        L.dn_profile_read.argtypes = [ctypes.c_int, ctypes.c_char_p, _sz,
+                                      ctypes.POINTER(ctypes.c_double),
+                                      ctypes.POINTER(ctypes.c_int64)]
+        L.dn_profile_read.restype = ctypes.c_int
         L.dn_last_error.restype = ctypes.c_char_p
         L.dn_version.restype = ctypes.c_char_p
         _LIB = L
@@ -229,3 +235,22 @@ def chunk_bwd_args(dy, dstate, q, k, v, erase, write, g, state, grads, chunk_len
 
 def run_chunk_bwd(args: ChunkBwdArgs) -> None:
     check(lib().dn_chunk_bwd(ctypes.byref(args), stream_handle()))
+
+
+def profile_enable(on: bool = True) -> None:
+    """Start (clearing earlier records) or stop per-kernel HIP-event timing."""
+    lib().dn_profile_enable(1 if on else 0)
+
+
+def profile_read() -> dict:
+    """{kernel name: (total_ms, launches)} for everything timed since enable."""
+    L = lib()
+    out = {}
+    count = L.dn_profile_read(-1, None, 0, None, None)
+    for i in range(count):
+        name = ctypes.create_string_buffer(128)
+        ms = ctypes.c_double()
+        n = ctypes.c_int64()
+        L.dn_profile_read(i, name, 128, ctypes.byref(ms), ctypes.byref(n))
+        out[name.value.decode()] = (ms.value, n.value)
+    return out

@@ -786,6 +786,7 @@ static hipError_t launch_intra(const Dims& d, int qkv_dtype, const void* q, cons
                                const void* v, const float* erase, const float* write,
                                const float* g, float* ws, hipStream_t stream) {
   IntraParams p{d, make_layout(d), q, k, v, erase, write, g, ws};
+  ProfScope ps("dn_generic_intra", stream);
   if (qkv_dtype == DN_BF16)
     hipLaunchKernelGGL(intra_kernel<bf16>, dim3(unsigned(G_of(d))), dim3(kThreads), 0, stream,
                        p);
@@ -806,6 +807,7 @@ hipError_t generic_fwd(const Dims& d, int qkv_dtype, int y_dtype, const void* q,
   ScanParams sp{d, make_layout(d), tile, ws, state_in, y, state_out, nullptr};
   dim3 grid((d.V + tile - 1) / tile, d.H, d.B);
   const size_t lds = scan_lds(d, tile, 1);
+  ProfScope ps("dn_generic_scan", stream);
   if (y_dtype == DN_BF16)
     hipLaunchKernelGGL(scan_kernel<bf16>, grid, dim3(kThreads), lds, stream, sp);
   else
@@ -835,20 +837,27 @@ hipError_t generic_bwd(const Dims& d, int qkv_dtype, int grad_dtype, const void*
   // Forward scan keeping the state entering each chunk; its final state goes
   // to d_state as scratch and is overwritten by the reverse scan.
   ScanParams sp{d, make_layout(d), tile, ws, state_in, nullptr, dstate, states};
-  hipLaunchKernelGGL(scan_kernel<float>, grid, dim3(kThreads), scan_lds(d, tile, 1), stream,
-                     sp);
+  {
+    ProfScope ps("dn_generic_scan_states", stream);
+    hipLaunchKernelGGL(scan_kernel<float>, grid, dim3(kThreads), scan_lds(d, tile, 1), stream,
+                       sp);
+  }
   if ((e = hipGetLastError()) != hipSuccess) return e;
   RevScanParams rp{d, make_layout(d), tile, ws, dy, dstate_final, dstate, ds_after};
-  if (grad_dtype == DN_BF16)
-    hipLaunchKernelGGL(rev_scan_kernel<bf16>, grid, dim3(kThreads), scan_lds(d, tile, 2),
-                       stream, rp);
-  else
-    hipLaunchKernelGGL(rev_scan_kernel<float>, grid, dim3(kThreads), scan_lds(d, tile, 2),
-                       stream, rp);
+  {
+    ProfScope ps("dn_generic_rev_scan", stream);
+    if (grad_dtype == DN_BF16)
+      hipLaunchKernelGGL(rev_scan_kernel<bf16>, grid, dim3(kThreads), scan_lds(d, tile, 2),
+                         stream, rp);
+    else
+      hipLaunchKernelGGL(rev_scan_kernel<float>, grid, dim3(kThreads), scan_lds(d, tile, 2),
+                         stream, rp);
+  }
   if ((e = hipGetLastError()) != hipSuccess) return e;
   ChunkBwdParams cp{d,     make_layout(d), make_bwd_layout(d), ws,     bws,   states,
                     ds_after, dy,           dq,                 dk,     dv,    derase,
                     dwrite,   dg};
+  ProfScope ps("dn_generic_chunk_bwd", stream);
   if (grad_dtype == DN_BF16)
     hipLaunchKernelGGL(chunk_bwd_kernel<bf16>, dim3(unsigned(G)), dim3(kThreads), 0, stream, cp);
   else

@@ -90,6 +90,15 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
                     const float* state_in, void* y, float* state_out, void* ws,
                     hipStream_t stream);
 
+// Per-kernel HIP-event timing (dn_profile_enable): a scope records a start
+// event on construction and a stop event on destruction, on `stream`.
+struct ProfScope {
+  ProfScope(const char* name, hipStream_t stream);
+  ~ProfScope();
+  int slot;
+  hipStream_t stream;
+};
+
 // NaN/Inf guard: sets *flag (device int) to 1 if any element is not finite.
 hipError_t launch_nonfinite_scan(const void* p, size_t n, int dtype, int* flag,
                                  hipStream_t stream);

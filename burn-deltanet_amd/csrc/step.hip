@@ -196,6 +196,7 @@ hipError_t launch_typed(const StepParams& p, hipStream_t stream) {
   const size_t lds = sizeof(float) * (4 * size_t(p.K) + 2 * kRowGroups * kTileV + kTileV + 1);
 #define DN_STEP_LAUNCH(RPT)                                                                   \
   do {                                                                                        \
+    ProfScope ps("dn_step_tile", stream);                                                     \
     if (vec4)                                                                                 \
       hipLaunchKernelGGL((step_tile_kernel<TQ, TY, RPT, true>), grid, dim3(kThreads), lds,   \
                          stream, p);                                                          \
@@ -211,6 +212,7 @@ hipError_t launch_typed(const StepParams& p, hipStream_t stream) {
   if (rpt_needed <= 16) DN_STEP_LAUNCH(16);
   if (rpt_needed <= 32) DN_STEP_LAUNCH(32);
 #undef DN_STEP_LAUNCH
+  ProfScope ps("dn_step_wide", stream);
   hipLaunchKernelGGL((step_wide_kernel<TQ, TY>), dim3(1, p.H, p.B), dim3(kThreads), 0, stream,
                      p);
   return hipGetLastError();

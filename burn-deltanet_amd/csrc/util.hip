@@ -32,3 +32,112 @@ hipError_t launch_nonfinite_scan(const void* p, size_t n, int dtype, int* flag,
 }
 
 }  // namespace dn
+
+// ---------------------------------------------------------------------------
+// Per-kernel timing with HIP events.
+// ---------------------------------------------------------------------------
+
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+namespace dn {
+namespace {
+
+struct ProfRecord {
+  const char* name;
+  hipEvent_t start, stop;
+};
+
+struct Profiler {
+  std::mutex mu;
+  bool on = false;
+  std::vector<ProfRecord> pending;
+  std::vector<hipEvent_t> free_events;
+  std::map<std::string, std::pair<double, int64_t>> totals;
+
+  hipEvent_t take() {
+    if (!free_events.empty()) {
+      hipEvent_t e = free_events.back();
+      free_events.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+  }
+
+  void flush() {
+    for (ProfRecord& r : pending) {
+      float ms = 0.f;
+      if (r.start && r.stop && hipEventSynchronize(r.stop) == hipSuccess &&
+          hipEventElapsedTime(&ms, r.start, r.stop) == hipSuccess) {
+        auto& t = totals[r.name];
+        t.first += ms;
+        t.second += 1;
+      }
+      if (r.start) free_events.push_back(r.start);
+      if (r.stop) free_events.push_back(r.stop);
+    }
+    pending.clear();
+  }
+};
+
+Profiler& prof() {
+  static Profiler* p = new Profiler();  // never destroyed: events outlive static teardown
+  return *p;
+}
+
+}  // namespace
+
+ProfScope::ProfScope(const char* name, hipStream_t s) : slot(-1), stream(s) {
+  Profiler& P = prof();
+  std::lock_guard<std::mutex> lock(P.mu);
+  if (!P.on) return;
+  ProfRecord r{name, P.take(), nullptr};
+  if (r.start) (void)hipEventRecord(r.start, stream);
+  P.pending.push_back(r);
+  slot = int(P.pending.size()) - 1;
+}
+
+ProfScope::~ProfScope() {
+  if (slot < 0) return;
+  Profiler& P = prof();
+  std::lock_guard<std::mutex> lock(P.mu);
+  if (slot >= int(P.pending.size())) return;
+  hipEvent_t e = P.take();
+  if (e) (void)hipEventRecord(e, stream);
+  P.pending[size_t(slot)].stop = e;
+}
+
+}  // namespace dn
+
+extern "C" int dn_profile_enable(int on) {
+  dn::Profiler& P = dn::prof();
+  std::lock_guard<std::mutex> lock(P.mu);
+  P.flush();
+  P.totals.clear();
+  P.on = on != 0;
+  return 0;
+}
+
+extern "C" int dn_profile_read(int index, char* name, size_t name_len, double* total_ms,
+                               int64_t* launches) {
+  dn::Profiler& P = dn::prof();
+  std::lock_guard<std::mutex> lock(P.mu);
+  P.flush();
+  const int count = int(P.totals.size());
+  if (index >= 0 && index < count) {
+    auto it = P.totals.begin();
+    std::advance(it, index);
+    if (name && name_len) {
+      std::strncpy(name, it->first.c_str(), name_len - 1);
+      name[name_len - 1] = '\0';
+    }
+    if (total_ms) *total_ms = it->second.first;
+    if (launches) *launches = it->second.second;
+  }
+  return count;
+}

@@ -159,6 +159,16 @@ size_t dn_chunk_bwd_workspace_bytes(const dn_chunk_bwd_args *args);
 int dn_chunk_fwd_algo(const dn_chunk_fwd_args *args);
 int dn_chunk_bwd_algo(const dn_chunk_bwd_args *args);
 
+/* Diagnostics; no counterpart in the reference, whose benches time whole calls
+ * (benches/layer.rs:161-181). While profiling is on, every kernel the library
+ * launches is bracketed by HIP events recorded on its own stream.
+ * dn_profile_enable(1) clears earlier records. dn_profile_read synchronises on
+ * the pending events and reports entry `index` (summed milliseconds and launch
+ * count of one kernel name); it returns the number of entries. */
+int dn_profile_enable(int on);
+int dn_profile_read(int index, char *name, size_t name_len, double *total_ms,
+                    int64_t *launches);
+
 /* Text of the last error on this thread (empty string if none). */
 const char *dn_last_error(void);
 

@@ -1,0 +1,112 @@
+"""The MFMA (bf16) chunk forward against the oracle, at the north_star's bf16
+bar (normwise relative ≤ 2e-2, fp32 state), on the shapes it serves:
+Gated DeltaNet / DeltaNet / DeltaProduct with per-head gates.
+
+The oracle is fed the bf16-rounded q/k/v the GPU actually reads."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import l2, rel_err
+from gpu_util import DEV, announce, as_oracle_inputs, np_of, pkg, to_gpu
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+MFMA = pkg.abi.DN_ALGO_MFMA
+TOL = 2e-2
+
+
+def gdn_inputs(rng, B, S, H, K, V, gated=True, beta_scale=1.0, state_std=0.0, split=False,
+               g_scale=0.05):
+    """Config-2 distributions: q,k L2(N(0,1)), v N(0,1), β = σ(N), g = −softplus(N)·g_scale."""
+    q = l2(rng.standard_normal((B, S, H, K)))
+    k = l2(rng.standard_normal((B, S, H, K)))
+    v = rng.standard_normal((B, S, H, V))
+    beta = beta_scale / (1.0 + np.exp(-rng.standard_normal((B, S, H, 1))))
+    write = (1.0 / (1.0 + np.exp(-rng.standard_normal((B, S, H, 1))))) if split else beta
+    g = (-np.log1p(np.exp(rng.standard_normal((B, S, H, 1)))) * g_scale) if gated else None
+    s0 = rng.normal(0.0, state_std, (B, H, K, V)) if state_std else np.zeros((B, H, K, V))
+    return [q, k, v, beta, write, g, s0]
+
+
+def run_mfma(g_args, y_dtype=torch.bfloat16, in_place=False):
+    q, k, v, e, w, g, s = g_args
+    B, S, H, K = q.shape
+    V = v.shape[3]
+    y = torch.empty((B, S, H, V), dtype=y_dtype, device=DEV)
+    s_out = s if in_place else torch.empty_like(s)
+    a = pkg.abi.chunk_fwd_args(q, k, v, e, w, g, s, y, s_out, 64, None, algo=MFMA)
+    assert pkg.abi.lib().dn_chunk_fwd_algo(a) == MFMA
+    pkg.abi.run_chunk_fwd(a)
+    torch.cuda.synchronize()
+    return np_of(y), np_of(s_out)
+
+
+CASES = [
+    # B, S, H, K, V, gated, beta_scale, state_std, split(erase≠write)
+    (1, 64, 1, 128, 64, True, 1.0, 0.0, False),
+    (2, 256, 4, 128, 256, True, 1.0, 0.0, False),
+    (1, 300, 2, 128, 128, True, 1.0, 0.02, False),
+    (2, 192, 2, 64, 64, True, 1.0, 0.02, False),
+    (1, 256, 2, 64, 192, False, 1.0, 0.02, False),
+    (1, 200, 3, 128, 128, True, 2.0, 0.02, False),
+    (1, 128, 2, 128, 64, True, 1.0, 0.02, True),
+    (1, 1000, 2, 128, 256, True, 1.0, 0.02, False),
+]
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_mfma_fwd_matches_oracle(rng, case):
+    B, S, H, K, V, gated, bs, sstd, split = case
+    announce(f"mfma fwd {case}")
+    args = gdn_inputs(rng, B, S, H, K, V, gated, bs, sstd, split)
+    g_args = to_gpu(args, torch.bfloat16)
+    y, s = run_mfma(g_args)
+    y0, s0 = O.chunk_fwd(*as_oracle_inputs(g_args), chunk_len=64, dtype=np.float32)
+    ey, es = rel_err(y, y0), rel_err(s, s0)
+    print(f"  rel err y {ey:.2e} state {es:.2e}", flush=True)
+    assert ey < TOL and es < TOL
+
+
+def test_mfma_fwd_in_place_state_fp32_y(rng):
+    announce("mfma fwd in place, fp32 y")
+    args = gdn_inputs(rng, 1, 256, 2, 128, 128, True, 1.0, 0.02)
+    g_args = to_gpu(args, torch.bfloat16)
+    ref_in = as_oracle_inputs(g_args)  # before the state buffer is overwritten
+    y, s = run_mfma(g_args, y_dtype=torch.float32, in_place=True)
+    y0, s0 = O.chunk_fwd(*ref_in, chunk_len=64, dtype=np.float32)
+    assert rel_err(y, y0) < TOL and rel_err(s, s0) < TOL
+
+
+def test_mfma_matches_generic_path(rng):
+    """Both GPU algorithms on one bf16 input; generic is fp32 arithmetic."""
+    announce("mfma vs generic")
+    g_args = to_gpu(gdn_inputs(rng, 2, 512, 2, 128, 256, True, 1.0, 0.02), torch.bfloat16)
+    y_m, s_m = run_mfma(g_args, y_dtype=torch.float32)
+    q, k, v, e, w, g, s = g_args
+    y_g, s_g = pkg.delta_chunk_recalculated(q, k, v, e, w, g, s, True, 64, None,
+                                            algo=pkg.abi.DN_ALGO_GENERIC, y_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert rel_err(y_m, np_of(y_g)) < TOL and rel_err(s_m, np_of(s_g)) < TOL
+
+
+def test_mfma_constant_keys_stay_bounded(rng):
+    """src/delta/tests.rs:373-460 at chunk 64: the WY inverse of a constant-key
+    chunk must stay exact (blocked substitution, never a series)."""
+    announce("mfma constant keys")
+    B, S, H, K, V = 1, 256, 2, 128, 64
+    hold = lambda a: np.broadcast_to(a, (B, S, H, a.shape[-1])).copy()
+    q = hold(l2(rng.standard_normal((B, 1, H, K))))
+    k = hold(l2(rng.standard_normal((B, 1, H, K))))
+    v = hold(rng.standard_normal((B, 1, H, V)))
+    for beta in (0.9, 1.8):
+        e = np.full((B, S, H, 1), beta)
+        g = np.full((B, S, H, 1), -0.05)
+        args = [q, k, v, e, e, g, np.zeros((B, H, K, V))]
+        g_args = to_gpu(args, torch.bfloat16)
+        y, s = run_mfma(g_args, y_dtype=torch.float32)
+        assert np.isfinite(y).all()
+        y0, s0 = O.recurrent(*as_oracle_inputs(g_args), dtype=np.float64)
+        assert rel_err(y, y0) < TOL and rel_err(s, s0) < TOL
