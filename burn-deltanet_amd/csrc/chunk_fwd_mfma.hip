@@ -48,7 +48,21 @@ __device__ inline f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c)
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
+
 __device__ inline bf16x8 ld8(const uint16_t* p) { return *reinterpret_cast<const bf16x8*>(p); }
+
+// Two floats → packed bf16 (round to nearest even), one v_cvt_pk_bf16_f32.
+__device__ inline uint32_t pk_bf16(float a, float b) {
+  const bf16x2 v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ inline float lo_f(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ inline float hi_f(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+
+__device__ inline f32x4 mfma_f32(float a, float b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
 
 __device__ inline bf16x8 zero8() { return __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u)); }
 
@@ -155,7 +169,7 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p) {
         const int i = 16 * rb + 4 * (lane >> 4) + r;
         const float decay = (j <= i) ? (p.gated ? __expf(gcs[i] - gcs[j]) : 1.f) : 0.f;
         A[i][j] = (j < i) ? ers[i] * acck[r] * decay : 0.f;
-        At[i * (kL + 8) + j] = f32_to_bf16(p.scale * accq[r] * decay);
+        At[i * (kL + 8) + j] = uint16_t(pk_bf16(p.scale * accq[r] * decay, 0.f));
       }
     }
   }
@@ -185,36 +199,51 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p) {
     if (j / 16 > i / 16) Tm[i][j] = 0.f;
   }
   __syncthreads();
-  // 16 → 32: T₁₀ = −T₁₁ A₁₀ T₀₀ for the two 32-blocks.
-  for (int idx = tid; idx < 2 * 256; idx += kThreads) {
-    const int pb = idx / 256, i = (idx / 16) % 16, j = idx % 16;
-    const int r0 = 32 * pb + 16, c0 = 32 * pb;
-    float acc = 0.f;
-    for (int k2 = j; k2 < 16; ++k2) acc += A[r0 + i][c0 + k2] * Tm[c0 + k2][c0 + j];
-    Xs[16 * pb + i][j] = acc;
+  // The merges run on fp32 MFMA (v_mfma_f32_16x16x4_f32: exact fp32 products):
+  // lane l holds A[l%16][l/16] and B[l/16][l%16] of a 16×4 · 4×16 step, and
+  // D[4(l/16)+r][l%16]. Full-block sums are exact: the triangular factors
+  // hold zeros outside their triangles.
+  const int m16 = lane & 15, g4 = lane >> 4;
+  // 16 → 32: T₁₀ = −T₁₁ A₁₀ T₀₀ for the two 32-blocks (waves 0 and 1).
+  if (wave < 2) {
+    const int r0 = 32 * wave + 16, c0 = 32 * wave;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4)
+      acc = mfma_f32(A[r0 + m16][c0 + 4 * s4 + g4], Tm[c0 + 4 * s4 + g4][c0 + m16], acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Xs[16 * wave + 4 * g4 + r][m16] = acc[r];
   }
   __syncthreads();
-  for (int idx = tid; idx < 2 * 256; idx += kThreads) {
-    const int pb = idx / 256, i = (idx / 16) % 16, j = idx % 16;
-    const int r0 = 32 * pb + 16, c0 = 32 * pb;
-    float acc = 0.f;
-    for (int k2 = 0; k2 <= i; ++k2) acc += Tm[r0 + i][r0 + k2] * Xs[16 * pb + k2][j];
-    Tm[r0 + i][c0 + j] = -acc;
+  if (wave < 2) {
+    const int r0 = 32 * wave + 16, c0 = 32 * wave;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4)
+      acc = mfma_f32(Tm[r0 + m16][r0 + 4 * s4 + g4], Xs[16 * wave + 4 * s4 + g4][m16], acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Tm[r0 + 4 * g4 + r][c0 + m16] = -acc[r];
   }
   __syncthreads();
-  // 32 → 64: T[32:,:32] = −T[32:,32:] A[32:,:32] T[:32,:32].
-  for (int idx = tid; idx < 32 * 32; idx += kThreads) {
-    const int i = idx / 32, j = idx % 32;
-    float acc = 0.f;
-    for (int k2 = j; k2 < 32; ++k2) acc += A[32 + i][k2] * Tm[k2][j];
-    Xs[i][j] = acc;
-  }
-  __syncthreads();
-  for (int idx = tid; idx < 32 * 32; idx += kThreads) {
-    const int i = idx / 32, j = idx % 32;
-    float acc = 0.f;
-    for (int k2 = 0; k2 <= i; ++k2) acc += Tm[32 + i][32 + k2] * Xs[k2][j];
-    Tm[32 + i][j] = -acc;
+  // 32 → 64: T[32:,:32] = −T[32:,32:] A[32:,:32] T[:32,:32]; wave w owns
+  // output tile (w/2, w%2) of the 32×32 block.
+  {
+    const int ti = wave >> 1, tj = wave & 1;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4)
+      acc = mfma_f32(A[32 + 16 * ti + m16][4 * s4 + g4], Tm[4 * s4 + g4][16 * tj + m16], acc);
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Xs[16 * ti + 4 * g4 + r][16 * tj + m16] = acc[r];
+    __syncthreads();
+    acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4)
+      acc = mfma_f32(Tm[32 + 16 * ti + m16][32 + 4 * s4 + g4], Xs[4 * s4 + g4][16 * tj + m16],
+                     acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Tm[32 + 16 * ti + 4 * g4 + r][16 * tj + m16] = -acc[r];
   }
   __syncthreads();
 
@@ -224,17 +253,17 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p) {
     uint16_t* tdst = p.T + size_t(cid) * kL * kL + row * kL + c0;
     uint16_t* ldst = p.Tlo + size_t(cid) * kL * kL + row * kL + c0;
     uint16_t* adst = p.attn + size_t(cid) * kL * kL + row * kL + c0;
-    alignas(16) uint16_t tv[16], tl[16];
+    uint32_t tv[8], tl[8];
 #pragma unroll
-    for (int c = 0; c < 16; ++c) {
-      const float x = Tm[row][c0 + c];
-      tv[c] = f32_to_bf16(x);
-      tl[c] = f32_to_bf16(x - bf16_to_f32(tv[c]));
+    for (int c = 0; c < 8; ++c) {
+      const float x0 = Tm[row][c0 + 2 * c], x1 = Tm[row][c0 + 2 * c + 1];
+      tv[c] = pk_bf16(x0, x1);
+      tl[c] = pk_bf16(x0 - lo_f(tv[c]), x1 - hi_f(tv[c]));
     }
-    *reinterpret_cast<bf16x8*>(tdst) = *reinterpret_cast<const bf16x8*>(&tv[0]);
-    *reinterpret_cast<bf16x8*>(tdst + 8) = *reinterpret_cast<const bf16x8*>(&tv[8]);
-    *reinterpret_cast<bf16x8*>(ldst) = *reinterpret_cast<const bf16x8*>(&tl[0]);
-    *reinterpret_cast<bf16x8*>(ldst + 8) = *reinterpret_cast<const bf16x8*>(&tl[8]);
+    *reinterpret_cast<uint4*>(tdst) = make_uint4(tv[0], tv[1], tv[2], tv[3]);
+    *reinterpret_cast<uint4*>(tdst + 8) = make_uint4(tv[4], tv[5], tv[6], tv[7]);
+    *reinterpret_cast<uint4*>(ldst) = make_uint4(tl[0], tl[1], tl[2], tl[3]);
+    *reinterpret_cast<uint4*>(ldst + 8) = make_uint4(tl[4], tl[5], tl[6], tl[7]);
     *reinterpret_cast<bf16x8*>(adst) = ld8(&At[row * (kL + 8) + c0]);
     *reinterpret_cast<bf16x8*>(adst + 8) = ld8(&At[row * (kL + 8) + c0 + 8]);
   }
@@ -247,6 +276,7 @@ template <int K, class TY>
 __global__ __launch_bounds__(kThreads) void mfma_scan_kernel(MfmaParams p) {
   constexpr int RB = K / 64;     // 16-row state blocks per wave
   constexpr int CB = kBV / 16;   // 16-column blocks per tile
+  constexpr int KK = K / 32;     // 32-deep k-steps over the key dimension
   constexpr int KP = K + 8;
   constexpr int LP = kL + 8;
   __shared__ __attribute__((aligned(16))) uint16_t KcT[K * LP];    // (e^{Gl−G}⊙K)ᵀ
@@ -255,7 +285,7 @@ __global__ __launch_bounds__(kThreads) void mfma_scan_kernel(MfmaParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t XbT[kBV * LP];  // bf16(X)ᵀ
   __shared__ __attribute__((aligned(16))) uint16_t XlT[kBV * LP];  // bf16(X − bf16(X))ᵀ
   __shared__ __attribute__((aligned(16))) uint16_t VpT[kBV * LP];  // bf16 V'ᵀ
-  __shared__ float egs[kL], xes[kL], wrs[kL];
+  __shared__ float xes[kL], wrs[kL];
   __shared__ float egl_s;
 
   const int tiles = p.V / kBV;
@@ -291,95 +321,149 @@ __global__ __launch_bounds__(kThreads) void mfma_scan_kernel(MfmaParams p) {
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
         const int d = wave * (K / 4) + 16 * rb + 4 * q4;
-        uint16_t hi[4], lo[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          hi[r] = f32_to_bf16(S[rb][cb][r]);
-          lo[r] = f32_to_bf16(S[rb][cb][r] - bf16_to_f32(hi[r]));
-        }
+        const f32x4& v = S[rb][cb];
+        const uint32_t h01 = pk_bf16(v[0], v[1]), h23 = pk_bf16(v[2], v[3]);
+        const uint32_t l01 = pk_bf16(v[0] - lo_f(h01), v[1] - hi_f(h01));
+        const uint32_t l23 = pk_bf16(v[2] - lo_f(h23), v[3] - hi_f(h23));
         const int at = (16 * cb + r16) * KP + d;
-        *reinterpret_cast<uint2*>(&ShT[at]) =
-            make_uint2(uint32_t(hi[0]) | (uint32_t(hi[1]) << 16),
-                       uint32_t(hi[2]) | (uint32_t(hi[3]) << 16));
-        *reinterpret_cast<uint2*>(&SlT[at]) =
-            make_uint2(uint32_t(lo[0]) | (uint32_t(lo[1]) << 16),
-                       uint32_t(lo[2]) | (uint32_t(lo[3]) << 16));
+        *reinterpret_cast<uint2*>(&ShT[at]) = make_uint2(h01, h23);
+        *reinterpret_cast<uint2*>(&SlT[at]) = make_uint2(l01, l23);
       }
   };
   write_state();
 
-  const size_t rowstride = size_t(p.H) * K;  // elements between tokens in q/k
-  for (int n = 0; n < p.N; ++n) {
-    const size_t cid = (size_t(b) * p.N + n) * p.H + h;
-    const int tok0 = n * kL;
-    const float glast = p.gated ? p.gc[cid * kL + kL - 1] : 0.f;
-    // Phase 0: (e^{G_last−G}⊙K)ᵀ of the chunk into LDS; per-token gates.
-    for (int idx = tid; idx < kL * K / 8; idx += kThreads) {
-      const int row = idx / (K / 8), c8 = idx % (K / 8);
-      const int tok = tok0 + row;
-      uint4 kv = make_uint4(0u, 0u, 0u, 0u);
-      if (tok < p.S)
-        kv = *reinterpret_cast<const uint4*>(p.k + ((size_t(b) * p.S + tok) * p.H + h) * K +
-                                             8 * c8);
-      const float ec = p.gated ? __expf(glast - p.gc[cid * kL + row]) : 1.f;
-      // Split the eight bf16 values with integer shifts (element reads of a
-      // __bf16 vector are not reliable in this compiler).
-      const uint32_t w4[4] = {kv.x, kv.y, kv.z, kv.w};
+  // Every global read of a chunk is issued one chunk ahead, right after the
+  // phase that consumed the previous buffer, so the serial chain over chunks
+  // never waits on HBM. Lane (wave w, r16, q4) reads token row 16w + r16.
+  const int my_tok = 16 * wave + r16;
+  uint4 kA[KK];             // K[my_tok][32kk + k8 …]    (phase 0 + phase 1)
+  float gcA, glA, erA, wrA;  // gate values of my_tok and G_last
+  uint32_t vA[CB][2];       // V[16w + 4q4 + r][j0 + 16cb + r16], bf16 pairs
+  uint4 tA[2], tlA[2];      // T hi/lo rows my_tok               (phase 2)
+  uint4 qA[KK], atA[2];     // Q row and attn row of my_tok      (phase 3a)
+
+  auto chunk_id = [&](int n) { return (size_t(b) * p.N + n) * p.H + h; };
+  auto load_k = [&](int n) {
+    const size_t cid = chunk_id(n);
+    const int tok = n * kL + my_tok;
+    const bool ok = tok < p.S;
+    const size_t row = (size_t(b) * p.S + tok) * p.H + h;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        KcT[(8 * c8 + 2 * e) * LP + row] = f32_to_bf16(bf16_to_f32(uint16_t(w4[e])) * ec);
-        KcT[(8 * c8 + 2 * e + 1) * LP + row] =
-            f32_to_bf16(bf16_to_f32(uint16_t(w4[e] >> 16)) * ec);
+    for (int kk = 0; kk < KK; ++kk)
+      kA[kk] = ok ? *reinterpret_cast<const uint4*>(p.k + row * K + 32 * kk + k8)
+                  : make_uint4(0u, 0u, 0u, 0u);
+    gcA = p.gated ? p.gc[cid * kL + my_tok] : 0.f;
+    glA = p.gated ? p.gc[cid * kL + kL - 1] : 0.f;
+    erA = ok ? p.erase[row] : 0.f;
+    wrA = ok ? p.write[row] : 0.f;
+  };
+  auto load_v = [&](int n) {
+#pragma unroll
+    for (int cb = 0; cb < CB; ++cb)
+#pragma unroll
+      for (int r2 = 0; r2 < 2; ++r2) {
+        uint32_t pair = 0;
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const int t = n * kL + 16 * wave + 4 * q4 + 2 * r2 + half;
+          const uint32_t x =
+              t < p.S ? p.v[((size_t(b) * p.S + t) * p.H + h) * p.V + j0 + 16 * cb + r16] : 0u;
+          pair |= x << (16 * half);
+        }
+        vA[cb][r2] = pair;
       }
+  };
+  auto load_t = [&](int n) {
+    const size_t off = chunk_id(n) * kL * kL + size_t(my_tok) * kL;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      tA[kk] = *reinterpret_cast<const uint4*>(p.T + off + 32 * kk + k8);
+      tlA[kk] = *reinterpret_cast<const uint4*>(p.Tlo + off + 32 * kk + k8);
     }
-    if (wave == 0) {
-      const float gcv = p.gated ? p.gc[cid * kL + lane] : 0.f;
-      const int tok = tok0 + lane;
-      const size_t row = (size_t(b) * p.S + tok) * p.H + h;
-      const float eg = p.gated ? __expf(gcv) : 1.f;
-      egs[lane] = eg;
-      xes[lane] = tok < p.S ? p.erase[row] * eg : 0.f;
-      wrs[lane] = tok < p.S ? p.write[row] : 0.f;
-      if (lane == 0) egl_s = p.gated ? __expf(glast) : 1.f;
+  };
+  auto load_q = [&](int n) {
+    const int tok = n * kL + my_tok;
+    const bool ok = tok < p.S;
+    const size_t row = (size_t(b) * p.S + tok) * p.H + h;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      qA[kk] = ok ? *reinterpret_cast<const uint4*>(p.q + row * K + 32 * kk + k8)
+                  : make_uint4(0u, 0u, 0u, 0u);
+    const size_t off = chunk_id(n) * kL * kL + size_t(my_tok) * kL;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+      atA[kk] = *reinterpret_cast<const uint4*>(p.attn + off + 32 * kk + k8);
+  };
+  auto as8 = [](const uint4& x) { return __builtin_bit_cast(bf16x8, x); };
+
+  load_k(0);
+  load_v(0);
+  load_t(0);
+  load_q(0);
+  for (int n = 0; n < p.N; ++n) {
+    const int tok0 = n * kL;
+    const bool more = n + 1 < p.N;
+
+    // Phase 0: (e^{G_last−G}⊙K)ᵀ into LDS from the prefetched rows; gates.
+    const float egA = p.gated ? __expf(gcA) : 1.f;
+    {
+      const float ec = p.gated ? __expf(glA - gcA) : 1.f;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const uint32_t w4[4] = {kA[kk].x, kA[kk].y, kA[kk].z, kA[kk].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int d = 32 * kk + k8 + 2 * e;
+          const uint32_t pk = p.gated ? pk_bf16(lo_f(w4[e]) * ec, hi_f(w4[e]) * ec) : w4[e];
+          KcT[d * LP + my_tok] = uint16_t(pk);
+          KcT[(d + 1) * LP + my_tok] = uint16_t(pk >> 16);
+        }
+      }
+      if (q4 == 0) {
+        xes[my_tok] = erA * egA;
+        wrs[my_tok] = wrA;
+      }
+      if (tid == 0) egl_s = p.gated ? __expf(glA) : 1.f;
     }
     __syncthreads();
 
     // Phase 1: X = w⊙V − (e⊙e^G)⊙(K·S), token rows 16·wave…
     {
-      const int tok = tok0 + 16 * wave + r16;
-      bf16x8 a[K / 32];
-#pragma unroll
-      for (int kk = 0; kk < K / 32; ++kk)
-        a[kk] = tok < p.S ? ld8(p.k + (size_t(b) * p.S + tok) * rowstride + size_t(h) * K +
-                                32 * kk + k8)
-                          : zero8();
+      f32x4 acc[CB];
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < K / 32; ++kk) {
-          acc = mfma16(a[kk], ld8(&ShT[(16 * cb + r16) * KP + 32 * kk + k8]), acc);
-          acc = mfma16(a[kk], ld8(&SlT[(16 * cb + r16) * KP + 32 * kk + k8]), acc);
+        for (int kk = 0; kk < KK; ++kk) {
+          acc[cb] = mfma16(as8(kA[kk]), ld8(&ShT[(16 * cb + r16) * KP + 32 * kk + k8]), acc[cb]);
+          acc[cb] = mfma16(as8(kA[kk]), ld8(&SlT[(16 * cb + r16) * KP + 32 * kk + k8]), acc[cb]);
         }
+      }
+      uint32_t vcur[CB][2];
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
+        vcur[cb][0] = vA[cb][0];
+        vcur[cb][1] = vA[cb][1];
+      }
+      if (more) {
+        load_k(n + 1);
+        load_v(n + 1);
+      }
+#pragma unroll
+      for (int cb = 0; cb < CB; ++cb) {
         const int j = 16 * cb + r16;
-        uint16_t xv[4], xl[4];
+        float x[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int i = 16 * wave + 4 * q4 + r;
-          const int t = tok0 + i;
-          const float vv = t < p.S ? bf16_to_f32(p.v[((size_t(b) * p.S + t) * p.H + h) * p.V +
-                                                     j0 + j])
-                                   : 0.f;
-          const float x = wrs[i] * vv - xes[i] * acc[r];
-          xv[r] = f32_to_bf16(x);
-          xl[r] = f32_to_bf16(x - bf16_to_f32(xv[r]));
+          const float vv = (r & 1) ? hi_f(vcur[cb][r >> 1]) : lo_f(vcur[cb][r >> 1]);
+          x[r] = wrs[i] * vv - xes[i] * acc[cb][r];
         }
-        *reinterpret_cast<uint2*>(&XbT[j * LP + 16 * wave + 4 * q4]) =
-            make_uint2(uint32_t(xv[0]) | (uint32_t(xv[1]) << 16),
-                       uint32_t(xv[2]) | (uint32_t(xv[3]) << 16));
-        *reinterpret_cast<uint2*>(&XlT[j * LP + 16 * wave + 4 * q4]) =
-            make_uint2(uint32_t(xl[0]) | (uint32_t(xl[1]) << 16),
-                       uint32_t(xl[2]) | (uint32_t(xl[3]) << 16));
+        const uint32_t h01 = pk_bf16(x[0], x[1]), h23 = pk_bf16(x[2], x[3]);
+        const uint32_t l01 = pk_bf16(x[0] - lo_f(h01), x[1] - hi_f(h01));
+        const uint32_t l23 = pk_bf16(x[2] - lo_f(h23), x[3] - hi_f(h23));
+        *reinterpret_cast<uint2*>(&XbT[j * LP + 16 * wave + 4 * q4]) = make_uint2(h01, h23);
+        *reinterpret_cast<uint2*>(&XlT[j * LP + 16 * wave + 4 * q4]) = make_uint2(l01, l23);
       }
     }
     __syncthreads();
@@ -387,64 +471,59 @@ __global__ __launch_bounds__(kThreads) void mfma_scan_kernel(MfmaParams p) {
     // Phase 2: V' = T·X, with both factors as bf16 hi + lo parts: for a
     // chunk of near-identical keys T differences near-equal rows of X.
     {
-      const uint16_t* Tc = p.T + cid * kL * kL;
-      const uint16_t* Tl = p.Tlo + cid * kL * kL;
-      bf16x8 a[2], al[2];
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        a[kk] = ld8(Tc + (16 * wave + r16) * kL + 32 * kk + k8);
-        al[kk] = ld8(Tl + (16 * wave + r16) * kL + 32 * kk + k8);
-      }
+      f32x4 acc[CB];
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           const bf16x8 xh = ld8(&XbT[(16 * cb + r16) * LP + 32 * kk + k8]);
-          acc = mfma16(a[kk], xh, acc);
-          acc = mfma16(al[kk], xh, acc);
-          acc = mfma16(a[kk], ld8(&XlT[(16 * cb + r16) * LP + 32 * kk + k8]), acc);
+          acc[cb] = mfma16(as8(tA[kk]), xh, acc[cb]);
+          acc[cb] = mfma16(as8(tlA[kk]), xh, acc[cb]);
+          acc[cb] = mfma16(as8(tA[kk]), ld8(&XlT[(16 * cb + r16) * LP + 32 * kk + k8]), acc[cb]);
         }
-        const int j = 16 * cb + r16;
-        uint16_t vp[4];
+      }
+      if (more) load_t(n + 1);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) vp[r] = f32_to_bf16(acc[r]);
+      for (int cb = 0; cb < CB; ++cb) {
+        const int j = 16 * cb + r16;
         *reinterpret_cast<uint2*>(&VpT[j * LP + 16 * wave + 4 * q4]) =
-            make_uint2(uint32_t(vp[0]) | (uint32_t(vp[1]) << 16),
-                       uint32_t(vp[2]) | (uint32_t(vp[3]) << 16));
+            make_uint2(pk_bf16(acc[cb][0], acc[cb][1]), pk_bf16(acc[cb][2], acc[cb][3]));
       }
     }
     __syncthreads();
 
-    // Phase 3a: y = (scale·e^G)⊙(Q·S) + attn·V'.
+    // Phase 3a: yᵀ = (Sᵀ·Qᵀ)⊙(scale·e^G) + V'ᵀ·attnᵀ. In this orientation
+    // lane (r16, q4) holds four consecutive value columns of its own token
+    // my_tok, so y leaves in 8- or 16-byte stores.
     {
-      const int tok = tok0 + 16 * wave + r16;
-      const uint16_t* Ac = p.attn + cid * kL * kL;
-      bf16x8 a[K / 32], at[2];
-#pragma unroll
-      for (int kk = 0; kk < K / 32; ++kk)
-        a[kk] = tok < p.S ? ld8(p.q + (size_t(b) * p.S + tok) * rowstride + size_t(h) * K +
-                                32 * kk + k8)
-                          : zero8();
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) at[kk] = ld8(Ac + (16 * wave + r16) * kL + 32 * kk + k8);
+      f32x4 qs[CB], av[CB];
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
-        f32x4 qs = {0.f, 0.f, 0.f, 0.f}, av = {0.f, 0.f, 0.f, 0.f};
+        qs[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+        av[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < K / 32; ++kk)
-          qs = mfma16(a[kk], ld8(&ShT[(16 * cb + r16) * KP + 32 * kk + k8]), qs);
+        for (int kk = 0; kk < KK; ++kk)
+          qs[cb] = mfma16(ld8(&ShT[(16 * cb + r16) * KP + 32 * kk + k8]), as8(qA[kk]), qs[cb]);
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
-          av = mfma16(at[kk], ld8(&VpT[(16 * cb + r16) * LP + 32 * kk + k8]), av);
-        const int j = j0 + 16 * cb + r16;
+          av[cb] = mfma16(ld8(&VpT[(16 * cb + r16) * LP + 32 * kk + k8]), as8(atA[kk]), av[cb]);
+      }
+      if (more) load_q(n + 1);
+      const int t = tok0 + my_tok;
+      const float ysc = p.scale * egA;
+      if (t < p.S) {
+        TY* yrow = static_cast<TY*>(p.y) + ((size_t(b) * p.S + t) * p.H + h) * p.V + j0;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = 16 * wave + 4 * q4 + r;
-          const int t = tok0 + i;
-          if (t < p.S)
-            st(static_cast<TY*>(p.y), ((size_t(b) * p.S + t) * p.H + h) * p.V + j,
-               p.scale * egs[i] * qs[r] + av[r]);
+        for (int cb = 0; cb < CB; ++cb) {
+          float o[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[r] = ysc * qs[cb][r] + av[cb][r];
+          TY* dst = yrow + 16 * cb + 4 * q4;
+          if constexpr (sizeof(TY) == 2)
+            *reinterpret_cast<uint2*>(dst) = make_uint2(pk_bf16(o[0], o[1]), pk_bf16(o[2], o[3]));
+          else
+            *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
         }
       }
     }
