@@ -43,6 +43,7 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 constexpr int kL = 64;        // chunk length
 constexpr int kThreads = 256;  // 4 waves
 constexpr int kBV = 64;       // value columns per scan workgroup
+constexpr int kZeroElems = 512;
 
 __device__ inline f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -78,6 +79,9 @@ struct MfmaParams {
   uint16_t* T;     // [G][64][64] bf16(T)
   uint16_t* Tlo;   // [G][64][64] bf16(T − bf16(T))
   uint16_t* attn;  // [G][64][64] bf16
+  uint16_t* KcT;   // [G][K][64] bf16 (e^{G_last−G}⊙K)ᵀ
+  uint16_t* zero;  // kZeroElems bf16 zeros: the source of padded tokens' reads
+  uint16_t* sink;  // one y row: the target of padded tokens' writes
   float* gc;       // [G][64]
 };
 
@@ -106,6 +110,9 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p) {
   const int h = cid % p.H, n = (cid / p.H) % p.N, b = cid / (p.H * p.N);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tok0 = n * kL;
+  if (cid == 0)
+    for (int i = tid; i < kZeroElems / 8; i += kThreads)
+      reinterpret_cast<uint4*>(p.zero)[i] = make_uint4(0u, 0u, 0u, 0u);
 
   // Stage the K and Q chunk tiles (zero past the sequence end).
   for (int idx = tid; idx < kL * K / 8; idx += kThreads) {
@@ -172,6 +179,27 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p) {
         At[i * (kL + 8) + j] = uint16_t(pk_bf16(p.scale * accq[r] * decay, 0.f));
       }
     }
+  }
+  __syncthreads();
+
+  // Kcᵀ = (e^{G_last−G} ⊙ K)ᵀ for the scan's state update, while the K tile
+  // is still in LDS: TPD lanes per key channel d, each packing a run of tokens.
+  {
+    constexpr int TPD = kThreads / K, RUN = kL / TPD;
+    const int d = tid / TPD, t0 = RUN * (tid % TPD);
+    const float glast = gcs[kL - 1];
+    uint32_t w[RUN / 2];
+#pragma unroll
+    for (int e = 0; e < RUN / 2; ++e) {
+      const int t = t0 + 2 * e;
+      const float k0 = bf16_to_f32(Ks[t * KP + d]), k1 = bf16_to_f32(Ks[(t + 1) * KP + d]);
+      w[e] = p.gated ? pk_bf16(k0 * __expf(glast - gcs[t]), k1 * __expf(glast - gcs[t + 1]))
+                     : pk_bf16(k0, k1);
+    }
+    uint32_t* dst = reinterpret_cast<uint32_t*>(p.KcT + (size_t(cid) * K + d) * kL + t0);
+#pragma unroll
+    for (int e = 0; e < RUN / 2; e += 4)
+      *reinterpret_cast<uint4*>(dst + e) = make_uint4(w[e], w[e + 1], w[e + 2], w[e + 3]);
   }
   __syncthreads();
 
@@ -273,20 +301,21 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p) {
 // scan
 // ---------------------------------------------------------------------------
 template <int K, class TY>
-__global__ __launch_bounds__(kThreads) void mfma_scan_kernel(MfmaParams p) {
+__global__ __launch_bounds__(kThreads, 2) void mfma_scan_kernel(MfmaParams p) {
   constexpr int RB = K / 64;     // 16-row state blocks per wave
   constexpr int CB = kBV / 16;   // 16-column blocks per tile
   constexpr int KK = K / 32;     // 32-deep k-steps over the key dimension
   constexpr int KP = K + 8;
   constexpr int LP = kL + 8;
-  __shared__ __attribute__((aligned(16))) uint16_t KcT[K * LP];    // (e^{Gl−G}⊙K)ᵀ
-  __shared__ __attribute__((aligned(16))) uint16_t ShT[kBV * KP];  // bf16(S)ᵀ
-  __shared__ __attribute__((aligned(16))) uint16_t SlT[kBV * KP];  // bf16(S − bf16(S))ᵀ
+  // bf16(S)ᵀ is double-buffered (the readout of chunk n and the state update
+  // writing chunk n+1's copy need no barrier between them); the low part
+  // bf16(S − bf16(S))ᵀ is only read by the retrieval.
+  __shared__ __attribute__((aligned(16))) uint16_t ShT[2][kBV * KP];
+  __shared__ __attribute__((aligned(16))) uint16_t SlT[kBV * KP];
   __shared__ __attribute__((aligned(16))) uint16_t XbT[kBV * LP];  // bf16(X)ᵀ
   __shared__ __attribute__((aligned(16))) uint16_t XlT[kBV * LP];  // bf16(X − bf16(X))ᵀ
   __shared__ __attribute__((aligned(16))) uint16_t VpT[kBV * LP];  // bf16 V'ᵀ
-  __shared__ float xes[kL], wrs[kL];
-  __shared__ float egl_s;
+  __shared__ float xes[kL], wrs[kL];  // written and read by one wave only
 
   const int tiles = p.V / kBV;
   const int BH = p.B * p.H;
@@ -315,7 +344,7 @@ __global__ __launch_bounds__(kThreads) void mfma_scan_kernel(MfmaParams p) {
       }
   // bf16 hi/lo copies of Sᵀ: the retrieval K·S cancels against v, so it
   // reads S to ~2⁻¹⁶; the readout Q·S reads the hi part only.
-  auto write_state = [&]() {
+  auto write_state = [&](uint16_t* sh) {
 #pragma unroll
     for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
@@ -326,73 +355,84 @@ __global__ __launch_bounds__(kThreads) void mfma_scan_kernel(MfmaParams p) {
         const uint32_t l01 = pk_bf16(v[0] - lo_f(h01), v[1] - hi_f(h01));
         const uint32_t l23 = pk_bf16(v[2] - lo_f(h23), v[3] - hi_f(h23));
         const int at = (16 * cb + r16) * KP + d;
-        *reinterpret_cast<uint2*>(&ShT[at]) = make_uint2(h01, h23);
+        *reinterpret_cast<uint2*>(&sh[at]) = make_uint2(h01, h23);
         *reinterpret_cast<uint2*>(&SlT[at]) = make_uint2(l01, l23);
       }
   };
-  write_state();
+  write_state(ShT[0]);
 
   // Every global read of a chunk is issued one chunk ahead, right after the
   // phase that consumed the previous buffer, so the serial chain over chunks
   // never waits on HBM. Lane (wave w, r16, q4) reads token row 16w + r16.
   const int my_tok = 16 * wave + r16;
-  uint4 kA[KK];             // K[my_tok][32kk + k8 …]    (phase 0 + phase 1)
+  uint4 kA[KK];             // K[my_tok][32kk + k8 …]                 (phase 1)
   float gcA, glA, erA, wrA;  // gate values of my_tok and G_last
   uint32_t vA[CB][2];       // V[16w + 4q4 + r][j0 + 16cb + r16], bf16 pairs
-  uint4 tA[2], tlA[2];      // T hi/lo rows my_tok               (phase 2)
-  uint4 qA[KK], atA[2];     // Q row and attn row of my_tok      (phase 3a)
+  uint4 tA[2], tlA[2];      // T hi/lo rows my_tok                    (phase 2)
+  uint4 qA[KK], atA[2];     // Q row and attn row of my_tok           (phase 3a)
+  uint4 kcA[RB][2];         // Kcᵀ rows of this wave's state rows     (phase 3b)
 
-  auto chunk_id = [&](int n) { return (size_t(b) * p.N + n) * p.H + h; };
+  const size_t tokstride = size_t(p.H);  // rows between consecutive tokens
+  const size_t bh_row0 = size_t(b) * p.S * p.H + h;
+  // Reads and writes are unconditional, with padded tokens' addresses
+  // redirected to a zero row or a sink row: every iteration then issues the
+  // same sequence of memory operations, which keeps the compiler's in-order
+  // vmcnt waits exact across the loop instead of draining every prefetch.
+  const float* zero32 = reinterpret_cast<const float*>(p.zero);
   auto load_k = [&](int n) {
-    const size_t cid = chunk_id(n);
+    const size_t cid = (size_t(b) * p.N + n) * p.H + h;
     const int tok = n * kL + my_tok;
     const bool ok = tok < p.S;
-    const size_t row = (size_t(b) * p.S + tok) * p.H + h;
+    const size_t row = bh_row0 + size_t(tok) * tokstride;
+    const uint16_t* kr = ok ? p.k + row * K + k8 : p.zero;
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      kA[kk] = ok ? *reinterpret_cast<const uint4*>(p.k + row * K + 32 * kk + k8)
-                  : make_uint4(0u, 0u, 0u, 0u);
-    gcA = p.gated ? p.gc[cid * kL + my_tok] : 0.f;
-    glA = p.gated ? p.gc[cid * kL + kL - 1] : 0.f;
-    erA = ok ? p.erase[row] : 0.f;
-    wrA = ok ? p.write[row] : 0.f;
+    for (int kk = 0; kk < KK; ++kk) kA[kk] = *reinterpret_cast<const uint4*>(kr + 32 * kk);
+    gcA = p.gc[cid * kL + my_tok];
+    glA = p.gc[cid * kL + kL - 1];
+    erA = *(ok ? p.erase + row : zero32);
+    wrA = *(ok ? p.write + row : zero32);
   };
   auto load_v = [&](int n) {
+    const int t0 = n * kL + 16 * wave + 4 * q4;
+    const uint16_t* vb = p.v + (bh_row0 + size_t(t0) * tokstride) * p.V + j0 + r16;
+    const size_t vstride = tokstride * p.V;
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
       for (int r2 = 0; r2 < 2; ++r2) {
-        uint32_t pair = 0;
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          const int t = n * kL + 16 * wave + 4 * q4 + 2 * r2 + half;
-          const uint32_t x =
-              t < p.S ? p.v[((size_t(b) * p.S + t) * p.H + h) * p.V + j0 + 16 * cb + r16] : 0u;
-          pair |= x << (16 * half);
-        }
-        vA[cb][r2] = pair;
+        const uint32_t x0 = *(t0 + 2 * r2 < p.S ? vb + (2 * r2) * vstride + 16 * cb : p.zero);
+        const uint32_t x1 =
+            *(t0 + 2 * r2 + 1 < p.S ? vb + (2 * r2 + 1) * vstride + 16 * cb : p.zero);
+        vA[cb][r2] = x0 | (x1 << 16);
       }
   };
   auto load_t = [&](int n) {
-    const size_t off = chunk_id(n) * kL * kL + size_t(my_tok) * kL;
+    const size_t off = ((size_t(b) * p.N + n) * p.H + h) * kL * kL + size_t(my_tok) * kL + k8;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      tA[kk] = *reinterpret_cast<const uint4*>(p.T + off + 32 * kk + k8);
-      tlA[kk] = *reinterpret_cast<const uint4*>(p.Tlo + off + 32 * kk + k8);
+      tA[kk] = *reinterpret_cast<const uint4*>(p.T + off + 32 * kk);
+      tlA[kk] = *reinterpret_cast<const uint4*>(p.Tlo + off + 32 * kk);
     }
   };
   auto load_q = [&](int n) {
     const int tok = n * kL + my_tok;
-    const bool ok = tok < p.S;
-    const size_t row = (size_t(b) * p.S + tok) * p.H + h;
+    const uint16_t* qr =
+        tok < p.S ? p.q + (bh_row0 + size_t(tok) * tokstride) * K + k8 : p.zero;
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      qA[kk] = ok ? *reinterpret_cast<const uint4*>(p.q + row * K + 32 * kk + k8)
-                  : make_uint4(0u, 0u, 0u, 0u);
-    const size_t off = chunk_id(n) * kL * kL + size_t(my_tok) * kL;
+    for (int kk = 0; kk < KK; ++kk) qA[kk] = *reinterpret_cast<const uint4*>(qr + 32 * kk);
+    const size_t off = ((size_t(b) * p.N + n) * p.H + h) * kL * kL + size_t(my_tok) * kL + k8;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
-      atA[kk] = *reinterpret_cast<const uint4*>(p.attn + off + 32 * kk + k8);
+      atA[kk] = *reinterpret_cast<const uint4*>(p.attn + off + 32 * kk);
+  };
+  auto load_kc = [&](int n) {
+    const uint16_t* kc = p.KcT + ((size_t(b) * p.N + n) * p.H + h) * K * kL + k8;
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        kcA[rb][kk] = *reinterpret_cast<const uint4*>(
+            kc + size_t(wave * (K / 4) + 16 * rb + r16) * kL + 32 * kk);
   };
   auto as8 = [](const uint4& x) { return __builtin_bit_cast(bf16x8, x); };
 
@@ -402,30 +442,17 @@ __global__ __launch_bounds__(kThreads) void mfma_scan_kernel(MfmaParams p) {
   load_q(0);
   for (int n = 0; n < p.N; ++n) {
     const int tok0 = n * kL;
-    const bool more = n + 1 < p.N;
+    const int nn = n + 1 < p.N ? n + 1 : n;  // the last chunk prefetches itself again
+    const uint16_t* sh = ShT[n & 1];
 
-    // Phase 0: (e^{G_last−G}⊙K)ᵀ into LDS from the prefetched rows; gates.
-    const float egA = p.gated ? __expf(gcA) : 1.f;
-    {
-      const float ec = p.gated ? __expf(glA - gcA) : 1.f;
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        const uint32_t w4[4] = {kA[kk].x, kA[kk].y, kA[kk].z, kA[kk].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int d = 32 * kk + k8 + 2 * e;
-          const uint32_t pk = p.gated ? pk_bf16(lo_f(w4[e]) * ec, hi_f(w4[e]) * ec) : w4[e];
-          KcT[d * LP + my_tok] = uint16_t(pk);
-          KcT[(d + 1) * LP + my_tok] = uint16_t(pk >> 16);
-        }
-      }
-      if (q4 == 0) {
-        xes[my_tok] = erA * egA;
-        wrs[my_tok] = wrA;
-      }
-      if (tid == 0) egl_s = p.gated ? __expf(glA) : 1.f;
+    // Gates of this wave's tokens (read back by this wave only); G is 0
+    // throughout when there is no forget gate.
+    const float egA = __expf(gcA);
+    const float egl = __expf(glA);
+    if (q4 == 0) {
+      xes[my_tok] = erA * egA;
+      wrs[my_tok] = wrA;
     }
-    __syncthreads();
 
     // Phase 1: X = w⊙V − (e⊙e^G)⊙(K·S), token rows 16·wave…
     {
@@ -435,29 +462,25 @@ __global__ __launch_bounds__(kThreads) void mfma_scan_kernel(MfmaParams p) {
         acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk) {
-          acc[cb] = mfma16(as8(kA[kk]), ld8(&ShT[(16 * cb + r16) * KP + 32 * kk + k8]), acc[cb]);
+          acc[cb] = mfma16(as8(kA[kk]), ld8(&sh[(16 * cb + r16) * KP + 32 * kk + k8]), acc[cb]);
           acc[cb] = mfma16(as8(kA[kk]), ld8(&SlT[(16 * cb + r16) * KP + 32 * kk + k8]), acc[cb]);
         }
       }
-      uint32_t vcur[CB][2];
+      float xe[4], wr[4];
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        vcur[cb][0] = vA[cb][0];
-        vcur[cb][1] = vA[cb][1];
+      for (int r = 0; r < 4; ++r) {
+        xe[r] = xes[16 * wave + 4 * q4 + r];
+        wr[r] = wrs[16 * wave + 4 * q4 + r];
       }
-      if (more) {
-        load_k(n + 1);
-        load_v(n + 1);
-      }
+      load_k(nn);
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
         const int j = 16 * cb + r16;
         float x[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int i = 16 * wave + 4 * q4 + r;
-          const float vv = (r & 1) ? hi_f(vcur[cb][r >> 1]) : lo_f(vcur[cb][r >> 1]);
-          x[r] = wrs[i] * vv - xes[i] * acc[cb][r];
+          const float vv = (r & 1) ? hi_f(vA[cb][r >> 1]) : lo_f(vA[cb][r >> 1]);
+          x[r] = wr[r] * vv - xe[r] * acc[cb][r];
         }
         const uint32_t h01 = pk_bf16(x[0], x[1]), h23 = pk_bf16(x[2], x[3]);
         const uint32_t l01 = pk_bf16(x[0] - lo_f(h01), x[1] - hi_f(h01));
@@ -465,6 +488,7 @@ __global__ __launch_bounds__(kThreads) void mfma_scan_kernel(MfmaParams p) {
         *reinterpret_cast<uint2*>(&XbT[j * LP + 16 * wave + 4 * q4]) = make_uint2(h01, h23);
         *reinterpret_cast<uint2*>(&XlT[j * LP + 16 * wave + 4 * q4]) = make_uint2(l01, l23);
       }
+      load_v(nn);
     }
     __syncthreads();
 
@@ -483,7 +507,8 @@ __global__ __launch_bounds__(kThreads) void mfma_scan_kernel(MfmaParams p) {
           acc[cb] = mfma16(as8(tA[kk]), ld8(&XlT[(16 * cb + r16) * LP + 32 * kk + k8]), acc[cb]);
         }
       }
-      if (more) load_t(n + 1);
+      load_t(nn);
+      load_kc(n);  // consumed in phase 3b, after phase 3a's MFMAs
 #pragma unroll
       for (int cb = 0; cb < CB; ++cb) {
         const int j = 16 * cb + r16;
@@ -504,40 +529,34 @@ __global__ __launch_bounds__(kThreads) void mfma_scan_kernel(MfmaParams p) {
         av[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < KK; ++kk)
-          qs[cb] = mfma16(ld8(&ShT[(16 * cb + r16) * KP + 32 * kk + k8]), as8(qA[kk]), qs[cb]);
+          qs[cb] = mfma16(ld8(&sh[(16 * cb + r16) * KP + 32 * kk + k8]), as8(qA[kk]), qs[cb]);
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk)
           av[cb] = mfma16(ld8(&VpT[(16 * cb + r16) * LP + 32 * kk + k8]), as8(atA[kk]), av[cb]);
       }
-      if (more) load_q(n + 1);
+      load_q(nn);
       const int t = tok0 + my_tok;
       const float ysc = p.scale * egA;
-      if (t < p.S) {
-        TY* yrow = static_cast<TY*>(p.y) + ((size_t(b) * p.S + t) * p.H + h) * p.V + j0;
+      TY* yrow = t < p.S ? static_cast<TY*>(p.y) + (bh_row0 + size_t(t) * tokstride) * p.V + j0
+                         : reinterpret_cast<TY*>(p.sink);
 #pragma unroll
-        for (int cb = 0; cb < CB; ++cb) {
-          float o[4];
+      for (int cb = 0; cb < CB; ++cb) {
+        float o[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) o[r] = ysc * qs[cb][r] + av[cb][r];
-          TY* dst = yrow + 16 * cb + 4 * q4;
-          if constexpr (sizeof(TY) == 2)
-            *reinterpret_cast<uint2*>(dst) = make_uint2(pk_bf16(o[0], o[1]), pk_bf16(o[2], o[3]));
-          else
-            *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
-        }
+        for (int r = 0; r < 4; ++r) o[r] = ysc * qs[cb][r] + av[cb][r];
+        TY* dst = yrow + 16 * cb + 4 * q4;
+        if constexpr (sizeof(TY) == 2)
+          *reinterpret_cast<uint2*>(dst) = make_uint2(pk_bf16(o[0], o[1]), pk_bf16(o[2], o[3]));
+        else
+          *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
       }
     }
-    __syncthreads();
 
-    // Phase 3b: S ← e^{G_last}⊙S + (e^{G_last−G}⊙K)ᵀ·V'.
+    // Phase 3b: S ← e^{G_last}⊙S + (e^{G_last−G}⊙K)ᵀ·V'; its bf16 copy goes
+    // to the other buffer, so the readout above needs no barrier.
     {
-      const float egl = egl_s;
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb) {
-        const int d = wave * (K / 4) + 16 * rb + r16;
-        bf16x8 a[2];
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) a[kk] = ld8(&KcT[d * LP + 32 * kk + k8]);
+      for (int rb = 0; rb < RB; ++rb)
 #pragma unroll
         for (int cb = 0; cb < CB; ++cb) {
           f32x4 acc = S[rb][cb];
@@ -545,11 +564,10 @@ __global__ __launch_bounds__(kThreads) void mfma_scan_kernel(MfmaParams p) {
           for (int r = 0; r < 4; ++r) acc[r] *= egl;
 #pragma unroll
           for (int kk = 0; kk < 2; ++kk)
-            acc = mfma16(a[kk], ld8(&VpT[(16 * cb + r16) * LP + 32 * kk + k8]), acc);
+            acc = mfma16(as8(kcA[rb][kk]), ld8(&VpT[(16 * cb + r16) * LP + 32 * kk + k8]), acc);
           S[rb][cb] = acc;
         }
-      }
-      write_state();
+      write_state(ShT[(n + 1) & 1]);
     }
     __syncthreads();
   }
@@ -578,7 +596,8 @@ bool mfma_fwd_supported(const Dims& d, int qkv_dtype, int y_dtype) {
 
 size_t mfma_fwd_workspace(const Dims& d) {
   const size_t G = size_t(d.B) * d.N * d.H;
-  return 3 * region(G * kL * kL * 2) + region(G * kL * 4);
+  return 3 * region(G * kL * kL * 2) + region(G * kL * 4) + region(G * size_t(d.K) * kL * 2) +
+         region(kZeroElems * 2) + region(size_t(kBV) * (d.V / kBV) * 4);
 }
 
 hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, const void* v,
@@ -611,6 +630,12 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
   p.attn = reinterpret_cast<uint16_t*>(base);
   base += region(G * kL * kL * 2);
   p.gc = reinterpret_cast<float*>(base);
+  base += region(G * kL * 4);
+  p.KcT = reinterpret_cast<uint16_t*>(base);
+  base += region(G * size_t(d.K) * kL * 2);
+  p.zero = reinterpret_cast<uint16_t*>(base);
+  base += region(kZeroElems * 2);
+  p.sink = reinterpret_cast<uint16_t*>(base);
 
   {
     ProfScope ps("dn_mfma_intra", stream);
