@@ -23,6 +23,12 @@
 // (I−N)T = I, unit-lower structure and the constant-key bound of
 // src/delta/tri/tests.rs.
 //
+// Parity unpinned: the per-channel decay when its clamp binds (an exponent
+// reaching MAX_EXPONENT = 48 within half a 16-row block, decay.rs:41-49).
+// block_decay/channel_scores_backward follow the reference's formula there,
+// but no reference-held vector or closed form fixes those "wrong-but-finite"
+// values; gates in the documented range [-5, 0) never reach the clamp.
+//
 // Layouts are the reference's (src/delta/path.rs:120-141): row-major
 //   q,k [B,S,H,K]  v [B,S,H,V]  erase [B,S,H,ew]  write [B,S,H,ww]
 //   g [B,S,H,dw] (dw = 0: ungated)  state [B,H,K,V]  y [B,S,H,V].
