@@ -146,9 +146,9 @@ def bench_decode(torch, pkg, steps, warmup):
     abi.profile_enable(False)
     us = start.elapsed_time(stop) * 1e3 / steps
     step_bytes = 2 * B * H * K * V * 4 + B * H * (2 * K + 2 * V + 2) * 4
-    name = "dn_step_tile"
-    k_us = prof[name][0] * 1e3 / prof[name][1] if name in prof else us
-    return dict(us=us, kernel_us=k_us, bytes=step_bytes, prof=prof)
+    name = max(prof, key=lambda n: prof[n][0]) if prof else None
+    k_us = prof[name][0] * 1e3 / prof[name][1] if name else us
+    return dict(us=us, kernel_us=k_us, bytes=step_bytes, prof=prof, kernel=name)
 
 
 def cpu_baseline(torch):
@@ -253,10 +253,10 @@ def main():
         gbs = dc["bytes"] / (dc["kernel_us"] * 1e-6) / 1e9
         decode = {"us_per_step": round(dc["us"], 2), "kernel_us": round(dc["kernel_us"], 2),
                   "steps": args.decode_steps, "bytes_per_step": dc["bytes"],
-                  "roofline": {"bound": "hbm", "kernel": "dn_step_tile",
+                  "roofline": {"bound": "hbm", "kernel": dc["kernel"],
                                "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                "frac": round(gbs / HBM_PEAK_GBS, 4),
-                               "traffic": traffic_from_profiles("dn_step_tile")}}
+                               "traffic": traffic_from_profiles(dc["kernel"])}}
         print(f"[bench] decode {decode}", file=sys.stderr, flush=True)
 
     cpu = None

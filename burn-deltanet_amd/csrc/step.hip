@@ -154,6 +154,115 @@ __global__ __launch_bounds__(kThreads) void step_tile_kernel(StepParams p) {
   }
 }
 
+// Row-streaming variant for head_v_dim ≤ 256: a workgroup of 8 waves owns a
+// column block of 64·C columns of one (head, batch) and all its K rows; a lane
+// owns C consecutive columns, so each wave reads and writes whole 64·C·4-byte
+// row segments. The reduction over the key axis crosses the 8 waves through
+// LDS. With C = 2 one (head, batch) spans two workgroups of half the
+// registers, which doubles the state bytes in flight per CU.
+constexpr int kRowWaves = 8;
+constexpr int kRowThreads = 64 * kRowWaves;
+constexpr int kRowCols = 2;  // columns per lane on the launch path
+template <int C>
+using ntv = float __attribute__((ext_vector_type(C)));
+
+template <class TQ, class TY, int RPT, int C>
+__global__ __launch_bounds__(kRowThreads) void step_row_kernel(StepParams p) {
+  constexpr int W = 64 * C;  // columns per workgroup
+  using vec = ntv<C>;
+  const int nblk = (p.V + W - 1) / W;
+  const int cb = blockIdx.x % nblk, bh_id = blockIdx.x / nblk;
+  const int h = bh_id % p.H, b = bh_id / p.H;
+  const int tid = threadIdx.x, lane = tid & 63, rg = tid >> 6;
+  const int K = p.K, V = p.V;
+  const int jb = cb * W;       // first column of the block
+  const int j0 = jb + C * lane;  // first column of the lane
+  const size_t bh = size_t(b) * p.H + h;
+
+  extern __shared__ float lds[];
+  float* s_k = lds;
+  float* s_ke = s_k + K;
+  float* s_q = s_ke + K;
+  float* s_a = s_q + K;
+  float* red_r = s_a + K;              // [8][W]
+  float* red_q = red_r + kRowWaves * W;  // [8][W]
+  float* s_u = red_q + kRowWaves * W;    // [W]
+  float* s_kq = s_u + W;                 // [1]
+
+  const TQ* q = static_cast<const TQ*>(p.q) + bh * K;
+  const TQ* k = static_cast<const TQ*>(p.k) + bh * K;
+  for (int i = tid; i < K; i += kRowThreads) {
+    const float ki = ld(k, i);
+    s_k[i] = ki;
+    s_ke[i] = ki * p.erase[bh * p.ew + (p.ew == 1 ? 0 : i)];
+    s_q[i] = p.scale * ld(q, i);
+    s_a[i] = p.dw ? expf(p.g[bh * p.dw + (p.dw == 1 ? 0 : i)]) : 1.0f;
+  }
+  __syncthreads();
+  if (tid < 64) {
+    float acc = 0.f;
+    for (int i = tid; i < K; i += 64) acc += s_k[i] * s_q[i];
+    acc = wave_sum(acc);
+    if (tid == 0) s_kq[0] = acc;
+  }
+
+  // The state streams through once per step: non-temporal loads and stores
+  // keep it from displacing anything in L2 / Infinity Cache. (Issuing these
+  // loads before the gate set-up above measured slower on config 3.)
+  const bool colok = j0 + C - 1 < V;
+  const float* sin = p.s_in + bh * size_t(K) * V + j0;
+  vec s[RPT];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg + kRowWaves * r;
+    s[r] = (i < K && colok)
+               ? __builtin_nontemporal_load(reinterpret_cast<const vec*>(sin + size_t(i) * V))
+               : vec(0.f);
+  }
+
+  vec pr = vec(0.f), pq = vec(0.f);
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg + kRowWaves * r;
+    if (i < K) {
+      s[r] *= s_a[i];
+      pr += s[r] * s_ke[i];
+      pq += s[r] * s_q[i];
+    }
+  }
+  *reinterpret_cast<vec*>(&red_r[rg * W + C * lane]) = pr;
+  *reinterpret_cast<vec*>(&red_q[rg * W + C * lane]) = pq;
+  __syncthreads();
+
+  if (tid < W) {
+    const int j = jb + tid;
+    float rr = 0.f, qs = 0.f;
+#pragma unroll
+    for (int x = 0; x < kRowWaves; ++x) {
+      rr += red_r[x * W + tid];
+      qs += red_q[x * W + tid];
+    }
+    float u = 0.f;
+    if (j < V) {
+      const TQ* v = static_cast<const TQ*>(p.v) + bh * V;
+      u = ld(v, j) * p.write[bh * p.ww + (p.ww == 1 ? 0 : j)] - rr;
+      st(static_cast<TY*>(p.y), bh * V + j, qs + u * s_kq[0]);
+    }
+    s_u[tid] = u;
+  }
+  __syncthreads();
+
+  const vec uv = *reinterpret_cast<const vec*>(&s_u[C * lane]);
+  float* sout = p.s_out + bh * size_t(K) * V + j0;
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg + kRowWaves * r;
+    if (i < K && colok)
+      __builtin_nontemporal_store(s[r] + s_k[i] * uv,
+                                  reinterpret_cast<vec*>(sout + size_t(i) * V));
+  }
+}
+
 // Fallback for head_k_dim > 512: one workgroup per (head, batch), two passes
 // over S (one lane per column).
 template <class TQ, class TY>
@@ -191,6 +300,22 @@ hipError_t launch_typed(const StepParams& p, hipStream_t stream) {
   const bool vec4 = (p.V % 4) == 0 &&
                     ((reinterpret_cast<uintptr_t>(p.s_in) | reinterpret_cast<uintptr_t>(p.s_out)) %
                      16) == 0;
+  if (vec4 && p.V <= 256 && p.V >= 128 && p.K <= 256) {
+    constexpr int W = 64 * kRowCols;
+    const size_t lds = sizeof(float) * (4 * size_t(p.K) + 2 * kRowWaves * W + W + 1);
+    const dim3 grid(unsigned(p.B * p.H * ((p.V + W - 1) / W)));
+    ProfScope ps("dn_step_row", stream);
+    if (p.K <= 64)
+      hipLaunchKernelGGL((step_row_kernel<TQ, TY, 8, kRowCols>), grid, dim3(kRowThreads), lds,
+                         stream, p);
+    else if (p.K <= 128)
+      hipLaunchKernelGGL((step_row_kernel<TQ, TY, 16, kRowCols>), grid, dim3(kRowThreads), lds,
+                         stream, p);
+    else
+      hipLaunchKernelGGL((step_row_kernel<TQ, TY, 32, kRowCols>), grid, dim3(kRowThreads), lds,
+                         stream, p);
+    return hipGetLastError();
+  }
   const int rpt_needed = (p.K + kRowGroups - 1) / kRowGroups;
   dim3 grid((p.V + kTileV - 1) / kTileV, p.H, p.B);
   const size_t lds = sizeof(float) * (4 * size_t(p.K) + 2 * kRowGroups * kTileV + kTileV + 1);

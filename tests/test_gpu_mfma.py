@@ -110,3 +110,14 @@ def test_mfma_constant_keys_stay_bounded(rng):
         assert np.isfinite(y).all()
         y0, s0 = O.recurrent(*as_oracle_inputs(g_args), dtype=np.float64)
         assert rel_err(y, y0) < TOL and rel_err(s, s0) < TOL
+
+
+def test_other_shapes_take_the_generic_path(rng):
+    """dk outside {64, 128} or chunk ≠ 64 are served by the generic kernels under AUTO."""
+    announce("mfma coverage")
+    for K, L in [(96, 64), (128, 32)]:
+        g_args = to_gpu(gdn_inputs(rng, 1, 100, 2, K, 64, True), torch.bfloat16)
+        q, k, v, e, w, g, s = g_args
+        y = torch.empty((1, 100, 2, 64), dtype=torch.bfloat16, device=DEV)
+        a = pkg.abi.chunk_fwd_args(q, k, v, e, w, g, s, y, torch.empty_like(s), L, None)
+        assert pkg.abi.lib().dn_chunk_fwd_algo(a) == pkg.abi.DN_ALGO_GENERIC
