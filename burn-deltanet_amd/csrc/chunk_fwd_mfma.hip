@@ -32,6 +32,8 @@
 //        The four tiles of one (b, h) are mapped to one XCD so their shared
 //        K/Q/T/attn reads hit the same L2.
 
+#include <algorithm>
+
 #include "dn_common.hpp"
 
 namespace dn {
@@ -65,6 +67,23 @@ __device__ inline f32x4 mfma_f32(float a, float b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Value of lane `src` of each group of four lanes, to the whole group (DPP
+// quad_perm); `src` folds to a constant once the caller's loop is unrolled.
+template <int SRC>
+__device__ inline float quad_bcast_c(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v),
+                                                 SRC | (SRC << 2) | (SRC << 4) | (SRC << 6),
+                                                 0xf, 0xf, false));
+}
+__device__ inline float quad_bcast(float v, int src) {
+  switch (src) {
+    case 0: return quad_bcast_c<0>(v);
+    case 1: return quad_bcast_c<1>(v);
+    case 2: return quad_bcast_c<2>(v);
+    default: return quad_bcast_c<3>(v);
+  }
+}
+
 __device__ inline bf16x8 zero8() { return __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u)); }
 
 struct MfmaParams {
@@ -88,213 +107,274 @@ struct MfmaParams {
 // ---------------------------------------------------------------------------
 // intra
 // ---------------------------------------------------------------------------
-template <int K>
-__global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p) {
-  constexpr int KP = K + 8;  // padded LDS row (bf16 elements)
-  // The K/Q tiles are dead once the scores are formed; T and the merge
-  // scratch reuse their space, which keeps two workgroups per CU.
-  constexpr int kTileBytes = 2 * kL * KP * 2;
+template <int K, bool GATED>
+__global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int G) {
+  constexpr int KP = K + 8;                     // padded LDS row (bf16 elements)
+  constexpr int KS8 = K / 8;                    // 16-byte segments per key row
+  constexpr int NLD = kL * KS8 / kThreads;      // 16-byte loads per lane per tile
+  constexpr int kQBytes = kL * KP * 2;
   constexpr int kSolveBytes = (kL * (kL + 1) + (kL / 2) * (kL / 2 + 1)) * 4;
+  // The Q tile is dead once the scores are formed; T and the merge scratch
+  // reuse its space, which keeps two workgroups per CU.
   __shared__ __attribute__((aligned(16)))
-  unsigned char stage[kTileBytes > kSolveBytes ? kTileBytes : kSolveBytes];
-  uint16_t* Ks = reinterpret_cast<uint16_t*>(stage);
-  uint16_t* Qs = Ks + kL * KP;
-  float(*Tm)[kL + 1] = reinterpret_cast<float(*)[kL + 1]>(stage);  // T, fp32
+  unsigned char qsolve[kQBytes > kSolveBytes ? kQBytes : kSolveBytes];
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kL * KP];
+  uint16_t* Qs = reinterpret_cast<uint16_t*>(qsolve);
+  float(*Tm)[kL + 1] = reinterpret_cast<float(*)[kL + 1]>(qsolve);  // T, fp32
   float(*Xs)[kL / 2 + 1] =
-      reinterpret_cast<float(*)[kL / 2 + 1]>(stage + kL * (kL + 1) * 4);
-  __shared__ float A[kL][kL + 1];  // strict-lower Akk, fp32
+      reinterpret_cast<float(*)[kL / 2 + 1]>(qsolve + kL * (kL + 1) * 4);
+  __shared__ float A[kL][kL + 1];  // strict-lower Akk, fp32 (upper blocks never read)
   __shared__ __attribute__((aligned(16))) uint16_t At[kL * (kL + 8)];  // attn, bf16
   __shared__ float gcs[kL], ers[kL];
 
-  const int cid = blockIdx.x;
-  const int h = cid % p.H, n = (cid / p.H) % p.N, b = cid / (p.H * p.N);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int tok0 = n * kL;
-  if (cid == 0)
+  if (blockIdx.x == 0)
     for (int i = tid; i < kZeroElems / 8; i += kThreads)
       reinterpret_cast<uint4*>(p.zero)[i] = make_uint4(0u, 0u, 0u, 0u);
-
-  // Stage the K and Q chunk tiles (zero past the sequence end).
-  for (int idx = tid; idx < kL * K / 8; idx += kThreads) {
-    const int row = idx / (K / 8), c8 = idx % (K / 8);
-    const int tok = tok0 + row;
-    bf16x8 kv = zero8(), qv = zero8();
-    if (tok < p.S) {
-      const size_t off = ((size_t(b) * p.S + tok) * p.H + h) * K + 8 * c8;
-      kv = ld8(p.k + off);
-      qv = ld8(p.q + off);
-    }
-    *reinterpret_cast<bf16x8*>(&Ks[row * KP + 8 * c8]) = kv;
-    *reinterpret_cast<bf16x8*>(&Qs[row * KP + 8 * c8]) = qv;
+  // attn's blocks above the diagonal are zero for every chunk.
+  for (int idx = tid; idx < kL * kL; idx += kThreads) {
+    const int i = idx / kL, j = idx % kL;
+    if (j / 16 > i / 16) At[i * (kL + 8) + j] = 0;
   }
-  // In-chunk cumulative gate and the erase gate, one token per lane.
-  if (wave == 0) {
-    const int tok = tok0 + lane;
-    const size_t row = (size_t(b) * p.S + tok) * p.H + h;
-    float gv = (p.gated && tok < p.S) ? p.g[row] : 0.f;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float up = __shfl_up(gv, off, 64);
-      if (lane >= off) gv += up;
-    }
-    gcs[lane] = gv;
-    ers[lane] = tok < p.S ? p.erase[row] : 0.f;
-    p.gc[size_t(cid) * kL + lane] = gv;
-  }
-  __syncthreads();
 
-  // Akk = e ⊙ (K Kᵀ) ⊙ decay (strict lower), attn = scale (Q Kᵀ) ⊙ decay.
-  {
-    const int rb = wave;
-    const int r16 = lane & 15, k8 = 8 * (lane >> 4);
-    bf16x8 ak[K / 32], aq[K / 32];
+  // The workgroup walks chunk-heads cid = blockIdx.x, + gridDim.x, …; the
+  // next chunk's K, Q and gates are loaded into registers while this one
+  // is processed.
+  uint4 kr[NLD], qr[NLD];
+  float gr = 0.f, er = 0.f;
+  auto load = [&](int cid) {
+    const int h = cid % p.H, n = (cid / p.H) % p.N, b = cid / (p.H * p.N);
 #pragma unroll
-    for (int kk = 0; kk < K / 32; ++kk) {
-      ak[kk] = ld8(&Ks[(16 * rb + r16) * KP + 32 * kk + k8]);
-      aq[kk] = ld8(&Qs[(16 * rb + r16) * KP + 32 * kk + k8]);
+    for (int m = 0; m < NLD; ++m) {
+      const int idx = tid + kThreads * m, row = idx / KS8, c8 = idx % KS8;
+      const int tok = n * kL + row;
+      kr[m] = qr[m] = make_uint4(0u, 0u, 0u, 0u);
+      if (tok < p.S) {
+        const size_t off = ((size_t(b) * p.S + tok) * p.H + h) * K + 8 * c8;
+        kr[m] = *reinterpret_cast<const uint4*>(p.k + off);
+        qr[m] = *reinterpret_cast<const uint4*>(p.q + off);
+      }
     }
-    for (int cb = 0; cb < 4; ++cb) {
-      const int j = 16 * cb + r16;
-      if (cb > rb) {
+    if (wave == 0) {
+      const int tok = n * kL + lane;
+      const size_t row = (size_t(b) * p.S + tok) * p.H + h;
+      gr = (GATED && tok < p.S) ? p.g[row] : 0.f;
+      er = tok < p.S ? p.erase[row] : 0.f;
+    }
+  };
+  if (int(blockIdx.x) < G) load(blockIdx.x);
+
+  // T (hi, lo) and attn of the previous chunk, 16 values of one row per lane:
+  // their global stores are issued after the next chunk is staged, so no
+  // wait on them lands at the top of the loop.
+  uint4 pend[6];
+  int pend_cid = -1;
+  auto store_pending = [&]() {
+    const int row = tid / 4, c0 = 16 * (tid % 4);
+    const size_t off = size_t(pend_cid) * kL * kL + row * kL + c0;
+    uint4* tdst = reinterpret_cast<uint4*>(p.T + off);
+    uint4* ldst = reinterpret_cast<uint4*>(p.Tlo + off);
+    uint4* adst = reinterpret_cast<uint4*>(p.attn + off);
+    tdst[0] = pend[0];
+    tdst[1] = pend[1];
+    ldst[0] = pend[2];
+    ldst[1] = pend[3];
+    adst[0] = pend[4];
+    adst[1] = pend[5];
+  };
+
+  for (int cid = blockIdx.x; cid < G; cid += gridDim.x) {
+#pragma unroll
+    for (int m = 0; m < NLD; ++m) {
+      const int idx = tid + kThreads * m, row = idx / KS8, c8 = idx % KS8;
+      *reinterpret_cast<uint4*>(&Ks[row * KP + 8 * c8]) = kr[m];
+      *reinterpret_cast<uint4*>(&Qs[row * KP + 8 * c8]) = qr[m];
+    }
+    // In-chunk cumulative gate and the erase gate, one token per lane.
+    if (wave == 0) {
+      float gv = gr;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float up = __shfl_up(gv, off, 64);
+        if (lane >= off) gv += up;
+      }
+      gcs[lane] = gv;
+      ers[lane] = er;
+      p.gc[size_t(cid) * kL + lane] = gv;
+    }
+    if (pend_cid >= 0) store_pending();
+    if (cid + int(gridDim.x) < G) load(cid + gridDim.x);
+    __syncthreads();
+
+    // Akk = e ⊙ (K Kᵀ) ⊙ decay (strict lower), attn = scale (Q Kᵀ) ⊙ decay:
+    // the ten lower 16×16 block pairs (rb ≥ cb) are dealt to the waves 3/3/2/2.
+    {
+      const int r16 = lane & 15, k8 = 8 * (lane >> 4);
+#pragma unroll
+      for (int pi = wave; pi < 10; pi += 4) {
+        const int rb = pi < 1 ? 0 : pi < 3 ? 1 : pi < 6 ? 2 : 3;
+        const int cb = pi - rb * (rb + 1) / 2;
+        f32x4 acck = {0.f, 0.f, 0.f, 0.f}, accq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < K / 32; ++kk) {
+          const bf16x8 ak = ld8(&Ks[(16 * rb + r16) * KP + 32 * kk + k8]);
+          const bf16x8 aq = ld8(&Qs[(16 * rb + r16) * KP + 32 * kk + k8]);
+          const bf16x8 bk = ld8(&Ks[(16 * cb + r16) * KP + 32 * kk + k8]);
+          acck = mfma16(ak, bk, acck);
+          accq = mfma16(aq, bk, accq);
+        }
+        const int j = 16 * cb + r16;
+        const float gj = gcs[j];
+        float gi[4], ei[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          gi[r] = gcs[16 * rb + 4 * (lane >> 4) + r];
+          ei[r] = ers[16 * rb + 4 * (lane >> 4) + r];
+        }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int i = 16 * rb + 4 * (lane >> 4) + r;
-          A[i][j] = 0.f;
-          At[i * (kL + 8) + j] = 0;
+          // G is non-increasing, so the exponent is ≤ 0 wherever it is kept;
+          // the clamp only keeps the masked (j > i) lanes finite.
+          const float e = GATED ? __expf(fminf(gi[r] - gj, 0.f)) : 1.f;
+          const float decay = (j <= i) ? e : 0.f;
+          const float a = ei[r] * acck[r] * decay;
+          A[i][j] = (j < i) ? a : 0.f;
+          At[i * (kL + 8) + j] = uint16_t(pk_bf16(p.scale * accq[r] * decay, 0.f));
         }
-        continue;
-      }
-      f32x4 acck = {0.f, 0.f, 0.f, 0.f}, accq = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < K / 32; ++kk) {
-        const bf16x8 bk = ld8(&Ks[(16 * cb + r16) * KP + 32 * kk + k8]);
-        acck = mfma16(ak[kk], bk, acck);
-        accq = mfma16(aq[kk], bk, accq);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = 16 * rb + 4 * (lane >> 4) + r;
-        const float decay = (j <= i) ? (p.gated ? __expf(gcs[i] - gcs[j]) : 1.f) : 0.f;
-        A[i][j] = (j < i) ? ers[i] * acck[r] * decay : 0.f;
-        At[i * (kL + 8) + j] = uint16_t(pk_bf16(p.scale * accq[r] * decay, 0.f));
       }
     }
-  }
-  __syncthreads();
-
-  // Kcᵀ = (e^{G_last−G} ⊙ K)ᵀ for the scan's state update, while the K tile
-  // is still in LDS: TPD lanes per key channel d, each packing a run of tokens.
-  {
-    constexpr int TPD = kThreads / K, RUN = kL / TPD;
-    const int d = tid / TPD, t0 = RUN * (tid % TPD);
-    const float glast = gcs[kL - 1];
-    uint32_t w[RUN / 2];
-#pragma unroll
-    for (int e = 0; e < RUN / 2; ++e) {
-      const int t = t0 + 2 * e;
-      const float k0 = bf16_to_f32(Ks[t * KP + d]), k1 = bf16_to_f32(Ks[(t + 1) * KP + d]);
-      w[e] = p.gated ? pk_bf16(k0 * __expf(glast - gcs[t]), k1 * __expf(glast - gcs[t + 1]))
-                     : pk_bf16(k0, k1);
-    }
-    uint32_t* dst = reinterpret_cast<uint32_t*>(p.KcT + (size_t(cid) * K + d) * kL + t0);
-#pragma unroll
-    for (int e = 0; e < RUN / 2; e += 4)
-      *reinterpret_cast<uint4*>(dst + e) = make_uint4(w[e], w[e + 1], w[e + 2], w[e + 3]);
-  }
-  __syncthreads();
-
-  // T: invert the four 16×16 diagonal blocks (one wave each, a lane per column).
-  if (lane < 16) {
-    const int base = 16 * wave, c = lane;
-    float t[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) t[i] = (i == c) ? 1.f : 0.f;
-#pragma unroll
-    for (int i = 1; i < 16; ++i) {
-      if (i > c) {
-        float acc = 0.f;
-#pragma unroll
-        for (int k2 = 0; k2 < i; ++k2) acc += A[base + i][base + k2] * t[k2];
-        t[i] = -acc;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) Tm[base + i][base + c] = t[i];
-  }
-  // Zero everything above the block diagonal that the merges do not write.
-  for (int idx = tid; idx < kL * kL; idx += kThreads) {
-    const int i = idx / kL, j = idx % kL;
-    if (j / 16 > i / 16) Tm[i][j] = 0.f;
-  }
-  __syncthreads();
-  // The merges run on fp32 MFMA (v_mfma_f32_16x16x4_f32: exact fp32 products):
-  // lane l holds A[l%16][l/16] and B[l/16][l%16] of a 16×4 · 4×16 step, and
-  // D[4(l/16)+r][l%16]. Full-block sums are exact: the triangular factors
-  // hold zeros outside their triangles.
-  const int m16 = lane & 15, g4 = lane >> 4;
-  // 16 → 32: T₁₀ = −T₁₁ A₁₀ T₀₀ for the two 32-blocks (waves 0 and 1).
-  if (wave < 2) {
-    const int r0 = 32 * wave + 16, c0 = 32 * wave;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4)
-      acc = mfma_f32(A[r0 + m16][c0 + 4 * s4 + g4], Tm[c0 + 4 * s4 + g4][c0 + m16], acc);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) Xs[16 * wave + 4 * g4 + r][m16] = acc[r];
-  }
-  __syncthreads();
-  if (wave < 2) {
-    const int r0 = 32 * wave + 16, c0 = 32 * wave;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4)
-      acc = mfma_f32(Tm[r0 + m16][r0 + 4 * s4 + g4], Xs[16 * wave + 4 * s4 + g4][m16], acc);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) Tm[r0 + 4 * g4 + r][c0 + m16] = -acc[r];
-  }
-  __syncthreads();
-  // 32 → 64: T[32:,:32] = −T[32:,32:] A[32:,:32] T[:32,:32]; wave w owns
-  // output tile (w/2, w%2) of the 32×32 block.
-  {
-    const int ti = wave >> 1, tj = wave & 1;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s4 = 0; s4 < 8; ++s4)
-      acc = mfma_f32(A[32 + 16 * ti + m16][4 * s4 + g4], Tm[4 * s4 + g4][16 * tj + m16], acc);
     __syncthreads();
-#pragma unroll
-    for (int r = 0; r < 4; ++r) Xs[16 * ti + 4 * g4 + r][16 * tj + m16] = acc[r];
-    __syncthreads();
-    acc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s4 = 0; s4 < 8; ++s4)
-      acc = mfma_f32(Tm[32 + 16 * ti + m16][32 + 4 * s4 + g4], Xs[4 * s4 + g4][16 * tj + m16],
-                     acc);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) Tm[32 + 16 * ti + 4 * g4 + r][16 * tj + m16] = -acc[r];
-  }
-  __syncthreads();
 
-  // Store T and attn as bf16, 16 values per lane.
-  {
-    const int row = tid / 4, c0 = 16 * (tid % 4);
-    uint16_t* tdst = p.T + size_t(cid) * kL * kL + row * kL + c0;
-    uint16_t* ldst = p.Tlo + size_t(cid) * kL * kL + row * kL + c0;
-    uint16_t* adst = p.attn + size_t(cid) * kL * kL + row * kL + c0;
-    uint32_t tv[8], tl[8];
+    {
+      // T's diagonal 16×16 block `wave` by column elimination: lane (c, g)
+      // holds rows g, g+4, g+8, g+12 of column c; step k₂ broadcasts x[k₂]
+      // inside the lane quad (DPP) and updates the rows below it.
+      const int base = 16 * wave, c = lane >> 2, g = lane & 3;
+      float x[4];
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const float x0 = Tm[row][c0 + 2 * c], x1 = Tm[row][c0 + 2 * c + 1];
-      tv[c] = pk_bf16(x0, x1);
-      tl[c] = pk_bf16(x0 - lo_f(tv[c]), x1 - hi_f(tv[c]));
+      for (int j = 0; j < 4; ++j) x[j] = (4 * j + g == c) ? 1.f : 0.f;
+      // Multipliers A[i][k₂] for i > k₂ (zero otherwise), read up front.
+      float mul[15][4];
+#pragma unroll
+      for (int k2 = 0; k2 < 15; ++k2)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int i = 4 * j + g;
+          mul[k2][j] = (4 * j + 3 > k2 && i > k2) ? A[base + i][base + k2] : 0.f;
+        }
+#pragma unroll
+      for (int k2 = 0; k2 < 15; ++k2) {
+        const float xk = quad_bcast(x[k2 >> 2], k2 & 3);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (4 * j + 3 > k2) x[j] -= mul[k2][j] * xk;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) Tm[base + 4 * j + g][base + c] = x[j];
     }
-    *reinterpret_cast<uint4*>(tdst) = make_uint4(tv[0], tv[1], tv[2], tv[3]);
-    *reinterpret_cast<uint4*>(tdst + 8) = make_uint4(tv[4], tv[5], tv[6], tv[7]);
-    *reinterpret_cast<uint4*>(ldst) = make_uint4(tl[0], tl[1], tl[2], tl[3]);
-    *reinterpret_cast<uint4*>(ldst + 8) = make_uint4(tl[4], tl[5], tl[6], tl[7]);
-    *reinterpret_cast<bf16x8*>(adst) = ld8(&At[row * (kL + 8) + c0]);
-    *reinterpret_cast<bf16x8*>(adst + 8) = ld8(&At[row * (kL + 8) + c0 + 8]);
+    {
+      // Kcᵀ = (e^{G_last−G} ⊙ K)ᵀ for the scan's state update, while the K
+      // tile is in LDS: an item is one key channel × 16 tokens, consecutive
+      // lanes taking consecutive channels (conflict-free column reads).
+      const float glast = gcs[kL - 1];
+      for (int it = tid; it < K * 2; it += kThreads) {
+        // Channels d, d+1 of 16 tokens: one 32-bit LDS read per token.
+        const int d = 2 * (it % (K / 2)), t0 = 16 * (it / (K / 2));
+        uint32_t w0[8], w1[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int t = t0 + 2 * e;
+          const uint32_t a = *reinterpret_cast<const uint32_t*>(&Ks[t * KP + d]);
+          const uint32_t b = *reinterpret_cast<const uint32_t*>(&Ks[(t + 1) * KP + d]);
+          const float s0 = GATED ? __expf(glast - gcs[t]) : 1.f;
+          const float s1 = GATED ? __expf(glast - gcs[t + 1]) : 1.f;
+          w0[e] = pk_bf16(lo_f(a) * s0, lo_f(b) * s1);
+          w1[e] = pk_bf16(hi_f(a) * s0, hi_f(b) * s1);
+        }
+        uint4* dst0 = reinterpret_cast<uint4*>(p.KcT + (size_t(cid) * K + d) * kL + t0);
+        uint4* dst1 = reinterpret_cast<uint4*>(p.KcT + (size_t(cid) * K + d + 1) * kL + t0);
+        dst0[0] = make_uint4(w0[0], w0[1], w0[2], w0[3]);
+        dst0[1] = make_uint4(w0[4], w0[5], w0[6], w0[7]);
+        dst1[0] = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+        dst1[1] = make_uint4(w1[4], w1[5], w1[6], w1[7]);
+      }
+      // Zero T above the block diagonal (the merges never write there).
+      for (int idx = tid; idx < kL * kL; idx += kThreads) {
+        const int i = idx / kL, j = idx % kL;
+        if (j / 16 > i / 16) Tm[i][j] = 0.f;
+      }
+    }
+    __syncthreads();
+    // The merges run on fp32 MFMA (v_mfma_f32_16x16x4_f32: exact fp32
+    // products): lane l holds A[l%16][l/16] and B[l/16][l%16] of a
+    // 16×4 · 4×16 step, and D[4(l/16)+r][l%16]. Full-block sums are exact:
+    // the triangular factors hold zeros outside their triangles.
+    const int m16 = lane & 15, g4 = lane >> 4;
+    // 16 → 32: T₁₀ = −T₁₁ A₁₀ T₀₀ for the two 32-blocks (waves 0 and 1).
+    if (wave < 2) {
+      const int r0 = 32 * wave + 16, c0 = 32 * wave;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+        acc = mfma_f32(A[r0 + m16][c0 + 4 * s4 + g4], Tm[c0 + 4 * s4 + g4][c0 + m16], acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Xs[16 * wave + 4 * g4 + r][m16] = acc[r];
+    }
+    __syncthreads();
+    if (wave < 2) {
+      const int r0 = 32 * wave + 16, c0 = 32 * wave;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+        acc = mfma_f32(Tm[r0 + m16][r0 + 4 * s4 + g4], Xs[16 * wave + 4 * s4 + g4][m16], acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Tm[r0 + 4 * g4 + r][c0 + m16] = -acc[r];
+    }
+    __syncthreads();
+    // 32 → 64: T[32:,:32] = −T[32:,32:] A[32:,:32] T[:32,:32]; wave w owns
+    // output tile (w/2, w%2) of the 32×32 block.
+    {
+      const int ti = wave >> 1, tj = wave & 1;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s4 = 0; s4 < 8; ++s4)
+        acc = mfma_f32(A[32 + 16 * ti + m16][4 * s4 + g4], Tm[4 * s4 + g4][16 * tj + m16], acc);
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Xs[16 * ti + 4 * g4 + r][16 * tj + m16] = acc[r];
+      __syncthreads();
+      acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s4 = 0; s4 < 8; ++s4)
+        acc = mfma_f32(Tm[32 + 16 * ti + m16][32 + 4 * s4 + g4], Xs[4 * s4 + g4][16 * tj + m16],
+                       acc);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) Tm[32 + 16 * ti + 4 * g4 + r][16 * tj + m16] = -acc[r];
+    }
+    __syncthreads();
+
+    // T and attn of this chunk as bf16 rows, 16 values per lane.
+    {
+      const int row = tid / 4, c0 = 16 * (tid % 4);
+      uint32_t tv[8], tl[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const float x0 = Tm[row][c0 + 2 * c], x1 = Tm[row][c0 + 2 * c + 1];
+        tv[c] = pk_bf16(x0, x1);
+        tl[c] = pk_bf16(x0 - lo_f(tv[c]), x1 - hi_f(tv[c]));
+      }
+      pend[0] = make_uint4(tv[0], tv[1], tv[2], tv[3]);
+      pend[1] = make_uint4(tv[4], tv[5], tv[6], tv[7]);
+      pend[2] = make_uint4(tl[0], tl[1], tl[2], tl[3]);
+      pend[3] = make_uint4(tl[4], tl[5], tl[6], tl[7]);
+      pend[4] = *reinterpret_cast<const uint4*>(&At[row * (kL + 8) + c0]);
+      pend[5] = *reinterpret_cast<const uint4*>(&At[row * (kL + 8) + c0 + 8]);
+      pend_cid = cid;
+    }
+    __syncthreads();  // LDS is restaged by the next chunk
   }
+  if (pend_cid >= 0) store_pending();
 }
 
 // ---------------------------------------------------------------------------
@@ -638,13 +718,18 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
   p.sink = reinterpret_cast<uint16_t*>(base);
 
   {
+    // Two resident workgroups per CU (LDS-bound) walk all chunk-heads.
+    const int grid = int(std::min<size_t>(G, size_t(2) * device_cu_count()));
     ProfScope ps("dn_mfma_intra", stream);
-    if (d.K == 128)
-      hipLaunchKernelGGL(mfma_intra_kernel<128>, dim3(unsigned(G)), dim3(kThreads), 0, stream,
-                         p);
-    else
-      hipLaunchKernelGGL(mfma_intra_kernel<64>, dim3(unsigned(G)), dim3(kThreads), 0, stream,
-                         p);
+#define DN_INTRA(KD, GT)                                                                   \
+  hipLaunchKernelGGL((mfma_intra_kernel<KD, GT>), dim3(unsigned(grid)), dim3(kThreads), 0, \
+                     stream, p, int(G))
+    if (d.K == 128) {
+      if (p.gated) DN_INTRA(128, true); else DN_INTRA(128, false);
+    } else {
+      if (p.gated) DN_INTRA(64, true); else DN_INTRA(64, false);
+    }
+#undef DN_INTRA
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

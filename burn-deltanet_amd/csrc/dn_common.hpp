@@ -99,6 +99,9 @@ struct ProfScope {
   hipStream_t stream;
 };
 
+// Compute units of the current device (cached per device; 256 on MI355X).
+int device_cu_count();
+
 // NaN/Inf guard: sets *flag (device int) to 1 if any element is not finite.
 hipError_t launch_nonfinite_scan(const void* p, size_t n, int dtype, int* flag,
                                  hipStream_t stream);

@@ -1,6 +1,8 @@
 // Small utility kernels: the NaN/Inf guard (the reference's `sanity`,
 // src/delta/path.rs:198-207, compiled in by its check-nan/check-inf features).
 
+#include <atomic>
+
 #include "dn_common.hpp"
 
 namespace dn {
@@ -17,6 +19,24 @@ __global__ __launch_bounds__(256) void nonfinite_kernel(const T* p, size_t n, in
 }
 
 }  // namespace
+
+int device_cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) dev = -1;
+  if (dev >= 0) {
+    const int c = cached[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev < 0 ? 0 : dev) !=
+          hipSuccess ||
+      n <= 0)
+    n = 256;
+  if (dev >= 0) cached[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
 
 hipError_t launch_nonfinite_scan(const void* p, size_t n, int dtype, int* flag,
                                  hipStream_t stream) {
