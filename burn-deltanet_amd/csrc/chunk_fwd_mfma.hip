@@ -380,288 +380,315 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
 // ---------------------------------------------------------------------------
 // scan
 // ---------------------------------------------------------------------------
-template <int K, class TY>
-__global__ __launch_bounds__(kThreads, 2) void mfma_scan_kernel(MfmaParams p) {
-  constexpr int RB = K / 64;     // 16-row state blocks per wave
-  constexpr int CB = kBV / 16;   // 16-column blocks per tile
-  constexpr int KK = K / 32;     // 32-deep k-steps over the key dimension
-  constexpr int KP = K + 8;
-  constexpr int LP = kL + 8;
-  // bf16(S)ᵀ is double-buffered (the readout of chunk n and the state update
-  // writing chunk n+1's copy need no barrier between them); the low part
-  // bf16(S − bf16(S))ᵀ is only read by the retrieval.
-  __shared__ __attribute__((aligned(16))) uint16_t ShT[2][kBV * KP];
-  __shared__ __attribute__((aligned(16))) uint16_t SlT[kBV * KP];
-  __shared__ __attribute__((aligned(16))) uint16_t XbT[kBV * LP];  // bf16(X)ᵀ
-  __shared__ __attribute__((aligned(16))) uint16_t XlT[kBV * LP];  // bf16(X − bf16(X))ᵀ
-  __shared__ __attribute__((aligned(16))) uint16_t VpT[kBV * LP];  // bf16 V'ᵀ
-  __shared__ float xes[kL], wrs[kL];  // written and read by one wave only
+// Operand tiles in LDS. Within every 32-deep k-step the contraction index is
+// stored permuted so that the 8 values an MFMA lane supplies (positions
+// 8q..8q+7 of the step) are rows 4q..4q+3 and 16+4q..16+4q+3 of it — exactly
+// the rows a 16×16 accumulator lane holds in two vertically adjacent tiles.
+// Accumulator tiles (S, X, V') thereby become MFMA operands in place, with
+// no LDS round trip. 16-byte chunks are XOR-swizzled by row (conflict-free
+// fragment reads without padding).
+__device__ inline int perm_pos(int k) {
+  const int m = k & 31;
+  return (k & ~31) + 8 * ((m & 15) >> 2) + 4 * (m >> 4) + (m & 3);
+}
+template <int COLS>
+__device__ inline int tile_at(int row, int pos) {
+  // The 16 rows of a fragment read land in 16 distinct 16-byte bank slots.
+  const int sw = COLS >= 128 ? (row & 15) : ((row >> 1) & 7);
+  return row * COLS + (((pos >> 3) ^ sw) << 3) + (pos & 7);
+}
 
-  const int tiles = p.V / kBV;
+// Two vertically adjacent 16×16 accumulator tiles → one bf16 operand
+// fragment of the permuted layout (hi part, and optionally the lo part).
+__device__ inline uint4 frag_hi(const f32x4& a, const f32x4& b) {
+  return make_uint4(pk_bf16(a[0], a[1]), pk_bf16(a[2], a[3]), pk_bf16(b[0], b[1]),
+                    pk_bf16(b[2], b[3]));
+}
+__device__ inline uint4 frag_lo(const f32x4& a, const f32x4& b, const uint4& h) {
+  return make_uint4(pk_bf16(a[0] - lo_f(h.x), a[1] - hi_f(h.x)),
+                    pk_bf16(a[2] - lo_f(h.y), a[3] - hi_f(h.y)),
+                    pk_bf16(b[0] - lo_f(h.z), b[1] - hi_f(h.z)),
+                    pk_bf16(b[2] - lo_f(h.w), b[3] - hi_f(h.w)));
+}
+
+template <int K, class TY, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
+  constexpr int KK = K / 32;      // 32-deep k-steps over the key axis
+  constexpr int RBK = K / 16;     // 16-row blocks of the state
+  constexpr int NT = 64 * WAVES;
+  constexpr int BW = 16 * WAVES;  // value columns per workgroup
+  // One chunk's operand tiles (bf16 elements): K, Q [64][K]; T, Tlo, attn
+  // [64][64]; Kcᵀ [K][64]. Double-buffered: the next chunk is staged while
+  // this one is consumed, so one barrier per chunk suffices.
+  constexpr int oK = 0, oQ = oK + kL * K, oT = oQ + kL * K, oTl = oT + kL * kL,
+                oAt = oTl + kL * kL, oKc = oAt + kL * kL, BUF = oKc + K * kL;
+  constexpr int C16 = BUF / 8;    // 16-byte chunks per chunk's tiles
+  static_assert(C16 % NT == 0, "staging assumes whole rounds");
+  constexpr int NPF = C16 / NT;   // chunks staged per lane
+  __shared__ __attribute__((aligned(16))) uint16_t tiles[2][BUF];
+  __shared__ float gxe[2][kL], gwr[2][kL], gys[2][kL], gegl[2];
+
+  const int ntile = p.V / BW;
   const int BH = p.B * p.H;
-  // XCD-aware: the `tiles` workgroups of one (b, h) get ids ≡ (mod 8).
+  // XCD-aware: the `ntile` workgroups of one (b, h) get ids ≡ (mod 8).
   const int id = blockIdx.x;
-  const int group = id / (8 * tiles), within = id % (8 * tiles);
+  const int group = id / (8 * ntile), within = id % (8 * ntile);
   const int tile = within / 8, bh = group * 8 + within % 8;
   if (bh >= BH) return;
   const int b = bh / p.H, h = bh % p.H;
-  const int j0 = tile * kBV;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r16 = lane & 15, q4 = lane >> 4, k8 = 8 * q4;
+  const int jw = tile * BW + 16 * wave;  // this wave's first value column
+  const int jl = jw + r16;               // this lane's column (accumulator layout)
 
-  // The state tile in accumulator layout: wave w holds rows
-  // [w·K/4, (w+1)·K/4) as RB row blocks × CB column blocks.
-  f32x4 S[RB][CB];
-  const float* sin = p.s_in + size_t(bh) * K * p.V;
+  // S[:, jw…jw+15] in accumulator layout: RBK row blocks of 16.
+  f32x4 S[RBK];
+  {
+    const float* sin = p.s_in + size_t(bh) * K * p.V + jl;
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
+    for (int rb = 0; rb < RBK; ++rb)
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d = wave * (K / 4) + 16 * rb + 4 * q4 + r;
-        S[rb][cb][r] = sin[size_t(d) * p.V + j0 + 16 * cb + r16];
-      }
-  // bf16 hi/lo copies of Sᵀ: the retrieval K·S cancels against v, so it
-  // reads S to ~2⁻¹⁶; the readout Q·S reads the hi part only.
-  auto write_state = [&](uint16_t* sh) {
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        const int d = wave * (K / 4) + 16 * rb + 4 * q4;
-        const f32x4& v = S[rb][cb];
-        const uint32_t h01 = pk_bf16(v[0], v[1]), h23 = pk_bf16(v[2], v[3]);
-        const uint32_t l01 = pk_bf16(v[0] - lo_f(h01), v[1] - hi_f(h01));
-        const uint32_t l23 = pk_bf16(v[2] - lo_f(h23), v[3] - hi_f(h23));
-        const int at = (16 * cb + r16) * KP + d;
-        *reinterpret_cast<uint2*>(&sh[at]) = make_uint2(h01, h23);
-        *reinterpret_cast<uint2*>(&SlT[at]) = make_uint2(l01, l23);
-      }
-  };
-  write_state(ShT[0]);
-
-  // Every global read of a chunk is issued one chunk ahead, right after the
-  // phase that consumed the previous buffer, so the serial chain over chunks
-  // never waits on HBM. Lane (wave w, r16, q4) reads token row 16w + r16.
-  const int my_tok = 16 * wave + r16;
-  uint4 kA[KK];             // K[my_tok][32kk + k8 …]                 (phase 1)
-  float gcA, glA, erA, wrA;  // gate values of my_tok and G_last
-  uint32_t vA[CB][2];       // V[16w + 4q4 + r][j0 + 16cb + r16], bf16 pairs
-  uint4 tA[2], tlA[2];      // T hi/lo rows my_tok                    (phase 2)
-  uint4 qA[KK], atA[2];     // Q row and attn row of my_tok           (phase 3a)
-  uint4 kcA[RB][2];         // Kcᵀ rows of this wave's state rows     (phase 3b)
+      for (int r = 0; r < 4; ++r) S[rb][r] = sin[size_t(16 * rb + 4 * q4 + r) * p.V];
+  }
 
   const size_t tokstride = size_t(p.H);  // rows between consecutive tokens
   const size_t bh_row0 = size_t(b) * p.S * p.H + h;
-  // Reads and writes are unconditional, with padded tokens' addresses
-  // redirected to a zero row or a sink row: every iteration then issues the
-  // same sequence of memory operations, which keeps the compiler's in-order
-  // vmcnt waits exact across the loop instead of draining every prefetch.
   const float* zero32 = reinterpret_cast<const float*>(p.zero);
-  auto load_k = [&](int n) {
-    const size_t cid = (size_t(b) * p.N + n) * p.H + h;
-    const int tok = n * kL + my_tok;
-    const bool ok = tok < p.S;
-    const size_t row = bh_row0 + size_t(tok) * tokstride;
-    const uint16_t* kr = ok ? p.k + row * K + k8 : p.zero;
+  auto chunk_of = [&](int n) { return (size_t(b) * p.N + n) * p.H + h; };
+
+  // Staging: every global read is unconditional (padded tokens read the
+  // zero row), so each iteration issues the same memory operations and the
+  // compiler's in-order vmcnt waits stay exact.
+  uint4 pf[NPF];
+  float pgc, pgl, per, pwr;
+  auto fetch = [&](int n) {
+    const size_t cid = chunk_of(n);
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) kA[kk] = *reinterpret_cast<const uint4*>(kr + 32 * kk);
-    gcA = p.gc[cid * kL + my_tok];
-    glA = p.gc[cid * kL + kL - 1];
-    erA = *(ok ? p.erase + row : zero32);
-    wrA = *(ok ? p.write + row : zero32);
-  };
-  auto load_v = [&](int n) {
-    const int t0 = n * kL + 16 * wave + 4 * q4;
-    const uint16_t* vb = p.v + (bh_row0 + size_t(t0) * tokstride) * p.V + j0 + r16;
-    const size_t vstride = tokstride * p.V;
-#pragma unroll
-    for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-      for (int r2 = 0; r2 < 2; ++r2) {
-        const uint32_t x0 = *(t0 + 2 * r2 < p.S ? vb + (2 * r2) * vstride + 16 * cb : p.zero);
-        const uint32_t x1 =
-            *(t0 + 2 * r2 + 1 < p.S ? vb + (2 * r2 + 1) * vstride + 16 * cb : p.zero);
-        vA[cb][r2] = x0 | (x1 << 16);
+    for (int m = 0; m < NPF; ++m) {
+      // The tile boundaries are multiples of NT, so the kind of chunk i
+      // depends on m only (a constant once the loop is unrolled).
+      const int i = tid + NT * m, i0 = NT * m;
+      const uint16_t* src;
+      if (i0 < 2 * kL * K / 8) {
+        const int qk = i0 >= kL * K / 8, ii = i - qk * (kL * K / 8);
+        const int row = ii / (K / 8), c = ii % (K / 8);
+        const int tok = n * kL + row;
+        src = tok < p.S ? (qk ? p.q : p.k) + (bh_row0 + size_t(tok) * tokstride) * K + 8 * c
+                        : p.zero;
+      } else if (i0 < (2 * kL * K + 3 * kL * kL) / 8) {
+        const int ii = i - 2 * kL * K / 8;
+        const int which = (i0 - 2 * kL * K / 8) / (kL * kL / 8), e = ii % (kL * kL / 8);
+        const uint16_t* base = which == 0 ? p.T : which == 1 ? p.Tlo : p.attn;
+        src = base + cid * kL * kL + 8 * e;
+      } else {
+        const int e = i - (2 * kL * K + 3 * kL * kL) / 8;
+        src = p.KcT + cid * K * kL + 8 * e;
       }
+      pf[m] = *reinterpret_cast<const uint4*>(src);
+    }
+    const int t = n * kL + lane;
+    const size_t row = bh_row0 + size_t(t) * tokstride;
+    pgc = p.gc[cid * kL + lane];
+    pgl = p.gc[cid * kL + kL - 1];
+    per = *(t < p.S ? p.erase + row : zero32);
+    pwr = *(t < p.S ? p.write + row : zero32);
   };
-  auto load_t = [&](int n) {
-    const size_t off = ((size_t(b) * p.N + n) * p.H + h) * kL * kL + size_t(my_tok) * kL + k8;
+  auto stage = [&](int buf) {
+    uint16_t* tl = tiles[buf];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      tA[kk] = *reinterpret_cast<const uint4*>(p.T + off + 32 * kk);
-      tlA[kk] = *reinterpret_cast<const uint4*>(p.Tlo + off + 32 * kk);
+    for (int m = 0; m < NPF; ++m) {
+      const int i = tid + NT * m, i0 = NT * m;
+      int off, row, c, cols;
+      if (i0 < 2 * kL * K / 8) {
+        const int qk = i0 >= kL * K / 8, ii = i - qk * (kL * K / 8);
+        off = qk ? oQ : oK;
+        row = ii / (K / 8);
+        c = ii % (K / 8);
+        cols = K;
+      } else if (i0 < (2 * kL * K + 3 * kL * kL) / 8) {
+        const int ii = i - 2 * kL * K / 8;
+        const int which = (i0 - 2 * kL * K / 8) / (kL * kL / 8), e = ii % (kL * kL / 8);
+        off = which == 0 ? oT : which == 1 ? oTl : oAt;
+        row = e / (kL / 8);
+        c = e % (kL / 8);
+        cols = kL;
+      } else {
+        const int e = i - (2 * kL * K + 3 * kL * kL) / 8;
+        off = oKc;
+        row = e / (kL / 8);
+        c = e % (kL / 8);
+        cols = kL;
+      }
+      const int p0 = perm_pos(8 * c), p1 = perm_pos(8 * c + 4);
+      const int a0 = cols == K ? tile_at<K>(row, p0) : tile_at<kL>(row, p0);
+      const int a1 = cols == K ? tile_at<K>(row, p1) : tile_at<kL>(row, p1);
+      *reinterpret_cast<uint2*>(&tl[off + a0]) = make_uint2(pf[m].x, pf[m].y);
+      *reinterpret_cast<uint2*>(&tl[off + a1]) = make_uint2(pf[m].z, pf[m].w);
+    }
+    if (wave == 0) {
+      const float eg = __expf(pgc);
+      gxe[buf][lane] = per * eg;
+      gwr[buf][lane] = pwr;
+      gys[buf][lane] = p.scale * eg;
+      if (lane == 0) gegl[buf] = __expf(pgl);
     }
   };
-  auto load_q = [&](int n) {
-    const int tok = n * kL + my_tok;
-    const uint16_t* qr =
-        tok < p.S ? p.q + (bh_row0 + size_t(tok) * tokstride) * K + k8 : p.zero;
+  // v[t][jl] for this lane's 16 tokens (4 row blocks × 4), as bf16 pairs.
+  uint32_t vA[4][2];
+  auto load_v = [&](int n) {
+    const uint16_t* vb = p.v + bh_row0 * p.V + jl;
+    const size_t vstride = tokstride * p.V;
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) qA[kk] = *reinterpret_cast<const uint4*>(qr + 32 * kk);
-    const size_t off = ((size_t(b) * p.N + n) * p.H + h) * kL * kL + size_t(my_tok) * kL + k8;
+    for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-      atA[kk] = *reinterpret_cast<const uint4*>(p.attn + off + 32 * kk);
-  };
-  auto load_kc = [&](int n) {
-    const uint16_t* kc = p.KcT + ((size_t(b) * p.N + n) * p.H + h) * K * kL + k8;
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-        kcA[rb][kk] = *reinterpret_cast<const uint4*>(
-            kc + size_t(wave * (K / 4) + 16 * rb + r16) * kL + 32 * kk);
+      for (int r2 = 0; r2 < 2; ++r2) {
+        const int t0 = n * kL + 16 * tb + 4 * q4 + 2 * r2;
+        const uint32_t x0 = *(t0 < p.S ? vb + size_t(t0) * vstride : p.zero);
+        const uint32_t x1 = *(t0 + 1 < p.S ? vb + size_t(t0 + 1) * vstride : p.zero);
+        vA[tb][r2] = (x0 & 0xffffu) | (x1 << 16);
+      }
   };
   auto as8 = [](const uint4& x) { return __builtin_bit_cast(bf16x8, x); };
 
-  load_k(0);
+  fetch(0);
   load_v(0);
-  load_t(0);
-  load_q(0);
+  stage(0);
+  __syncthreads();
   for (int n = 0; n < p.N; ++n) {
-    const int tok0 = n * kL;
+    const int cur = n & 1;
     const int nn = n + 1 < p.N ? n + 1 : n;  // the last chunk prefetches itself again
-    const uint16_t* sh = ShT[n & 1];
+    const uint16_t* tl = tiles[cur];
+    const float egl = gegl[cur];
 
-    // Gates of this wave's tokens (read back by this wave only); G is 0
-    // throughout when there is no forget gate.
-    const float egA = __expf(gcA);
-    const float egl = __expf(glA);
-    if (q4 == 0) {
-      xes[my_tok] = erA * egA;
-      wrs[my_tok] = wrA;
+    // Phase 1: X = w⊙V − (e⊙e^G)⊙(K·S) in [token][column] orientation, and
+    // yᵀ = Sᵀ·Qᵀ in [column][token] orientation. The S fragments (hi, lo) of
+    // k-step kk are the B operand of K·S and the A operand of Sᵀ·Qᵀ (same
+    // lane layout). Fragment reads run one (kk, tb) step ahead of the MFMAs.
+    f32x4 X[4], yt[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      X[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      yt[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
-
-    // Phase 1: X = w⊙V − (e⊙e^G)⊙(K·S), token rows 16·wave…
     {
-      f32x4 acc[CB];
+      bf16x8 kf[2], qf[2];
+      kf[0] = ld8(&tl[oK + tile_at<K>(r16, k8)]);
+      qf[0] = ld8(&tl[oQ + tile_at<K>(r16, k8)]);
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int kk = 0; kk < KK; ++kk) {
+        const uint4 sh = frag_hi(S[2 * kk], S[2 * kk + 1]);
+        const uint4 sl = frag_lo(S[2 * kk], S[2 * kk + 1], sh);
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-          acc[cb] = mfma16(as8(kA[kk]), ld8(&sh[(16 * cb + r16) * KP + 32 * kk + k8]), acc[cb]);
-          acc[cb] = mfma16(as8(kA[kk]), ld8(&SlT[(16 * cb + r16) * KP + 32 * kk + k8]), acc[cb]);
+        for (int tb = 0; tb < 4; ++tb) {
+          const int step = 4 * kk + tb, nx = step + 1;
+          if (nx < 4 * KK) {
+            const int at = tile_at<K>(16 * (nx & 3) + r16, 32 * (nx >> 2) + k8);
+            kf[nx & 1] = ld8(&tl[oK + at]);
+            qf[nx & 1] = ld8(&tl[oQ + at]);
+          }
+          X[tb] = mfma16(kf[step & 1], as8(sh), X[tb]);
+          X[tb] = mfma16(kf[step & 1], as8(sl), X[tb]);
+          yt[tb] = mfma16(as8(sh), qf[step & 1], yt[tb]);
         }
       }
-      float xe[4], wr[4];
+    }
+    fetch(nn);
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        xe[r] = xes[16 * wave + 4 * q4 + r];
-        wr[r] = wrs[16 * wave + 4 * q4 + r];
+        const int t = 16 * tb + 4 * q4 + r;
+        const float vv = (r & 1) ? hi_f(vA[tb][r >> 1]) : lo_f(vA[tb][r >> 1]);
+        X[tb][r] = gwr[cur][t] * vv - gxe[cur][t] * X[tb][r];
       }
-      load_k(nn);
+      const float ysc = gys[cur][16 * tb + r16];
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        const int j = 16 * cb + r16;
-        float x[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float vv = (r & 1) ? hi_f(vA[cb][r >> 1]) : lo_f(vA[cb][r >> 1]);
-          x[r] = wr[r] * vv - xe[r] * acc[cb][r];
-        }
-        const uint32_t h01 = pk_bf16(x[0], x[1]), h23 = pk_bf16(x[2], x[3]);
-        const uint32_t l01 = pk_bf16(x[0] - lo_f(h01), x[1] - hi_f(h01));
-        const uint32_t l23 = pk_bf16(x[2] - lo_f(h23), x[3] - hi_f(h23));
-        *reinterpret_cast<uint2*>(&XbT[j * LP + 16 * wave + 4 * q4]) = make_uint2(h01, h23);
-        *reinterpret_cast<uint2*>(&XlT[j * LP + 16 * wave + 4 * q4]) = make_uint2(l01, l23);
-      }
-      load_v(nn);
+      for (int r = 0; r < 4; ++r) yt[tb][r] *= ysc;
     }
-    __syncthreads();
+    load_v(nn);
 
-    // Phase 2: V' = T·X, with both factors as bf16 hi + lo parts: for a
-    // chunk of near-identical keys T differences near-equal rows of X.
-    {
-      f32x4 acc[CB];
+    // Phase 2: V' = T·X with hi + lo parts of both factors (for a chunk of
+    // near-identical keys T differences near-equal rows of X).
+    uint4 xh[2], xl[2];
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        acc[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kk = 0; kk < 2; ++kk) {
+      xh[kk] = frag_hi(X[2 * kk], X[2 * kk + 1]);
+      xl[kk] = frag_lo(X[2 * kk], X[2 * kk + 1], xh[kk]);
+    }
+    f32x4 Vp[4];
+    {
+      bf16x8 th[2], tlo[2];
+      th[0] = ld8(&tl[oT + tile_at<kL>(r16, k8)]);
+      tlo[0] = ld8(&tl[oTl + tile_at<kL>(r16, k8)]);
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        Vp[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
-          const bf16x8 xh = ld8(&XbT[(16 * cb + r16) * LP + 32 * kk + k8]);
-          acc[cb] = mfma16(as8(tA[kk]), xh, acc[cb]);
-          acc[cb] = mfma16(as8(tlA[kk]), xh, acc[cb]);
-          acc[cb] = mfma16(as8(tA[kk]), ld8(&XlT[(16 * cb + r16) * LP + 32 * kk + k8]), acc[cb]);
+          const int step = 2 * tb + kk, nx = step + 1;
+          if (nx < 8) {
+            const int at = tile_at<kL>(16 * (nx >> 1) + r16, 32 * (nx & 1) + k8);
+            th[nx & 1] = ld8(&tl[oT + at]);
+            tlo[nx & 1] = ld8(&tl[oTl + at]);
+          }
+          Vp[tb] = mfma16(th[step & 1], as8(xh[kk]), Vp[tb]);
+          Vp[tb] = mfma16(tlo[step & 1], as8(xh[kk]), Vp[tb]);
+          Vp[tb] = mfma16(th[step & 1], as8(xl[kk]), Vp[tb]);
         }
       }
-      load_t(nn);
-      load_kc(n);  // consumed in phase 3b, after phase 3a's MFMAs
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        const int j = 16 * cb + r16;
-        *reinterpret_cast<uint2*>(&VpT[j * LP + 16 * wave + 4 * q4]) =
-            make_uint2(pk_bf16(acc[cb][0], acc[cb][1]), pk_bf16(acc[cb][2], acc[cb][3]));
-      }
     }
-    __syncthreads();
 
-    // Phase 3a: yᵀ = (Sᵀ·Qᵀ)⊙(scale·e^G) + V'ᵀ·attnᵀ. In this orientation
-    // lane (r16, q4) holds four consecutive value columns of its own token
-    // my_tok, so y leaves in 8- or 16-byte stores.
+    // Phase 3: yᵀ += V'ᵀ·attnᵀ and S ← e^{G_last}⊙S + (e^{G_last−G}⊙K)ᵀ·V';
+    // the bf16 V' fragment is the A operand of the first and the B operand
+    // of the second.
+    uint4 vf[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) vf[kk] = frag_hi(Vp[2 * kk], Vp[2 * kk + 1]);
     {
-      f32x4 qs[CB], av[CB];
+      // 8 attn steps, then 2·RBK Kcᵀ steps, reads one step ahead.
+      constexpr int NS = 8 + 2 * RBK;
+      auto addr = [&](int st) {
+        return st < 8 ? oAt + tile_at<kL>(16 * (st >> 1) + r16, 32 * (st & 1) + k8)
+                      : oKc + tile_at<kL>(16 * ((st - 8) >> 1) + r16, 32 * ((st - 8) & 1) + k8);
+      };
+      bf16x8 fr[2];
+      fr[0] = ld8(&tl[addr(0)]);
 #pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        qs[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
-        av[cb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int rb = 0; rb < RBK; ++rb)
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk)
-          qs[cb] = mfma16(ld8(&sh[(16 * cb + r16) * KP + 32 * kk + k8]), as8(qA[kk]), qs[cb]);
+        for (int r = 0; r < 4; ++r) S[rb][r] *= egl;
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk)
-          av[cb] = mfma16(ld8(&VpT[(16 * cb + r16) * LP + 32 * kk + k8]), as8(atA[kk]), av[cb]);
-      }
-      load_q(nn);
-      const int t = tok0 + my_tok;
-      const float ysc = p.scale * egA;
-      TY* yrow = t < p.S ? static_cast<TY*>(p.y) + (bh_row0 + size_t(t) * tokstride) * p.V + j0
-                         : reinterpret_cast<TY*>(p.sink);
-#pragma unroll
-      for (int cb = 0; cb < CB; ++cb) {
-        float o[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o[r] = ysc * qs[cb][r] + av[cb][r];
-        TY* dst = yrow + 16 * cb + 4 * q4;
-        if constexpr (sizeof(TY) == 2)
-          *reinterpret_cast<uint2*>(dst) = make_uint2(pk_bf16(o[0], o[1]), pk_bf16(o[2], o[3]));
+      for (int st = 0; st < NS; ++st) {
+        if (st + 1 < NS) fr[(st + 1) & 1] = ld8(&tl[addr(st + 1)]);
+        const int kk = st & 1;
+        if (st < 8)
+          yt[st >> 1] = mfma16(as8(vf[kk]), fr[st & 1], yt[st >> 1]);
         else
-          *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+          S[(st - 8) >> 1] = mfma16(fr[st & 1], as8(vf[kk]), S[(st - 8) >> 1]);
       }
     }
-
-    // Phase 3b: S ← e^{G_last}⊙S + (e^{G_last−G}⊙K)ᵀ·V'; its bf16 copy goes
-    // to the other buffer, so the readout above needs no barrier.
-    {
+    // y: lane (r16, q4) holds columns jw + 4q4 … +3 of token 16tb + r16.
 #pragma unroll
-      for (int rb = 0; rb < RB; ++rb)
-#pragma unroll
-        for (int cb = 0; cb < CB; ++cb) {
-          f32x4 acc = S[rb][cb];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) acc[r] *= egl;
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk)
-            acc = mfma16(as8(kcA[rb][kk]), ld8(&VpT[(16 * cb + r16) * LP + 32 * kk + k8]), acc);
-          S[rb][cb] = acc;
-        }
-      write_state(ShT[(n + 1) & 1]);
+    for (int tb = 0; tb < 4; ++tb) {
+      const int t = n * kL + 16 * tb + r16;
+      TY* dst = t < p.S ? static_cast<TY*>(p.y) + (bh_row0 + size_t(t) * tokstride) * p.V + jw +
+                              4 * q4
+                        : reinterpret_cast<TY*>(p.sink) + jw + 4 * q4;
+      if constexpr (sizeof(TY) == 2)
+        *reinterpret_cast<uint2*>(dst) =
+            make_uint2(pk_bf16(yt[tb][0], yt[tb][1]), pk_bf16(yt[tb][2], yt[tb][3]));
+      else
+        *reinterpret_cast<float4*>(dst) = make_float4(yt[tb][0], yt[tb][1], yt[tb][2], yt[tb][3]);
     }
+    stage(cur ^ 1);
     __syncthreads();
   }
 
-  float* sout = p.s_out + size_t(bh) * K * p.V;
+  float* sout = p.s_out + size_t(bh) * K * p.V + jl;
 #pragma unroll
-  for (int rb = 0; rb < RB; ++rb)
+  for (int rb = 0; rb < RBK; ++rb)
 #pragma unroll
-    for (int cb = 0; cb < CB; ++cb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int d = wave * (K / 4) + 16 * rb + 4 * q4 + r;
-        sout[size_t(d) * p.V + j0 + 16 * cb + r16] = S[rb][cb][r];
-      }
+    for (int r = 0; r < 4; ++r) sout[size_t(16 * rb + 4 * q4 + r) * p.V] = S[rb][r];
 }
 
 size_t region(size_t bytes) { return align_up(bytes, 256); }
@@ -733,18 +760,27 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int tiles = d.V / kBV;
+  // Workgroup width: 128 value columns (8 waves) when that still yields a
+  // workgroup per CU, else narrower so more CUs share the sequence.
   const int BH = d.B * d.H;
-  const unsigned blocks = unsigned(((BH + 7) / 8) * 8 * tiles);
+  const int groups = (BH + 7) / 8;
   const bool yb = y_dtype == DN_BF16;
+  const int cus = device_cu_count();
+  int waves = 2;
+  if (d.V % 128 == 0 && size_t(groups) * 8 * (d.V / 128) >= size_t(cus)) waves = 8;
+  else if (d.V % 64 == 0 && size_t(groups) * 8 * (d.V / 64) >= size_t(cus) / 2) waves = 4;
+  const unsigned blocks = unsigned(groups * 8 * (d.V / (16 * waves)));
   ProfScope ps("dn_mfma_scan", stream);
-#define DN_SCAN(KD, TY) \
-  hipLaunchKernelGGL((mfma_scan_kernel<KD, TY>), dim3(blocks), dim3(kThreads), 0, stream, p)
+#define DN_SCAN(KD, TY, W)                                                                   \
+  hipLaunchKernelGGL((mfma_scan_kernel<KD, TY, W>), dim3(blocks), dim3(64 * W), 0, stream, p)
+#define DN_SCAN_W(KD, TY) \
+  do { if (waves == 8) DN_SCAN(KD, TY, 8); else if (waves == 4) DN_SCAN(KD, TY, 4); else DN_SCAN(KD, TY, 2); } while (0)
   if (d.K == 128) {
-    if (yb) DN_SCAN(128, bf16); else DN_SCAN(128, float);
+    if (yb) DN_SCAN_W(128, bf16); else DN_SCAN_W(128, float);
   } else {
-    if (yb) DN_SCAN(64, bf16); else DN_SCAN(64, float);
+    if (yb) DN_SCAN_W(64, bf16); else DN_SCAN_W(64, float);
   }
+#undef DN_SCAN_W
 #undef DN_SCAN
   return hipGetLastError();
 }
