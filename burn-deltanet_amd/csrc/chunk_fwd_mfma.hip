@@ -84,7 +84,6 @@ __device__ inline float quad_bcast(float v, int src) {
   }
 }
 
-__device__ inline bf16x8 zero8() { return __builtin_bit_cast(bf16x8, make_uint4(0u, 0u, 0u, 0u)); }
 
 struct MfmaParams {
   int B, S, H, V, N;
@@ -453,77 +452,92 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
 
   const size_t tokstride = size_t(p.H);  // rows between consecutive tokens
   const size_t bh_row0 = size_t(b) * p.S * p.H + h;
-  const float* zero32 = reinterpret_cast<const float*>(p.zero);
   auto chunk_of = [&](int n) { return (size_t(b) * p.N + n) * p.H + h; };
 
-  // Staging: every global read is unconditional (padded tokens read the
-  // zero row), so each iteration issues the same memory operations and the
-  // compiler's in-order vmcnt waits stay exact.
+  // Staging. Global reads use a wave-uniform base (per chunk) plus a 32-bit
+  // lane offset, and are unconditional: rows past the sequence end are
+  // clamped to its last row (their gates are zero, so those values only ever
+  // meet zero factors), which keeps every iteration's memory operations
+  // identical and the compiler's in-order vmcnt waits exact.
+  const int HK = p.H * K;
   uint4 pf[NPF];
   float pgc, pgl, per, pwr;
+  auto ld16 = [](const uint16_t* base, uint32_t elems) {
+    return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + 2u * elems);
+  };
   auto fetch = [&](int n) {
     const size_t cid = chunk_of(n);
+    const int rl = min(kL, p.S - n * kL);  // valid rows of this chunk (≥ 1)
+    const size_t row0 = bh_row0 + size_t(n) * kL * tokstride;
 #pragma unroll
     for (int m = 0; m < NPF; ++m) {
-      // The tile boundaries are multiples of NT, so the kind of chunk i
-      // depends on m only (a constant once the loop is unrolled).
-      const int i = tid + NT * m, i0 = NT * m;
-      const uint16_t* src;
+      // The tile boundaries are multiples of NT, so the kind of chunk
+      // tid + NT·m depends on m only (a constant once the loop is unrolled).
+      const int i0 = NT * m;
       if (i0 < 2 * kL * K / 8) {
-        const int qk = i0 >= kL * K / 8, ii = i - qk * (kL * K / 8);
-        const int row = ii / (K / 8), c = ii % (K / 8);
-        const int tok = n * kL + row;
-        src = tok < p.S ? (qk ? p.q : p.k) + (bh_row0 + size_t(tok) * tokstride) * K + 8 * c
-                        : p.zero;
+        const int qk = i0 >= kL * K / 8;
+        const int row = tid / (K / 8) + (i0 - qk * (kL * K / 8)) / (K / 8);
+        const uint32_t off = uint32_t(min(row, rl - 1) * HK + 8 * (tid % (K / 8)));
+        pf[m] = ld16((qk ? p.q : p.k) + row0 * K, off);
       } else if (i0 < (2 * kL * K + 3 * kL * kL) / 8) {
-        const int ii = i - 2 * kL * K / 8;
-        const int which = (i0 - 2 * kL * K / 8) / (kL * kL / 8), e = ii % (kL * kL / 8);
+        const int ii0 = i0 - 2 * kL * K / 8;
+        const int which = ii0 / (kL * kL / 8);
         const uint16_t* base = which == 0 ? p.T : which == 1 ? p.Tlo : p.attn;
-        src = base + cid * kL * kL + 8 * e;
+        pf[m] = ld16(base + cid * kL * kL + 8 * (ii0 - which * (kL * kL / 8)), 8u * tid);
       } else {
-        const int e = i - (2 * kL * K + 3 * kL * kL) / 8;
-        src = p.KcT + cid * K * kL + 8 * e;
+        const int e0 = i0 - (2 * kL * K + 3 * kL * kL) / 8;
+        pf[m] = ld16(p.KcT + cid * K * kL + 8 * e0, 8u * tid);
       }
-      pf[m] = *reinterpret_cast<const uint4*>(src);
     }
-    const int t = n * kL + lane;
-    const size_t row = bh_row0 + size_t(t) * tokstride;
+    const int lc = min(lane, rl - 1);
     pgc = p.gc[cid * kL + lane];
     pgl = p.gc[cid * kL + kL - 1];
-    per = *(t < p.S ? p.erase + row : zero32);
-    pwr = *(t < p.S ? p.write + row : zero32);
+    const float e = p.erase[row0 + size_t(lc) * tokstride];
+    const float w = p.write[row0 + size_t(lc) * tokstride];
+    per = lane < rl ? e : 0.f;
+    pwr = lane < rl ? w : 0.f;
   };
+  // Staging addresses are loop invariant: lane tid writes the halves of
+  // 16-byte chunk (row r, column group c) of every tile, rows advancing by a
+  // multiple of 8 per round m (which flips the K-wide swizzle by m-constant
+  // bits only).
+  constexpr int KC8 = K / 8, LC8 = kL / 8;
+  const int rK = tid / KC8, cK = tid % KC8, r6 = tid / LC8, c6 = tid % LC8;
+  auto addr_k = [&](int flip, int half) {
+    const int pos = perm_pos(8 * cK + 4 * half);
+    return rK * K + ((((pos >> 3) ^ (rK & 15) ^ flip) & (KC8 - 1)) << 3) + (pos & 7);
+  };
+  const int aK0 = K >= 128 ? addr_k(0, 0) : tile_at<K>(rK, perm_pos(8 * cK));
+  const int aK1 = K >= 128 ? addr_k(0, 1) : tile_at<K>(rK, perm_pos(8 * cK + 4));
+  const int aK0x = K >= 128 ? addr_k(8, 0) : aK0;
+  const int aK1x = K >= 128 ? addr_k(8, 1) : aK1;
+  const int a60 = tile_at<kL>(r6, perm_pos(8 * c6)), a61 = tile_at<kL>(r6, perm_pos(8 * c6 + 4));
   auto stage = [&](int buf) {
     uint16_t* tl = tiles[buf];
 #pragma unroll
     for (int m = 0; m < NPF; ++m) {
-      const int i = tid + NT * m, i0 = NT * m;
-      int off, row, c, cols;
+      const int i0 = NT * m;
+      int b0, b1;
       if (i0 < 2 * kL * K / 8) {
-        const int qk = i0 >= kL * K / 8, ii = i - qk * (kL * K / 8);
-        off = qk ? oQ : oK;
-        row = ii / (K / 8);
-        c = ii % (K / 8);
-        cols = K;
+        const int qk = i0 >= kL * K / 8;
+        const int dr = (i0 - qk * (kL * K / 8)) / KC8;  // row advance, a multiple of 8
+        const int base = (qk ? oQ : oK) + dr * K;
+        const bool flip = K >= 128 && (dr & 8);
+        b0 = base + (flip ? aK0x : aK0);
+        b1 = base + (flip ? aK1x : aK1);
       } else if (i0 < (2 * kL * K + 3 * kL * kL) / 8) {
-        const int ii = i - 2 * kL * K / 8;
-        const int which = (i0 - 2 * kL * K / 8) / (kL * kL / 8), e = ii % (kL * kL / 8);
-        off = which == 0 ? oT : which == 1 ? oTl : oAt;
-        row = e / (kL / 8);
-        c = e % (kL / 8);
-        cols = kL;
+        const int ii0 = i0 - 2 * kL * K / 8;
+        const int which = ii0 / (kL * kL / 8), dr = (ii0 - which * (kL * kL / 8)) / LC8;
+        const int base = (which == 0 ? oT : which == 1 ? oTl : oAt) + dr * kL;
+        b0 = base + a60;
+        b1 = base + a61;
       } else {
-        const int e = i - (2 * kL * K + 3 * kL * kL) / 8;
-        off = oKc;
-        row = e / (kL / 8);
-        c = e % (kL / 8);
-        cols = kL;
+        const int dr = (i0 - (2 * kL * K + 3 * kL * kL) / 8) / LC8;
+        b0 = oKc + dr * kL + a60;
+        b1 = oKc + dr * kL + a61;
       }
-      const int p0 = perm_pos(8 * c), p1 = perm_pos(8 * c + 4);
-      const int a0 = cols == K ? tile_at<K>(row, p0) : tile_at<kL>(row, p0);
-      const int a1 = cols == K ? tile_at<K>(row, p1) : tile_at<kL>(row, p1);
-      *reinterpret_cast<uint2*>(&tl[off + a0]) = make_uint2(pf[m].x, pf[m].y);
-      *reinterpret_cast<uint2*>(&tl[off + a1]) = make_uint2(pf[m].z, pf[m].w);
+      *reinterpret_cast<uint2*>(&tl[b0]) = make_uint2(pf[m].x, pf[m].y);
+      *reinterpret_cast<uint2*>(&tl[b1]) = make_uint2(pf[m].z, pf[m].w);
     }
     if (wave == 0) {
       const float eg = __expf(pgc);
@@ -535,17 +549,22 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   };
   // v[t][jl] for this lane's 16 tokens (4 row blocks × 4), as bf16 pairs.
   uint32_t vA[4][2];
+  const int HV = p.H * p.V;
   auto load_v = [&](int n) {
-    const uint16_t* vb = p.v + bh_row0 * p.V + jl;
-    const size_t vstride = tokstride * p.V;
+    const int rl = min(kL, p.S - n * kL);
+    const uint16_t* vb = p.v + (bh_row0 + size_t(n) * kL * tokstride) * p.V;
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
       for (int r2 = 0; r2 < 2; ++r2) {
-        const int t0 = n * kL + 16 * tb + 4 * q4 + 2 * r2;
-        const uint32_t x0 = *(t0 < p.S ? vb + size_t(t0) * vstride : p.zero);
-        const uint32_t x1 = *(t0 + 1 < p.S ? vb + size_t(t0 + 1) * vstride : p.zero);
-        vA[tb][r2] = (x0 & 0xffffu) | (x1 << 16);
+        const int t0 = 16 * tb + 4 * q4 + 2 * r2;
+        const uint32_t o0 = uint32_t(min(t0, rl - 1) * HV + jl);
+        const uint32_t o1 = uint32_t(min(t0 + 1, rl - 1) * HV + jl);
+        const uint32_t x0 = *reinterpret_cast<const uint16_t*>(
+            reinterpret_cast<const char*>(vb) + 2u * o0);
+        const uint32_t x1 = *reinterpret_cast<const uint16_t*>(
+            reinterpret_cast<const char*>(vb) + 2u * o1);
+        vA[tb][r2] = x0 | (x1 << 16);
       }
   };
   auto as8 = [](const uint4& x) { return __builtin_bit_cast(bf16x8, x); };
@@ -667,18 +686,24 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
           S[(st - 8) >> 1] = mfma16(fr[st & 1], as8(vf[kk]), S[(st - 8) >> 1]);
       }
     }
-    // y: lane (r16, q4) holds columns jw + 4q4 … +3 of token 16tb + r16.
+    // y: lane (r16, q4) holds columns jw + 4q4 … +3 of token 16tb + r16;
+    // rows past the sequence end go to the sink row.
+    {
+      TY* yb = static_cast<TY*>(p.y) + (bh_row0 + size_t(n) * kL * tokstride) * p.V;
+      const int rl = p.S - n * kL;
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      const int t = n * kL + 16 * tb + r16;
-      TY* dst = t < p.S ? static_cast<TY*>(p.y) + (bh_row0 + size_t(t) * tokstride) * p.V + jw +
-                              4 * q4
-                        : reinterpret_cast<TY*>(p.sink) + jw + 4 * q4;
-      if constexpr (sizeof(TY) == 2)
-        *reinterpret_cast<uint2*>(dst) =
-            make_uint2(pk_bf16(yt[tb][0], yt[tb][1]), pk_bf16(yt[tb][2], yt[tb][3]));
-      else
-        *reinterpret_cast<float4*>(dst) = make_float4(yt[tb][0], yt[tb][1], yt[tb][2], yt[tb][3]);
+      for (int tb = 0; tb < 4; ++tb) {
+        const int t = 16 * tb + r16;
+        TY* dst = t < rl ? reinterpret_cast<TY*>(reinterpret_cast<char*>(yb) +
+                                                 sizeof(TY) * uint32_t(t * HV + jw + 4 * q4))
+                         : reinterpret_cast<TY*>(p.sink) + jw + 4 * q4;
+        if constexpr (sizeof(TY) == 2)
+          *reinterpret_cast<uint2*>(dst) =
+              make_uint2(pk_bf16(yt[tb][0], yt[tb][1]), pk_bf16(yt[tb][2], yt[tb][3]));
+        else
+          *reinterpret_cast<float4*>(dst) =
+              make_float4(yt[tb][0], yt[tb][1], yt[tb][2], yt[tb][3]);
+      }
     }
     stage(cur ^ 1);
     __syncthreads();
