@@ -5,32 +5,33 @@
 // chunk_len 64, erase/write/forget gates of width 1 (or no forget gate).
 // Everything else takes the generic kernels.
 //
-// Two kernels, both on v_mfma_f32_16x16x32_bf16 (64-lane waves):
+// Two kernels on v_mfma_f32_16x16x32_bf16 (64-lane waves):
 //
-// intra  one workgroup per chunk-head (b, n, h); fully parallel.
-//        K and Q chunk tiles are staged in LDS; K·Kᵀ and Q·Kᵀ (lower block
-//        triangle only) run on MFMA; the per-head decay e^{Gᵢ−Gⱼ}, the erase
-//        gate and the readout scale are applied to the fp32 accumulators;
-//        T = (I + tril(Akk, −1))⁻¹ is a blocked forward substitution in fp32
-//        LDS (four 16×16 diagonal inverses, then two doubling merges
-//        T₂₁ = −T₂₂ A₂₁ T₁₁) — the reference's ladder (tri/prim.rs:28-51) at
-//        L³/3 instead of 24·L³ flops. Writes T as bf16 hi + lo parts,
-//        attn = tril(Aqk) as bf16 and the in-chunk cumulative gate G as fp32:
-//        24.25 KiB per chunk-head.
+// intra  chunk-heads (b, n, h) are fully parallel; two resident workgroups
+//        per CU walk them, prefetching the next chunk's K/Q/gates into
+//        registers. K·Kᵀ and Q·Kᵀ (the ten lower 16×16 block pairs) run on
+//        MFMA with the per-head decay e^{Gᵢ−Gⱼ}, the erase gate and the
+//        readout scale applied to the fp32 accumulators; T = (I + tril(Akk,
+//        −1))⁻¹ is a blocked forward substitution in fp32 (four 16×16
+//        diagonal blocks by column elimination, then two doubling merges
+//        T₂₁ = −T₂₂ A₂₁ T₁₁ on fp32 MFMA) — the reference's ladder
+//        (tri/prim.rs:28-51) at L³/3 instead of 24·L³ flops. Writes T as bf16
+//        hi + lo parts, attn = tril(Aqk) and Kcᵀ = (e^{G_last−G}⊙K)ᵀ as bf16,
+//        and the in-chunk cumulative gate G as fp32.
 //
-// scan   one workgroup per (64-column value tile, head, batch); serial over
-//        chunks. The fp32 state tile S [K × 64] lives in MFMA accumulator
-//        registers for the whole sequence; a bf16 copy in LDS feeds the
-//        products that read it. Per chunk, with U − W S = T (w⊙V − e⊙e^G⊙(K S))
-//        so that neither U nor W is ever formed:
-//          X  = w⊙V − (e⊙e^G)⊙(K·S)                 MFMA, K rows from HBM/L2;
-//                                                   S read as bf16 hi + lo parts
-//                                                   (the retrieval cancels)
-//          V' = T·X                                 MFMA, hi + lo parts of T and X
-//          y  = (scale·e^G)⊙(Q·S) + attn·V'         MFMA, written as bf16
-//          S  ← e^{G_last}⊙S + (e^{G_last−G}⊙K)ᵀ·V' MFMA into the accumulators
-//        The four tiles of one (b, h) are mapped to one XCD so their shared
-//        K/Q/T/attn reads hit the same L2.
+// scan   one workgroup per (b, h, block of 16·W value columns), serial over
+//        chunks; each of its W waves owns 16 value columns and all K state
+//        rows, in fp32 MFMA accumulators for the whole sequence. A chunk's
+//        operand tiles (K, Q, T hi/lo, attn, Kcᵀ) are staged once in LDS
+//        (double-buffered: one barrier per chunk); everything that depends on
+//        the state stays in the wave. Per chunk, with U − W S = T (w⊙V −
+//        e⊙e^G⊙(K S)) so that neither U nor W is ever formed:
+//          X  = w⊙V − (e⊙e^G)⊙(K·S)                 S as bf16 hi + lo parts
+//          yᵀ = (scale·e^G)⊙(Sᵀ·Qᵀ)                 same S fragments
+//          V' = T·X                                 hi + lo parts of T and X
+//          yᵀ += V'ᵀ·attnᵀ;  S ← e^{G_last}⊙S + Kcᵀ·V'   one V' fragment
+//        The contraction index of the staged tiles is permuted inside each
+//        32-deep k-step so accumulator tiles serve as MFMA operands in place.
 
 #include <algorithm>
 
@@ -44,8 +45,7 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
 
 constexpr int kL = 64;        // chunk length
 constexpr int kThreads = 256;  // 4 waves
-constexpr int kBV = 64;       // value columns per scan workgroup
-constexpr int kZeroElems = 512;
+constexpr int kBV = 64;       // head_v_dim granularity of the MFMA path
 
 __device__ inline f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -98,7 +98,6 @@ struct MfmaParams {
   uint16_t* Tlo;   // [G][64][64] bf16(T − bf16(T))
   uint16_t* attn;  // [G][64][64] bf16
   uint16_t* KcT;   // [G][K][64] bf16 (e^{G_last−G}⊙K)ᵀ
-  uint16_t* zero;  // kZeroElems bf16 zeros: the source of padded tokens' reads
   uint16_t* sink;  // one y row: the target of padded tokens' writes
   float* gc;       // [G][64]
 };
@@ -127,9 +126,6 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
   __shared__ float gcs[kL], ers[kL];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (blockIdx.x == 0)
-    for (int i = tid; i < kZeroElems / 8; i += kThreads)
-      reinterpret_cast<uint4*>(p.zero)[i] = make_uint4(0u, 0u, 0u, 0u);
   // attn's blocks above the diagonal are zero for every chunk.
   for (int idx = tid; idx < kL * kL; idx += kThreads) {
     const int i = idx / kL, j = idx % kL;
@@ -729,7 +725,7 @@ bool mfma_fwd_supported(const Dims& d, int qkv_dtype, int y_dtype) {
 size_t mfma_fwd_workspace(const Dims& d) {
   const size_t G = size_t(d.B) * d.N * d.H;
   return 3 * region(G * kL * kL * 2) + region(G * kL * 4) + region(G * size_t(d.K) * kL * 2) +
-         region(kZeroElems * 2) + region(size_t(kBV) * (d.V / kBV) * 4);
+         region(size_t(d.V) * 4);
 }
 
 hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, const void* v,
@@ -765,8 +761,6 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
   base += region(G * kL * 4);
   p.KcT = reinterpret_cast<uint16_t*>(base);
   base += region(G * size_t(d.K) * kL * 2);
-  p.zero = reinterpret_cast<uint16_t*>(base);
-  base += region(kZeroElems * 2);
   p.sink = reinterpret_cast<uint16_t*>(base);
 
   {

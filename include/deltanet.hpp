@@ -1,0 +1,178 @@
+// deltanet.hpp — C++ host interface of the MI355X delta-rule core.
+//
+// Mirrors the Rust interface of burn-deltanet's delta-rule core with the same
+// names, argument meaning and error behaviour, over device tensors:
+//   DeltaPath, DeltaInput::{dims, resolved_scale, has_channel_decay, sanity,
+//   run, delta_recurrent, delta_chunk_recalculated}, beta_gates
+//                                         src/delta/path.rs:21-231
+//   delta_step                            src/delta/recurrent.rs:41-99
+//   DeltaChunkGrads, combined_backward    src/delta/chunk_recalculated/
+//                                         combined_backward.rs:50-189
+// Every computation is a call through the C ABI of deltanet_core.h. Where
+// the reference panics on an assert!, these functions throw deltanet::Error
+// carrying the same message (and the dn_status the C ABI uses for it).
+//
+// The reference is functional: its functions return fresh tensors, and so do
+// these (device memory owned by the returned Tensor). delta_step_in_place is
+// the one addition: the in-place state update a decode loop wants.
+//
+// Library: libdeltanet.so (links libdeltanet_core.so and libamdhip64.so).
+#ifndef DELTANET_HPP
+#define DELTANET_HPP
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <optional>
+#include <stdexcept>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "deltanet_core.h"
+
+namespace deltanet {
+
+enum class DType : int32_t { F32 = DN_F32, BF16 = DN_BF16 };
+
+size_t dtype_size(DType dtype);
+
+// The reference's assert! failures, as exceptions. status() is the dn_status
+// the C ABI returns for the same condition.
+class Error : public std::runtime_error {
+ public:
+  Error(int status, const std::string& what);
+  int status() const noexcept { return status_; }
+
+ private:
+  int status_;
+};
+
+// A dense row-major device tensor: either owning (reference-counted device
+// memory from Tensor::empty) or a view of memory the caller owns.
+class Tensor {
+ public:
+  Tensor() = default;
+  // Fresh device allocation (contents undefined).
+  static Tensor empty(std::vector<int64_t> dims, DType dtype);
+  // Non-owning view of `data` (device memory the caller keeps alive).
+  static Tensor view(void* data, std::vector<int64_t> dims, DType dtype);
+
+  bool defined() const { return data_ != nullptr; }
+  int rank() const { return int(dims_.size()); }
+  int64_t dim(int axis) const { return dims_.at(size_t(axis)); }
+  const std::vector<int64_t>& dims() const { return dims_; }
+  DType dtype() const { return dtype_; }
+  void* data() const { return data_; }
+  size_t numel() const;
+  size_t bytes() const { return numel() * dtype_size(dtype_); }
+  // Same storage, new shape of the same element count.
+  Tensor reshape(std::vector<int64_t> dims) const;
+
+ private:
+  std::shared_ptr<void> owner_;
+  void* data_ = nullptr;
+  std::vector<int64_t> dims_;
+  DType dtype_ = DType::F32;
+};
+
+// How the WY transform's (I − N)⁻¹ is evaluated (src/delta/tri.rs:53-64).
+// Both evaluate the same exact inverse here (blocked forward substitution).
+enum class TriSolve { Blocked, Neumann };
+
+// Which evaluation of the delta rule runs (src/delta/path.rs:21-99).
+struct DeltaPath {
+  enum class Kind { Recurrent, Chunk, ChunkRecalculated };
+  static constexpr int64_t DEFAULT_CHUNK_LEN = 64;
+
+  Kind kind = Kind::ChunkRecalculated;
+  std::optional<int64_t> chunk_len;  // nullopt ⇒ DEFAULT_CHUNK_LEN
+  TriSolve solve = TriSolve::Blocked;
+
+  static DeltaPath recurrent() { return DeltaPath{Kind::Recurrent, std::nullopt, TriSolve::Blocked}; }
+  // The default: chunkwise at the default chunk length and backward.
+  static DeltaPath chunk() { return DeltaPath{}; }
+  // DeltaPath::chunk_len(n) of the reference (a static and a field cannot
+  // share a name in C++).
+  static DeltaPath with_chunk_len(int64_t n) {
+    return DeltaPath{Kind::ChunkRecalculated, n, TriSolve::Blocked};
+  }
+  static DeltaPath chunk_len_on_tape(int64_t n) { return DeltaPath{Kind::Chunk, n, TriSolve::Blocked}; }
+  // Recurrent answers 1: it is the chunk length of a token-at-a-time pass.
+  int64_t resolved_chunk_len() const {
+    return kind == Kind::Recurrent ? 1 : chunk_len.value_or(DEFAULT_CHUNK_LEN);
+  }
+};
+
+// (erase, write) for a per-head β: the same values broadcast over both
+// channel axes. [batch, .., nheads] → two views [batch, .., nheads, 1].
+std::pair<Tensor, Tensor> beta_gates(const Tensor& beta);
+
+// Everything the delta-rule core consumes (src/delta/path.rs:120-141).
+// q/k arrive L2-normalised and unscaled; gates arrive squashed (g = log α ≤ 0).
+// q, k, v share one dtype (f32 or bf16); gates and state are f32.
+struct DeltaInput {
+  Tensor q_bshk;       // [batch, sequence, nheads, head_k_dim]
+  Tensor k_bshk;       // [batch, sequence, nheads, head_k_dim]
+  Tensor v_bshv;       // [batch, sequence, nheads, head_v_dim]
+  Tensor erase_bshK;   // [batch, sequence, nheads, 1 | head_k_dim]
+  Tensor write_bshV;   // [batch, sequence, nheads, 1 | head_v_dim]
+  std::optional<Tensor> g_bshK;  // [batch, sequence, nheads, 1 | head_k_dim]
+  Tensor state_bhkv;   // [batch, nheads, head_k_dim, head_v_dim]
+  std::optional<double> scale;   // nullopt ⇒ 1/√head_k_dim
+
+  struct Dims {
+    int64_t batch, sequence, nheads, head_k_dim, head_v_dim;
+  };
+  Dims dims() const;
+  double resolved_scale() const;
+  bool has_channel_decay() const;
+  // Shape and gate-width checks (path.rs:177-197). The NaN/Inf guards of
+  // the reference's check-nan/check-inf features run on the device when a
+  // call is made with check_finite = true.
+  void sanity() const;
+  // path.rs:215-231. Returns (y_bshv, final_state_bhkv).
+  std::pair<Tensor, Tensor> run(const DeltaPath& path = DeltaPath{}, hipStream_t stream = nullptr,
+                                bool check_finite = false) const;
+  // recurrent.rs:107-142: delta_step unrolled over the sequence.
+  std::pair<Tensor, Tensor> delta_recurrent(hipStream_t stream = nullptr,
+                                            bool check_finite = false) const;
+  // chunk_recalculated.rs:36-83 → DeltaChunkBackendExt::delta_chunk_recalculated.
+  std::pair<Tensor, Tensor> delta_chunk_recalculated(int64_t chunk_len,
+                                                     hipStream_t stream = nullptr,
+                                                     bool check_finite = false) const;
+};
+
+// recurrent.rs:41-99. Returns (y_bhv, next_state_bhkv).
+std::pair<Tensor, Tensor> delta_step(const Tensor& q_bhk, const Tensor& k_bhk, const Tensor& v_bhv,
+                                     const Tensor& erase_bhK, const Tensor& write_bhV,
+                                     const std::optional<Tensor>& g_bhK, const Tensor& state_bhkv,
+                                     double scale, hipStream_t stream = nullptr,
+                                     bool check_finite = false);
+
+// delta_step with the state updated in place and y written to `y_bhv`.
+void delta_step_in_place(const Tensor& q_bhk, const Tensor& k_bhk, const Tensor& v_bhv,
+                         const Tensor& erase_bhK, const Tensor& write_bhV,
+                         const std::optional<Tensor>& g_bhK, Tensor& state_bhkv, Tensor& y_bhv,
+                         double scale, hipStream_t stream = nullptr, bool check_finite = false);
+
+// combined_backward.rs:50-65: gradients of the seven leaves. d_erase,
+// d_write and d_g have their gate's own width; d_g is with respect to g.
+struct DeltaChunkGrads {
+  Tensor d_q_bshk, d_k_bshk, d_v_bshv, d_erase_bshK, d_write_bshV;
+  std::optional<Tensor> d_g_bshK;
+  Tensor d_state_bhkv;
+};
+
+// combined_backward.rs:72-189. d_final_state_bhkv = nullopt means zeros.
+DeltaChunkGrads combined_backward(const Tensor& d_y_bshv,
+                                  const std::optional<Tensor>& d_final_state_bhkv,
+                                  const Tensor& q_bshk, const Tensor& k_bshk, const Tensor& v_bshv,
+                                  const Tensor& erase_bshK, const Tensor& write_bshV,
+                                  const std::optional<Tensor>& g_bshK, const Tensor& state_bhkv,
+                                  int64_t chunk_len, double scale, hipStream_t stream = nullptr,
+                                  bool check_finite = false);
+
+}  // namespace deltanet
+
+#endif  // DELTANET_HPP

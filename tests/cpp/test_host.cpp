@@ -1,0 +1,453 @@
+// Tests of the C++ host mirror (include/deltanet.hpp), in the manner of the
+// reference's own tests of src/delta (src/delta/tests.rs): shape/gate-width
+// assertions, the algorithm selector, and the forward / step / backward
+// values against the CPU oracle (oracle/liboracle.so, float64).
+//
+//   test_host --host-only   argument checks only; no HIP call is made
+//   test_host --gpu         everything (needs a GPU)
+//
+// Prints "ok <case>" per case; exits nonzero at the first failure.
+
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "deltanet.hpp"
+
+extern "C" {
+int or_chunk_fwd_f64(long B, long S, long H, long K, long V, long ew, long ww, long dw, long L,
+                     const double* q, const double* k, const double* v, const double* erase,
+                     const double* write, const double* g, const double* state, double scale,
+                     double* y, double* state_out);
+int or_delta_step_f64(long B, long H, long K, long V, long ew, long ww, long dw, const double* q,
+                      const double* k, const double* v, const double* erase, const double* write,
+                      const double* g, const double* state, double scale, double* y,
+                      double* state_out);
+int or_chunk_bwd_f64(long B, long S, long H, long K, long V, long ew, long ww, long dw, long L,
+                     const double* dy, const double* dstate, const double* q, const double* k,
+                     const double* v, const double* erase, const double* write, const double* g,
+                     const double* state, double scale, double* dq, double* dk, double* dv,
+                     double* de, double* dwr, double* dg, double* dstate_out);
+}
+
+using namespace deltanet;
+using Vec = std::vector<double>;
+
+namespace {
+
+[[noreturn]] void fail(const std::string& what) {
+  std::fprintf(stderr, "FAIL %s\n", what.c_str());
+  std::fflush(stderr);
+  std::exit(1);
+}
+
+void ok(const char* name) {
+  std::printf("ok %s\n", name);
+  std::fflush(stdout);
+}
+
+// Expect `fn` to throw deltanet::Error with this status and message.
+void expect_error(const char* name, int status, const std::string& message,
+                  const std::function<void()>& fn) {
+  try {
+    fn();
+  } catch (const Error& e) {
+    if (e.status() != status || message != e.what())
+      fail(std::string(name) + ": got status " + std::to_string(e.status()) + " \"" + e.what() +
+           "\"; want " + std::to_string(status) + " \"" + message + "\"");
+    ok(name);
+    return;
+  }
+  fail(std::string(name) + ": no error raised");
+}
+
+// splitmix64 + Box–Muller.
+struct Rng {
+  uint64_t s;
+  explicit Rng(uint64_t seed) : s(seed) {}
+  uint64_t next() {
+    uint64_t z = (s += 0x9e3779b97f4a7c15ull);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+  }
+  double uniform() { return (double(next() >> 11) + 0.5) * (1.0 / 9007199254740992.0); }
+  double normal() {
+    const double u1 = uniform(), u2 = uniform();
+    return std::sqrt(-2.0 * std::log(u1)) * std::cos(6.283185307179586 * u2);
+  }
+  Vec normals(size_t n, double std_ = 1.0) {
+    Vec x(n);
+    for (auto& v : x) v = std_ * normal();
+    return x;
+  }
+};
+
+Vec l2_rows(Vec x, size_t width) {
+  for (size_t r = 0; r < x.size() / width; ++r) {
+    double ss = 0;
+    for (size_t c = 0; c < width; ++c) ss += x[r * width + c] * x[r * width + c];
+    const double inv = 1.0 / std::sqrt(ss + 1e-6);
+    for (size_t c = 0; c < width; ++c) x[r * width + c] *= inv;
+  }
+  return x;
+}
+Vec sigmoid(Vec x) {
+  for (auto& v : x) v = 1.0 / (1.0 + std::exp(-v));
+  return x;
+}
+Vec neg_softplus(Vec x, double s) {
+  for (auto& v : x) v = -std::log1p(std::exp(v)) * s;
+  return x;
+}
+
+uint16_t to_bf16(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+float from_bf16(uint16_t h) {
+  const uint32_t u = uint32_t(h) << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+void hip_ok(hipError_t e, const char* what) {
+  if (e != hipSuccess) fail(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+// Upload as `dtype`; `x` is replaced by the values the device holds (bf16
+// rounding), so the oracle sees exactly what the GPU reads.
+Tensor upload(Vec& x, std::vector<int64_t> dims, DType dtype) {
+  Tensor t = Tensor::empty(std::move(dims), dtype);
+  if (t.numel() != x.size()) fail("upload: size mismatch");
+  if (dtype == DType::F32) {
+    std::vector<float> h(x.begin(), x.end());
+    for (size_t i = 0; i < x.size(); ++i) x[i] = h[i];
+    hip_ok(hipMemcpy(t.data(), h.data(), t.bytes(), hipMemcpyHostToDevice), "hipMemcpy");
+  } else {
+    std::vector<uint16_t> h(x.size());
+    for (size_t i = 0; i < x.size(); ++i) {
+      h[i] = to_bf16(float(x[i]));
+      x[i] = from_bf16(h[i]);
+    }
+    hip_ok(hipMemcpy(t.data(), h.data(), t.bytes(), hipMemcpyHostToDevice), "hipMemcpy");
+  }
+  return t;
+}
+
+Vec download(const Tensor& t) {
+  hip_ok(hipDeviceSynchronize(), "hipDeviceSynchronize");
+  Vec x(t.numel());
+  if (t.dtype() == DType::F32) {
+    std::vector<float> h(t.numel());
+    hip_ok(hipMemcpy(h.data(), t.data(), t.bytes(), hipMemcpyDeviceToHost), "hipMemcpy");
+    for (size_t i = 0; i < x.size(); ++i) x[i] = h[i];
+  } else {
+    std::vector<uint16_t> h(t.numel());
+    hip_ok(hipMemcpy(h.data(), t.data(), t.bytes(), hipMemcpyDeviceToHost), "hipMemcpy");
+    for (size_t i = 0; i < x.size(); ++i) x[i] = from_bf16(h[i]);
+  }
+  return x;
+}
+
+// Normwise relative error max|a − b| / max|b|.
+double rel_err(const Vec& a, const Vec& b) {
+  double num = 0, den = 0;
+  for (size_t i = 0; i < a.size(); ++i) {
+    num = std::max(num, std::fabs(a[i] - b[i]));
+    den = std::max(den, std::fabs(b[i]));
+  }
+  return num / (den > 0 ? den : 1.0);
+}
+
+void expect_close(const char* name, const Vec& got, const Vec& want, double tol) {
+  if (got.size() != want.size()) fail(std::string(name) + ": size mismatch");
+  for (double x : got)
+    if (!std::isfinite(x)) fail(std::string(name) + ": non-finite value");
+  const double e = rel_err(got, want);
+  if (!(e <= tol)) fail(std::string(name) + ": relative error " + std::to_string(e));
+}
+
+// ---------------------------------------------------------------------------
+// Argument checks (no device memory is touched: views of a dummy address).
+// ---------------------------------------------------------------------------
+void host_cases() {
+  void* fake = reinterpret_cast<void*>(uintptr_t(0x1000));
+  auto v4 = [&](std::vector<int64_t> d, DType t = DType::F32) { return Tensor::view(fake, d, t); };
+  const int64_t B = 2, S = 9, H = 2, K = 4, V = 6;
+  auto good = [&]() {
+    return DeltaInput{v4({B, S, H, K}), v4({B, S, H, K}), v4({B, S, H, V}), v4({B, S, H, 1}),
+                      v4({B, S, H, 1}), v4({B, S, H, 1}), v4({B, H, K, V}), std::nullopt};
+  };
+  good().sanity();
+  ok("sanity_accepts_broadcast_gates");
+  {
+    DeltaInput in = good();
+    in.erase_bshK = v4({B, S, H, K});
+    in.write_bshV = v4({B, S, H, V});
+    in.g_bshK = v4({B, S, H, K});
+    in.sanity();
+    if (!in.has_channel_decay()) fail("has_channel_decay: per-channel g not seen");
+    if (good().has_channel_decay()) fail("has_channel_decay: per-head g seen as per-channel");
+    ok("sanity_accepts_channel_gates");
+  }
+  expect_error("k_shape", DN_ERR_SHAPE, "k: expected shape [2, 9, 2, 4], got [2, 9, 2, 5]", [&] {
+    DeltaInput in = good();
+    in.k_bshk = v4({B, S, H, 5});
+    in.sanity();
+  });
+  expect_error("state_shape", DN_ERR_SHAPE, "state: expected shape [2, 2, 4, 6], got [2, 2, 6, 4]",
+               [&] {
+                 DeltaInput in = good();
+                 in.state_bhkv = v4({B, H, V, K});
+                 in.sanity();
+               });
+  expect_error("erase_width", DN_ERR_GATE_WIDTH, "erase gate: last axis must be 1 or 4, got 3",
+               [&] {
+                 DeltaInput in = good();
+                 in.erase_bshK = v4({B, S, H, 3});
+                 in.sanity();
+               });
+  expect_error("write_width", DN_ERR_GATE_WIDTH, "write gate: last axis must be 1 or 6, got 4",
+               [&] {
+                 DeltaInput in = good();
+                 in.write_bshV = v4({B, S, H, 4});
+                 in.sanity();
+               });
+  expect_error("forget_width", DN_ERR_GATE_WIDTH, "forget gate: last axis must be 1 or 4, got 6",
+               [&] {
+                 DeltaInput in = good();
+                 in.g_bshK = v4({B, S, H, 6});
+                 in.sanity();
+               });
+  expect_error("gate_leading_dims", DN_ERR_SHAPE,
+               "erase gate: expected leading dims [2, 9, 2], got [2, 8, 2, 1]", [&] {
+                 DeltaInput in = good();
+                 in.erase_bshK = v4({B, S - 1, H, 1});
+                 in.sanity();
+               });
+  expect_error("empty_sequence", DN_ERR_SEQUENCE, "sequence length must be at least 1", [&] {
+    DeltaInput in{v4({B, 0, H, K}), v4({B, 0, H, K}), v4({B, 0, H, V}), v4({B, 0, H, 1}),
+                  v4({B, 0, H, 1}), std::nullopt, v4({B, H, K, V}), std::nullopt};
+    in.run();
+  });
+  expect_error("chunk_len_zero", DN_ERR_CHUNK_LEN, "chunk_len must be at least 1",
+               [&] { good().run(DeltaPath::with_chunk_len(0)); });
+  expect_error("qkv_dtypes", DN_ERR_DTYPE, "q, k and v must share one dtype", [&] {
+    DeltaInput in = good();
+    in.q_bshk = v4({B, S, H, K}, DType::BF16);
+    in.sanity();
+  });
+  expect_error("gate_dtype", DN_ERR_DTYPE, "erase gate: gates and state must be float32", [&] {
+    DeltaInput in = good();
+    in.erase_bshK = v4({B, S, H, 1}, DType::BF16);
+    in.sanity();
+  });
+  expect_error("step_state_shape", DN_ERR_SHAPE,
+               "state: expected shape [2, 2, 4, 6], got [2, 2, 4, 5]", [&] {
+                 delta_step(v4({B, H, K}), v4({B, H, K}), v4({B, H, V}), v4({B, H, 1}),
+                            v4({B, H, 1}), std::nullopt, v4({B, H, K, 5}), 0.5);
+               });
+  expect_error("step_erase_width", DN_ERR_GATE_WIDTH,
+               "erase gate: last axis must be 1 or 4, got 2", [&] {
+                 delta_step(v4({B, H, K}), v4({B, H, K}), v4({B, H, V}), v4({B, H, 2}),
+                            v4({B, H, 1}), std::nullopt, v4({B, H, K, V}), 0.5);
+               });
+  expect_error("backward_dy_shape", DN_ERR_SHAPE, "d_y: expected shape [2, 9, 2, 6], got [2, 9, 2, 4]",
+               [&] {
+                 DeltaInput in = good();
+                 combined_backward(v4({B, S, H, K}), std::nullopt, in.q_bshk, in.k_bshk, in.v_bshv,
+                                   in.erase_bshK, in.write_bshV, in.g_bshK, in.state_bhkv, 16,
+                                   0.5);
+               });
+  // The algorithm selector (path.rs:21-99).
+  if (DeltaPath::recurrent().resolved_chunk_len() != 1 ||
+      DeltaPath::chunk().resolved_chunk_len() != DeltaPath::DEFAULT_CHUNK_LEN ||
+      DeltaPath{}.kind != DeltaPath::Kind::ChunkRecalculated ||
+      DeltaPath::with_chunk_len(16).resolved_chunk_len() != 16 ||
+      DeltaPath::chunk_len_on_tape(8).kind != DeltaPath::Kind::Chunk)
+    fail("delta_path");
+  ok("delta_path");
+  // Default scale 1/√head_k_dim (path.rs:161-165).
+  {
+    DeltaInput in = good();
+    if (std::fabs(in.resolved_scale() - 0.5) > 1e-15) fail("resolved_scale default");
+    in.scale = 0.25;
+    if (in.resolved_scale() != 0.25) fail("resolved_scale explicit");
+    ok("resolved_scale");
+  }
+  // beta_gates: one per-head β as both gates, [b, s, h] → [b, s, h, 1].
+  {
+    auto [e, w] = beta_gates(Tensor::view(fake, {B, S, H}, DType::F32));
+    if (e.dims() != std::vector<int64_t>{B, S, H, 1} || w.dims() != e.dims() ||
+        e.data() != fake || w.data() != fake)
+      fail("beta_gates");
+    ok("beta_gates");
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Values against the oracle (float64), on the GPU.
+// ---------------------------------------------------------------------------
+struct Case {
+  long B, S, H, K, V, ew, ww, dw;
+  Vec q, k, v, e, w, g, s;
+};
+
+Case make_case(uint64_t seed, long B, long S, long H, long K, long V, long ew, long ww, long dw,
+               double g_scale, double state_std, double beta_scale = 1.0) {
+  Rng r(seed);
+  Case c{B, S, H, K, V, ew, ww, dw, {}, {}, {}, {}, {}, {}, {}};
+  const size_t rows = size_t(B * S * H);
+  c.q = l2_rows(r.normals(rows * K), size_t(K));
+  c.k = l2_rows(r.normals(rows * K), size_t(K));
+  c.v = r.normals(rows * V);
+  c.e = sigmoid(r.normals(rows * ew));
+  for (auto& x : c.e) x *= beta_scale;
+  c.w = ew == 1 && ww == 1 ? c.e : sigmoid(r.normals(rows * ww));
+  if (dw) c.g = neg_softplus(r.normals(rows * dw), g_scale);
+  c.s = r.normals(size_t(B * H * K * V), state_std);
+  return c;
+}
+
+DeltaInput to_device(Case& c, DType qkv) {
+  DeltaInput in{upload(c.q, {c.B, c.S, c.H, c.K}, qkv),
+                upload(c.k, {c.B, c.S, c.H, c.K}, qkv),
+                upload(c.v, {c.B, c.S, c.H, c.V}, qkv),
+                upload(c.e, {c.B, c.S, c.H, c.ew}, DType::F32),
+                upload(c.w, {c.B, c.S, c.H, c.ww}, DType::F32),
+                std::nullopt,
+                upload(c.s, {c.B, c.H, c.K, c.V}, DType::F32),
+                std::nullopt};
+  if (c.dw) in.g_bshK = upload(c.g, {c.B, c.S, c.H, c.dw}, DType::F32);
+  return in;
+}
+
+std::pair<Vec, Vec> oracle_fwd(const Case& c, long L, double scale) {
+  Vec y(size_t(c.B * c.S * c.H * c.V)), s(c.s.size());
+  if (or_chunk_fwd_f64(c.B, c.S, c.H, c.K, c.V, c.ew, c.ww, c.dw, L, c.q.data(), c.k.data(),
+                       c.v.data(), c.e.data(), c.w.data(), c.dw ? c.g.data() : nullptr,
+                       c.s.data(), scale, y.data(), s.data()))
+    fail("oracle chunk_fwd rejected the case");
+  return {y, s};
+}
+
+void gpu_cases() {
+  // B=1, H=4, T=512, dk=dv=64, chunk 64, fp32, β gates,
+  // g = −softplus(N)·0.1, S₀ = 0 — through both DeltaPath arms.
+  {
+    Case c = make_case(20260827, 1, 512, 4, 64, 64, 1, 1, 1, 0.1, 0.0);
+    DeltaInput in = to_device(c, DType::F32);
+    const auto [y0, s0] = oracle_fwd(c, 64, 1.0 / 8.0);
+    auto [y, s] = in.run();
+    expect_close("config1_chunk_y", download(y), y0, 1e-4);
+    expect_close("config1_chunk_state", download(s), s0, 1e-4);
+    ok("config1_chunk");
+    auto [yr, sr] = in.run(DeltaPath::recurrent());
+    expect_close("config1_recurrent_y", download(yr), y0, 1e-4);
+    expect_close("config1_recurrent_state", download(sr), s0, 1e-4);
+    ok("config1_recurrent");
+  }
+  // GDN-2 gate widths (per-channel erase, write and decay), nonzero S₀,
+  // a ragged last chunk, explicit scale and chunk length.
+  {
+    Case c = make_case(7, 2, 100, 2, 32, 48, 32, 48, 32, 0.05, 0.05);
+    DeltaInput in = to_device(c, DType::F32);
+    in.scale = 0.3;
+    const auto [y0, s0] = oracle_fwd(c, 16, 0.3);
+    auto [y, s] = in.run(DeltaPath::with_chunk_len(16));
+    expect_close("channel_gates_y", download(y), y0, 1e-4);
+    expect_close("channel_gates_state", download(s), s0, 1e-4);
+    ok("channel_gates_chunk16");
+  }
+  // delta_step: out of place and in place agree, and match the oracle.
+  {
+    Case c = make_case(11, 3, 1, 2, 16, 24, 16, 1, 16, 0.05, 0.1);
+    Vec q = c.q, k = c.k, v = c.v, e = c.e, w = c.w, g = c.g, s = c.s;
+    Tensor tq = upload(q, {3, 2, 16}, DType::F32), tk = upload(k, {3, 2, 16}, DType::F32);
+    Tensor tv = upload(v, {3, 2, 24}, DType::F32), te = upload(e, {3, 2, 16}, DType::F32);
+    Tensor tw = upload(w, {3, 2, 1}, DType::F32), tg = upload(g, {3, 2, 16}, DType::F32);
+    Tensor ts = upload(s, {3, 2, 16, 24}, DType::F32);
+    Vec y0(3 * 2 * 24), s0(s.size());
+    if (or_delta_step_f64(3, 2, 16, 24, 16, 1, 16, q.data(), k.data(), v.data(), e.data(),
+                          w.data(), g.data(), s.data(), 0.25, y0.data(), s0.data()))
+      fail("oracle delta_step rejected the case");
+    auto [y, sn] = delta_step(tq, tk, tv, te, tw, tg, ts, 0.25);
+    expect_close("step_y", download(y), y0, 1e-5);
+    expect_close("step_state", download(sn), s0, 1e-5);
+    if (rel_err(download(ts), s) != 0.0) fail("step: the input state was modified");
+    Tensor yi = Tensor::empty({3, 2, 24}, DType::F32);
+    delta_step_in_place(tq, tk, tv, te, tw, tg, ts, yi, 0.25);
+    expect_close("step_in_place_y", download(yi), download(y), 0.0);
+    expect_close("step_in_place_state", download(ts), download(sn), 0.0);
+    ok("delta_step");
+  }
+  // combined_backward: all seven gradients at GDN-2 gate widths.
+  {
+    Case c = make_case(13, 1, 70, 2, 16, 24, 16, 24, 16, 0.05, 0.1);
+    DeltaInput in = to_device(c, DType::F32);
+    Rng r(99);
+    Vec dy = r.normals(size_t(1 * 70 * 2 * 24)), dsf = r.normals(c.s.size(), 0.5);
+    Tensor tdy = upload(dy, {1, 70, 2, 24}, DType::F32);
+    Tensor tds = upload(dsf, {1, 2, 16, 24}, DType::F32);
+    const double scale = 0.25;
+    DeltaChunkGrads gr = combined_backward(tdy, tds, in.q_bshk, in.k_bshk, in.v_bshv,
+                                           in.erase_bshK, in.write_bshV, in.g_bshK,
+                                           in.state_bhkv, 16, scale);
+    Vec dq(c.q.size()), dk(c.k.size()), dv(c.v.size()), de(c.e.size()), dw(c.w.size()),
+        dg(c.g.size()), ds(c.s.size());
+    if (or_chunk_bwd_f64(1, 70, 2, 16, 24, 16, 24, 16, 16, dy.data(), dsf.data(), c.q.data(),
+                         c.k.data(), c.v.data(), c.e.data(), c.w.data(), c.g.data(), c.s.data(),
+                         scale, dq.data(), dk.data(), dv.data(), de.data(), dw.data(), dg.data(),
+                         ds.data()))
+      fail("oracle chunk_bwd rejected the case");
+    expect_close("bwd_dq", download(gr.d_q_bshk), dq, 1e-4);
+    expect_close("bwd_dk", download(gr.d_k_bshk), dk, 1e-4);
+    expect_close("bwd_dv", download(gr.d_v_bshv), dv, 1e-4);
+    expect_close("bwd_derase", download(gr.d_erase_bshK), de, 1e-4);
+    expect_close("bwd_dwrite", download(gr.d_write_bshV), dw, 1e-4);
+    expect_close("bwd_dg", download(*gr.d_g_bshK), dg, 1e-4);
+    expect_close("bwd_dstate", download(gr.d_state_bhkv), ds, 1e-4);
+    ok("combined_backward");
+  }
+  // bf16 q/k/v at the Gated DeltaNet shape (the MFMA path), at the bf16 bar.
+  {
+    Case c = make_case(17, 1, 256, 2, 128, 128, 1, 1, 1, 0.05, 0.02);
+    DeltaInput in = to_device(c, DType::BF16);
+    const auto [y0, s0] = oracle_fwd(c, 64, 1.0 / std::sqrt(128.0));
+    auto [y, s] = in.run();
+    if (y.dtype() != DType::BF16) fail("bf16: y dtype");
+    expect_close("bf16_y", download(y), y0, 2e-2);
+    expect_close("bf16_state", download(s), s0, 2e-2);
+    ok("bf16_mfma_path");
+  }
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  const bool gpu = argc > 1 && std::strcmp(argv[1], "--gpu") == 0;
+  const bool host = argc > 1 && std::strcmp(argv[1], "--host-only") == 0;
+  if (!gpu && !host) {
+    std::fprintf(stderr, "usage: %s --host-only | --gpu\n", argv[0]);
+    return 2;
+  }
+  try {
+    host_cases();
+    if (gpu) gpu_cases();
+  } catch (const std::exception& e) {
+    fail(std::string("unexpected exception: ") + e.what());
+  }
+  std::printf("all passed\n");
+  return 0;
+}
