@@ -13,6 +13,9 @@ dk128) at 1 GPU; % roofline"):
 * roofline = the dominant kernel of the forward, timed with HIP events on its
   own stream by the library's profiler (dn_profile_*), against algorithmic
   bytes per launch (DESIGN.md lists the per-unit figures).
+* config4 / config5 = BASELINE configs 4 (DeltaProduct u=2, folded core
+  forward) and 5 (GDN-2 per-channel gates, forward + custom backward), each
+  with its own HBM roofline; not part of `value`.
 * cpu_baseline = the CPU oracle (a C++ restatement of the reference algorithm,
   incl. its 24·L³ ladder) on a bounded sample of config 2, all host threads.
 
@@ -151,6 +154,123 @@ def bench_decode(torch, pkg, steps, warmup):
     return dict(us=us, kernel_us=k_us, bytes=step_bytes, prof=prof, kernel=name)
 
 
+def _timed(torch, abi, fn, steps, warmup):
+    """Mean ms per call of fn() over `steps` calls after `warmup`, with the
+    library's per-kernel HIP-event profile of the timed calls."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    abi.profile_enable(True)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    prof = abi.profile_read()
+    abi.profile_enable(False)
+    kern = {n: {"avg_us": round(v[0] / v[1] * 1e3, 2), "launches": v[1]} for n, v in prof.items()}
+    return start.elapsed_time(stop) / steps, kern
+
+
+def _hbm(nbytes, ms):
+    gbs = nbytes / (ms / 1e3) / 1e9
+    return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4), "algorithmic_bytes": int(nbytes)}
+
+
+def bench_config4(torch, pkg, steps, warmup):
+    """DeltaProduct with 2 Householder micro-steps per token
+    (allow_neg_eigval: β = 2σ(N)), B=4, T=8192 (core sequence 16384), H=16,
+    dk=dv=128, chunk 64, bf16 q/k/v, fp32 state. The core sees the folded
+    sequence of delta_product.rs:178-205: q only on the last micro-step of a
+    token, the forget gate only on the first."""
+    B, T, H, K, V, u = 4, 8192, 16, 128, 128, 2
+    S = T * u
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20260830)
+    l2 = lambda x: x / torch.sqrt((x * x).sum(-1, keepdim=True) + 1e-6)
+    q = torch.zeros((B, T, u, H, K), device=dev)
+    q[:, :, u - 1] = l2(torch.randn((B, T, H, K), generator=gen, device=dev))
+    q = q.reshape(B, S, H, K).to(torch.bfloat16)
+    k = l2(torch.randn((B, S, H, K), generator=gen, device=dev)).to(torch.bfloat16)
+    v = torch.randn((B, S, H, V), generator=gen, device=dev).to(torch.bfloat16)
+    beta = 2 * torch.sigmoid(torch.randn((B, S, H, 1), generator=gen, device=dev))
+    g = torch.zeros((B, T, u, H, 1), device=dev)
+    g[:, :, 0] = -torch.nn.functional.softplus(
+        torch.randn((B, T, H, 1), generator=gen, device=dev)) * 0.1
+    g = g.reshape(B, S, H, 1)
+    s0 = torch.zeros((B, H, K, V), device=dev)
+    y = torch.empty((B, S, H, V), dtype=torch.bfloat16, device=dev)
+    s1 = torch.empty_like(s0)
+    abi = pkg.abi
+    args = abi.chunk_fwd_args(q, k, v, beta, beta, g, s0, y, s1, 64, None)
+    ws = torch.empty(max(abi.lib().dn_chunk_fwd_workspace_bytes(args), 1), dtype=torch.uint8,
+                     device=dev)
+    args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
+    algo = abi.lib().dn_chunk_fwd_algo(args)
+    ms, kern = _timed(torch, abi, lambda: abi.run_chunk_fwd(args), steps, warmup)
+    rows = B * S * H
+    nbytes = rows * (2 * K + 2 * V) * 2 + rows * 3 * 4 + 2 * B * H * K * V * 4
+    return {"workload": "config 4: DeltaProduct u=2 (allow_neg_eigval), folded core forward",
+            "batch": B, "seq_len": T, "core_seq_len": S, "nheads": H, "head_k_dim": K,
+            "head_v_dim": V, "algo": {1: "generic", 2: "mfma"}.get(algo, algo),
+            "ms_per_step": round(ms, 4), "tokens_per_s": round(B * T / (ms / 1e3), 1),
+            "roofline": _hbm(nbytes, ms), "kernels": kern}
+
+
+def bench_config5(torch, pkg, steps, warmup):
+    """GDN-2 forward plus the custom backward, B=2,
+    T=16384, H=16, dk=dv=128, chunk 64; per-key-channel erase b and decay α,
+    per-value-channel write w (fp32), bf16 q/k/v and dO."""
+    B, T, H, K, V = 2, 16384, 16, 128, 128
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20260831)
+    l2 = lambda x: x / torch.sqrt((x * x).sum(-1, keepdim=True) + 1e-6)
+    rn = lambda *shape: torch.randn(shape, generator=gen, device=dev)
+    q = l2(rn(B, T, H, K)).to(torch.bfloat16)
+    k = l2(rn(B, T, H, K)).to(torch.bfloat16)
+    v = rn(B, T, H, V).to(torch.bfloat16)
+    e = torch.sigmoid(rn(B, T, H, K))
+    w = torch.sigmoid(rn(B, T, H, V))
+    g = -torch.nn.functional.softplus(rn(B, T, H, K)) * 0.05
+    s0 = torch.zeros((B, H, K, V), device=dev)
+    y = torch.empty((B, T, H, V), dtype=torch.bfloat16, device=dev)
+    s1 = torch.empty_like(s0)
+    abi = pkg.abi
+    fargs = abi.chunk_fwd_args(q, k, v, e, w, g, s0, y, s1, 64, None)
+    wsf = torch.empty(max(abi.lib().dn_chunk_fwd_workspace_bytes(fargs), 1), dtype=torch.uint8,
+                      device=dev)
+    fargs.workspace, fargs.workspace_bytes = wsf.data_ptr(), wsf.numel()
+    dy = rn(B, T, H, V).to(torch.bfloat16)
+    grads = (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v), torch.empty_like(e),
+             torch.empty_like(w), torch.empty_like(g), torch.empty_like(s0))
+    bargs = abi.chunk_bwd_args(dy, None, q, k, v, e, w, g, s0, grads, 64, None)
+    wsb = torch.empty(max(abi.lib().dn_chunk_bwd_workspace_bytes(bargs), 1), dtype=torch.uint8,
+                      device=dev)
+    bargs.workspace, bargs.workspace_bytes = wsb.data_ptr(), wsb.numel()
+    fa, ba = abi.lib().dn_chunk_fwd_algo(fargs), abi.lib().dn_chunk_bwd_algo(bargs)
+    fms, fk = _timed(torch, abi, lambda: abi.run_chunk_fwd(fargs), steps, warmup)
+    bms, bk = _timed(torch, abi, lambda: abi.run_chunk_bwd(bargs), steps, warmup)
+    rows = B * T * H
+    st = B * H * K * V * 4
+    f_bytes = rows * (2 * K + V) * 2 + rows * V * 2 + rows * (2 * K + V) * 4 + 2 * st
+    # backward: reads q, k, v, dO, the gates and S0; writes dq, dk, dv, the three
+    # gate gradients and dS0.
+    b_bytes = rows * (2 * K + 2 * V) * 2 + rows * (2 * K + V) * 4 + st + \
+        rows * (2 * K + V) * 2 + rows * (2 * K + V) * 4 + st
+    name = {1: "generic", 2: "mfma"}
+    return {"workload": "config 5: GDN-2 per-channel gates, forward + custom backward",
+            "batch": B, "seq_len": T, "nheads": H, "head_k_dim": K, "head_v_dim": V,
+            "algo": {"forward": name.get(fa, fa), "backward": name.get(ba, ba)},
+            "fwd_ms": round(fms, 3), "bwd_ms": round(bms, 3),
+            "tokens_per_s_fwd_bwd": round(B * T / ((fms + bms) / 1e3), 1),
+            "roofline_fwd": _hbm(f_bytes, fms), "roofline_bwd": _hbm(b_bytes, bms),
+            "kernels_fwd": fk, "kernels_bwd": bk}
+
+
 def cpu_baseline(torch):
     """The oracle on the whole config-2 workload (B=8, H=16, T=4096: 32768
     tokens), fp32, all available host threads (OMP_NUM_THREADS)."""
@@ -198,6 +318,10 @@ def main():
     ap.add_argument("--algo", choices=["auto", "generic", "mfma"], default="auto")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the config 4 and config 5 measurements")
+    ap.add_argument("--extra-steps", type=int, default=3,
+                    help="timed calls for configs 4 and 5 (after one warmup)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="short run for rocprofv3 --pmc: a 1 GiB copy (calibration), then 2 "
                          "forward and 2 decode launches; prints no JSON")
@@ -259,6 +383,17 @@ def main():
                                "traffic": traffic_from_profiles(dc["kernel"])}}
         print(f"[bench] decode {decode}", file=sys.stderr, flush=True)
 
+    extra = {}
+    if not args.no_extra:
+        print("[bench] config 4 (DeltaProduct fold)", file=sys.stderr, flush=True)
+        extra["config4"] = bench_config4(torch, pkg, args.extra_steps, 1)
+        print(f"[bench] config4 {extra['config4']}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+        print("[bench] config 5 (GDN-2 forward + backward)", file=sys.stderr, flush=True)
+        extra["config5"] = bench_config5(torch, pkg, args.extra_steps, 1)
+        print(f"[bench] config5 {extra['config5']}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+
     cpu = None
     if not args.no_cpu:
         print("[bench] cpu baseline (oracle)", file=sys.stderr, flush=True)
@@ -291,6 +426,7 @@ def main():
                           "mfma_TFLOPs": round(fw["path_flops"] / (fw["ms"] / 1e3) / 1e12, 2)},
         "kernels": per_kernel,
         "decode": decode,
+        **extra,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
