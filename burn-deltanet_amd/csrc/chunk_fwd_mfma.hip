@@ -100,11 +100,101 @@ struct MfmaParams {
   uint16_t* KcT;   // [G][K][64] bf16 (e^{G_last−G}⊙K)ᵀ
   uint16_t* sink;  // one y row: the target of padded tokens' writes
   float* gc;       // [G][64]
+  // Per-channel gates (GDN-2) only:
+  int ew, ww;      // erase / write gate widths (1 or K / 1 or V); the decay has width K
+  uint16_t* Kg;    // [G][64][K] bf16(e⊙e^G⊙K), hi part
+  uint16_t* Kglo;  // [G][64][K] its lo part
+  uint16_t* Qg;    // [G][64][K] bf16(scale·e^G⊙Q)
+  float* egl;      // [G][K] e^{G_last} per key channel
 };
 
 // ---------------------------------------------------------------------------
 // intra
 // ---------------------------------------------------------------------------
+// T's diagonal 16×16 block `wave` of T = (I + A)⁻¹ (A strict lower, fp32 in
+// LDS) by column elimination; one wave per block.
+__device__ inline void diag_inverse(const float (*A)[kL + 1], float (*Tm)[kL + 1], int wave,
+                                    int lane) {
+  // T's diagonal 16×16 block `wave` by column elimination: lane (c, g)
+  // holds rows g, g+4, g+8, g+12 of column c; step k₂ broadcasts x[k₂]
+  // inside the lane quad (DPP) and updates the rows below it.
+  const int base = 16 * wave, c = lane >> 2, g = lane & 3;
+  float x[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) x[j] = (4 * j + g == c) ? 1.f : 0.f;
+  // Multipliers A[i][k₂] for i > k₂ (zero otherwise), read up front.
+  float mul[15][4];
+#pragma unroll
+  for (int k2 = 0; k2 < 15; ++k2)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = 4 * j + g;
+      mul[k2][j] = (4 * j + 3 > k2 && i > k2) ? A[base + i][base + k2] : 0.f;
+    }
+#pragma unroll
+  for (int k2 = 0; k2 < 15; ++k2) {
+    const float xk = quad_bcast(x[k2 >> 2], k2 & 3);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (4 * j + 3 > k2) x[j] -= mul[k2][j] * xk;
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) Tm[base + 4 * j + g][base + c] = x[j];
+}
+
+// The two doubling merges that complete T from its diagonal blocks (all
+// four waves call it; it synchronises the workgroup).
+__device__ inline void merge_T(const float (*A)[kL + 1], float (*Tm)[kL + 1],
+                               float (*Xs)[kL / 2 + 1], int wave, int lane) {
+  // The merges run on fp32 MFMA (v_mfma_f32_16x16x4_f32: exact fp32
+  // products): lane l holds A[l%16][l/16] and B[l/16][l%16] of a
+  // 16×4 · 4×16 step, and D[4(l/16)+r][l%16]. Full-block sums are exact:
+  // the triangular factors hold zeros outside their triangles.
+  const int m16 = lane & 15, g4 = lane >> 4;
+  // 16 → 32: T₁₀ = −T₁₁ A₁₀ T₀₀ for the two 32-blocks (waves 0 and 1).
+  if (wave < 2) {
+    const int r0 = 32 * wave + 16, c0 = 32 * wave;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4)
+      acc = mfma_f32(A[r0 + m16][c0 + 4 * s4 + g4], Tm[c0 + 4 * s4 + g4][c0 + m16], acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Xs[16 * wave + 4 * g4 + r][m16] = acc[r];
+  }
+  __syncthreads();
+  if (wave < 2) {
+    const int r0 = 32 * wave + 16, c0 = 32 * wave;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4)
+      acc = mfma_f32(Tm[r0 + m16][r0 + 4 * s4 + g4], Xs[16 * wave + 4 * s4 + g4][m16], acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Tm[r0 + 4 * g4 + r][c0 + m16] = -acc[r];
+  }
+  __syncthreads();
+  // 32 → 64: T[32:,:32] = −T[32:,32:] A[32:,:32] T[:32,:32]; wave w owns
+  // output tile (w/2, w%2) of the 32×32 block.
+  {
+    const int ti = wave >> 1, tj = wave & 1;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4)
+      acc = mfma_f32(A[32 + 16 * ti + m16][4 * s4 + g4], Tm[4 * s4 + g4][16 * tj + m16], acc);
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Xs[16 * ti + 4 * g4 + r][16 * tj + m16] = acc[r];
+    __syncthreads();
+    acc = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s4 = 0; s4 < 8; ++s4)
+      acc = mfma_f32(Tm[32 + 16 * ti + m16][32 + 4 * s4 + g4], Xs[4 * s4 + g4][16 * tj + m16],
+                     acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Tm[32 + 16 * ti + 4 * g4 + r][16 * tj + m16] = -acc[r];
+  }
+  __syncthreads();
+}
+
 template <int K, bool GATED>
 __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int G) {
   constexpr int KP = K + 8;                     // padded LDS row (bf16 elements)
@@ -241,33 +331,7 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
     }
     __syncthreads();
 
-    {
-      // T's diagonal 16×16 block `wave` by column elimination: lane (c, g)
-      // holds rows g, g+4, g+8, g+12 of column c; step k₂ broadcasts x[k₂]
-      // inside the lane quad (DPP) and updates the rows below it.
-      const int base = 16 * wave, c = lane >> 2, g = lane & 3;
-      float x[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) x[j] = (4 * j + g == c) ? 1.f : 0.f;
-      // Multipliers A[i][k₂] for i > k₂ (zero otherwise), read up front.
-      float mul[15][4];
-#pragma unroll
-      for (int k2 = 0; k2 < 15; ++k2)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int i = 4 * j + g;
-          mul[k2][j] = (4 * j + 3 > k2 && i > k2) ? A[base + i][base + k2] : 0.f;
-        }
-#pragma unroll
-      for (int k2 = 0; k2 < 15; ++k2) {
-        const float xk = quad_bcast(x[k2 >> 2], k2 & 3);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (4 * j + 3 > k2) x[j] -= mul[k2][j] * xk;
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) Tm[base + 4 * j + g][base + c] = x[j];
-    }
+    diag_inverse(A, Tm, wave, lane);
     {
       // Kcᵀ = (e^{G_last−G} ⊙ K)ᵀ for the scan's state update, while the K
       // tile is in LDS: an item is one key channel × 16 tokens, consecutive
@@ -301,53 +365,7 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
       }
     }
     __syncthreads();
-    // The merges run on fp32 MFMA (v_mfma_f32_16x16x4_f32: exact fp32
-    // products): lane l holds A[l%16][l/16] and B[l/16][l%16] of a
-    // 16×4 · 4×16 step, and D[4(l/16)+r][l%16]. Full-block sums are exact:
-    // the triangular factors hold zeros outside their triangles.
-    const int m16 = lane & 15, g4 = lane >> 4;
-    // 16 → 32: T₁₀ = −T₁₁ A₁₀ T₀₀ for the two 32-blocks (waves 0 and 1).
-    if (wave < 2) {
-      const int r0 = 32 * wave + 16, c0 = 32 * wave;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4)
-        acc = mfma_f32(A[r0 + m16][c0 + 4 * s4 + g4], Tm[c0 + 4 * s4 + g4][c0 + m16], acc);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) Xs[16 * wave + 4 * g4 + r][m16] = acc[r];
-    }
-    __syncthreads();
-    if (wave < 2) {
-      const int r0 = 32 * wave + 16, c0 = 32 * wave;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4)
-        acc = mfma_f32(Tm[r0 + m16][r0 + 4 * s4 + g4], Xs[16 * wave + 4 * s4 + g4][m16], acc);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) Tm[r0 + 4 * g4 + r][c0 + m16] = -acc[r];
-    }
-    __syncthreads();
-    // 32 → 64: T[32:,:32] = −T[32:,32:] A[32:,:32] T[:32,:32]; wave w owns
-    // output tile (w/2, w%2) of the 32×32 block.
-    {
-      const int ti = wave >> 1, tj = wave & 1;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s4 = 0; s4 < 8; ++s4)
-        acc = mfma_f32(A[32 + 16 * ti + m16][4 * s4 + g4], Tm[4 * s4 + g4][16 * tj + m16], acc);
-      __syncthreads();
-#pragma unroll
-      for (int r = 0; r < 4; ++r) Xs[16 * ti + 4 * g4 + r][16 * tj + m16] = acc[r];
-      __syncthreads();
-      acc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s4 = 0; s4 < 8; ++s4)
-        acc = mfma_f32(Tm[32 + 16 * ti + m16][32 + 4 * s4 + g4], Xs[4 * s4 + g4][16 * tj + m16],
-                       acc);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) Tm[32 + 16 * ti + 4 * g4 + r][16 * tj + m16] = -acc[r];
-    }
-    __syncthreads();
+    merge_T(A, Tm, Xs, wave, lane);
 
     // T and attn of this chunk as bf16 rows, 16 values per lane.
     {
@@ -370,6 +388,256 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
     __syncthreads();  // LDS is restaged by the next chunk
   }
   if (pend_cid >= 0) store_pending();
+}
+
+// ---------------------------------------------------------------------------
+// intra, per-channel gates (GDN-2: decay of width K, erase of width 1 or K)
+// ---------------------------------------------------------------------------
+// The scores follow the reference's block decay (decay.rs:39-60,
+// forward.rs:451-556): for the 16-row block holding row i, with reference row
+// r = 16·(i div 16) + 8,
+//   Akk[i][j] = Σ_d (k⊙e)[i][d]·e^{min(G[i][d]−G[r][d], 48)} · k[j][d]·e^{min(G[r][d]−G[j][d], 48)}
+// (j < i; Aqk likewise with scale·q and j ≤ i). The row factors are formed
+// once per chunk as bf16 tiles (hi + lo for Akk, which feeds the inverse);
+// the column factors, which depend on the row block, are formed per MFMA
+// fragment in registers. Besides T/attn/Kcᵀ the kernel writes what the scan
+// needs in place of K, Q and the scalar gates: kg = e⊙e^G⊙K (hi + lo),
+// qg = scale·e^G⊙Q and e^{G_last} per channel. One workgroup per chunk-head.
+template <int K>
+__global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p) {
+  constexpr int KP = K + 8;  // bf16 row pitch
+  constexpr int GP = K + 4;  // fp32 row pitch of G
+  constexpr int KS8 = K / 8;
+  constexpr int NLD = kL * KS8 / kThreads;
+  constexpr int kTile = kL * KP * 2;
+  constexpr int kSolveBytes = (kL * (kL + 1) + (kL / 2) * (kL / 2 + 1)) * 4;
+  constexpr float kMaxExp = 48.f;  // MAX_EXPONENT, decay.rs:49
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kL * KP];
+  __shared__ __attribute__((aligned(16))) float Gc[kL * GP];
+  // Row-factor tiles; T and the merge scratch reuse their space afterwards.
+  __shared__ __attribute__((aligned(16)))
+  unsigned char rows[3 * kTile > kSolveBytes ? 3 * kTile : kSolveBytes];
+  uint16_t* AKh = reinterpret_cast<uint16_t*>(rows);
+  uint16_t* AKl = AKh + kL * KP;
+  uint16_t* AQ = AKl + kL * KP;
+  float(*Tm)[kL + 1] = reinterpret_cast<float(*)[kL + 1]>(rows);
+  float(*Xs)[kL / 2 + 1] = reinterpret_cast<float(*)[kL / 2 + 1]>(rows + kL * (kL + 1) * 4);
+  __shared__ float A[kL][kL + 1];
+  __shared__ __attribute__((aligned(16))) uint16_t At[kL * (kL + 8)];
+
+  const int cid = blockIdx.x;
+  const int h = cid % p.H, n = (cid / p.H) % p.N, b = cid / (p.H * p.N);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tok0 = n * kL;
+  const size_t row0 = size_t(b) * p.S * p.H + h + size_t(tok0) * p.H;
+  auto row_of = [&](int t) { return row0 + size_t(t) * p.H; };
+  auto f8 = [](const uint4& u, float* f) {
+    f[0] = lo_f(u.x); f[1] = hi_f(u.x); f[2] = lo_f(u.y); f[3] = hi_f(u.y);
+    f[4] = lo_f(u.z); f[5] = hi_f(u.z); f[6] = lo_f(u.w); f[7] = hi_f(u.w);
+  };
+
+  for (int idx = tid; idx < kL * kL; idx += kThreads) {
+    const int i = idx / kL, j = idx % kL;
+    if (j / 16 > i / 16) At[i * (kL + 8) + j] = 0;
+  }
+  // K tile to LDS, Q rows to registers (zero past the sequence end).
+  uint4 qr[NLD];
+#pragma unroll
+  for (int m = 0; m < NLD; ++m) {
+    const int idx = tid + kThreads * m, row = idx / KS8, c8 = idx % KS8;
+    uint4 kv = make_uint4(0u, 0u, 0u, 0u);
+    qr[m] = kv;
+    if (tok0 + row < p.S) {
+      const size_t off = row_of(row) * K + 8 * c8;
+      kv = *reinterpret_cast<const uint4*>(p.k + off);
+      qr[m] = *reinterpret_cast<const uint4*>(p.q + off);
+    }
+    *reinterpret_cast<uint4*>(&Ks[row * KP + 8 * c8]) = kv;
+  }
+  // G = in-chunk cumulative sum of g per channel: KPART lanes per channel,
+  // each summing a run of tokens, then the runs' totals are carried over.
+  {
+    constexpr int KPART = kThreads / K, RUN = kL / KPART;
+    const int d = tid % K, part = tid / K;
+    float vals[RUN];
+#pragma unroll
+    for (int t = 0; t < RUN; ++t) {
+      const int tt = part * RUN + t;
+      vals[t] = tok0 + tt < p.S ? p.g[row_of(tt) * K + d] : 0.f;
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int t = 0; t < RUN; ++t) {
+      acc += vals[t];
+      vals[t] = acc;
+    }
+    if (KPART > 1) Gc[(part * RUN + RUN - 1) * GP + d] = acc;
+    __syncthreads();
+    float carry = 0.f;
+    for (int pp = 0; pp < part; ++pp) carry += Gc[(pp * RUN + RUN - 1) * GP + d];
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < RUN; ++t) Gc[(part * RUN + t) * GP + d] = vals[t] + carry;
+  }
+  __syncthreads();
+
+  // Row factors e^{min(G[i]−G[r], 48)} into the A-operand tiles, and the
+  // scan's kg / qg (e^G ≤ 1: G ≤ 0).
+#pragma unroll
+  for (int m = 0; m < NLD; ++m) {
+    const int idx = tid + kThreads * m, i = idx / KS8, d0 = 8 * (idx % KS8);
+    const int r = 16 * (i / 16) + 8;
+    const bool ok = tok0 + i < p.S;
+    float gi[8], gr[8], kf[8], qf[8], ef[8];
+    *reinterpret_cast<float4*>(gi) = *reinterpret_cast<const float4*>(&Gc[i * GP + d0]);
+    *reinterpret_cast<float4*>(gi + 4) = *reinterpret_cast<const float4*>(&Gc[i * GP + d0 + 4]);
+    *reinterpret_cast<float4*>(gr) = *reinterpret_cast<const float4*>(&Gc[r * GP + d0]);
+    *reinterpret_cast<float4*>(gr + 4) = *reinterpret_cast<const float4*>(&Gc[r * GP + d0 + 4]);
+    f8(*reinterpret_cast<const uint4*>(&Ks[i * KP + d0]), kf);
+    f8(qr[m], qf);
+    if (p.ew == 1) {
+      const float e = ok ? p.erase[row_of(i)] : 0.f;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) ef[x] = e;
+    } else if (ok) {
+      *reinterpret_cast<float4*>(ef) =
+          *reinterpret_cast<const float4*>(p.erase + row_of(i) * K + d0);
+      *reinterpret_cast<float4*>(ef + 4) =
+          *reinterpret_cast<const float4*>(p.erase + row_of(i) * K + d0 + 4);
+    } else {
+#pragma unroll
+      for (int x = 0; x < 8; ++x) ef[x] = 0.f;
+    }
+    float ak[8], aq[8], kg[8], qg[8];
+#pragma unroll
+    for (int x = 0; x < 8; ++x) {
+      const float rf = __expf(fminf(gi[x] - gr[x], kMaxExp));
+      const float eg = __expf(gi[x]);
+      const float ke = kf[x] * ef[x], qs = qf[x] * p.scale;
+      ak[x] = ke * rf;
+      aq[x] = qs * rf;
+      kg[x] = ke * eg;
+      qg[x] = qs * eg;
+    }
+    uint32_t ah[4], al[4], qh[4], gh[4], gl[4], qq[4];
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+      ah[x] = pk_bf16(ak[2 * x], ak[2 * x + 1]);
+      al[x] = pk_bf16(ak[2 * x] - lo_f(ah[x]), ak[2 * x + 1] - hi_f(ah[x]));
+      qh[x] = pk_bf16(aq[2 * x], aq[2 * x + 1]);
+      gh[x] = pk_bf16(kg[2 * x], kg[2 * x + 1]);
+      gl[x] = pk_bf16(kg[2 * x] - lo_f(gh[x]), kg[2 * x + 1] - hi_f(gh[x]));
+      qq[x] = pk_bf16(qg[2 * x], qg[2 * x + 1]);
+    }
+    *reinterpret_cast<uint4*>(&AKh[i * KP + d0]) = make_uint4(ah[0], ah[1], ah[2], ah[3]);
+    *reinterpret_cast<uint4*>(&AKl[i * KP + d0]) = make_uint4(al[0], al[1], al[2], al[3]);
+    *reinterpret_cast<uint4*>(&AQ[i * KP + d0]) = make_uint4(qh[0], qh[1], qh[2], qh[3]);
+    const size_t go = (size_t(cid) * kL + i) * K + d0;
+    *reinterpret_cast<uint4*>(p.Kg + go) = make_uint4(gh[0], gh[1], gh[2], gh[3]);
+    *reinterpret_cast<uint4*>(p.Kglo + go) = make_uint4(gl[0], gl[1], gl[2], gl[3]);
+    *reinterpret_cast<uint4*>(p.Qg + go) = make_uint4(qq[0], qq[1], qq[2], qq[3]);
+  }
+  __syncthreads();
+
+  // Scores: the ten lower 16×16 block pairs (rb ≥ cb), dealt 3/3/2/2.
+  {
+    const int r16 = lane & 15, q4 = lane >> 4, k8 = 8 * q4;
+#pragma unroll
+    for (int pi = wave; pi < 10; pi += 4) {
+      const int rb = pi < 1 ? 0 : pi < 3 ? 1 : pi < 6 ? 2 : 3;
+      const int cb = pi - rb * (rb + 1) / 2;
+      const int r = 16 * rb + 8, j = 16 * cb + r16, ia = 16 * rb + r16;
+      f32x4 acck = {0.f, 0.f, 0.f, 0.f}, accq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < K / 32; ++kk) {
+        const int d0 = 32 * kk + k8;
+        float kf[8], gj[8], gr[8];
+        f8(*reinterpret_cast<const uint4*>(&Ks[j * KP + d0]), kf);
+        *reinterpret_cast<float4*>(gj) = *reinterpret_cast<const float4*>(&Gc[j * GP + d0]);
+        *reinterpret_cast<float4*>(gj + 4) = *reinterpret_cast<const float4*>(&Gc[j * GP + d0 + 4]);
+        *reinterpret_cast<float4*>(gr) = *reinterpret_cast<const float4*>(&Gc[r * GP + d0]);
+        *reinterpret_cast<float4*>(gr + 4) = *reinterpret_cast<const float4*>(&Gc[r * GP + d0 + 4]);
+        float c[8];
+#pragma unroll
+        for (int x = 0; x < 8; ++x) c[x] = kf[x] * __expf(fminf(gr[x] - gj[x], kMaxExp));
+        uint4 bh, bl;
+        bh.x = pk_bf16(c[0], c[1]);
+        bh.y = pk_bf16(c[2], c[3]);
+        bh.z = pk_bf16(c[4], c[5]);
+        bh.w = pk_bf16(c[6], c[7]);
+        bl.x = pk_bf16(c[0] - lo_f(bh.x), c[1] - hi_f(bh.x));
+        bl.y = pk_bf16(c[2] - lo_f(bh.y), c[3] - hi_f(bh.y));
+        bl.z = pk_bf16(c[4] - lo_f(bh.z), c[5] - hi_f(bh.z));
+        bl.w = pk_bf16(c[6] - lo_f(bh.w), c[7] - hi_f(bh.w));
+        const bf16x8 b_h = __builtin_bit_cast(bf16x8, bh), b_l = __builtin_bit_cast(bf16x8, bl);
+        const bf16x8 a_h = ld8(&AKh[ia * KP + d0]);
+        acck = mfma16(a_h, b_h, acck);
+        acck = mfma16(ld8(&AKl[ia * KP + d0]), b_h, acck);
+        acck = mfma16(a_h, b_l, acck);
+        accq = mfma16(ld8(&AQ[ia * KP + d0]), b_h, accq);
+      }
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int i = 16 * rb + 4 * q4 + rr;
+        A[i][j] = (j < i) ? acck[rr] : 0.f;
+        At[i * (kL + 8) + j] = uint16_t(pk_bf16((j <= i) ? accq[rr] : 0.f, 0.f));
+      }
+    }
+  }
+  __syncthreads();
+
+  diag_inverse(A, Tm, wave, lane);
+  {
+    // Kcᵀ = (e^{G_last−G}⊙K)ᵀ, two channels per item; e^{G_last}.
+    for (int it = tid; it < K * 2; it += kThreads) {
+      const int d = 2 * (it % (K / 2)), t0 = 16 * (it / (K / 2));
+      const float gl0 = Gc[(kL - 1) * GP + d], gl1 = Gc[(kL - 1) * GP + d + 1];
+      uint32_t w0[8], w1[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int t = t0 + 2 * e;
+        const uint32_t a = *reinterpret_cast<const uint32_t*>(&Ks[t * KP + d]);
+        const uint32_t c = *reinterpret_cast<const uint32_t*>(&Ks[(t + 1) * KP + d]);
+        const float2 ga = *reinterpret_cast<const float2*>(&Gc[t * GP + d]);
+        const float2 gb = *reinterpret_cast<const float2*>(&Gc[(t + 1) * GP + d]);
+        w0[e] = pk_bf16(lo_f(a) * __expf(gl0 - ga.x), lo_f(c) * __expf(gl0 - gb.x));
+        w1[e] = pk_bf16(hi_f(a) * __expf(gl1 - ga.y), hi_f(c) * __expf(gl1 - gb.y));
+      }
+      uint4* dst0 = reinterpret_cast<uint4*>(p.KcT + (size_t(cid) * K + d) * kL + t0);
+      uint4* dst1 = reinterpret_cast<uint4*>(p.KcT + (size_t(cid) * K + d + 1) * kL + t0);
+      dst0[0] = make_uint4(w0[0], w0[1], w0[2], w0[3]);
+      dst0[1] = make_uint4(w0[4], w0[5], w0[6], w0[7]);
+      dst1[0] = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+      dst1[1] = make_uint4(w1[4], w1[5], w1[6], w1[7]);
+    }
+    for (int d = tid; d < K; d += kThreads) p.egl[size_t(cid) * K + d] = __expf(Gc[(kL - 1) * GP + d]);
+    for (int idx = tid; idx < kL * kL; idx += kThreads) {
+      const int i = idx / kL, j = idx % kL;
+      if (j / 16 > i / 16) Tm[i][j] = 0.f;
+    }
+  }
+  __syncthreads();
+  merge_T(A, Tm, Xs, wave, lane);
+  {
+    const int row = tid / 4, c0 = 16 * (tid % 4);
+    const size_t off = size_t(cid) * kL * kL + row * kL + c0;
+    uint32_t tv[8], tl[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const float x0 = Tm[row][c0 + 2 * c], x1 = Tm[row][c0 + 2 * c + 1];
+      tv[c] = pk_bf16(x0, x1);
+      tl[c] = pk_bf16(x0 - lo_f(tv[c]), x1 - hi_f(tv[c]));
+    }
+    uint4* tdst = reinterpret_cast<uint4*>(p.T + off);
+    uint4* ldst = reinterpret_cast<uint4*>(p.Tlo + off);
+    uint4* adst = reinterpret_cast<uint4*>(p.attn + off);
+    tdst[0] = make_uint4(tv[0], tv[1], tv[2], tv[3]);
+    tdst[1] = make_uint4(tv[4], tv[5], tv[6], tv[7]);
+    ldst[0] = make_uint4(tl[0], tl[1], tl[2], tl[3]);
+    ldst[1] = make_uint4(tl[4], tl[5], tl[6], tl[7]);
+    adst[0] = *reinterpret_cast<const uint4*>(&At[row * (kL + 8) + c0]);
+    adst[1] = *reinterpret_cast<const uint4*>(&At[row * (kL + 8) + c0 + 8]);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -406,22 +674,27 @@ __device__ inline uint4 frag_lo(const f32x4& a, const f32x4& b, const uint4& h) 
                     pk_bf16(b[2] - lo_f(h.w), b[3] - hi_f(h.w)));
 }
 
-template <int K, class TY, int WAVES>
+template <int K, class TY, int WAVES, bool PC>
 __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   constexpr int KK = K / 32;      // 32-deep k-steps over the key axis
   constexpr int RBK = K / 16;     // 16-row blocks of the state
   constexpr int NT = 64 * WAVES;
   constexpr int BW = 16 * WAVES;  // value columns per workgroup
-  // One chunk's operand tiles (bf16 elements): K, Q [64][K]; T, Tlo, attn
-  // [64][64]; Kcᵀ [K][64]. Double-buffered: the next chunk is staged while
-  // this one is consumed, so one barrier per chunk suffices.
-  constexpr int oK = 0, oQ = oK + kL * K, oT = oQ + kL * K, oTl = oT + kL * kL,
-                oAt = oTl + kL * kL, oKc = oAt + kL * kL, BUF = oKc + K * kL;
+  // One chunk's operand tiles (bf16 elements): K, Q [64][K] (per-channel
+  // gates: kg hi, qg and kg lo instead); T, Tlo, attn [64][64]; Kcᵀ [K][64].
+  // Double-buffered for per-head gates: the next chunk is staged while this
+  // one is consumed, so one barrier per chunk suffices. The per-channel
+  // tiles do not fit twice in LDS: they are staged between two barriers.
+  constexpr int NKQ = PC ? 3 : 2;  // K-wide tiles
+  constexpr int oK = 0, oQ = oK + kL * K, oKl = oQ + kL * K, oT = NKQ * kL * K,
+                oTl = oT + kL * kL, oAt = oTl + kL * kL, oKc = oAt + kL * kL, BUF = oKc + K * kL;
   constexpr int C16 = BUF / 8;    // 16-byte chunks per chunk's tiles
   static_assert(C16 % NT == 0, "staging assumes whole rounds");
   constexpr int NPF = C16 / NT;   // chunks staged per lane
-  __shared__ __attribute__((aligned(16))) uint16_t tiles[2][BUF];
-  __shared__ float gxe[2][kL], gwr[2][kL], gys[2][kL], gegl[2];
+  constexpr int NBUF = PC ? 1 : 2;
+  __shared__ __attribute__((aligned(16))) uint16_t tiles[NBUF][BUF];
+  __shared__ float gxe[NBUF][kL], gwr[NBUF][kL], gys[NBUF][kL], gegl[NBUF];
+  __shared__ float gch[PC ? K : 1];  // e^{G_last} per key channel (per-channel gates)
 
   const int ntile = p.V / BW;
   const int BH = p.B * p.H;
@@ -457,7 +730,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   // identical and the compiler's in-order vmcnt waits exact.
   const int HK = p.H * K;
   uint4 pf[NPF];
-  float pgc, pgl, per, pwr;
+  float pgc, pgl, per, pwr, pch;
   auto ld16 = [](const uint16_t* base, uint32_t elems) {
     return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + 2u * elems);
   };
@@ -470,28 +743,39 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
       // The tile boundaries are multiples of NT, so the kind of chunk
       // tid + NT·m depends on m only (a constant once the loop is unrolled).
       const int i0 = NT * m;
-      if (i0 < 2 * kL * K / 8) {
-        const int qk = i0 >= kL * K / 8;
-        const int row = tid / (K / 8) + (i0 - qk * (kL * K / 8)) / (K / 8);
-        const uint32_t off = uint32_t(min(row, rl - 1) * HK + 8 * (tid % (K / 8)));
-        pf[m] = ld16((qk ? p.q : p.k) + row0 * K, off);
-      } else if (i0 < (2 * kL * K + 3 * kL * kL) / 8) {
-        const int ii0 = i0 - 2 * kL * K / 8;
+      if (i0 < NKQ * kL * K / 8) {
+        const int which = i0 / (kL * K / 8);
+        if constexpr (PC) {
+          // kg, qg and kg lo: written by the intra kernel per chunk-head
+          // (zero past the sequence end).
+          const uint16_t* base = which == 0 ? p.Kg : which == 1 ? p.Qg : p.Kglo;
+          pf[m] = ld16(base + cid * kL * K + 8 * (i0 - which * (kL * K / 8)), 8u * tid);
+        } else {
+          const int row = tid / (K / 8) + (i0 - which * (kL * K / 8)) / (K / 8);
+          const uint32_t off = uint32_t(min(row, rl - 1) * HK + 8 * (tid % (K / 8)));
+          pf[m] = ld16((which ? p.q : p.k) + row0 * K, off);
+        }
+      } else if (i0 < (NKQ * kL * K + 3 * kL * kL) / 8) {
+        const int ii0 = i0 - NKQ * kL * K / 8;
         const int which = ii0 / (kL * kL / 8);
         const uint16_t* base = which == 0 ? p.T : which == 1 ? p.Tlo : p.attn;
         pf[m] = ld16(base + cid * kL * kL + 8 * (ii0 - which * (kL * kL / 8)), 8u * tid);
       } else {
-        const int e0 = i0 - (2 * kL * K + 3 * kL * kL) / 8;
+        const int e0 = i0 - (NKQ * kL * K + 3 * kL * kL) / 8;
         pf[m] = ld16(p.KcT + cid * K * kL + 8 * e0, 8u * tid);
       }
     }
-    const int lc = min(lane, rl - 1);
-    pgc = p.gc[cid * kL + lane];
-    pgl = p.gc[cid * kL + kL - 1];
-    const float e = p.erase[row0 + size_t(lc) * tokstride];
-    const float w = p.write[row0 + size_t(lc) * tokstride];
-    per = lane < rl ? e : 0.f;
-    pwr = lane < rl ? w : 0.f;
+    if constexpr (PC) {
+      pch = p.egl[cid * K + (tid % K)];
+    } else {
+      const int lc = min(lane, rl - 1);
+      pgc = p.gc[cid * kL + lane];
+      pgl = p.gc[cid * kL + kL - 1];
+      const float e = p.erase[row0 + size_t(lc) * tokstride];
+      const float w = p.write[row0 + size_t(lc) * tokstride];
+      per = lane < rl ? e : 0.f;
+      pwr = lane < rl ? w : 0.f;
+    }
   };
   // Staging addresses are loop invariant: lane tid writes the halves of
   // 16-byte chunk (row r, column group c) of every tile, rows advancing by a
@@ -514,28 +798,30 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
     for (int m = 0; m < NPF; ++m) {
       const int i0 = NT * m;
       int b0, b1;
-      if (i0 < 2 * kL * K / 8) {
-        const int qk = i0 >= kL * K / 8;
-        const int dr = (i0 - qk * (kL * K / 8)) / KC8;  // row advance, a multiple of 8
-        const int base = (qk ? oQ : oK) + dr * K;
+      if (i0 < NKQ * kL * K / 8) {
+        const int which = i0 / (kL * K / 8);
+        const int dr = (i0 - which * (kL * K / 8)) / KC8;  // row advance, a multiple of 8
+        const int base = (which == 0 ? oK : which == 1 ? oQ : oKl) + dr * K;
         const bool flip = K >= 128 && (dr & 8);
         b0 = base + (flip ? aK0x : aK0);
         b1 = base + (flip ? aK1x : aK1);
-      } else if (i0 < (2 * kL * K + 3 * kL * kL) / 8) {
-        const int ii0 = i0 - 2 * kL * K / 8;
+      } else if (i0 < (NKQ * kL * K + 3 * kL * kL) / 8) {
+        const int ii0 = i0 - NKQ * kL * K / 8;
         const int which = ii0 / (kL * kL / 8), dr = (ii0 - which * (kL * kL / 8)) / LC8;
         const int base = (which == 0 ? oT : which == 1 ? oTl : oAt) + dr * kL;
         b0 = base + a60;
         b1 = base + a61;
       } else {
-        const int dr = (i0 - (2 * kL * K + 3 * kL * kL) / 8) / LC8;
+        const int dr = (i0 - (NKQ * kL * K + 3 * kL * kL) / 8) / LC8;
         b0 = oKc + dr * kL + a60;
         b1 = oKc + dr * kL + a61;
       }
       *reinterpret_cast<uint2*>(&tl[b0]) = make_uint2(pf[m].x, pf[m].y);
       *reinterpret_cast<uint2*>(&tl[b1]) = make_uint2(pf[m].z, pf[m].w);
     }
-    if (wave == 0) {
+    if constexpr (PC) {
+      if (tid < K) gch[tid] = pch;
+    } else if (wave == 0) {
       const float eg = __expf(pgc);
       gxe[buf][lane] = per * eg;
       gwr[buf][lane] = pwr;
@@ -563,17 +849,37 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
         vA[tb][r2] = x0 | (x1 << 16);
       }
   };
+  // Per-channel gates: the write gate w[t][jl] for the same 16 tokens (width
+  // V, or one value per token); zero past the sequence end.
+  float wA[4][4];
+  auto load_w = [&](int n) {
+    if constexpr (PC) {
+      const int rl = min(kL, p.S - n * kL);
+      const float* wb = p.write + (bh_row0 + size_t(n) * kL * tokstride) * p.ww +
+                        (p.ww == 1 ? 0 : jl);
+      const int hw = p.H * p.ww;
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int t = 16 * tb + 4 * q4 + r;
+          const float w = wb[size_t(min(t, rl - 1)) * hw];
+          wA[tb][r] = t < rl ? w : 0.f;
+        }
+    }
+  };
   auto as8 = [](const uint4& x) { return __builtin_bit_cast(bf16x8, x); };
 
   fetch(0);
   load_v(0);
+  load_w(0);
   stage(0);
   __syncthreads();
   for (int n = 0; n < p.N; ++n) {
-    const int cur = n & 1;
+    const int cur = PC ? 0 : (n & 1);
     const int nn = n + 1 < p.N ? n + 1 : n;  // the last chunk prefetches itself again
     const uint16_t* tl = tiles[cur];
-    const float egl = gegl[cur];
+    const float egl = PC ? 1.f : gegl[cur];
 
     // Phase 1: X = w⊙V − (e⊙e^G)⊙(K·S) in [token][column] orientation, and
     // yᵀ = Sᵀ·Qᵀ in [column][token] orientation. The S fragments (hi, lo) of
@@ -586,9 +892,10 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
       yt[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     {
-      bf16x8 kf[2], qf[2];
+      bf16x8 kf[2], qf[2], kl[2];
       kf[0] = ld8(&tl[oK + tile_at<K>(r16, k8)]);
       qf[0] = ld8(&tl[oQ + tile_at<K>(r16, k8)]);
+      if constexpr (PC) kl[0] = ld8(&tl[oKl + tile_at<K>(r16, k8)]);
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
         const uint4 sh = frag_hi(S[2 * kk], S[2 * kk + 1]);
@@ -600,9 +907,12 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
             const int at = tile_at<K>(16 * (nx & 3) + r16, 32 * (nx >> 2) + k8);
             kf[nx & 1] = ld8(&tl[oK + at]);
             qf[nx & 1] = ld8(&tl[oQ + at]);
+            if constexpr (PC) kl[nx & 1] = ld8(&tl[oKl + at]);
           }
           X[tb] = mfma16(kf[step & 1], as8(sh), X[tb]);
           X[tb] = mfma16(kf[step & 1], as8(sl), X[tb]);
+          // kg carries the fp32 gate factors, so it has a lo part too.
+          if constexpr (PC) X[tb] = mfma16(kl[step & 1], as8(sh), X[tb]);
           yt[tb] = mfma16(as8(sh), qf[step & 1], yt[tb]);
         }
       }
@@ -614,13 +924,17 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
       for (int r = 0; r < 4; ++r) {
         const int t = 16 * tb + 4 * q4 + r;
         const float vv = (r & 1) ? hi_f(vA[tb][r >> 1]) : lo_f(vA[tb][r >> 1]);
-        X[tb][r] = gwr[cur][t] * vv - gxe[cur][t] * X[tb][r];
+        // Per-channel gates: e⊙e^G is inside kg, scale·e^G inside qg.
+        X[tb][r] = PC ? wA[tb][r] * vv - X[tb][r] : gwr[cur][t] * vv - gxe[cur][t] * X[tb][r];
       }
-      const float ysc = gys[cur][16 * tb + r16];
+      if constexpr (!PC) {
+        const float ysc = gys[cur][16 * tb + r16];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) yt[tb][r] *= ysc;
+        for (int r = 0; r < 4; ++r) yt[tb][r] *= ysc;
+      }
     }
     load_v(nn);
+    load_w(nn);
 
     // Phase 2: V' = T·X with hi + lo parts of both factors (for a chunk of
     // near-identical keys T differences near-equal rows of X).
@@ -671,7 +985,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
 #pragma unroll
       for (int rb = 0; rb < RBK; ++rb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) S[rb][r] *= egl;
+        for (int r = 0; r < 4; ++r) S[rb][r] *= PC ? gch[16 * rb + 4 * q4 + r] : egl;
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
         if (st + 1 < NS) fr[(st + 1) & 1] = ld8(&tl[addr(st + 1)]);
@@ -701,7 +1015,12 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
               make_float4(yt[tb][0], yt[tb][1], yt[tb][2], yt[tb][3]);
       }
     }
-    stage(cur ^ 1);
+    if constexpr (PC) {
+      __syncthreads();  // every wave is done with this chunk's tiles
+      stage(0);
+    } else {
+      stage(cur ^ 1);
+    }
     __syncthreads();
   }
 
@@ -716,16 +1035,23 @@ size_t region(size_t bytes) { return align_up(bytes, 256); }
 
 }  // namespace
 
+// Per-key-channel decay (GDN-2): the block-decay scores and the kg/qg tiles.
+bool per_channel(const Dims& d) { return d.dw == d.K && d.K > 1; }
+
 bool mfma_fwd_supported(const Dims& d, int qkv_dtype, int y_dtype) {
   (void)y_dtype;
-  return qkv_dtype == DN_BF16 && (d.K == 64 || d.K == 128) && d.V % kBV == 0 && d.L == kL &&
-         d.ew == 1 && d.ww == 1 && d.dw <= 1;
+  if (!(qkv_dtype == DN_BF16 && (d.K == 64 || d.K == 128) && d.V % kBV == 0 && d.L == kL))
+    return false;
+  if (per_channel(d)) return (d.ew == 1 || d.ew == d.K) && (d.ww == 1 || d.ww == d.V);
+  return d.ew == 1 && d.ww == 1 && d.dw <= 1;
 }
 
 size_t mfma_fwd_workspace(const Dims& d) {
   const size_t G = size_t(d.B) * d.N * d.H;
-  return 3 * region(G * kL * kL * 2) + region(G * kL * 4) + region(G * size_t(d.K) * kL * 2) +
-         region(size_t(d.V) * 4);
+  size_t bytes = 3 * region(G * kL * kL * 2) + region(G * kL * 4) +
+                 region(G * size_t(d.K) * kL * 2) + region(size_t(d.V) * 4);
+  if (per_channel(d)) bytes += 3 * region(G * kL * size_t(d.K) * 2) + region(G * size_t(d.K) * 4);
+  return bytes;
 }
 
 hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, const void* v,
@@ -750,6 +1076,9 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
   p.s_in = state_in;
   p.y = y;
   p.s_out = state_out;
+  p.ew = int(d.ew);
+  p.ww = int(d.ww);
+  const bool pc = per_channel(d);
   char* base = static_cast<char*>(ws);
   p.T = reinterpret_cast<uint16_t*>(base);
   base += region(G * kL * kL * 2);
@@ -762,8 +1091,28 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
   p.KcT = reinterpret_cast<uint16_t*>(base);
   base += region(G * size_t(d.K) * kL * 2);
   p.sink = reinterpret_cast<uint16_t*>(base);
+  base += region(size_t(d.V) * 4);
+  p.Kg = p.Kglo = p.Qg = nullptr;
+  p.egl = nullptr;
+  if (pc) {
+    p.Kg = reinterpret_cast<uint16_t*>(base);
+    base += region(G * kL * size_t(d.K) * 2);
+    p.Kglo = reinterpret_cast<uint16_t*>(base);
+    base += region(G * kL * size_t(d.K) * 2);
+    p.Qg = reinterpret_cast<uint16_t*>(base);
+    base += region(G * kL * size_t(d.K) * 2);
+    p.egl = reinterpret_cast<float*>(base);
+  }
 
-  {
+  if (pc) {
+    ProfScope ps("dn_mfma_intra_pc", stream);
+    if (d.K == 128)
+      hipLaunchKernelGGL(mfma_intra_pc_kernel<128>, dim3(unsigned(G)), dim3(kThreads), 0, stream,
+                         p);
+    else
+      hipLaunchKernelGGL(mfma_intra_pc_kernel<64>, dim3(unsigned(G)), dim3(kThreads), 0, stream,
+                         p);
+  } else {
     // Two resident workgroups per CU (LDS-bound) walk all chunk-heads.
     const int grid = int(std::min<size_t>(G, size_t(2) * device_cu_count()));
     ProfScope ps("dn_mfma_intra", stream);
@@ -789,9 +1138,16 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
   if (d.V % 128 == 0 && size_t(groups) * 8 * (d.V / 128) >= size_t(cus)) waves = 8;
   else if (d.V % 64 == 0 && size_t(groups) * 8 * (d.V / 64) >= size_t(cus) / 2) waves = 4;
   const unsigned blocks = unsigned(groups * 8 * (d.V / (16 * waves)));
-  ProfScope ps("dn_mfma_scan", stream);
-#define DN_SCAN(KD, TY, W)                                                                   \
-  hipLaunchKernelGGL((mfma_scan_kernel<KD, TY, W>), dim3(blocks), dim3(64 * W), 0, stream, p)
+  ProfScope ps(pc ? "dn_mfma_scan_pc" : "dn_mfma_scan", stream);
+#define DN_SCAN(KD, TY, W)                                                                      \
+  do {                                                                                          \
+    if (pc)                                                                                     \
+      hipLaunchKernelGGL((mfma_scan_kernel<KD, TY, W, true>), dim3(blocks), dim3(64 * W), 0,    \
+                         stream, p);                                                            \
+    else                                                                                        \
+      hipLaunchKernelGGL((mfma_scan_kernel<KD, TY, W, false>), dim3(blocks), dim3(64 * W), 0,   \
+                         stream, p);                                                            \
+  } while (0)
 #define DN_SCAN_W(KD, TY) \
   do { if (waves == 8) DN_SCAN(KD, TY, 8); else if (waves == 4) DN_SCAN(KD, TY, 4); else DN_SCAN(KD, TY, 2); } while (0)
   if (d.K == 128) {
