@@ -122,9 +122,46 @@ BwdLayout make_bwd_layout(const Dims& d) {
 
 // C (M×N) = alpha·op(A)·op(B) + beta·C over the workgroup. `tri`: 0 keeps
 // every entry, 1 keeps j ≤ i, 2 keeps j < i (the rest is written as 0).
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
 __device__ void wg_mm(float* C, int ldc, const float* A, int lda, bool tA, const float* B,
                       int ldb, bool tB, int M, int N, int Kd, float alpha, float beta,
                       int tri = 0) {
+  if (M % 16 == 0 && N % 16 == 0 && Kd % 4 == 0 && blockDim.x % 64 == 0) {
+    // On fp32 MFMA (v_mfma_f32_16x16x4_f32: fp32 products, fp32 accumulation):
+    // one 16×16 output tile per wave at a time; lane l feeds A[l%16][l/16]
+    // and B[l/16][l%16] of each 16×4·4×16 step and ends with
+    // D[4(l/16)+r][l%16]. A given (M, N) always maps an element to the same
+    // lane, so successive accumulations into C need no barrier between them.
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int m16 = lane & 15, g4 = lane >> 4;
+    const int tn = N / 16, tiles = (M / 16) * tn;
+    for (int t = wave; t < tiles; t += nw) {
+      const int i0 = (t / tn) * 16, j0 = (t % tn) * 16;
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      const bool skip = (tri == 1 && j0 > i0 + 15) || (tri == 2 && j0 >= i0 + 15);
+      if (!skip) {
+        for (int k0 = 0; k0 < Kd; k0 += 4) {
+          const int kk = k0 + g4;
+          const float a = tA ? A[size_t(kk) * lda + i0 + m16] : A[size_t(i0 + m16) * lda + kk];
+          const float b = tB ? B[size_t(j0 + m16) * ldb + kk] : B[size_t(kk) * ldb + j0 + m16];
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = i0 + 4 * g4 + r, j = j0 + m16;
+        float* c = &C[size_t(i) * ldc + j];
+        if ((tri == 1 && j > i) || (tri == 2 && j >= i)) {
+          *c = 0.f;
+        } else {
+          const float prev = beta != 0.f ? beta * *c : 0.f;
+          *c = alpha * acc[r] + prev;
+        }
+      }
+    }
+    return;
+  }
   for (int idx = threadIdx.x; idx < M * N; idx += blockDim.x) {
     const int i = idx / N, j = idx - i * N;
     if ((tri == 1 && j > i) || (tri == 2 && j >= i)) {
@@ -473,14 +510,14 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_kernel(ChunkBwdParams p) {
         *deg = bw + bo.deg, *dcarry = bw + bo.dcarry, *dgl = bw + bo.dgl, *dref = bw + bo.dref;
   const TG* dy = static_cast<const TG*>(p.dy);
 
-  // V' rebuilt, dy chunk loaded.
+  // V' = U − W·S₀ rebuilt, dy chunk loaded.
   for (int idx = threadIdx.x; idx < L * V; idx += blockDim.x) {
     const int i = idx / V, c = idx - i * V, tok = n * L + i;
     dyc[idx] = tok < d.S ? ld(dy, ((size_t(b) * d.S + tok) * d.H + h) * V + c) : 0.f;
-    float acc = U[idx];
-    for (int r = 0; r < K; ++r) acc -= W[size_t(i) * K + r] * S0[size_t(r) * V + c];
-    vnew[idx] = acc;
+    vnew[idx] = U[idx];
   }
+  __syncthreads();
+  wg_mm(vnew, V, W, K, false, S0, V, false, L, V, K, -1.f, 1.f);
   __syncthreads();
   // Scan cotangents of this chunk (combined_backward.rs:272-282).
   wg_mm(dattn, L, dyc, V, false, vnew, V, true, L, L, V, 1.f, 0.f);     // dy V'ᵀ
