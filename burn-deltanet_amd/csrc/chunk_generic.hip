@@ -336,8 +336,9 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanParams p) {
   const int bt = min(p.tile, d.V - j0);
   const int L = d.L, K = d.K, V = d.V;
   extern __shared__ float lds[];
-  float* S = lds;             // [K][tile]
+  float* S = lds;              // [K][tile]
   float* vn = S + K * p.tile;  // [L][tile]
+  float* yb = vn + L * p.tile;  // [L][tile] (when y is written)
   const size_t bh = size_t(b) * d.H + h;
 
   for (int idx = threadIdx.x; idx < K * bt; idx += blockDim.x) {
@@ -358,30 +359,31 @@ __global__ __launch_bounds__(kThreads) void scan_kernel(ScanParams p) {
     // V' = U − W S₀ (forward.rs:395)
     for (int idx = threadIdx.x; idx < L * bt; idx += blockDim.x) {
       const int i = idx / bt, c = idx - i * bt;
-      float acc = U[size_t(i) * V + j0 + c];
-      for (int r = 0; r < K; ++r) acc -= W[size_t(i) * K + r] * S[r * p.tile + c];
-      vn[i * p.tile + c] = acc;
+      vn[i * p.tile + c] = U[size_t(i) * V + j0 + c];
     }
+    __syncthreads();
+    wg_mm(vn, p.tile, W, K, false, S, p.tile, false, L, bt, K, -1.f, 1.f);
     __syncthreads();
     if (p.y) {
-      // y = (Q ⊙ e^G) S₀ + attn V' (forward.rs:397-408)
+      // y = (Q ⊙ e^G) S₀ + attn V' (forward.rs:397-408); attn is zero above
+      // its diagonal.
+      wg_mm(yb, p.tile, qr, K, false, S, p.tile, false, L, bt, K, 1.f, 0.f);
+      wg_mm(yb, p.tile, attn, L, false, vn, p.tile, false, L, bt, L, 1.f, 1.f);
+      __syncthreads();
       for (int idx = threadIdx.x; idx < L * bt; idx += blockDim.x) {
         const int i = idx / bt, c = idx - i * bt, tok = n * L + i;
-        if (tok >= d.S) continue;
-        float acc = 0.f;
-        for (int r = 0; r < K; ++r) acc += qr[size_t(i) * K + r] * S[r * p.tile + c];
-        for (int s = 0; s <= i; ++s) acc += attn[size_t(i) * L + s] * vn[s * p.tile + c];
-        st(static_cast<TY*>(p.y), ((size_t(b) * d.S + tok) * d.H + h) * V + j0 + c, acc);
+        if (tok < d.S)
+          st(static_cast<TY*>(p.y), ((size_t(b) * d.S + tok) * d.H + h) * V + j0 + c,
+             yb[i * p.tile + c]);
       }
     }
-    __syncthreads();
     // S ← S ⊙ e^{G_last} + (K ⊙ e^{G_last − G})ᵀ V' (forward.rs:412-424)
     for (int idx = threadIdx.x; idx < K * bt; idx += blockDim.x) {
       const int r = idx / bt, c = idx - r * bt;
-      float acc = S[r * p.tile + c] * egl[r];
-      for (int i = 0; i < L; ++i) acc += kc[size_t(i) * K + r] * vn[i * p.tile + c];
-      S[r * p.tile + c] = acc;
+      S[r * p.tile + c] *= egl[r];
     }
+    __syncthreads();
+    wg_mm(S, p.tile, kc, K, true, vn, p.tile, false, K, bt, L, 1.f, 1.f);
     __syncthreads();
   }
   for (int idx = threadIdx.x; idx < K * bt; idx += blockDim.x) {
@@ -442,22 +444,17 @@ __global__ __launch_bounds__(kThreads) void rev_scan_kernel(RevScanParams p) {
     }
     __syncthreads();
     // dV' = attnᵀ dy + kc dS
-    for (int idx = threadIdx.x; idx < L * bt; idx += blockDim.x) {
-      const int i = idx / bt, c = idx - i * bt;
-      float acc = 0.f;
-      for (int s = i; s < L; ++s) acc += attn[size_t(s) * L + i] * dyt[s * p.tile + c];
-      for (int r = 0; r < K; ++r) acc += kc[size_t(i) * K + r] * dS[r * p.tile + c];
-      dvn[i * p.tile + c] = acc;
-    }
+    wg_mm(dvn, p.tile, attn, L, true, dyt, p.tile, false, L, bt, L, 1.f, 0.f);
+    wg_mm(dvn, p.tile, kc, K, false, dS, p.tile, false, L, bt, K, 1.f, 1.f);
     __syncthreads();
     // dS₀ = e^{G_last} ⊙ dS + qrᵀ dy − Wᵀ dV'
     for (int idx = threadIdx.x; idx < K * bt; idx += blockDim.x) {
       const int r = idx / bt, c = idx - r * bt;
-      float acc = dS[r * p.tile + c] * egl[r];
-      for (int i = 0; i < L; ++i)
-        acc += qr[size_t(i) * K + r] * dyt[i * p.tile + c] - W[size_t(i) * K + r] * dvn[i * p.tile + c];
-      dS[r * p.tile + c] = acc;
+      dS[r * p.tile + c] *= egl[r];
     }
+    __syncthreads();
+    wg_mm(dS, p.tile, qr, K, true, dyt, p.tile, false, K, bt, L, 1.f, 1.f);
+    wg_mm(dS, p.tile, W, K, true, dvn, p.tile, false, K, bt, L, -1.f, 1.f);
     __syncthreads();
   }
   for (int idx = threadIdx.x; idx < K * bt; idx += blockDim.x) {
@@ -843,7 +840,7 @@ hipError_t generic_fwd(const Dims& d, int qkv_dtype, int y_dtype, const void* q,
   const int tile = scan_tile(d);
   ScanParams sp{d, make_layout(d), tile, ws, state_in, y, state_out, nullptr};
   dim3 grid((d.V + tile - 1) / tile, d.H, d.B);
-  const size_t lds = scan_lds(d, tile, 1);
+  const size_t lds = scan_lds(d, tile, 2);  // S, V' and the y rows
   ProfScope ps("dn_generic_scan", stream);
   if (y_dtype == DN_BF16)
     hipLaunchKernelGGL(scan_kernel<bf16>, grid, dim3(kThreads), lds, stream, sp);
