@@ -29,6 +29,7 @@ constexpr float kMaxExponent = 48.0f;  // src/delta/decay.rs:49
 // Per-chunk-head workspace layout (float offsets).
 struct Layout {
   size_t qs, kk, vv, ee, wg, gc, eg, ec, egl, ke, kg, vw, qr, kc, akk, aqk, t, w, u;
+  size_t rowk, rowq, colb;  // per-channel decay: row-factor tables, one column table
   size_t per;  // floats per chunk-head
 };
 
@@ -60,6 +61,9 @@ Layout make_layout(const Dims& d) {
   o.t = take(L * L);
   o.w = take(L * K);
   o.u = take(L * V);
+  o.rowk = take(d.dw > 1 ? L * K : 0);
+  o.rowq = take(d.dw > 1 ? L * K : 0);
+  o.colb = take(d.dw > 1 ? L * K : 0);
   o.per = at;
   return o;
 }
@@ -67,7 +71,7 @@ Layout make_layout(const Dims& d) {
 // Backward scratch per chunk-head.
 struct BwdLayout {
   size_t vnew, dy, dvnew, dvw, dattn, dt, tmp, dakk, daqk, drkk, drqk, dkc, dqr, dw, dkg, dke,
-      dq, dk, drke, drq, drow, drarg, dcol, degl, dgc, deg, dcarry, dgl, dref;
+      dq, dk, drke, drq, drow, drarg, dcol, degl, dgc, deg, dcarry, dgl, dref, colb;
   size_t per;
 };
 
@@ -116,6 +120,7 @@ BwdLayout make_bwd_layout(const Dims& d) {
   o.dcarry = take(L * dwx);
   o.dgl = take(dwx);
   o.dref = take(d.dw > 1 ? nb * K : 0);
+  o.colb = take(d.dw > 1 ? L * K : 0);
   o.per = at;
   return o;
 }
@@ -265,23 +270,47 @@ __global__ __launch_bounds__(kThreads) void intra_kernel(IntraParams p) {
 
   // Scores, lower triangle incl. the diagonal (forward.rs:271-318; decay.rs).
   const int mb = decay_block_len(L);
-  for (int idx = threadIdx.x; idx < L * L; idx += blockDim.x) {
-    const int i = idx / L, j = idx - i * L;
-    float skk = 0.f, sqk = 0.f;
-    if (j <= i) {
-      if (d.dw > 1) {
-        // Per-channel decay through the block reference point of row i's
-        // block (BlockDecayPrim, forward.rs:468-556), with its clamp.
-        const int ref = (i / mb) * mb + mb / 2;
-        for (int c = 0; c < K; ++c) {
-          const float gref = gc[size_t(ref) * dwx + c];
-          const float row = expf(fminf(gc[size_t(i) * dwx + c] - gref, kMaxExponent));
-          const float col = kk[size_t(j) * K + c] *
-                            expf(fminf(gref - gc[size_t(j) * dwx + c], kMaxExponent));
-          skk += ke[size_t(i) * K + c] * row * col;
-          sqk += qs[size_t(i) * K + c] * row * col;
-        }
-      } else {
+  if (d.dw > 1) {
+    // Per-channel decay through the block reference point of row i's block
+    // (BlockDecayPrim, forward.rs:468-556), with its clamp: the row factors
+    // e^{min(G[i]−G[ref], 48)} fold into ke and q·scale once; for each row
+    // block the column factors k[j]·e^{min(G[ref]−G[j], 48)} (zero for later
+    // column blocks, the −∞ band) are tabulated and the block's rows of Akk
+    // and Aqk are two products.
+    float *rowk = ws + o.rowk, *rowq = ws + o.rowq, *colb = ws + o.colb;
+    for (int idx = threadIdx.x; idx < L * K; idx += blockDim.x) {
+      const int i = idx / K, c = idx - i * K, ref = (i / mb) * mb + mb / 2;
+      const float rf =
+          expf(fminf(gc[size_t(i) * dwx + c] - gc[size_t(ref) * dwx + c], kMaxExponent));
+      rowk[idx] = ke[idx] * rf;
+      rowq[idx] = qs[idx] * rf;
+    }
+    for (int pb = 0; pb < L / mb; ++pb) {
+      const int ref = pb * mb + mb / 2;
+      __syncthreads();  // the previous block's products are done with colb
+      for (int idx = threadIdx.x; idx < L * K; idx += blockDim.x) {
+        const int j = idx / K, c = idx - j * K;
+        colb[idx] = j / mb > pb ? 0.f
+                                : kk[idx] * expf(fminf(gc[size_t(ref) * dwx + c] -
+                                                           gc[size_t(j) * dwx + c],
+                                                       kMaxExponent));
+      }
+      __syncthreads();
+      wg_mm(akk + size_t(pb) * mb * L, L, rowk + size_t(pb) * mb * K, K, false, colb, K, true,
+            mb, L, K, 1.f, 0.f);
+      wg_mm(aqk + size_t(pb) * mb * L, L, rowq + size_t(pb) * mb * K, K, false, colb, K, true,
+            mb, L, K, 1.f, 0.f);
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < L * L; idx += blockDim.x) {
+      const int i = idx / L, j = idx - i * L;
+      if (j > i) akk[idx] = aqk[idx] = 0.f;
+    }
+  } else {
+    for (int idx = threadIdx.x; idx < L * L; idx += blockDim.x) {
+      const int i = idx / L, j = idx - i * L;
+      float skk = 0.f, sqk = 0.f;
+      if (j <= i) {
         for (int c = 0; c < K; ++c) {
           skk += ke[size_t(i) * K + c] * kk[size_t(j) * K + c];
           sqk += qs[size_t(i) * K + c] * kk[size_t(j) * K + c];
@@ -292,9 +321,9 @@ __global__ __launch_bounds__(kThreads) void intra_kernel(IntraParams p) {
           sqk *= m;
         }
       }
+      akk[idx] = skk;
+      aqk[idx] = sqk;  // = attn, tril(Aqk, 0) (forward.rs:255)
     }
-    akk[idx] = skk;
-    aqk[idx] = sqk;  // = attn, tril(Aqk, 0) (forward.rs:255)
   }
   __syncthreads();
 
@@ -655,26 +684,26 @@ __global__ __launch_bounds__(kThreads) void chunk_bwd_kernel(ChunkBwdParams p) {
       const int ref = pb * mb + mb / 2;
       return expf(fminf(gc[size_t(ref) * dwx + c] - gc[size_t(j) * dwx + c], kMaxExponent));
     };
-    for (int idx = threadIdx.x; idx < L * K; idx += blockDim.x) {
-      const int i = idx / K, c = idx - i * K, pb = i / mb;
-      float a = 0.f, bq = 0.f;
-      for (int j = 0; j < L; ++j) {
-        const float col = kk[size_t(j) * K + c] * colexp(pb, j, c);
-        a += dakk[size_t(i) * L + j] * col;
-        bq += daqk[size_t(i) * L + j] * col;
+    // Per row block pb, with the column-factor table of pb:
+    //   d(ke⊙rf), d(q⊙rf) rows of pb = dAkk, dAqk rows of pb · colb_pb
+    //   dcol[pb] = dAkkᵀ·(ke⊙rf) + dAqkᵀ·(q⊙rf) over the rows of pb.
+    const float *rowk = ws + o.rowk, *rowq = ws + o.rowq;  // written by the intra kernel
+    float* colb = bw + bo.colb;
+    for (int pb = 0; pb < nb; ++pb) {
+      __syncthreads();  // the previous block's products are done with colb
+      for (int idx = threadIdx.x; idx < L * K; idx += blockDim.x) {
+        const int j = idx / K, c = idx - j * K;
+        colb[idx] = kk[idx] * colexp(pb, j, c);
       }
-      drke[idx] = a;
-      drq[idx] = bq;
-    }
-    for (int idx = threadIdx.x; idx < nb * L * K; idx += blockDim.x) {
-      const int pb = idx / (L * K), rem = idx - pb * L * K, j = rem / K, c = rem - j * K;
-      float acc = 0.f;
-      for (int i = pb * mb; i < (pb + 1) * mb; ++i) {
-        const float rf = rowf(i, c);
-        acc += dakk[size_t(i) * L + j] * ke[size_t(i) * K + c] * rf +
-               daqk[size_t(i) * L + j] * qs[size_t(i) * K + c] * rf;
-      }
-      dcol[idx] = acc;
+      __syncthreads();
+      wg_mm(drke + size_t(pb) * mb * K, K, dakk + size_t(pb) * mb * L, L, false, colb, K, false,
+            mb, K, L, 1.f, 0.f);
+      wg_mm(drq + size_t(pb) * mb * K, K, daqk + size_t(pb) * mb * L, L, false, colb, K, false,
+            mb, K, L, 1.f, 0.f);
+      wg_mm(dcol + size_t(pb) * L * K, K, dakk + size_t(pb) * mb * L, L, true,
+            rowk + size_t(pb) * mb * K, K, false, L, K, mb, 1.f, 0.f);
+      wg_mm(dcol + size_t(pb) * L * K, K, daqk + size_t(pb) * mb * L, L, true,
+            rowq + size_t(pb) * mb * K, K, false, L, K, mb, 1.f, 1.f);
     }
     __syncthreads();
     for (int idx = threadIdx.x; idx < L * K; idx += blockDim.x) {
