@@ -145,13 +145,27 @@ __device__ void wg_mm(float* C, int ldc, const float* A, int lda, bool tA, const
       const int i0 = (t / tn) * 16, j0 = (t % tn) * 16;
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
       const bool skip = (tri == 1 && j0 > i0 + 15) || (tri == 2 && j0 >= i0 + 15);
-      if (!skip) {
-        for (int k0 = 0; k0 < Kd; k0 += 4) {
-          const int kk = k0 + g4;
-          const float a = tA ? A[size_t(kk) * lda + i0 + m16] : A[size_t(i0 + m16) * lda + kk];
-          const float b = tB ? B[size_t(j0 + m16) * ldb + kk] : B[size_t(kk) * ldb + j0 + m16];
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+      auto opa = [&](int kk) {
+        return tA ? A[size_t(kk) * lda + i0 + m16] : A[size_t(i0 + m16) * lda + kk];
+      };
+      auto opb = [&](int kk) {
+        return tB ? B[size_t(j0 + m16) * ldb + kk] : B[size_t(kk) * ldb + j0 + m16];
+      };
+      if (!skip && Kd % 16 == 0) {
+        // Four k-steps' operands are read before their four MFMAs.
+        for (int k0 = 0; k0 < Kd; k0 += 16) {
+          float a[4], b[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            a[u] = opa(k0 + 4 * u + g4);
+            b[u] = opb(k0 + 4 * u + g4);
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc, 0, 0, 0);
         }
+      } else if (!skip) {
+        for (int k0 = 0; k0 < Kd; k0 += 4)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(opa(k0 + g4), opb(k0 + g4), acc, 0, 0, 0);
       }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
