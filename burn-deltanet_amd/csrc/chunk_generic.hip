@@ -132,50 +132,62 @@ typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
 __device__ void wg_mm(float* C, int ldc, const float* A, int lda, bool tA, const float* B,
                       int ldb, bool tB, int M, int N, int Kd, float alpha, float beta,
                       int tri = 0) {
-  if (M % 16 == 0 && N % 16 == 0 && Kd % 4 == 0 && blockDim.x % 64 == 0) {
+  if (M % 16 == 0 && N % 16 == 0 && Kd % 16 == 0 && blockDim.x % 64 == 0) {
     // On fp32 MFMA (v_mfma_f32_16x16x4_f32: fp32 products, fp32 accumulation):
-    // one 16×16 output tile per wave at a time; lane l feeds A[l%16][l/16]
-    // and B[l/16][l%16] of each 16×4·4×16 step and ends with
-    // D[4(l/16)+r][l%16]. A given (M, N) always maps an element to the same
-    // lane, so successive accumulations into C need no barrier between them.
+    // 16×16 output tiles dealt to the waves, up to four per wave in flight
+    // together (their operand reads overlap); lane l feeds A[l%16][l/16] and
+    // B[l/16][l%16] of each 16×4·4×16 step and ends with D[4(l/16)+r][l%16].
+    // A given (M, N) always maps an element to the same lane, so successive
+    // accumulations into C need no barrier between them.
+    constexpr int kTiles = 4;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int m16 = lane & 15, g4 = lane >> 4;
     const int tn = N / 16, tiles = (M / 16) * tn;
-    for (int t = wave; t < tiles; t += nw) {
-      const int i0 = (t / tn) * 16, j0 = (t % tn) * 16;
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-      const bool skip = (tri == 1 && j0 > i0 + 15) || (tri == 2 && j0 >= i0 + 15);
-      auto opa = [&](int kk) {
-        return tA ? A[size_t(kk) * lda + i0 + m16] : A[size_t(i0 + m16) * lda + kk];
-      };
-      auto opb = [&](int kk) {
-        return tB ? B[size_t(j0 + m16) * ldb + kk] : B[size_t(kk) * ldb + j0 + m16];
-      };
-      if (!skip && Kd % 16 == 0) {
-        // Four k-steps' operands are read before their four MFMAs.
-        for (int k0 = 0; k0 < Kd; k0 += 16) {
-          float a[4], b[4];
+    for (int t0 = wave; t0 < tiles; t0 += kTiles * nw) {
+      int i0[kTiles], j0[kTiles];
+      bool live[kTiles];
+      f32x4_t acc[kTiles];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            a[u] = opa(k0 + 4 * u + g4);
-            b[u] = opb(k0 + 4 * u + g4);
-          }
+      for (int u = 0; u < kTiles; ++u) {
+        const int t = t0 + u * nw;
+        live[u] = t < tiles;
+        i0[u] = live[u] ? (t / tn) * 16 : 0;
+        j0[u] = live[u] ? (t % tn) * 16 : 0;
+        // Tiles wholly masked by `tri` need no products.
+        if ((tri == 1 && j0[u] > i0[u] + 15) || (tri == 2 && j0[u] >= i0[u] + 15)) live[u] = false;
+        acc[u] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      }
+      for (int k0 = 0; k0 < Kd; k0 += 4) {
+        const int kk = k0 + g4;
+        float a[kTiles], bv[kTiles];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc, 0, 0, 0);
+        for (int u = 0; u < kTiles; ++u) {
+          a[u] = live[u] ? (tA ? A[size_t(kk) * lda + i0[u] + m16]
+                               : A[size_t(i0[u] + m16) * lda + kk])
+                         : 0.f;
+          bv[u] = live[u] ? (tB ? B[size_t(j0[u] + m16) * ldb + kk]
+                                : B[size_t(kk) * ldb + j0[u] + m16])
+                          : 0.f;
         }
-      } else if (!skip) {
-        for (int k0 = 0; k0 < Kd; k0 += 4)
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(opa(k0 + g4), opb(k0 + g4), acc, 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < kTiles; ++u)
+          acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], bv[u], acc[u], 0, 0, 0);
       }
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = i0 + 4 * g4 + r, j = j0 + m16;
-        float* c = &C[size_t(i) * ldc + j];
-        if ((tri == 1 && j > i) || (tri == 2 && j >= i)) {
-          *c = 0.f;
-        } else {
-          const float prev = beta != 0.f ? beta * *c : 0.f;
-          *c = alpha * acc[r] + prev;
+      for (int u = 0; u < kTiles; ++u) {
+        const int t = t0 + u * nw;
+        if (t >= tiles) continue;
+        const int ti = (t / tn) * 16, tj = (t % tn) * 16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = ti + 4 * g4 + r, j = tj + m16;
+          float* c = &C[size_t(i) * ldc + j];
+          if ((tri == 1 && j > i) || (tri == 2 && j >= i)) {
+            *c = 0.f;
+          } else {
+            const float prev = beta != 0.f ? beta * *c : 0.f;
+            *c = alpha * acc[u][r] + prev;
+          }
         }
       }
     }
