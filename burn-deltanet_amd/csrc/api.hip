@@ -187,6 +187,25 @@ int fwd_algo(const dn_chunk_fwd_args* a, const Dims& d) {
   return fits ? DN_ALGO_MFMA : DN_ALGO_GENERIC;
 }
 
+Dims bwd_dims(const dn_chunk_bwd_args* a) {
+  return make_dims(a->batch, a->sequence, a->nheads, a->head_k_dim, a->head_v_dim,
+                   a->erase_width, a->write_width, a->decay_width, a->has_gate, a->chunk_len,
+                   a->scale);
+}
+
+// MFMA: the two scans of the backward on bf16 MFMA (the forward MFMA path's
+// shapes, bf16 q/k/v); the chunk-local gradients stay in fp32.
+int bwd_algo(const dn_chunk_bwd_args* a, const Dims& d) {
+  if (a->algo == DN_ALGO_GENERIC) return DN_ALGO_GENERIC;
+  const bool fits = mfma_fwd_supported(d, a->qkv_dtype, DN_BF16);
+  if (a->algo == DN_ALGO_MFMA) return fits ? DN_ALGO_MFMA : DN_ERR_UNSUPPORTED;
+  return fits ? DN_ALGO_MFMA : DN_ALGO_GENERIC;
+}
+
+size_t bwd_workspace(const Dims& d, int algo) {
+  return align_up(generic_bwd_workspace(d), 256) + (algo == DN_ALGO_MFMA ? mfma_bwd_workspace(d) : 0);
+}
+
 }  // namespace
 }  // namespace dn
 
@@ -264,27 +283,25 @@ int dn_chunk_fwd(const dn_chunk_fwd_args* a, hipStream_t stream) {
 
 int dn_chunk_bwd_algo(const dn_chunk_bwd_args* a) {
   if (int rc = check_bwd(a)) return rc;
-  if (a->algo == DN_ALGO_MFMA) return DN_ERR_UNSUPPORTED;
-  return DN_ALGO_GENERIC;
+  return bwd_algo(a, bwd_dims(a));
 }
 
 size_t dn_chunk_bwd_workspace_bytes(const dn_chunk_bwd_args* a) {
   if (check_bwd(a)) return 0;
-  Dims d = make_dims(a->batch, a->sequence, a->nheads, a->head_k_dim, a->head_v_dim,
-                     a->erase_width, a->write_width, a->decay_width, a->has_gate, a->chunk_len,
-                     a->scale);
-  return generic_bwd_workspace(d);
+  const Dims d = bwd_dims(a);
+  const int algo = bwd_algo(a, d);
+  return algo < 0 ? 0 : bwd_workspace(d, algo);
 }
 
 int dn_chunk_bwd(const dn_chunk_bwd_args* a, hipStream_t stream) {
   g_last_error.clear();
   if (int rc = check_bwd(a)) return rc;
-  if (a->algo == DN_ALGO_MFMA)
-    return fail(DN_ERR_UNSUPPORTED, "the backward has no DN_ALGO_MFMA path yet");
-  Dims d = make_dims(a->batch, a->sequence, a->nheads, a->head_k_dim, a->head_v_dim,
-                     a->erase_width, a->write_width, a->decay_width, a->has_gate, a->chunk_len,
-                     a->scale);
-  const size_t need = generic_bwd_workspace(d);
+  const Dims d = bwd_dims(a);
+  const int algo = bwd_algo(a, d);
+  if (algo < 0)
+    return fail(DN_ERR_UNSUPPORTED, "DN_ALGO_MFMA needs bf16 q/k/v, head_k_dim 64 or 128, "
+                                    "head_v_dim a multiple of 64 and chunk_len 64");
+  const size_t need = bwd_workspace(d, algo);
   void* ws = a->workspace;
   if (ws) {
     if (a->workspace_bytes < need)
@@ -310,7 +327,10 @@ int dn_chunk_bwd(const dn_chunk_bwd_args* a, hipStream_t stream) {
   hipError_t e = generic_bwd(d, a->qkv_dtype, a->grad_dtype, a->d_y, a->d_state_final, a->q,
                              a->k, a->v, a->erase, a->write, a->has_gate ? a->g : nullptr,
                              a->state_in, a->d_q, a->d_k, a->d_v, a->d_erase, a->d_write,
-                             a->has_gate ? a->d_g : nullptr, a->d_state, ws, stream);
+                             a->has_gate ? a->d_g : nullptr, a->d_state, ws, stream,
+                             algo == DN_ALGO_MFMA
+                                 ? static_cast<char*>(ws) + align_up(generic_bwd_workspace(d), 256)
+                                 : nullptr);
   if (e != hipSuccess) return hip_fail(e, "dn_chunk_bwd launch");
   if (a->check_finite) {
     std::vector<Guarded> out = {{a->d_q, nq * d.K, a->grad_dtype},

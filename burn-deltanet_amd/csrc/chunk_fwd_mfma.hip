@@ -106,6 +106,7 @@ struct MfmaParams {
   uint16_t* Kglo;  // [G][64][K] its lo part
   uint16_t* Qg;    // [G][64][K] bf16(scale·e^G⊙Q)
   float* egl;      // [G][K] e^{G_last} per key channel
+  float* states;   // [G][K][V] fp32 state entering each chunk (states mode of the scan)
 };
 
 // ---------------------------------------------------------------------------
@@ -674,7 +675,9 @@ __device__ inline uint4 frag_lo(const f32x4& a, const f32x4& b, const uint4& h) 
                     pk_bf16(b[2] - lo_f(h.w), b[3] - hi_f(h.w)));
 }
 
-template <int K, class TY, int WAVES, bool PC>
+// ST (states mode, for the backward's recompute): the fp32 state entering
+// each chunk is written to p.states and y is not written.
+template <int K, class TY, int WAVES, bool PC, bool ST = false>
 __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   constexpr int KK = K / 32;      // 32-deep k-steps over the key axis
   constexpr int RBK = K / 16;     // 16-row blocks of the state
@@ -880,6 +883,13 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
     const int nn = n + 1 < p.N ? n + 1 : n;  // the last chunk prefetches itself again
     const uint16_t* tl = tiles[cur];
     const float egl = PC ? 1.f : gegl[cur];
+    if constexpr (ST) {
+      float* sdst = p.states + chunk_of(n) * K * p.V + jl;
+#pragma unroll
+      for (int rb = 0; rb < RBK; ++rb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sdst[size_t(16 * rb + 4 * q4 + r) * p.V] = S[rb][r];
+    }
 
     // Phase 1: X = w⊙V − (e⊙e^G)⊙(K·S) in [token][column] orientation, and
     // yᵀ = Sᵀ·Qᵀ in [column][token] orientation. The S fragments (hi, lo) of
@@ -998,7 +1008,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
     }
     // y: lane (r16, q4) holds columns jw + 4q4 … +3 of token 16tb + r16;
     // rows past the sequence end go to the sink row.
-    {
+    if constexpr (!ST) {
       TY* yb = static_cast<TY*>(p.y) + (bh_row0 + size_t(n) * kL * tokstride) * p.V;
       const int rl = p.S - n * kL;
 #pragma unroll
@@ -1031,33 +1041,359 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
     for (int r = 0; r < 4; ++r) sout[size_t(16 * rb + 4 * q4 + r) * p.V] = S[rb][r];
 }
 
-size_t region(size_t bytes) { return align_up(bytes, 256); }
+// ---------------------------------------------------------------------------
+// Backward: the reverse scan's operand tiles
+// ---------------------------------------------------------------------------
+// The reverse scan contracts over a chunk's tokens where the forward
+// contracts over its rows, so it reads the transposes of the forward's
+// tiles: Tᵀ (hi, lo), attnᵀ, Kc = (Kcᵀ)ᵀ, and Qgᵀ = (scale·e^G⊙Q)ᵀ,
+// Kgᵀ = (e⊙e^G⊙K)ᵀ (combined_backward.rs:272-282: the state cotangent picks
+// up qrᵀ·dy and Wᵀ·dV' = kgᵀ·(Tᵀ·dV')). One workgroup per chunk-head; tiles
+// are transposed through LDS.
+struct BwdTiles {
+  uint16_t *Tt, *Ttl, *AtT;  // [G][64][64]
+  uint16_t* Kc;              // [G][64][K]
+  uint16_t *QgT, *KgT;       // [G][K][64]
+  float* egl;                // [G][K] e^{G_last} per key channel
+};
 
-}  // namespace
+template <int K, bool PC>
+__global__ __launch_bounds__(kThreads) void mfma_bwd_tiles_kernel(MfmaParams p, BwdTiles bt) {
+  constexpr int RP = (K > kL ? K : kL) + 2;  // LDS row pitch (elements) of the staged tile
+  __shared__ __attribute__((aligned(16))) uint16_t buf[(K > kL ? K : kL) * RP];
+  __shared__ float rowsc[kL];
+  const int cid = blockIdx.x;
+  const int h = cid % p.H, n = (cid / p.H) % p.N, b = cid / (p.H * p.N);
+  const int tid = threadIdx.x;
+  const int tok0 = n * kL;
+  const size_t row0 = size_t(b) * p.S * p.H + h + size_t(tok0) * p.H;
+
+  // dst[C][R] = src[R][C]ᵀ for a tile already in `buf` ([R][C], pitch RP).
+  auto write_t = [&](uint16_t* dst, int R, int C) {
+    for (int idx = tid; idx < C * R / 8; idx += kThreads) {
+      const int c = idx / (R / 8), r8 = 8 * (idx % (R / 8));
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        w[e] = uint32_t(buf[(r8 + 2 * e) * RP + c]) | (uint32_t(buf[(r8 + 2 * e + 1) * RP + c]) << 16);
+      *reinterpret_cast<uint4*>(dst + size_t(c) * R + r8) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  };
+  // buf ← src[R][C] (contiguous rows).
+  auto load = [&](const uint16_t* src, int R, int C) {
+    for (int idx = tid; idx < R * C / 8; idx += kThreads) {
+      const int r = idx / (C / 8), c8 = 8 * (idx % (C / 8));
+      const uint4 v = *reinterpret_cast<const uint4*>(src + size_t(r) * C + c8);
+      uint32_t* d = reinterpret_cast<uint32_t*>(&buf[r * RP + c8]);
+      d[0] = v.x;
+      d[1] = v.y;
+      d[2] = v.z;
+      d[3] = v.w;
+    }
+  };
+  auto transpose = [&](const uint16_t* src, uint16_t* dst, int R, int C) {
+    load(src, R, C);
+    __syncthreads();
+    write_t(dst, R, C);
+    __syncthreads();
+  };
+  const size_t o64 = size_t(cid) * kL * kL, oK = size_t(cid) * kL * K;
+  transpose(p.T + o64, bt.Tt + o64, kL, kL);
+  transpose(p.Tlo + o64, bt.Ttl + o64, kL, kL);
+  transpose(p.attn + o64, bt.AtT + o64, kL, kL);
+  transpose(p.KcT + oK, bt.Kc + oK, K, kL);
+  if constexpr (PC) {
+    transpose(p.Qg + oK, bt.QgT + oK, kL, K);
+    transpose(p.Kg + oK, bt.KgT + oK, kL, K);
+    for (int d = tid; d < K; d += kThreads) bt.egl[size_t(cid) * K + d] = p.egl[size_t(cid) * K + d];
+  } else {
+    // Per-head gates: Qg = scale·e^G·q and Kg = e·e^G·k row by row (zero
+    // past the sequence end).
+    for (int which = 0; which < 2; ++which) {
+      if (tid < kL) {
+        const int t = tid;
+        const bool ok = tok0 + t < p.S;
+        const float eg = p.gated ? __expf(p.gc[size_t(cid) * kL + t]) : 1.f;
+        rowsc[t] = !ok ? 0.f : which == 0 ? p.scale * eg : p.erase[row0 + size_t(t) * p.H] * eg;
+      }
+      __syncthreads();
+      const uint16_t* src = which == 0 ? p.q : p.k;
+      for (int idx = tid; idx < kL * K / 8; idx += kThreads) {
+        const int r = idx / (K / 8), c8 = 8 * (idx % (K / 8));
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (tok0 + r < p.S) v = *reinterpret_cast<const uint4*>(src + (row0 + size_t(r) * p.H) * K + c8);
+        const float sc = rowsc[r];
+        uint32_t* d = reinterpret_cast<uint32_t*>(&buf[r * RP + c8]);
+        d[0] = pk_bf16(lo_f(v.x) * sc, hi_f(v.x) * sc);
+        d[1] = pk_bf16(lo_f(v.y) * sc, hi_f(v.y) * sc);
+        d[2] = pk_bf16(lo_f(v.z) * sc, hi_f(v.z) * sc);
+        d[3] = pk_bf16(lo_f(v.w) * sc, hi_f(v.w) * sc);
+      }
+      __syncthreads();
+      write_t(which == 0 ? bt.QgT + oK : bt.KgT + oK, kL, K);
+      __syncthreads();
+    }
+    const float egl = p.gated ? __expf(p.gc[size_t(cid) * kL + kL - 1]) : 1.f;
+    for (int d = tid; d < K; d += kThreads) bt.egl[size_t(cid) * K + d] = egl;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Backward: the reverse scan carrying the state cotangent dS
+// ---------------------------------------------------------------------------
+// combined_backward.rs:240-319, the dS recurrence, walking the chunks in
+// reverse: with dS the cotangent of the state leaving chunk n,
+//   dV' = attnᵀ·dY + Kc·dS
+//   Z   = Tᵀ·dV'
+//   dS  ← e^{G_last}⊙dS + Qgᵀ·dY − Kgᵀ·Z        (Wᵀ·dV' = kgᵀ·(Tᵀ·dV'))
+// and writes each chunk's leaving dS (fp32) for the chunk-local gradients.
+// Same layout as the forward scan: one workgroup per (b, h, 16·W value
+// columns), a wave owns 16 columns and all K state rows of dS in fp32 MFMA
+// accumulators; the chunk's tiles (Kc, attnᵀ, Tᵀ hi/lo, Qgᵀ, Kgᵀ) are staged
+// once in double-buffered LDS with the same k-permutation. dS is read as bf16
+// hi + lo parts, dV' likewise for Tᵀ·dV'.
+struct RevParams {
+  int B, S, H, V, N;
+  const void* dy;            // [B, S, H, V], bf16 or fp32
+  const float* dstate_final;  // [B, H, K, V] or null (zeros)
+  float* ds_after;            // [G][K][V]
+  float* dstate;              // [B, H, K, V] cotangent of the initial state
+  BwdTiles bt;
+};
+
+template <int K, class TG, int WAVES>
+__global__ __launch_bounds__(64 * WAVES) void mfma_rev_scan_kernel(RevParams p) {
+  constexpr int KK = K / 32;
+  constexpr int RBK = K / 16;
+  constexpr int NT = 64 * WAVES;
+  constexpr int BW = 16 * WAVES;
+  // Tiles: Kc [64][K]; attnᵀ, Tᵀ, Tᵀlo [64][64]; Qgᵀ, Kgᵀ [K][64].
+  constexpr int oKc = 0, oAt = kL * K, oTt = oAt + kL * kL, oTtl = oTt + kL * kL,
+                oQg = oTtl + kL * kL, oKg = oQg + K * kL, BUF = oKg + K * kL;
+  constexpr int C16 = BUF / 8;
+  static_assert(C16 % NT == 0, "staging assumes whole rounds");
+  constexpr int NPF = C16 / NT;
+  constexpr int NK = kL * K / 8;                   // 16-byte chunks of the K-wide tile
+  constexpr int N64 = 3 * kL * kL / 8;             // of the three 64×64 tiles
+  __shared__ __attribute__((aligned(16))) uint16_t tiles[2][BUF];
+  __shared__ float gch[2][K];
+
+  const int ntile = p.V / BW;
+  const int BH = p.B * p.H;
+  const int id = blockIdx.x;
+  const int group = id / (8 * ntile), within = id % (8 * ntile);
+  const int tile = within / 8, bh = group * 8 + within % 8;
+  if (bh >= BH) return;
+  const int b = bh / p.H, h = bh % p.H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, q4 = lane >> 4, k8 = 8 * q4;
+  const int jw = tile * BW + 16 * wave;
+  const int jl = jw + r16;
+  const size_t tokstride = size_t(p.H);
+  const size_t bh_row0 = size_t(b) * p.S * p.H + h;
+  auto chunk_of = [&](int n) { return (size_t(b) * p.N + n) * p.H + h; };
+
+  f32x4 dS[RBK];
+#pragma unroll
+  for (int rb = 0; rb < RBK; ++rb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      dS[rb][r] = p.dstate_final
+                      ? p.dstate_final[(size_t(bh) * K + 16 * rb + 4 * q4 + r) * p.V + jl]
+                      : 0.f;
+
+  uint4 pf[NPF];
+  float pch;
+  auto ld16 = [](const uint16_t* base, uint32_t elems) {
+    return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + 2u * elems);
+  };
+  auto fetch = [&](int n) {
+    const size_t cid = chunk_of(n);
+#pragma unroll
+    for (int m = 0; m < NPF; ++m) {
+      const int i0 = NT * m;
+      if (i0 < NK) {
+        pf[m] = ld16(p.bt.Kc + cid * kL * K + 8 * i0, 8u * tid);
+      } else if (i0 < NK + N64) {
+        const int ii0 = i0 - NK, which = ii0 / (kL * kL / 8);
+        const uint16_t* base = which == 0 ? p.bt.AtT : which == 1 ? p.bt.Tt : p.bt.Ttl;
+        pf[m] = ld16(base + cid * kL * kL + 8 * (ii0 - which * (kL * kL / 8)), 8u * tid);
+      } else {
+        const int ii0 = i0 - NK - N64, which = ii0 / (K * kL / 8);
+        const uint16_t* base = which == 0 ? p.bt.QgT : p.bt.KgT;
+        pf[m] = ld16(base + cid * K * kL + 8 * (ii0 - which * (K * kL / 8)), 8u * tid);
+      }
+    }
+    pch = p.bt.egl[cid * K + (tid % K)];
+  };
+  constexpr int KC8 = K / 8, LC8 = kL / 8;
+  const int rK = tid / KC8, cK = tid % KC8, r6 = tid / LC8, c6 = tid % LC8;
+  auto addr_k = [&](int flip, int half) {
+    const int pos = perm_pos(8 * cK + 4 * half);
+    return rK * K + ((((pos >> 3) ^ (rK & 15) ^ flip) & (KC8 - 1)) << 3) + (pos & 7);
+  };
+  const int aK0 = K >= 128 ? addr_k(0, 0) : tile_at<K>(rK, perm_pos(8 * cK));
+  const int aK1 = K >= 128 ? addr_k(0, 1) : tile_at<K>(rK, perm_pos(8 * cK + 4));
+  const int aK0x = K >= 128 ? addr_k(8, 0) : aK0;
+  const int aK1x = K >= 128 ? addr_k(8, 1) : aK1;
+  const int a60 = tile_at<kL>(r6, perm_pos(8 * c6)), a61 = tile_at<kL>(r6, perm_pos(8 * c6 + 4));
+  auto stage = [&](int buf) {
+    uint16_t* tl = tiles[buf];
+#pragma unroll
+    for (int m = 0; m < NPF; ++m) {
+      const int i0 = NT * m;
+      int b0, b1;
+      if (i0 < NK) {
+        const int dr = i0 / KC8;
+        const bool flip = K >= 128 && (dr & 8);
+        b0 = oKc + dr * K + (flip ? aK0x : aK0);
+        b1 = oKc + dr * K + (flip ? aK1x : aK1);
+      } else if (i0 < NK + N64) {
+        const int ii0 = i0 - NK, which = ii0 / (kL * kL / 8);
+        const int dr = (ii0 - which * (kL * kL / 8)) / LC8;
+        const int base = (which == 0 ? oAt : which == 1 ? oTt : oTtl) + dr * kL;
+        b0 = base + a60;
+        b1 = base + a61;
+      } else {
+        const int ii0 = i0 - NK - N64, which = ii0 / (K * kL / 8);
+        const int dr = (ii0 - which * (K * kL / 8)) / LC8;
+        const int base = (which == 0 ? oQg : oKg) + dr * kL;
+        b0 = base + a60;
+        b1 = base + a61;
+      }
+      *reinterpret_cast<uint2*>(&tl[b0]) = make_uint2(pf[m].x, pf[m].y);
+      *reinterpret_cast<uint2*>(&tl[b1]) = make_uint2(pf[m].z, pf[m].w);
+    }
+    if (tid < K) gch[buf][tid] = pch;
+  };
+  // dY[t][jl] for the 16 tokens of this lane's two B fragments (k = token,
+  // permuted: position 8q+e ↔ token 4q+e, 8q+4+e ↔ token 16+4q+e of each
+  // 32-token step); zero past the sequence end.
+  float dyR[2][8];
+  auto load_dy = [&](int n) {
+    const int rl = min(kL, p.S - n * kL);
+    const size_t base = (bh_row0 + size_t(n) * kL * tokstride) * p.V + jl;
+    const size_t stride = tokstride * p.V;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int t = 32 * kk + (e < 4 ? 4 * q4 + e : 16 + 4 * q4 + e - 4);
+        const size_t at = base + size_t(min(t, rl - 1)) * stride;
+        const float v = ld(static_cast<const TG*>(p.dy), at);
+        dyR[kk][e] = t < rl ? v : 0.f;
+      }
+  };
+  auto as8 = [](const uint4& x) { return __builtin_bit_cast(bf16x8, x); };
+
+  fetch(p.N - 1);
+  load_dy(p.N - 1);
+  stage(0);
+  __syncthreads();
+  for (int it = 0; it < p.N; ++it) {
+    const int n = p.N - 1 - it;
+    const int cur = it & 1;
+    const int nn = n > 0 ? n - 1 : n;  // the first chunk prefetches itself again
+    const uint16_t* tl = tiles[cur];
+    {
+      float* dst = p.ds_after + chunk_of(n) * K * p.V + jl;
+#pragma unroll
+      for (int rb = 0; rb < RBK; ++rb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[size_t(16 * rb + 4 * q4 + r) * p.V] = dS[rb][r];
+    }
+    fetch(nn);
+    uint4 dyf[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+      dyf[kk] = make_uint4(pk_bf16(dyR[kk][0], dyR[kk][1]), pk_bf16(dyR[kk][2], dyR[kk][3]),
+                           pk_bf16(dyR[kk][4], dyR[kk][5]), pk_bf16(dyR[kk][6], dyR[kk][7]));
+
+    // Phase 1: dV' = attnᵀ·dY + Kc·dS in [token][column] orientation.
+    f32x4 dV[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      dV[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk)
+        dV[tb] = mfma16(ld8(&tl[oAt + tile_at<kL>(16 * tb + r16, 32 * kk + k8)]), as8(dyf[kk]),
+                        dV[tb]);
+    }
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      const uint4 sh = frag_hi(dS[2 * kk], dS[2 * kk + 1]);
+      const uint4 sl = frag_lo(dS[2 * kk], dS[2 * kk + 1], sh);
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const bf16x8 kf = ld8(&tl[oKc + tile_at<K>(16 * tb + r16, 32 * kk + k8)]);
+        dV[tb] = mfma16(kf, as8(sh), dV[tb]);
+        dV[tb] = mfma16(kf, as8(sl), dV[tb]);
+      }
+    }
+    load_dy(nn);
+
+    // Phase 2: Z = Tᵀ·dV' with hi + lo parts of both factors.
+    uint4 vh[2], vl[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      vh[kk] = frag_hi(dV[2 * kk], dV[2 * kk + 1]);
+      vl[kk] = frag_lo(dV[2 * kk], dV[2 * kk + 1], vh[kk]);
+    }
+    f32x4 Z[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+      Z[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int at = tile_at<kL>(16 * tb + r16, 32 * kk + k8);
+        const bf16x8 th = ld8(&tl[oTt + at]), tlo = ld8(&tl[oTtl + at]);
+        Z[tb] = mfma16(th, as8(vh[kk]), Z[tb]);
+        Z[tb] = mfma16(tlo, as8(vh[kk]), Z[tb]);
+        Z[tb] = mfma16(th, as8(vl[kk]), Z[tb]);
+      }
+    }
+
+    // Phase 3: dS ← e^{G_last}⊙dS + Qgᵀ·dY − Kgᵀ·Z.
+    uint4 zf[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      f32x4 a = Z[2 * kk], c = Z[2 * kk + 1];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        a[r] = -a[r];
+        c[r] = -c[r];
+      }
+      zf[kk] = frag_hi(a, c);
+    }
+#pragma unroll
+    for (int rb = 0; rb < RBK; ++rb) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dS[rb][r] *= gch[cur][16 * rb + 4 * q4 + r];
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int at = tile_at<kL>(16 * rb + r16, 32 * kk + k8);
+        dS[rb] = mfma16(ld8(&tl[oQg + at]), as8(dyf[kk]), dS[rb]);
+        dS[rb] = mfma16(ld8(&tl[oKg + at]), as8(zf[kk]), dS[rb]);
+      }
+    }
+    stage(cur ^ 1);
+    __syncthreads();
+  }
+  float* dout = p.dstate + size_t(bh) * K * p.V + jl;
+#pragma unroll
+  for (int rb = 0; rb < RBK; ++rb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dout[size_t(16 * rb + 4 * q4 + r) * p.V] = dS[rb][r];
+}
+
+size_t region(size_t bytes) { return align_up(bytes, 256); }
 
 // Per-key-channel decay (GDN-2): the block-decay scores and the kg/qg tiles.
 bool per_channel(const Dims& d) { return d.dw == d.K && d.K > 1; }
 
-bool mfma_fwd_supported(const Dims& d, int qkv_dtype, int y_dtype) {
-  (void)y_dtype;
-  if (!(qkv_dtype == DN_BF16 && (d.K == 64 || d.K == 128) && d.V % kBV == 0 && d.L == kL))
-    return false;
-  if (per_channel(d)) return (d.ew == 1 || d.ew == d.K) && (d.ww == 1 || d.ww == d.V);
-  return d.ew == 1 && d.ww == 1 && d.dw <= 1;
-}
-
-size_t mfma_fwd_workspace(const Dims& d) {
-  const size_t G = size_t(d.B) * d.N * d.H;
-  size_t bytes = 3 * region(G * kL * kL * 2) + region(G * kL * 4) +
-                 region(G * size_t(d.K) * kL * 2) + region(size_t(d.V) * 4);
-  if (per_channel(d)) bytes += 3 * region(G * kL * size_t(d.K) * 2) + region(G * size_t(d.K) * 4);
-  return bytes;
-}
-
-hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, const void* v,
-                    const float* erase, const float* write, const float* g,
-                    const float* state_in, void* y, float* state_out, void* ws,
-                    hipStream_t stream) {
+MfmaParams make_params(const Dims& d, const void* q, const void* k, const void* v,
+                       const float* erase, const float* write, const float* g,
+                       const float* state_in, void* y, float* state_out, void* ws) {
   const size_t G = size_t(d.B) * d.N * d.H;
   MfmaParams p;
   p.B = d.B;
@@ -1078,7 +1414,7 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
   p.s_out = state_out;
   p.ew = int(d.ew);
   p.ww = int(d.ww);
-  const bool pc = per_channel(d);
+  p.states = nullptr;
   char* base = static_cast<char*>(ws);
   p.T = reinterpret_cast<uint16_t*>(base);
   base += region(G * kL * kL * 2);
@@ -1094,7 +1430,7 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
   base += region(size_t(d.V) * 4);
   p.Kg = p.Kglo = p.Qg = nullptr;
   p.egl = nullptr;
-  if (pc) {
+  if (per_channel(d)) {
     p.Kg = reinterpret_cast<uint16_t*>(base);
     base += region(G * kL * size_t(d.K) * 2);
     p.Kglo = reinterpret_cast<uint16_t*>(base);
@@ -1103,8 +1439,12 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
     base += region(G * kL * size_t(d.K) * 2);
     p.egl = reinterpret_cast<float*>(base);
   }
+  return p;
+}
 
-  if (pc) {
+hipError_t launch_intra(const MfmaParams& p, const Dims& d, hipStream_t stream) {
+  const size_t G = size_t(d.B) * d.N * d.H;
+  if (per_channel(d)) {
     ProfScope ps("dn_mfma_intra_pc", stream);
     if (d.K == 128)
       hipLaunchKernelGGL(mfma_intra_pc_kernel<128>, dim3(unsigned(G)), dim3(kThreads), 0, stream,
@@ -1126,37 +1466,140 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
     }
 #undef DN_INTRA
   }
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  // Workgroup width: 128 value columns (8 waves) when that still yields a
-  // workgroup per CU, else narrower so more CUs share the sequence.
-  const int BH = d.B * d.H;
-  const int groups = (BH + 7) / 8;
-  const bool yb = y_dtype == DN_BF16;
+  return hipGetLastError();
+}
+
+// Scan workgroup width: 128 value columns (8 waves) when that still yields a
+// workgroup per CU, else narrower so more CUs share the sequence.
+int scan_waves(const Dims& d) {
+  const int groups = (d.B * d.H + 7) / 8;
   const int cus = device_cu_count();
-  int waves = 2;
-  if (d.V % 128 == 0 && size_t(groups) * 8 * (d.V / 128) >= size_t(cus)) waves = 8;
-  else if (d.V % 64 == 0 && size_t(groups) * 8 * (d.V / 64) >= size_t(cus) / 2) waves = 4;
-  const unsigned blocks = unsigned(groups * 8 * (d.V / (16 * waves)));
-  ProfScope ps(pc ? "dn_mfma_scan_pc" : "dn_mfma_scan", stream);
-#define DN_SCAN(KD, TY, W)                                                                      \
-  do {                                                                                          \
-    if (pc)                                                                                     \
-      hipLaunchKernelGGL((mfma_scan_kernel<KD, TY, W, true>), dim3(blocks), dim3(64 * W), 0,    \
-                         stream, p);                                                            \
-    else                                                                                        \
-      hipLaunchKernelGGL((mfma_scan_kernel<KD, TY, W, false>), dim3(blocks), dim3(64 * W), 0,   \
-                         stream, p);                                                            \
+  if (d.V % 128 == 0 && size_t(groups) * 8 * (d.V / 128) >= size_t(cus)) return 8;
+  if (d.V % 64 == 0 && size_t(groups) * 8 * (d.V / 64) >= size_t(cus) / 2) return 4;
+  return 2;
+}
+
+template <bool ST>
+hipError_t launch_scan(const MfmaParams& p, const Dims& d, bool yb, hipStream_t stream) {
+  const bool pc = per_channel(d);
+  const int waves = scan_waves(d);
+  const unsigned blocks = unsigned(((d.B * d.H + 7) / 8) * 8 * (d.V / (16 * waves)));
+  ProfScope ps(ST ? (pc ? "dn_mfma_scan_pc_states" : "dn_mfma_scan_states")
+                  : (pc ? "dn_mfma_scan_pc" : "dn_mfma_scan"),
+               stream);
+#define DN_SCAN(KD, TY, W)                                                                        \
+  do {                                                                                            \
+    if (pc)                                                                                       \
+      hipLaunchKernelGGL((mfma_scan_kernel<KD, TY, W, true, ST>), dim3(blocks), dim3(64 * W), 0,  \
+                         stream, p);                                                              \
+    else                                                                                          \
+      hipLaunchKernelGGL((mfma_scan_kernel<KD, TY, W, false, ST>), dim3(blocks), dim3(64 * W), 0, \
+                         stream, p);                                                              \
   } while (0)
 #define DN_SCAN_W(KD, TY) \
   do { if (waves == 8) DN_SCAN(KD, TY, 8); else if (waves == 4) DN_SCAN(KD, TY, 4); else DN_SCAN(KD, TY, 2); } while (0)
   if (d.K == 128) {
-    if (yb) DN_SCAN_W(128, bf16); else DN_SCAN_W(128, float);
+    if (yb && !ST) DN_SCAN_W(128, bf16); else DN_SCAN_W(128, float);
   } else {
-    if (yb) DN_SCAN_W(64, bf16); else DN_SCAN_W(64, float);
+    if (yb && !ST) DN_SCAN_W(64, bf16); else DN_SCAN_W(64, float);
   }
 #undef DN_SCAN_W
 #undef DN_SCAN
+  return hipGetLastError();
+}
+
+
+}  // namespace
+
+bool mfma_fwd_supported(const Dims& d, int qkv_dtype, int y_dtype) {
+  (void)y_dtype;
+  if (!(qkv_dtype == DN_BF16 && (d.K == 64 || d.K == 128) && d.V % kBV == 0 && d.L == kL))
+    return false;
+  if (per_channel(d)) return (d.ew == 1 || d.ew == d.K) && (d.ww == 1 || d.ww == d.V);
+  return d.ew == 1 && d.ww == 1 && d.dw <= 1;
+}
+
+size_t mfma_fwd_workspace(const Dims& d) {
+  const size_t G = size_t(d.B) * d.N * d.H;
+  size_t bytes = 3 * region(G * kL * kL * 2) + region(G * kL * 4) +
+                 region(G * size_t(d.K) * kL * 2) + region(size_t(d.V) * 4);
+  if (per_channel(d)) bytes += 3 * region(G * kL * size_t(d.K) * 2) + region(G * size_t(d.K) * 4);
+  return bytes;
+}
+
+hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, const void* v,
+                    const float* erase, const float* write, const float* g,
+                    const float* state_in, void* y, float* state_out, void* ws,
+                    hipStream_t stream) {
+  MfmaParams p = make_params(d, q, k, v, erase, write, g, state_in, y, state_out, ws);
+  hipError_t e = launch_intra(p, d, stream);
+  if (e != hipSuccess) return e;
+  return launch_scan<false>(p, d, y_dtype == DN_BF16, stream);
+}
+
+size_t mfma_bwd_workspace(const Dims& d) {
+  const size_t G = size_t(d.B) * d.N * d.H, K = size_t(d.K);
+  return mfma_fwd_workspace(d) + 3 * region(G * kL * kL * 2) + region(G * kL * K * 2) +
+         2 * region(G * K * kL * 2) + region(G * K * 4);
+}
+
+hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
+                          const float* dstate_final, const void* q, const void* k, const void* v,
+                          const float* erase, const float* write, const float* g,
+                          const float* state_in, float* states, float* ds_after, float* dstate,
+                          void* ws, hipStream_t stream) {
+  const size_t G = size_t(d.B) * d.N * d.H, K = size_t(d.K);
+  // The forward recompute in states mode: its final state lands in dstate,
+  // which the reverse scan overwrites.
+  MfmaParams p = make_params(d, q, k, v, erase, write, g, state_in, nullptr, dstate, ws);
+  p.states = states;
+  hipError_t e = launch_intra(p, d, stream);
+  if (e != hipSuccess) return e;
+  if ((e = launch_scan<true>(p, d, false, stream)) != hipSuccess) return e;
+  char* base = static_cast<char*>(ws) + mfma_fwd_workspace(d);
+  BwdTiles bt;
+  bt.Tt = reinterpret_cast<uint16_t*>(base);
+  base += region(G * kL * kL * 2);
+  bt.Ttl = reinterpret_cast<uint16_t*>(base);
+  base += region(G * kL * kL * 2);
+  bt.AtT = reinterpret_cast<uint16_t*>(base);
+  base += region(G * kL * kL * 2);
+  bt.Kc = reinterpret_cast<uint16_t*>(base);
+  base += region(G * kL * K * 2);
+  bt.QgT = reinterpret_cast<uint16_t*>(base);
+  base += region(G * K * kL * 2);
+  bt.KgT = reinterpret_cast<uint16_t*>(base);
+  base += region(G * K * kL * 2);
+  bt.egl = reinterpret_cast<float*>(base);
+  const bool pc = per_channel(d);
+  {
+    ProfScope ps("dn_mfma_bwd_tiles", stream);
+#define DN_TILES(KD, PCV)                                                                   \
+  hipLaunchKernelGGL((mfma_bwd_tiles_kernel<KD, PCV>), dim3(unsigned(G)), dim3(kThreads), 0, \
+                     stream, p, bt)
+    if (d.K == 128) {
+      if (pc) DN_TILES(128, true); else DN_TILES(128, false);
+    } else {
+      if (pc) DN_TILES(64, true); else DN_TILES(64, false);
+    }
+#undef DN_TILES
+  }
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  RevParams rp{d.B, d.S, d.H, d.V, d.N, dy, dstate_final, ds_after, dstate, bt};
+  const int waves = scan_waves(d);
+  const unsigned blocks = unsigned(((d.B * d.H + 7) / 8) * 8 * (d.V / (16 * waves)));
+  ProfScope ps("dn_mfma_rev_scan", stream);
+#define DN_REV(KD, TG, W) \
+  hipLaunchKernelGGL((mfma_rev_scan_kernel<KD, TG, W>), dim3(blocks), dim3(64 * W), 0, stream, rp)
+#define DN_REV_W(KD, TG) \
+  do { if (waves == 8) DN_REV(KD, TG, 8); else if (waves == 4) DN_REV(KD, TG, 4); else DN_REV(KD, TG, 2); } while (0)
+  if (d.K == 128) {
+    if (grad_dtype == DN_BF16) DN_REV_W(128, bf16); else DN_REV_W(128, float);
+  } else {
+    if (grad_dtype == DN_BF16) DN_REV_W(64, bf16); else DN_REV_W(64, float);
+  }
+#undef DN_REV_W
+#undef DN_REV
   return hipGetLastError();
 }
 

@@ -904,11 +904,17 @@ hipError_t generic_fwd(const Dims& d, int qkv_dtype, int y_dtype, const void* q,
   return hipGetLastError();
 }
 
+static hipError_t generic_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
+                                    const float* dstate_final, const float* state_in,
+                                    const float* ws, float* states, float* ds_after,
+                                    float* dstate, hipStream_t stream);
+
 hipError_t generic_bwd(const Dims& d, int qkv_dtype, int grad_dtype, const void* dy,
                        const float* dstate_final, const void* q, const void* k, const void* v,
                        const float* erase, const float* write, const float* g,
                        const float* state_in, void* dq, void* dk, void* dv, float* derase,
-                       float* dwrite, float* dg, float* dstate, void* wsv, hipStream_t stream) {
+                       float* dwrite, float* dg, float* dstate, void* wsv, hipStream_t stream,
+                       void* mfma_ws) {
   const size_t G = G_of(d);
   char* base = static_cast<char*>(wsv);
   float* ws = reinterpret_cast<float*>(base);
@@ -921,6 +927,32 @@ hipError_t generic_bwd(const Dims& d, int qkv_dtype, int grad_dtype, const void*
 
   hipError_t e = launch_intra(d, qkv_dtype, q, k, v, erase, write, g, ws, stream);
   if (e != hipSuccess) return e;
+  if (mfma_ws) {
+    // Both scans on MFMA; the chunk-local gradients below are unchanged.
+    e = mfma_bwd_scans(d, grad_dtype, dy, dstate_final, q, k, v, erase, write, g, state_in,
+                       states, ds_after, dstate, mfma_ws, stream);
+    if (e != hipSuccess) return e;
+  } else if ((e = generic_bwd_scans(d, grad_dtype, dy, dstate_final, state_in, ws, states,
+                                    ds_after, dstate, stream)) != hipSuccess) {
+    return e;
+  }
+  ChunkBwdParams cp{d,     make_layout(d), make_bwd_layout(d), ws,     bws,   states,
+                    ds_after, dy,           dq,                 dk,     dv,    derase,
+                    dwrite,   dg};
+  ProfScope ps("dn_generic_chunk_bwd", stream);
+  if (grad_dtype == DN_BF16)
+    hipLaunchKernelGGL(chunk_bwd_kernel<bf16>, dim3(unsigned(G)), dim3(kThreads), 0, stream, cp);
+  else
+    hipLaunchKernelGGL(chunk_bwd_kernel<float>, dim3(unsigned(G)), dim3(kThreads), 0, stream,
+                       cp);
+  return hipGetLastError();
+}
+
+static hipError_t generic_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
+                                    const float* dstate_final, const float* state_in,
+                                    const float* ws, float* states, float* ds_after,
+                                    float* dstate, hipStream_t stream) {
+  hipError_t e;
   const int tile = scan_tile(d);
   dim3 grid((d.V + tile - 1) / tile, d.H, d.B);
   // Forward scan keeping the state entering each chunk; its final state goes
@@ -942,16 +974,6 @@ hipError_t generic_bwd(const Dims& d, int qkv_dtype, int grad_dtype, const void*
       hipLaunchKernelGGL(rev_scan_kernel<float>, grid, dim3(kThreads), scan_lds(d, tile, 2),
                          stream, rp);
   }
-  if ((e = hipGetLastError()) != hipSuccess) return e;
-  ChunkBwdParams cp{d,     make_layout(d), make_bwd_layout(d), ws,     bws,   states,
-                    ds_after, dy,           dq,                 dk,     dv,    derase,
-                    dwrite,   dg};
-  ProfScope ps("dn_generic_chunk_bwd", stream);
-  if (grad_dtype == DN_BF16)
-    hipLaunchKernelGGL(chunk_bwd_kernel<bf16>, dim3(unsigned(G)), dim3(kThreads), 0, stream, cp);
-  else
-    hipLaunchKernelGGL(chunk_bwd_kernel<float>, dim3(unsigned(G)), dim3(kThreads), 0, stream,
-                       cp);
   return hipGetLastError();
 }
 

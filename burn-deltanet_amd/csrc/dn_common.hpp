@@ -81,7 +81,8 @@ hipError_t generic_bwd(const Dims& d, int qkv_dtype, int grad_dtype, const void*
                        const float* dstate_final, const void* q, const void* k, const void* v,
                        const float* erase, const float* write, const float* g,
                        const float* state_in, void* dq, void* dk, void* dv, float* derase,
-                       float* dwrite, float* dg, float* dstate, void* ws, hipStream_t stream);
+                       float* dwrite, float* dg, float* dstate, void* ws, hipStream_t stream,
+                       void* mfma_ws = nullptr);
 
 bool mfma_fwd_supported(const Dims& d, int qkv_dtype, int y_dtype);
 size_t mfma_fwd_workspace(const Dims& d);
@@ -89,6 +90,15 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
                     const float* erase, const float* write, const float* g,
                     const float* state_in, void* y, float* state_out, void* ws,
                     hipStream_t stream);
+// The backward's two scans on MFMA (bf16 q/k/v, the shapes mfma_fwd_supported
+// accepts): the states entering each chunk and the state cotangents leaving
+// each chunk, fp32 [G][K][V], plus the initial state's cotangent.
+size_t mfma_bwd_workspace(const Dims& d);
+hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
+                          const float* dstate_final, const void* q, const void* k, const void* v,
+                          const float* erase, const float* write, const float* g,
+                          const float* state_in, float* states, float* ds_after, float* dstate,
+                          void* ws, hipStream_t stream);
 
 // Per-kernel HIP-event timing (dn_profile_enable): a scope records a start
 // event on construction and a stop event on destruction, on `stream`.

@@ -180,3 +180,78 @@ def test_mfma_channel_gates_constant_keys(rng):
     ey, es = rel_err(y, y0), rel_err(s, s0)
     print(f"  rel err y {ey:.2e} state {es:.2e}", flush=True)
     assert ey < TOL and es < TOL
+
+
+# ---------------------------------------------------------------------------
+# Backward with the MFMA scans (bf16 q/k/v): all seven gradients
+# ---------------------------------------------------------------------------
+
+BWD_CASES = [
+    # B, S, H, K, V, gates: None (ungated) | "head" | (ew, ww) with a per-channel decay
+    (1, 256, 2, 128, 128, "head"),
+    (2, 200, 2, 128, 64, "head"),
+    (1, 192, 2, 64, 128, None),
+    (1, 256, 2, 128, 128, (128, 128)),
+    (1, 130, 2, 128, 64, (1, 64)),
+    (2, 128, 2, 64, 64, (64, 1)),
+]
+
+
+def bwd_inputs(rng, B, S, H, K, V, gates):
+    if gates is None or gates == "head":
+        args = gdn_inputs(rng, B, S, H, K, V, gated=gates == "head", state_std=0.05)
+    else:
+        args = gdn2_inputs(rng, B, S, H, K, V, gates[0], gates[1], state_std=0.05)
+    dy = rng.standard_normal((B, S, H, V))
+    ds = rng.standard_normal((B, H, K, V)) * 0.5
+    return args, dy, ds
+
+
+@pytest.mark.parametrize("case", BWD_CASES)
+@pytest.mark.parametrize("dy_dtype", [torch.float32, torch.bfloat16])
+def test_mfma_bwd_matches_oracle(rng, case, dy_dtype):
+    B, S, H, K, V, gates = case
+    announce(f"mfma bwd {case} dy {dy_dtype}")
+    args, dy, ds = bwd_inputs(rng, B, S, H, K, V, gates)
+    g_args = to_gpu(args, torch.bfloat16)
+    tdy = torch.tensor(dy, dtype=torch.float32, device=DEV).to(dy_dtype)
+    tds = torch.tensor(ds, dtype=torch.float32, device=DEV)
+    q, k, v, e, w, g, s = g_args
+    grads = pkg.combined_backward(tdy, tds, q, k, v, e, w, g, s, 64, 1.0 / np.sqrt(K))
+    torch.cuda.synchronize()
+    want = O.chunk_bwd(np_of(tdy), ds, *as_oracle_inputs(g_args), chunk_len=64)
+    names = ["d_q", "d_k", "d_v", "d_erase", "d_write", "d_g", "d_state"]
+    vals = [grads.d_q_bshk, grads.d_k_bshk, grads.d_v_bshv, grads.d_erase_bshK,
+            grads.d_write_bshV, grads.d_g_bshK, grads.d_state_bhkv]
+    for name, a, b in zip(names, vals, want):
+        if b is None:
+            assert a is None
+            continue
+        err = rel_err(np_of(a), b)
+        print(f"  {name} rel err {err:.2e}", flush=True)
+        assert err < TOL, name
+
+
+def test_mfma_bwd_is_chosen_and_matches_generic(rng):
+    announce("mfma bwd vs generic")
+    B, S, H, K, V = 1, 256, 2, 128, 128
+    args, dy, ds = bwd_inputs(rng, B, S, H, K, V, "head")
+    g_args = to_gpu(args, torch.bfloat16)
+    q, k, v, e, w, g, s = g_args
+    tdy = torch.tensor(dy, dtype=torch.float32, device=DEV)
+    tds = torch.tensor(ds, dtype=torch.float32, device=DEV)
+    grads = (torch.empty(q.shape, device=DEV), torch.empty(k.shape, device=DEV),
+             torch.empty(v.shape, device=DEV), torch.empty_like(e), torch.empty_like(w),
+             torch.empty_like(g), torch.empty_like(s))
+    a = pkg.abi.chunk_bwd_args(tdy, tds, q, k, v, e, w, g, s, grads, 64, None)
+    assert pkg.abi.lib().dn_chunk_bwd_algo(a) == MFMA
+    out = {}
+    for algo in (MFMA, pkg.abi.DN_ALGO_GENERIC):
+        got = pkg.combined_backward(tdy, tds, q, k, v, e, w, g, s, 64, 1.0 / np.sqrt(K),
+                                    algo=algo)
+        torch.cuda.synchronize()
+        out[algo] = [np_of(x) for x in (got.d_q_bshk, got.d_k_bshk, got.d_v_bshv,
+                                         got.d_erase_bshK, got.d_write_bshV, got.d_g_bshK,
+                                         got.d_state_bhkv)]
+    for m, gnr in zip(out[MFMA], out[pkg.abi.DN_ALGO_GENERIC]):
+        assert rel_err(m, gnr) < TOL
