@@ -194,7 +194,8 @@ Dims bwd_dims(const dn_chunk_bwd_args* a) {
 }
 
 // MFMA: the two scans of the backward on bf16 MFMA (the forward MFMA path's
-// shapes, bf16 q/k/v); the chunk-local gradients stay in fp32.
+// shapes, bf16 q/k/v), and for head_v_dim 64 or 128 the chunk-local
+// gradients too; otherwise those stay on the generic fp32 kernel.
 int bwd_algo(const dn_chunk_bwd_args* a, const Dims& d) {
   if (a->algo == DN_ALGO_GENERIC) return DN_ALGO_GENERIC;
   const bool fits = mfma_fwd_supported(d, a->qkv_dtype, DN_BF16);
@@ -202,7 +203,17 @@ int bwd_algo(const dn_chunk_bwd_args* a, const Dims& d) {
   return fits ? DN_ALGO_MFMA : DN_ALGO_GENERIC;
 }
 
-size_t bwd_workspace(const Dims& d, int algo) {
+bool bwd_all_mfma(const Dims& d, int qkv_dtype, int algo) {
+  return algo == DN_ALGO_MFMA && mfma_chunk_bwd_supported(d, qkv_dtype);
+}
+
+// Per-chunk states and state cotangents, fp32 [G][K][V] each.
+size_t bwd_state_bytes(const Dims& d) {
+  return align_up(size_t(d.B) * d.N * d.H * d.K * d.V * sizeof(float), 256);
+}
+
+size_t bwd_workspace(const Dims& d, int algo, int qkv_dtype) {
+  if (bwd_all_mfma(d, qkv_dtype, algo)) return 2 * bwd_state_bytes(d) + mfma_bwd_workspace(d);
   return align_up(generic_bwd_workspace(d), 256) + (algo == DN_ALGO_MFMA ? mfma_bwd_workspace(d) : 0);
 }
 
@@ -290,7 +301,7 @@ size_t dn_chunk_bwd_workspace_bytes(const dn_chunk_bwd_args* a) {
   if (check_bwd(a)) return 0;
   const Dims d = bwd_dims(a);
   const int algo = bwd_algo(a, d);
-  return algo < 0 ? 0 : bwd_workspace(d, algo);
+  return algo < 0 ? 0 : bwd_workspace(d, algo, a->qkv_dtype);
 }
 
 int dn_chunk_bwd(const dn_chunk_bwd_args* a, hipStream_t stream) {
@@ -301,7 +312,7 @@ int dn_chunk_bwd(const dn_chunk_bwd_args* a, hipStream_t stream) {
   if (algo < 0)
     return fail(DN_ERR_UNSUPPORTED, "DN_ALGO_MFMA needs bf16 q/k/v, head_k_dim 64 or 128, "
                                     "head_v_dim a multiple of 64 and chunk_len 64");
-  const size_t need = bwd_workspace(d, algo);
+  const size_t need = bwd_workspace(d, algo, a->qkv_dtype);
   void* ws = a->workspace;
   if (ws) {
     if (a->workspace_bytes < need)
@@ -324,13 +335,27 @@ int dn_chunk_bwd(const dn_chunk_bwd_args* a, hipStream_t stream) {
                                {a->state_in, ns, DN_F32}};
     if (int rc = nonfinite_check(in, stream, "inputs")) return rc;
   }
-  hipError_t e = generic_bwd(d, a->qkv_dtype, a->grad_dtype, a->d_y, a->d_state_final, a->q,
-                             a->k, a->v, a->erase, a->write, a->has_gate ? a->g : nullptr,
-                             a->state_in, a->d_q, a->d_k, a->d_v, a->d_erase, a->d_write,
-                             a->has_gate ? a->d_g : nullptr, a->d_state, ws, stream,
-                             algo == DN_ALGO_MFMA
-                                 ? static_cast<char*>(ws) + align_up(generic_bwd_workspace(d), 256)
-                                 : nullptr);
+  hipError_t e;
+  const float* g = a->has_gate ? a->g : nullptr;
+  if (bwd_all_mfma(d, a->qkv_dtype, algo)) {
+    char* base = static_cast<char*>(ws);
+    float* states = reinterpret_cast<float*>(base);
+    float* ds_after = reinterpret_cast<float*>(base + bwd_state_bytes(d));
+    void* mws = base + 2 * bwd_state_bytes(d);
+    e = mfma_bwd_scans(d, a->grad_dtype, a->d_y, a->d_state_final, a->q, a->k, a->v, a->erase,
+                       a->write, g, a->state_in, states, ds_after, a->d_state, mws, stream);
+    if (e == hipSuccess)
+      e = mfma_chunk_bwd(d, a->grad_dtype, a->d_y, a->q, a->k, a->v, a->erase, a->write, g,
+                         states, ds_after, a->d_q, a->d_k, a->d_v, a->d_erase, a->d_write,
+                         a->has_gate ? a->d_g : nullptr, mfma_bwd_tiles(d, mws), stream);
+  } else {
+    e = generic_bwd(d, a->qkv_dtype, a->grad_dtype, a->d_y, a->d_state_final, a->q, a->k, a->v,
+                    a->erase, a->write, g, a->state_in, a->d_q, a->d_k, a->d_v, a->d_erase,
+                    a->d_write, a->has_gate ? a->d_g : nullptr, a->d_state, ws, stream,
+                    algo == DN_ALGO_MFMA
+                        ? static_cast<char*>(ws) + align_up(generic_bwd_workspace(d), 256)
+                        : nullptr);
+  }
   if (e != hipSuccess) return hip_fail(e, "dn_chunk_bwd launch");
   if (a->check_finite) {
     std::vector<Guarded> out = {{a->d_q, nq * d.K, a->grad_dtype},

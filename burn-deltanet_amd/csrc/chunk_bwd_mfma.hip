@@ -1,0 +1,964 @@
+// The chunk-local gradients of the chunkwise WY form on CDNA4 matrix cores.
+//
+// combined_backward.rs:103-188 (WY and front-end terms), :240-319 (the
+// per-chunk terms of the reverse walk) and :376-513 (both score backwards),
+// for one chunk-head per workgroup (8 waves), given what the two MFMA scans
+// leave behind: the state S₀ entering the chunk and the cotangent dS of the
+// state leaving it (fp32), and the intra kernel's T, Tᵀ (bf16 hi + lo) and
+// attnᵀ tiles. With X = w⊙V − kg·S₀ (so that V' = U − W·S₀ = T·X):
+//
+//   phase A  (a wave per 16 value columns)
+//            X;  V' = T·X;  dV' = attnᵀ·dY + kc·dS;  dVw = Tᵀ·dV'
+//            d_v = w⊙dVw, d_write from dVw⊙v
+//   phase B  (a wave per 16 key channels; contractions over the value axis)
+//            d_kc = V'·dSᵀ;  d_qr = dY·S₀ᵀ;  d_kg = −dVw·S₀ᵀ (= Tᵀ·dW with
+//            dW = −dV'·S₀ᵀ);  Σ_v dS⊙S₀;  dattn = dY·V'ᵀ
+//   phase C  dT = dV'·Xᵀ (= dU·Vwᵀ + dW·kgᵀ, without the cancellation of the
+//            two terms);  dAkk = −tril(Tᵀ·dT·Tᵀ, −1) as (dTᵀ·T)ᵀ·Tᵀ
+//   phase D  (a wave per 16 key channels) the score backward of the head
+//            decay or of the per-channel block decay (BlockDecayPrim), the
+//            gate terms and the reverse cumulative sum of d_g.
+//
+// Every product runs on v_mfma_f32_16x16x32_bf16 with fp32 intermediates as
+// bf16 hi + lo parts (three MFMAs; two when one side is an exact bf16 input),
+// which keeps the gradients at fp32-like accuracy. Intermediates pass between
+// the phases through one LDS region that each phase re-carves.
+
+#include <type_traits>
+
+#include "dn_common.hpp"
+#include "mfma_util.hpp"
+
+namespace dn {
+namespace {
+
+constexpr int kL = 64;
+constexpr int kW = 8;
+constexpr int kNT = 64 * kW;
+constexpr float kMaxExp = 48.f;  // MAX_EXPONENT, decay.rs:49
+
+struct CbParams {
+  int S, H, N, ew, ww;
+  int gated;
+  float scale;
+  const uint16_t *q, *k, *v;
+  const float *erase, *write, *g;
+  const void* dy;
+  const uint16_t *T, *Tlo, *Tt, *Ttl, *AtT;  // [G][64][64]
+  const uint16_t* Kc;                        // [G][64][K] bf16(e^{G_last−G}⊙K)
+  const uint16_t *Kg, *Kglo;                 // [G][64][K] e⊙e^G⊙K hi / lo (per-channel decay)
+  const float* gc;                           // [G][64] in-chunk cumulative gate (per-head)
+  const float* states;                       // [G][K][V]
+  const float* ds_after;                     // [G][K][V]
+  void *dq, *dk, *dv;
+  float *derase, *dwrite, *dg;
+};
+
+__device__ inline uint16_t bf_bits(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
+
+// Four floats → packed bf16 hi parts and lo parts (8-byte LDS stores).
+__device__ inline void split4(const float* f, uint2& h, uint2& l) {
+  h = make_uint2(pk_bf16(f[0], f[1]), pk_bf16(f[2], f[3]));
+  l = make_uint2(pk_bf16(f[0] - lo_f(h.x), f[1] - hi_f(h.x)),
+                 pk_bf16(f[2] - lo_f(h.y), f[3] - hi_f(h.y)));
+}
+
+// v[0..15] summed over the 16 lanes that share lane/16; lane l receives the
+// total of index l%16 (a halving exchange: 15 shuffles instead of 64).
+__device__ inline float reduce16(const float (&v)[16], int lane) {
+  float a[8], b[4], c[2];
+  const bool u8 = lane & 8, u4 = lane & 4, u2 = lane & 2, u1 = lane & 1;
+#pragma unroll
+  for (int j = 0; j < 8; ++j)
+    a[j] = (u8 ? v[8 + j] : v[j]) + __shfl_xor(u8 ? v[j] : v[8 + j], 8);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    b[j] = (u4 ? a[4 + j] : a[j]) + __shfl_xor(u4 ? a[j] : a[4 + j], 4);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    c[j] = (u2 ? b[2 + j] : b[j]) + __shfl_xor(u2 ? b[j] : b[2 + j], 2);
+  return (u1 ? c[1] : c[0]) + __shfl_xor(u1 ? c[0] : c[1], 1);
+}
+
+// 64 rows of C bf16 (global, row pitch C) → LDS tile, natural order.
+template <int C>
+__device__ inline void stage_rows(uint16_t* R, int dst, const uint16_t* src, int tid) {
+#pragma unroll
+  for (int idx = tid; idx < kL * C / 8; idx += kNT) {
+    const int row = idx / (C / 8), c8 = idx % (C / 8);
+    *reinterpret_cast<uint4*>(&R[dst + tile_at<C>(row, 8 * c8)]) =
+        *reinterpret_cast<const uint4*>(src + size_t(row) * C + 8 * c8);
+  }
+}
+
+// A 64×64 bf16 tile (global, row-major) → LDS with the permuted column order.
+__device__ inline void stage_perm(uint16_t* R, int dst, const uint16_t* src, int tid) {
+  const int row = tid >> 3, c8 = tid & 7;  // 512 threads: one 16-byte chunk each
+  const uint4 v = *reinterpret_cast<const uint4*>(src + row * kL + 8 * c8);
+  *reinterpret_cast<uint2*>(&R[dst + tile_at<kL>(row, perm_pos(8 * c8))]) = make_uint2(v.x, v.y);
+  *reinterpret_cast<uint2*>(&R[dst + tile_at<kL>(row, perm_pos(8 * c8 + 4))]) =
+      make_uint2(v.z, v.w);
+}
+
+// The 16 lower-or-diagonal and upper 16×16 tiles of a 64×64 matrix, two per
+// wave: tile t = wave + 8u is (t/4, t%4).
+
+template <int K, int V, bool PC, class TG>
+__global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
+  constexpr bool F32DY = std::is_same<TG, float>::value;
+  constexpr int TT = kL * kL, TK = kL * K, TV = kL * V;
+  constexpr int OFF_A1 = 4 * TV > 8 * TT ? 4 * TV : 8 * TT;
+  constexpr int RBIG = OFF_A1 + 4 * TT;
+  static_assert(5 * TT + (PC ? 3 : 1) * TK <= RBIG, "phase-A operands fit");
+  static_assert((F32DY ? 6 : 5) * TV <= RBIG, "phase-B operands fit");
+  static_assert(4 * TT + 2 * TK <= OFF_A1, "score operands fit");
+  constexpr int GP = K + 4;  // fp32 row pitch of the per-channel cumulative gate
+  // Carvings of R (bf16 elements):
+  //  A  T hi/lo, Tᵀ hi/lo (permuted), attnᵀ (permuted), kg (hi/lo), kc
+  constexpr int oTh = 0, oTl = TT, oTth = 2 * TT, oTtl = 3 * TT, oAt = 4 * TT, oKop = 5 * TT,
+                oKgl = 5 * TT + TK, oKc = PC ? 5 * TT + 2 * TK : 5 * TT;
+  //  B  V' hi/lo, dVw hi/lo, dY hi(/lo)
+  constexpr int oVh = 0, oVl = TV, oWh = 2 * TV, oWl = 3 * TV, oYh = 4 * TV, oYl = 5 * TV;
+  //  C  X hi/lo, dV' hi/lo; dAqk as [i][j] and [j][i] (hi/lo) at OFF_A1 until the end
+  constexpr int oXh = 0, oXl = TV, oDh = 2 * TV, oDl = 3 * TV;
+  constexpr int oA1h = OFF_A1, oA1l = OFF_A1 + TT, oA1th = OFF_A1 + 2 * TT,
+                oA1tl = OFF_A1 + 3 * TT;
+  //     then T and Tᵀ again, dTᵀ (permuted over dT's rows), M₁ = Tᵀ·dT
+  constexpr int oDTh = 4 * TT, oDTl = 5 * TT, oM1h = 6 * TT, oM1l = 7 * TT;
+  //  D  dAkk as [i][j] and [j][i] (hi/lo); Kᵀ, Qᵀ
+  constexpr int oA0h = 0, oA0l = TT, oA0th = 2 * TT, oA0tl = 3 * TT, oKC = 4 * TT,
+                oQC = 4 * TT + TK;
+  __shared__ __attribute__((aligned(16))) uint16_t R[RBIG];
+  __shared__ __attribute__((aligned(16))) float Gc[PC ? kL * GP : kL];
+  __shared__ float er_s[kL], wr_s[kL], eg_s[kL], ec_s[kL];
+  __shared__ float racc[3][kL];  // row sums: d_write, d_erase, d_g (per-head)
+  __shared__ float cacc[K];      // per-channel decay: d(G_last) per channel
+
+  const int cid = blockIdx.x;
+  const int h = cid % p.H, n = (cid / p.H) % p.N, b = cid / (p.H * p.N);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r16 = lane & 15, g4 = lane >> 4, k8 = 8 * g4;
+  const int tok0 = n * kL;
+  const int valid = min(kL, p.S - tok0);
+  const size_t row0 = size_t(b) * p.S * p.H + h + size_t(tok0) * p.H;
+  auto row_of = [&](int t) { return row0 + size_t(t) * p.H; };
+  const size_t o64 = size_t(cid) * kL * kL, oLK = size_t(cid) * kL * K;
+  const float* S0 = p.states + size_t(cid) * K * V;
+  const float* dSa = p.ds_after + size_t(cid) * K * V;
+  const TG* dy = static_cast<const TG*>(p.dy);
+  const bool gated = PC || p.gated;
+  auto rowi = [&](int ib, int r) { return 16 * ib + 4 * g4 + r; };
+  // Row of the value reduce16 leaves in this lane (index 4·ib + r).
+  const int red_row = 16 * (r16 >> 2) + 4 * g4 + (r16 & 3);
+
+  // ---- staging -----------------------------------------------------------
+  if (tid < kL) {
+    const int t = tid;
+    const bool ok = t < valid;
+    er_s[t] = (ok && p.ew == 1) ? p.erase[row_of(t)] : 0.f;
+    wr_s[t] = (ok && p.ww == 1) ? p.write[row_of(t)] : 0.f;
+    if constexpr (!PC) {
+      const float gct = gated ? p.gc[size_t(cid) * kL + t] : 0.f;
+      const float gl = gated ? p.gc[size_t(cid) * kL + kL - 1] : 0.f;
+      Gc[t] = gct;
+      eg_s[t] = gated ? __expf(gct) : 1.f;
+      ec_s[t] = gated ? __expf(gl - gct) : 1.f;
+    }
+    racc[0][t] = racc[1][t] = racc[2][t] = 0.f;
+  }
+  for (int c = tid; c < K; c += kNT) cacc[c] = 0.f;
+  if constexpr (PC) {
+    // G = in-chunk cumulative sum of g per channel (KPART lanes per channel).
+    constexpr int KPART = kNT / K, RUN = kL / KPART;
+    const int d = tid % K, part = tid / K;
+    float vals[RUN];
+#pragma unroll
+    for (int t = 0; t < RUN; ++t) {
+      const int tt = part * RUN + t;
+      vals[t] = tt < valid ? p.g[row_of(tt) * K + d] : 0.f;
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int t = 0; t < RUN; ++t) {
+      acc += vals[t];
+      vals[t] = acc;
+    }
+    Gc[(part * RUN + RUN - 1) * GP + d] = acc;
+    __syncthreads();
+    float carry = 0.f;
+    for (int pp = 0; pp < part; ++pp) carry += Gc[(pp * RUN + RUN - 1) * GP + d];
+    __syncthreads();
+#pragma unroll
+    for (int t = 0; t < RUN; ++t) Gc[(part * RUN + t) * GP + d] = vals[t] + carry;
+  }
+  stage_perm(R, oTh, p.T + o64, tid);
+  stage_perm(R, oTl, p.Tlo + o64, tid);
+  stage_perm(R, oTth, p.Tt + o64, tid);
+  stage_perm(R, oTtl, p.Ttl + o64, tid);
+  stage_perm(R, oAt, p.AtT + o64, tid);
+  if constexpr (PC) {
+    stage_rows<K>(R, oKop, p.Kg + oLK, tid);
+    stage_rows<K>(R, oKgl, p.Kglo + oLK, tid);
+    stage_rows<K>(R, oKc, p.Kc + oLK, tid);
+  } else {
+    for (int idx = tid; idx < kL * K / 8; idx += kNT) {
+      const int row = idx / (K / 8), c8 = idx % (K / 8);
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (row < valid) v = *reinterpret_cast<const uint4*>(p.k + row_of(row) * K + 8 * c8);
+      *reinterpret_cast<uint4*>(&R[oKop + tile_at<K>(row, 8 * c8)]) = v;
+    }
+  }
+  __syncthreads();
+
+  // ---- phase A: value columns ---------------------------------------------
+  const bool vwave = wave < V / 16;
+  const int col = 16 * wave + r16;
+  f32x4 X[4], dV[4], Vn[4], dW[4];
+  if (vwave) {
+    float vv[4][4], wv[4][4];
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = rowi(ib, r);
+        const bool ok = i < valid;
+        vv[ib][r] = ok ? bf16_to_f32(p.v[row_of(i) * V + col]) : 0.f;
+        wv[ib][r] = p.ww == 1 ? wr_s[i] : (ok ? p.write[row_of(i) * V + col] : 0.f);
+      }
+    // X = w⊙V − kg·S₀ (S₀ as hi + lo parts; per-head: k exact, e·e^G per row).
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) X[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < K / 32; ++s) {
+      float sv[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) sv[t] = S0[size_t(32 * s + k8 + t) * V + col];
+      uint4 sh, sl;
+      split8(sv, sh, sl);
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) {
+        const int at = tile_at<K>(16 * ib + r16, 32 * s + k8);
+        const uint4 a = ld8u(&R[oKop + at]);
+        X[ib] = mfma16(a, sh, X[ib]);
+        X[ib] = mfma16(a, sl, X[ib]);
+        if constexpr (PC) X[ib] = mfma16(ld8u(&R[oKgl + at]), sh, X[ib]);
+      }
+    }
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = rowi(ib, r);
+        const float sc = PC ? 1.f : er_s[i] * eg_s[i];
+        X[ib][r] = vv[ib][r] * wv[ib][r] - sc * X[ib][r];
+      }
+    // V' = T·X (hi + lo parts of both).
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) Vn[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const uint4 xh = frag_hi(X[2 * kk], X[2 * kk + 1]);
+      const uint4 xl = frag_lo(X[2 * kk], X[2 * kk + 1], xh);
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) {
+        const int at = tile_at<kL>(16 * ib + r16, 32 * kk + k8);
+        const uint4 th = ld8u(&R[oTh + at]), tl = ld8u(&R[oTl + at]);
+        Vn[ib] = mfma16(th, xh, Vn[ib]);
+        Vn[ib] = mfma16(tl, xh, Vn[ib]);
+        Vn[ib] = mfma16(th, xl, Vn[ib]);
+      }
+    }
+    // dV' = attnᵀ·dY + kc·dS (dY fragments: token 4q+e / 16+4q+e of each
+    // 32-token step at position 8q+e / 8q+4+e, the permuted order).
+    uint4 yh[2], yl[2];
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int t = 32 * kk + (e < 4 ? 4 * g4 + e : 16 + 4 * g4 + e - 4);
+        f[e] = t < valid ? ld(dy, row_of(t) * V + col) : 0.f;
+      }
+      split8(f, yh[kk], yl[kk]);
+    }
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+      dV[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const uint4 a = ld8u(&R[oAt + tile_at<kL>(16 * ib + r16, 32 * kk + k8)]);
+        dV[ib] = mfma16(a, yh[kk], dV[ib]);
+        if constexpr (F32DY) dV[ib] = mfma16(a, yl[kk], dV[ib]);
+      }
+    }
+    {
+      f32x4 kd[4];
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) kd[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < K / 32; ++s) {
+        float dv8[8];
+#pragma unroll
+        for (int t = 0; t < 8; ++t) dv8[t] = dSa[size_t(32 * s + k8 + t) * V + col];
+        uint4 dh, dl;
+        split8(dv8, dh, dl);
+#pragma unroll
+        for (int ib = 0; ib < 4; ++ib) {
+          const uint4 a = ld8u(&R[oKc + tile_at<K>(16 * ib + r16, 32 * s + k8)]);
+          kd[ib] = mfma16(a, dh, kd[ib]);
+          kd[ib] = mfma16(a, dl, kd[ib]);
+        }
+      }
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dV[ib][r] += (PC ? 1.f : ec_s[rowi(ib, r)]) * kd[ib][r];
+    }
+    // dVw = Tᵀ·dV'.
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) dW[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const uint4 vh = frag_hi(dV[2 * kk], dV[2 * kk + 1]);
+      const uint4 vl = frag_lo(dV[2 * kk], dV[2 * kk + 1], vh);
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) {
+        const int at = tile_at<kL>(16 * ib + r16, 32 * kk + k8);
+        const uint4 th = ld8u(&R[oTth + at]), tl = ld8u(&R[oTtl + at]);
+        dW[ib] = mfma16(th, vh, dW[ib]);
+        dW[ib] = mfma16(tl, vh, dW[ib]);
+        dW[ib] = mfma16(th, vl, dW[ib]);
+      }
+    }
+    // d_v = w⊙dVw; d_write = dVw⊙v, summed over the value axis for width 1.
+    TG* gv = static_cast<TG*>(p.dv);
+    float rs[16];
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = rowi(ib, r);
+        if (i < valid) st(gv, row_of(i) * V + col, dW[ib][r] * wv[ib][r]);
+        rs[4 * ib + r] = dW[ib][r] * vv[ib][r];
+        if (p.ww != 1 && i < valid) p.dwrite[row_of(i) * V + col] = rs[4 * ib + r];
+      }
+    if (p.ww == 1) atomicAdd(&racc[0][red_row], reduce16(rs, lane));
+  }
+  __syncthreads();
+
+  // ---- V', dVw and dY rows into LDS ---------------------------------------
+  if (vwave) {
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int at = tile_at<V>(rowi(ib, r), col);
+        const uint16_t vh = bf_bits(Vn[ib][r]), wh = bf_bits(dW[ib][r]);
+        R[oVh + at] = vh;
+        R[oVl + at] = bf_bits(Vn[ib][r] - bf16_to_f32(vh));
+        R[oWh + at] = wh;
+        R[oWl + at] = bf_bits(dW[ib][r] - bf16_to_f32(wh));
+      }
+  }
+  for (int idx = tid; idx < kL * V / 8; idx += kNT) {
+    const int i = idx / (V / 8), c8 = idx % (V / 8);
+    const int at = tile_at<V>(i, 8 * c8);
+    if constexpr (F32DY) {
+      float f[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (i < valid) {
+        const float4* src = reinterpret_cast<const float4*>(dy + row_of(i) * V + 8 * c8);
+        *reinterpret_cast<float4*>(f) = src[0];
+        *reinterpret_cast<float4*>(f + 4) = src[1];
+      }
+      uint4 hh, ll;
+      split8(f, hh, ll);
+      *reinterpret_cast<uint4*>(&R[oYh + at]) = hh;
+      *reinterpret_cast<uint4*>(&R[oYl + at]) = ll;
+    } else {
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (i < valid)
+        v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(dy) +
+                                            row_of(i) * V + 8 * c8);
+      *reinterpret_cast<uint4*>(&R[oYh + at]) = v;
+    }
+  }
+  __syncthreads();
+
+  // ---- phase B: key channels; contractions over the value axis ------------
+  const bool kwave = wave < K / 16;
+  const int c = 16 * wave + r16;  // this lane's key channel in phases B and D
+  f32x4 dkA[4], dqA[4], dkeA[4];
+  float dgA[4][4], eA[4][4];
+  if (kwave) {
+    f32x4 aKc[4], aQr[4], aKg[4];
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib)
+      aKc[ib] = aQr[ib] = aKg[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float degl = 0.f;
+#pragma unroll
+    for (int s = 0; s < V / 32; ++s) {
+      float sv[8], dv8[8];
+      const float4* s0r = reinterpret_cast<const float4*>(S0 + size_t(c) * V + 32 * s + k8);
+      const float4* dsr = reinterpret_cast<const float4*>(dSa + size_t(c) * V + 32 * s + k8);
+      *reinterpret_cast<float4*>(sv) = s0r[0];
+      *reinterpret_cast<float4*>(sv + 4) = s0r[1];
+      *reinterpret_cast<float4*>(dv8) = dsr[0];
+      *reinterpret_cast<float4*>(dv8 + 4) = dsr[1];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) degl += sv[t] * dv8[t];
+      uint4 sh, sl, dh, dl;
+      split8(sv, sh, sl);
+      split8(dv8, dh, dl);
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) {
+        const int at = tile_at<V>(16 * ib + r16, 32 * s + k8);
+        const uint4 vh = ld8u(&R[oVh + at]), vl = ld8u(&R[oVl + at]);
+        aKc[ib] = mfma16(vh, dh, aKc[ib]);
+        aKc[ib] = mfma16(vl, dh, aKc[ib]);
+        aKc[ib] = mfma16(vh, dl, aKc[ib]);
+        const uint4 yh = ld8u(&R[oYh + at]);
+        aQr[ib] = mfma16(yh, sh, aQr[ib]);
+        aQr[ib] = mfma16(yh, sl, aQr[ib]);
+        if constexpr (F32DY) aQr[ib] = mfma16(ld8u(&R[oYl + at]), sh, aQr[ib]);
+        const uint4 wh = ld8u(&R[oWh + at]), wl = ld8u(&R[oWl + at]);
+        aKg[ib] = mfma16(wh, sh, aKg[ib]);
+        aKg[ib] = mfma16(wl, sh, aKg[ib]);
+        aKg[ib] = mfma16(wh, sl, aKg[ib]);
+      }
+    }
+    degl += __shfl_xor(degl, 16);
+    degl += __shfl_xor(degl, 32);
+    // The scan's cotangents through the gates (combined_backward.rs:284-313):
+    // d_k = d_kc⊙e^{G_last−G}, d_q = d_qr⊙e^G, d_ke = d_kg⊙e^G, and the
+    // pieces of d_G: −d_carry + (d_qr⊙qs + d_kg⊙ke)⊙e^G, plus d(G_last).
+    const float gl_c = PC ? Gc[(kL - 1) * GP + c] : 0.f;
+    float carry = 0.f, rowv[16];
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = rowi(ib, r);
+        const bool ok = i < valid;
+        float eg, ec, e;
+        if constexpr (PC) {
+          const float gci = Gc[i * GP + c];
+          eg = __expf(gci);
+          ec = __expf(gl_c - gci);
+          e = p.ew == 1 ? er_s[i] : (ok ? p.erase[row_of(i) * K + c] : 0.f);
+          eA[ib][r] = e;
+        } else {
+          eg = eg_s[i];
+          ec = ec_s[i];
+          e = er_s[i];
+        }
+        dkA[ib][r] = aKc[ib][r] * ec;
+        dqA[ib][r] = aQr[ib][r] * eg;
+        dkeA[ib][r] = -aKg[ib][r] * eg;
+        float val = 0.f;
+        if (gated) {
+          const float kv = ok ? bf16_to_f32(p.k[row_of(i) * K + c]) : 0.f;
+          const float qv = ok ? bf16_to_f32(p.q[row_of(i) * K + c]) : 0.f;
+          const float dcarry = aKc[ib][r] * kv * ec;
+          const float deg = aQr[ib][r] * qv * p.scale - aKg[ib][r] * kv * e;
+          carry += dcarry;
+          val = -dcarry + deg * eg;
+        }
+        if constexpr (PC) dgA[ib][r] = val;
+        rowv[4 * ib + r] = val;
+      }
+    if constexpr (PC) {
+      carry += __shfl_xor(carry, 16);
+      carry += __shfl_xor(carry, 32);
+      if (g4 == 0) cacc[c] = carry + degl * __expf(gl_c);
+    } else if (gated) {
+      atomicAdd(&racc[2][red_row], reduce16(rowv, lane));
+      // d(G_last) of the whole head: Σ d_carry + Σ_channels (dS⊙S₀)·e^{G_last}.
+      float tot = carry + (g4 == 0 ? degl * eg_s[kL - 1] : 0.f);
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) tot += __shfl_xor(tot, m);
+      if (lane == 0) atomicAdd(&racc[2][kL - 1], tot);
+    }
+  }
+  // dattn = dY·V'ᵀ on the lower tiles.
+  f32x4 dat[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int t = wave + 8 * u, ti = t >> 2, tj = t & 3;
+    dat[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (tj <= ti) {
+#pragma unroll
+      for (int s = 0; s < V / 32; ++s) {
+        const int aa = tile_at<V>(16 * ti + r16, 32 * s + k8);
+        const int ab = tile_at<V>(16 * tj + r16, 32 * s + k8);
+        const uint4 yh = ld8u(&R[oYh + aa]);
+        const uint4 bh = ld8u(&R[oVh + ab]), bl = ld8u(&R[oVl + ab]);
+        dat[u] = mfma16(yh, bh, dat[u]);
+        dat[u] = mfma16(yh, bl, dat[u]);
+        if constexpr (F32DY) dat[u] = mfma16(ld8u(&R[oYl + aa]), bh, dat[u]);
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- X, dV' rows and the dAqk layouts into LDS --------------------------
+  if (vwave) {
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int at = tile_at<V>(rowi(ib, r), col);
+        const uint16_t xh = bf_bits(X[ib][r]), dh = bf_bits(dV[ib][r]);
+        R[oXh + at] = xh;
+        R[oXl + at] = bf_bits(X[ib][r] - bf16_to_f32(xh));
+        R[oDh + at] = dh;
+        R[oDl + at] = bf_bits(dV[ib][r] - bf16_to_f32(dh));
+      }
+  }
+  // dAqk = tril(dattn) (per-head decay: ⊙ e^{Gᵢ−Gⱼ}, the head mask) as
+  // [i][j] and as [j][i] (per-head: times the readout scale).
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int t = wave + 8 * u, ti = t >> 2, tj = t & 3;
+    const int j = 16 * tj + r16;
+    float f[4], ft[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * ti + 4 * g4 + r;
+      float val = 0.f;
+      if (j <= i) {
+        val = dat[u][r];
+        if (!PC && gated) val *= __expf(Gc[i] - Gc[j]);
+      }
+      f[r] = val;
+      ft[r] = PC ? val : val * p.scale;
+      const int at = tile_at<kL>(i, j);
+      const uint16_t vh = bf_bits(val);
+      R[oA1h + at] = vh;
+      R[oA1l + at] = bf_bits(val - bf16_to_f32(vh));
+    }
+    uint2 hh, ll;
+    split4(ft, hh, ll);
+    const int at = tile_at<kL>(j, 16 * ti + 4 * g4);
+    *reinterpret_cast<uint2*>(&R[oA1th + at]) = hh;
+    *reinterpret_cast<uint2*>(&R[oA1tl + at]) = ll;
+  }
+  __syncthreads();
+
+  // ---- phase C: dT = dV'·Xᵀ (strict lower) --------------------------------
+  f32x4 dTt[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int t = wave + 8 * u, ti = t >> 2, tj = t & 3;
+    dTt[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (tj <= ti) {
+#pragma unroll
+      for (int s = 0; s < V / 32; ++s) {
+        const int aa = tile_at<V>(16 * ti + r16, 32 * s + k8);
+        const int ab = tile_at<V>(16 * tj + r16, 32 * s + k8);
+        const uint4 ah = ld8u(&R[oDh + aa]), al = ld8u(&R[oDl + aa]);
+        const uint4 bh = ld8u(&R[oXh + ab]), bl = ld8u(&R[oXl + ab]);
+        dTt[u] = mfma16(ah, bh, dTt[u]);
+        dTt[u] = mfma16(al, bh, dTt[u]);
+        dTt[u] = mfma16(ah, bl, dTt[u]);
+      }
+    }
+  }
+  __syncthreads();
+  // dTᵀ with dT's row index permuted (it is the contraction index of dTᵀ·T);
+  // T and Tᵀ staged again.
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int t = wave + 8 * u, ti = t >> 2, tj = t & 3;
+    float f[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int a = 16 * ti + 4 * g4 + r, bcol = 16 * tj + r16;
+      f[r] = bcol < a ? dTt[u][r] : 0.f;
+    }
+    uint2 hh, ll;
+    split4(f, hh, ll);
+    const int at = tile_at<kL>(16 * tj + r16, 32 * (ti >> 1) + 8 * g4 + 4 * (ti & 1));
+    *reinterpret_cast<uint2*>(&R[oDTh + at]) = hh;
+    *reinterpret_cast<uint2*>(&R[oDTl + at]) = ll;
+  }
+  stage_perm(R, oTh, p.T + o64, tid);
+  stage_perm(R, oTl, p.Tlo + o64, tid);
+  stage_perm(R, oTth, p.Tt + o64, tid);
+  stage_perm(R, oTtl, p.Ttl + o64, tid);
+  __syncthreads();
+  // M₁ᵀ = dTᵀ·T (all 16 tiles), stored as M₁ with its column index permuted.
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int t = wave + 8 * u, bt = t >> 2, it = t & 3;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int aa = tile_at<kL>(16 * bt + r16, 32 * kk + k8);
+      const int ab = tile_at<kL>(16 * it + r16, 32 * kk + k8);
+      const uint4 ah = ld8u(&R[oDTh + aa]), al = ld8u(&R[oDTl + aa]);
+      const uint4 bh = ld8u(&R[oTth + ab]), bl = ld8u(&R[oTtl + ab]);
+      acc = mfma16(ah, bh, acc);
+      acc = mfma16(al, bh, acc);
+      acc = mfma16(ah, bl, acc);
+    }
+    float f[4] = {acc[0], acc[1], acc[2], acc[3]};
+    uint2 hh, ll;
+    split4(f, hh, ll);
+    const int at = tile_at<kL>(16 * it + r16, 32 * (bt >> 1) + 8 * g4 + 4 * (bt & 1));
+    *reinterpret_cast<uint2*>(&R[oM1h + at]) = hh;
+    *reinterpret_cast<uint2*>(&R[oM1l + at]) = ll;
+  }
+  __syncthreads();
+  // dAkk = −tril(M₁·Tᵀ, −1); T[j][b] vanishes for b > j.
+  f32x4 dak[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int t = wave + 8 * u, ti = t >> 2, tj = t & 3;
+    dak[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (tj <= ti) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        if (kk > (tj >> 1)) continue;
+        const int aa = tile_at<kL>(16 * ti + r16, 32 * kk + k8);
+        const int ab = tile_at<kL>(16 * tj + r16, 32 * kk + k8);
+        const uint4 ah = ld8u(&R[oM1h + aa]), al = ld8u(&R[oM1l + aa]);
+        const uint4 bh = ld8u(&R[oTh + ab]), bl = ld8u(&R[oTl + ab]);
+        dak[u] = mfma16(ah, bh, dak[u]);
+        dak[u] = mfma16(al, bh, dak[u]);
+        dak[u] = mfma16(ah, bl, dak[u]);
+      }
+    }
+  }
+  __syncthreads();
+  // dAkk (per-head decay: ⊙ the head mask) as [i][j] and as [j][i]
+  // (per-head: times the erase gate of row i); Kᵀ and Qᵀ.
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int t = wave + 8 * u, ti = t >> 2, tj = t & 3;
+    const int j = 16 * tj + r16;
+    float ft[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * ti + 4 * g4 + r;
+      float val = 0.f;
+      if (j < i) {
+        val = -dak[u][r];
+        if (!PC && gated) val *= __expf(Gc[i] - Gc[j]);
+      }
+      ft[r] = PC ? val : val * er_s[i];
+      const int at = tile_at<kL>(i, j);
+      const uint16_t vh = bf_bits(val);
+      R[oA0h + at] = vh;
+      R[oA0l + at] = bf_bits(val - bf16_to_f32(vh));
+    }
+    uint2 hh, ll;
+    split4(ft, hh, ll);
+    const int at = tile_at<kL>(j, 16 * ti + 4 * g4);
+    *reinterpret_cast<uint2*>(&R[oA0th + at]) = hh;
+    *reinterpret_cast<uint2*>(&R[oA0tl + at]) = ll;
+  }
+  for (int idx = tid; idx < kL * K / 8; idx += kNT) {
+    const int i = idx / (K / 8), c8 = idx % (K / 8);
+    uint4 kv = make_uint4(0u, 0u, 0u, 0u), qv = kv;
+    if (i < valid) {
+      kv = *reinterpret_cast<const uint4*>(p.k + row_of(i) * K + 8 * c8);
+      qv = *reinterpret_cast<const uint4*>(p.q + row_of(i) * K + 8 * c8);
+    }
+    const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, qw[4] = {qv.x, qv.y, qv.z, qv.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int at = tile_at<kL>(8 * c8 + e, i);
+      R[oKC + at] = uint16_t(kw[e >> 1] >> (16 * (e & 1)));
+      R[oQC + at] = uint16_t(qw[e >> 1] >> (16 * (e & 1)));
+    }
+  }
+  __syncthreads();
+
+  // ---- phase D: score backward, gates, stores -----------------------------
+  if (kwave) {
+    if constexpr (!PC) {
+      // head_scores_backward (combined_backward.rs:376-416) with drkk = dAkk⊙M,
+      // drqk = dAqk⊙M: d_ke += drkk·K, d_qs += drqk·K, d_k += drkkᵀ·ke +
+      // drqkᵀ·qs. The d_G term Σⱼ d_diff[i][j] − d_diff[j][i] of
+      // d_diff = (dAkk⊙KeKᵀ + dAqk⊙QsKᵀ)⊙M equals, per row, Σ_c of
+      // ke⊙(drkk·K) + qs⊙(drqk·K) − k⊙(drkkᵀ·ke + drqkᵀ·qs).
+      f32x4 SK1[4], SQ1[4], SK2[4], SQ2[4];
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib)
+        SK1[ib] = SQ1[ib] = SK2[ib] = SQ2[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const uint4 kb = ld8u(&R[oKC + tile_at<kL>(c, 32 * s + k8)]);
+        const uint4 qb = ld8u(&R[oQC + tile_at<kL>(c, 32 * s + k8)]);
+#pragma unroll
+        for (int ib = 0; ib < 4; ++ib) {
+          const int at = tile_at<kL>(16 * ib + r16, 32 * s + k8);
+          if (s <= (ib >> 1)) {
+            SK1[ib] = mfma16(ld8u(&R[oA0h + at]), kb, SK1[ib]);
+            SK1[ib] = mfma16(ld8u(&R[oA0l + at]), kb, SK1[ib]);
+            SQ1[ib] = mfma16(ld8u(&R[oA1h + at]), kb, SQ1[ib]);
+            SQ1[ib] = mfma16(ld8u(&R[oA1l + at]), kb, SQ1[ib]);
+          }
+          if (s >= (ib >> 1)) {
+            SK2[ib] = mfma16(ld8u(&R[oA0th + at]), kb, SK2[ib]);
+            SK2[ib] = mfma16(ld8u(&R[oA0tl + at]), kb, SK2[ib]);
+            SQ2[ib] = mfma16(ld8u(&R[oA1th + at]), qb, SQ2[ib]);
+            SQ2[ib] = mfma16(ld8u(&R[oA1tl + at]), qb, SQ2[ib]);
+          }
+        }
+      }
+      float rowv[16];
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) {
+        float kv[4], qv[4];
+        {
+          const uint2 k4 = *reinterpret_cast<const uint2*>(&R[oKC + tile_at<kL>(c, 16 * ib + 4 * g4)]);
+          const uint2 q4 = *reinterpret_cast<const uint2*>(&R[oQC + tile_at<kL>(c, 16 * ib + 4 * g4)]);
+          kv[0] = lo_f(k4.x); kv[1] = hi_f(k4.x); kv[2] = lo_f(k4.y); kv[3] = hi_f(k4.y);
+          qv[0] = lo_f(q4.x); qv[1] = hi_f(q4.x); qv[2] = lo_f(q4.y); qv[3] = hi_f(q4.y);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = rowi(ib, r);
+          dkeA[ib][r] += SK1[ib][r];
+          dqA[ib][r] += SQ1[ib][r];
+          dkA[ib][r] += SK2[ib][r] + SQ2[ib][r];
+          rowv[4 * ib + r] = er_s[i] * kv[r] * SK1[ib][r] + p.scale * qv[r] * SQ1[ib][r] -
+                             kv[r] * (SK2[ib][r] + SQ2[ib][r]);
+        }
+      }
+      if (gated) atomicAdd(&racc[2][red_row], reduce16(rowv, lane));
+    } else {
+      // channel_scores_backward (combined_backward.rs:421-513): per row block
+      // pb with reference row r = 16·pb + 8, row factors e^{min(G[i]−G[r], 48)}
+      // and column factors k[j]·e^{min(G[r]−G[j], 48)} (zero past block pb).
+#pragma unroll
+      for (int pb = 0; pb < 4; ++pb) {
+        const float gref = Gc[(16 * pb + 8) * GP + c];
+        // d(ke⊙rf), d(qs⊙rf) of the block's rows = dAkk, dAqk rows · colb.
+        f32x4 drke = {0.f, 0.f, 0.f, 0.f}, drq = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          if (s > (pb >> 1)) continue;
+          float kf[8], cb[8];
+          unpack8(ld8u(&R[oKC + tile_at<kL>(c, 32 * s + k8)]), kf);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            const int j = 32 * s + k8 + t;
+            cb[t] = (j >> 4) <= pb ? kf[t] * __expf(fminf(gref - Gc[j * GP + c], kMaxExp)) : 0.f;
+          }
+          uint4 bh, bl;
+          split8(cb, bh, bl);
+          const int at = tile_at<kL>(16 * pb + r16, 32 * s + k8);
+          const uint4 a0h = ld8u(&R[oA0h + at]), a1h = ld8u(&R[oA1h + at]);
+          drke = mfma16(a0h, bh, drke);
+          drke = mfma16(ld8u(&R[oA0l + at]), bh, drke);
+          drke = mfma16(a0h, bl, drke);
+          drq = mfma16(a1h, bh, drq);
+          drq = mfma16(ld8u(&R[oA1l + at]), bh, drq);
+          drq = mfma16(a1h, bl, drq);
+        }
+        // dcol[j][c] = Σ_{i∈pb} dAkk[i][j]·(ke⊙rf)[i][c] + dAqk[i][j]·(qs⊙rf)[i][c]
+        // as one 32-deep step: positions 0..15 the dAkk rows, 16..31 the dAqk rows.
+        uint4 rh, rl;
+        {
+          const bool isq = g4 >= 2;
+          const int i0 = 16 * pb + (k8 & 15);
+          float xf[8], rv[8];
+          unpack8(ld8u(&R[(isq ? oQC : oKC) + tile_at<kL>(c, i0)]), xf);
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            const int i = i0 + t;
+            const float rf = __expf(fminf(Gc[i * GP + c] - gref, kMaxExp));
+            const float e = isq ? p.scale
+                                : (p.ew == 1 ? er_s[i]
+                                             : (i < valid ? p.erase[row_of(i) * K + c] : 0.f));
+            rv[t] = xf[t] * e * rf;
+          }
+          split8(rv, rh, rl);
+        }
+        f32x4 dcol[4];
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+          dcol[jb] = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (jb > pb) continue;
+          const int at = tile_at<kL>(16 * jb + r16, 16 * pb + (k8 & 15));
+          const uint4 ah = ld8u(&R[(g4 >= 2 ? oA1th : oA0th) + at]);
+          const uint4 al = ld8u(&R[(g4 >= 2 ? oA1tl : oA0tl) + at]);
+          dcol[jb] = mfma16(ah, rh, dcol[jb]);
+          dcol[jb] = mfma16(al, rh, dcol[jb]);
+          dcol[jb] = mfma16(ah, rl, dcol[jb]);
+        }
+        // The block's rows: d_ke, d_qs through the row factor; d_G of its
+        // exponent where the clamp does not bind.
+        float drsum = 0.f;
+        {
+          float kv[4], qv[4];
+          const uint2 k4 = *reinterpret_cast<const uint2*>(&R[oKC + tile_at<kL>(c, 16 * pb + 4 * g4)]);
+          const uint2 q4 = *reinterpret_cast<const uint2*>(&R[oQC + tile_at<kL>(c, 16 * pb + 4 * g4)]);
+          kv[0] = lo_f(k4.x); kv[1] = hi_f(k4.x); kv[2] = lo_f(k4.y); kv[3] = hi_f(k4.y);
+          qv[0] = lo_f(q4.x); qv[1] = hi_f(q4.x); qv[2] = lo_f(q4.y); qv[3] = hi_f(q4.y);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int i = rowi(pb, r);
+            const float arg = Gc[i * GP + c] - gref;
+            const float rf = __expf(fminf(arg, kMaxExp));
+            dkeA[pb][r] += drke[r] * rf;
+            dqA[pb][r] += drq[r] * rf;
+            const float drow = drke[r] * kv[r] * eA[pb][r] + drq[r] * qv[r] * p.scale;
+            const float dra = arg < kMaxExp ? drow * rf : 0.f;
+            dgA[pb][r] += dra;
+            drsum += dra;
+          }
+        }
+        // The columns: d_k through the column factor, d_G of its exponent.
+        float dref = 0.f;
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+          if (jb > pb) continue;
+          const uint2 k4 = *reinterpret_cast<const uint2*>(&R[oKC + tile_at<kL>(c, 16 * jb + 4 * g4)]);
+          const float kv[4] = {lo_f(k4.x), hi_f(k4.x), lo_f(k4.y), hi_f(k4.y)};
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int j = rowi(jb, r);
+            const float arg = gref - Gc[j * GP + c];
+            const float ce = __expf(fminf(arg, kMaxExp));
+            dkA[jb][r] += dcol[jb][r] * ce;
+            const float tv = arg < kMaxExp ? dcol[jb][r] * kv[r] * ce : 0.f;
+            dgA[jb][r] -= tv;
+            dref += tv;
+          }
+        }
+        // d_G of the reference row: the column exponents' total minus the row
+        // exponents' (both are relative to it).
+        float tot = dref - drsum;
+        tot += __shfl_xor(tot, 16);
+        tot += __shfl_xor(tot, 32);
+        if (g4 == 2) dgA[pb][0] += tot;
+      }
+    }
+    // Front end (combined_backward.rs:153-188) and the stores.
+    TG* gq = static_cast<TG*>(p.dq);
+    TG* gk = static_cast<TG*>(p.dk);
+    float rde[16];
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib) {
+      const uint2 k4 = *reinterpret_cast<const uint2*>(&R[oKC + tile_at<kL>(c, 16 * ib + 4 * g4)]);
+      const float kv[4] = {lo_f(k4.x), hi_f(k4.x), lo_f(k4.y), hi_f(k4.y)};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = rowi(ib, r);
+        const bool ok = i < valid;
+        const float e = PC ? eA[ib][r] : er_s[i];
+        if (ok) {
+          st(gq, row_of(i) * K + c, dqA[ib][r] * p.scale);
+          st(gk, row_of(i) * K + c, dkA[ib][r] + dkeA[ib][r] * e);
+        }
+        rde[4 * ib + r] = dkeA[ib][r] * kv[r];
+        if (p.ew != 1 && ok) p.derase[row_of(i) * K + c] = rde[4 * ib + r];
+      }
+    }
+    if (p.ew == 1) atomicAdd(&racc[1][red_row], reduce16(rde, lane));
+  }
+  __syncthreads();
+  if constexpr (PC) {
+    // d_G per channel: (i = L−1 also takes d(G_last)), then the reverse
+    // cumulative sum over the chunk (the cotangent of g from that of G).
+    if (kwave)
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Gc[rowi(ib, r) * GP + c] = dgA[ib][r];
+    __syncthreads();
+    for (int cc = tid; cc < K; cc += kNT) {
+      float acc = cacc[cc];
+      for (int i = kL - 1; i >= 0; --i) {
+        acc += Gc[i * GP + cc];
+        if (i < valid) p.dg[row_of(i) * K + cc] = acc;
+      }
+    }
+  } else if (gated && tid == 0) {
+    float acc = 0.f;
+    for (int i = kL - 1; i >= 0; --i) {
+      acc += racc[2][i];
+      if (i < valid) p.dg[row_of(i)] = acc;
+    }
+  }
+  if (tid < valid) {
+    if (p.ww == 1) p.dwrite[row_of(tid)] = racc[0][tid];
+    if (p.ew == 1) p.derase[row_of(tid)] = racc[1][tid];
+  }
+}
+
+}  // namespace
+
+bool mfma_chunk_bwd_supported(const Dims& d, int qkv_dtype) {
+  return mfma_fwd_supported(d, qkv_dtype, DN_BF16) && (d.V == 64 || d.V == 128);
+}
+
+hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const void* q,
+                          const void* k, const void* v, const float* erase, const float* write,
+                          const float* g, const float* states, const float* ds_after, void* dq,
+                          void* dk, void* dv, float* derase, float* dwrite, float* dg,
+                          const MfmaTiles& tiles, hipStream_t stream) {
+  CbParams p;
+  p.S = d.S;
+  p.H = d.H;
+  p.N = d.N;
+  p.ew = d.ew;
+  p.ww = d.ww;
+  p.gated = d.dw > 0;
+  p.scale = d.scale;
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.erase = erase;
+  p.write = write;
+  p.g = g;
+  p.dy = dy;
+  p.T = tiles.T;
+  p.Tlo = tiles.Tlo;
+  p.Tt = tiles.Tt;
+  p.Ttl = tiles.Ttl;
+  p.AtT = tiles.AtT;
+  p.Kc = tiles.Kc;
+  p.Kg = tiles.Kg;
+  p.Kglo = tiles.Kglo;
+  p.gc = tiles.gc;
+  p.states = states;
+  p.ds_after = ds_after;
+  p.dq = dq;
+  p.dk = dk;
+  p.dv = dv;
+  p.derase = derase;
+  p.dwrite = dwrite;
+  p.dg = dg;
+  const size_t G = size_t(d.B) * d.N * d.H;
+  const bool pc = d.dw == d.K && d.K > 1;
+  const bool f32 = grad_dtype == DN_F32;
+  ProfScope ps("dn_mfma_chunk_bwd", stream);
+#define DN_CB(KD, VD, PCV, TG)                                                                  \
+  hipLaunchKernelGGL((mfma_chunk_bwd_kernel<KD, VD, PCV, TG>), dim3(unsigned(G)), dim3(kNT), 0, \
+                     stream, p)
+#define DN_CB_T(KD, VD, PCV)              \
+  do {                                    \
+    if (f32) DN_CB(KD, VD, PCV, float);   \
+    else DN_CB(KD, VD, PCV, bf16);        \
+  } while (0)
+#define DN_CB_P(KD, VD)                   \
+  do {                                    \
+    if (pc) DN_CB_T(KD, VD, true);        \
+    else DN_CB_T(KD, VD, false);          \
+  } while (0)
+  if (d.K == 128) {
+    if (d.V == 128) DN_CB_P(128, 128); else DN_CB_P(128, 64);
+  } else {
+    if (d.V == 128) DN_CB_P(64, 128); else DN_CB_P(64, 64);
+  }
+#undef DN_CB_P
+#undef DN_CB_T
+#undef DN_CB
+  return hipGetLastError();
+}
+
+}  // namespace dn

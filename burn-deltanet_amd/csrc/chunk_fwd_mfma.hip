@@ -36,36 +36,14 @@
 #include <algorithm>
 
 #include "dn_common.hpp"
+#include "mfma_util.hpp"
 
 namespace dn {
 namespace {
 
-typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8;
-typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4;
-
 constexpr int kL = 64;        // chunk length
 constexpr int kThreads = 256;  // 4 waves
 constexpr int kBV = 64;       // head_v_dim granularity of the MFMA path
-
-__device__ inline f32x4 mfma16(const bf16x8& a, const bf16x8& b, const f32x4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
-
-typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 bf16x2;
-
-__device__ inline bf16x8 ld8(const uint16_t* p) { return *reinterpret_cast<const bf16x8*>(p); }
-
-// Two floats → packed bf16 (round to nearest even), one v_cvt_pk_bf16_f32.
-__device__ inline uint32_t pk_bf16(float a, float b) {
-  const bf16x2 v = {(__bf16)a, (__bf16)b};
-  return __builtin_bit_cast(uint32_t, v);
-}
-__device__ inline float lo_f(uint32_t u) { return __uint_as_float(u << 16); }
-__device__ inline float hi_f(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
-
-__device__ inline f32x4 mfma_f32(float a, float b, const f32x4& c) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
-}
 
 // Value of lane `src` of each group of four lanes, to the whole group (DPP
 // quad_perm); `src` folds to a constant once the caller's loop is unrolled.
@@ -644,36 +622,8 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p) {
 // ---------------------------------------------------------------------------
 // scan
 // ---------------------------------------------------------------------------
-// Operand tiles in LDS. Within every 32-deep k-step the contraction index is
-// stored permuted so that the 8 values an MFMA lane supplies (positions
-// 8q..8q+7 of the step) are rows 4q..4q+3 and 16+4q..16+4q+3 of it — exactly
-// the rows a 16×16 accumulator lane holds in two vertically adjacent tiles.
-// Accumulator tiles (S, X, V') thereby become MFMA operands in place, with
-// no LDS round trip. 16-byte chunks are XOR-swizzled by row (conflict-free
-// fragment reads without padding).
-__device__ inline int perm_pos(int k) {
-  const int m = k & 31;
-  return (k & ~31) + 8 * ((m & 15) >> 2) + 4 * (m >> 4) + (m & 3);
-}
-template <int COLS>
-__device__ inline int tile_at(int row, int pos) {
-  // The 16 rows of a fragment read land in 16 distinct 16-byte bank slots.
-  const int sw = COLS >= 128 ? (row & 15) : ((row >> 1) & 7);
-  return row * COLS + (((pos >> 3) ^ sw) << 3) + (pos & 7);
-}
-
-// Two vertically adjacent 16×16 accumulator tiles → one bf16 operand
-// fragment of the permuted layout (hi part, and optionally the lo part).
-__device__ inline uint4 frag_hi(const f32x4& a, const f32x4& b) {
-  return make_uint4(pk_bf16(a[0], a[1]), pk_bf16(a[2], a[3]), pk_bf16(b[0], b[1]),
-                    pk_bf16(b[2], b[3]));
-}
-__device__ inline uint4 frag_lo(const f32x4& a, const f32x4& b, const uint4& h) {
-  return make_uint4(pk_bf16(a[0] - lo_f(h.x), a[1] - hi_f(h.x)),
-                    pk_bf16(a[2] - lo_f(h.y), a[3] - hi_f(h.y)),
-                    pk_bf16(b[0] - lo_f(h.z), b[1] - hi_f(h.z)),
-                    pk_bf16(b[2] - lo_f(h.w), b[3] - hi_f(h.w)));
-}
+// The staged operand tiles use the permuted contraction index of perm_pos
+// (mfma_util.hpp): S, X and V' accumulator tiles feed the MFMAs in place.
 
 // ST (states mode, for the backward's recompute): the fp32 state entering
 // each chunk is written to p.states and y is not written.
@@ -1442,6 +1392,27 @@ MfmaParams make_params(const Dims& d, const void* q, const void* k, const void* 
   return p;
 }
 
+// The backward's transposed tiles, after the forward's workspace.
+BwdTiles carve_bwd_tiles(const Dims& d, void* ws) {
+  const size_t G = size_t(d.B) * d.N * d.H, K = size_t(d.K);
+  char* base = static_cast<char*>(ws) + mfma_fwd_workspace(d);
+  BwdTiles bt;
+  bt.Tt = reinterpret_cast<uint16_t*>(base);
+  base += region(G * kL * kL * 2);
+  bt.Ttl = reinterpret_cast<uint16_t*>(base);
+  base += region(G * kL * kL * 2);
+  bt.AtT = reinterpret_cast<uint16_t*>(base);
+  base += region(G * kL * kL * 2);
+  bt.Kc = reinterpret_cast<uint16_t*>(base);
+  base += region(G * kL * K * 2);
+  bt.QgT = reinterpret_cast<uint16_t*>(base);
+  base += region(G * K * kL * 2);
+  bt.KgT = reinterpret_cast<uint16_t*>(base);
+  base += region(G * K * kL * 2);
+  bt.egl = reinterpret_cast<float*>(base);
+  return bt;
+}
+
 hipError_t launch_intra(const MfmaParams& p, const Dims& d, hipStream_t stream) {
   const size_t G = size_t(d.B) * d.N * d.H;
   if (per_channel(d)) {
@@ -1537,6 +1508,13 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
   return launch_scan<false>(p, d, y_dtype == DN_BF16, stream);
 }
 
+MfmaTiles mfma_bwd_tiles(const Dims& d, void* ws) {
+  const MfmaParams p =
+      make_params(d, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, ws);
+  const BwdTiles bt = carve_bwd_tiles(d, ws);
+  return MfmaTiles{p.T, p.Tlo, bt.Tt, bt.Ttl, bt.AtT, bt.Kc, p.Kg, p.Kglo, p.gc};
+}
+
 size_t mfma_bwd_workspace(const Dims& d) {
   const size_t G = size_t(d.B) * d.N * d.H, K = size_t(d.K);
   return mfma_fwd_workspace(d) + 3 * region(G * kL * kL * 2) + region(G * kL * K * 2) +
@@ -1548,7 +1526,7 @@ hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
                           const float* erase, const float* write, const float* g,
                           const float* state_in, float* states, float* ds_after, float* dstate,
                           void* ws, hipStream_t stream) {
-  const size_t G = size_t(d.B) * d.N * d.H, K = size_t(d.K);
+  const size_t G = size_t(d.B) * d.N * d.H;
   // The forward recompute in states mode: its final state lands in dstate,
   // which the reverse scan overwrites.
   MfmaParams p = make_params(d, q, k, v, erase, write, g, state_in, nullptr, dstate, ws);
@@ -1556,21 +1534,7 @@ hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
   hipError_t e = launch_intra(p, d, stream);
   if (e != hipSuccess) return e;
   if ((e = launch_scan<true>(p, d, false, stream)) != hipSuccess) return e;
-  char* base = static_cast<char*>(ws) + mfma_fwd_workspace(d);
-  BwdTiles bt;
-  bt.Tt = reinterpret_cast<uint16_t*>(base);
-  base += region(G * kL * kL * 2);
-  bt.Ttl = reinterpret_cast<uint16_t*>(base);
-  base += region(G * kL * kL * 2);
-  bt.AtT = reinterpret_cast<uint16_t*>(base);
-  base += region(G * kL * kL * 2);
-  bt.Kc = reinterpret_cast<uint16_t*>(base);
-  base += region(G * kL * K * 2);
-  bt.QgT = reinterpret_cast<uint16_t*>(base);
-  base += region(G * K * kL * 2);
-  bt.KgT = reinterpret_cast<uint16_t*>(base);
-  base += region(G * K * kL * 2);
-  bt.egl = reinterpret_cast<float*>(base);
+  const BwdTiles bt = carve_bwd_tiles(d, ws);
   const bool pc = per_channel(d);
   {
     ProfScope ps("dn_mfma_bwd_tiles", stream);

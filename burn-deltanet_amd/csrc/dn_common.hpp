@@ -99,6 +99,22 @@ hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
                           const float* erase, const float* write, const float* g,
                           const float* state_in, float* states, float* ds_after, float* dstate,
                           void* ws, hipStream_t stream);
+// The per-chunk tiles mfma_bwd_scans leaves in its workspace: T (hi, lo) and
+// Tᵀ (hi, lo), attnᵀ [G][64][64]; kc = e^{G_last−G}⊙K [G][64][K]; per-channel
+// decay: kg = e⊙e^G⊙K hi, lo [G][64][K]; per-head: the cumulative gate [G][64].
+struct MfmaTiles {
+  const uint16_t *T, *Tlo, *Tt, *Ttl, *AtT, *Kc, *Kg, *Kglo;
+  const float* gc;
+};
+MfmaTiles mfma_bwd_tiles(const Dims& d, void* ws);
+// The chunk-local gradients on MFMA (head_v_dim 64 or 128 on top of the
+// shapes of mfma_fwd_supported), after mfma_bwd_scans.
+bool mfma_chunk_bwd_supported(const Dims& d, int qkv_dtype);
+hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const void* q,
+                          const void* k, const void* v, const float* erase, const float* write,
+                          const float* g, const float* states, const float* ds_after, void* dq,
+                          void* dk, void* dv, float* derase, float* dwrite, float* dg,
+                          const MfmaTiles& tiles, hipStream_t stream);
 
 // Per-kernel HIP-event timing (dn_profile_enable): a scope records a start
 // event on construction and a stop event on destruction, on `stream`.

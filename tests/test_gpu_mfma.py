@@ -194,14 +194,26 @@ BWD_CASES = [
     (1, 256, 2, 128, 128, (128, 128)),
     (1, 130, 2, 128, 64, (1, 64)),
     (2, 128, 2, 64, 64, (64, 1)),
+    # a repeated key in every chunk (the retrieval cancels), β ∈ (0, 2)
+    (1, 256, 2, 128, 128, "head", {"const_keys": True}),
+    (1, 256, 2, 128, 128, (128, 128), {"const_keys": True}),
+    (1, 192, 2, 128, 128, "head", {"beta_scale": 2.0}),
+    # head_v_dim 256: MFMA scans, chunk-local gradients on the generic kernel
+    (1, 128, 2, 128, 256, "head"),
 ]
 
 
-def bwd_inputs(rng, B, S, H, K, V, gates):
+def bwd_inputs(rng, B, S, H, K, V, gates, opts=None):
+    opts = opts or {}
+    beta_scale = opts.get("beta_scale", 1.0)
     if gates is None or gates == "head":
-        args = gdn_inputs(rng, B, S, H, K, V, gated=gates == "head", state_std=0.05)
+        args = gdn_inputs(rng, B, S, H, K, V, gated=gates == "head", state_std=0.05,
+                          beta_scale=beta_scale)
     else:
-        args = gdn2_inputs(rng, B, S, H, K, V, gates[0], gates[1], state_std=0.05)
+        args = gdn2_inputs(rng, B, S, H, K, V, gates[0], gates[1], state_std=0.05,
+                           beta_scale=beta_scale)
+    if opts.get("const_keys"):
+        args[1] = np.repeat(args[1][:, :1], S, axis=1)
     dy = rng.standard_normal((B, S, H, V))
     ds = rng.standard_normal((B, H, K, V)) * 0.5
     return args, dy, ds
@@ -210,9 +222,9 @@ def bwd_inputs(rng, B, S, H, K, V, gates):
 @pytest.mark.parametrize("case", BWD_CASES)
 @pytest.mark.parametrize("dy_dtype", [torch.float32, torch.bfloat16])
 def test_mfma_bwd_matches_oracle(rng, case, dy_dtype):
-    B, S, H, K, V, gates = case
+    B, S, H, K, V, gates = case[:6]
     announce(f"mfma bwd {case} dy {dy_dtype}")
-    args, dy, ds = bwd_inputs(rng, B, S, H, K, V, gates)
+    args, dy, ds = bwd_inputs(rng, B, S, H, K, V, gates, case[6] if len(case) > 6 else None)
     g_args = to_gpu(args, torch.bfloat16)
     tdy = torch.tensor(dy, dtype=torch.float32, device=DEV).to(dy_dtype)
     tds = torch.tensor(ds, dtype=torch.float32, device=DEV)
