@@ -682,6 +682,8 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   // meet zero factors), which keeps every iteration's memory operations
   // identical and the compiler's in-order vmcnt waits exact.
   const int HK = p.H * K;
+  const uint32_t kcol = uint32_t(8 * (tid % (K / 8)));
+  const uint32_t koff = uint32_t((tid / (K / 8)) * HK) + kcol;
   uint4 pf[NPF];
   float pgc, pgl, per, pwr, pch;
   auto ld16 = [](const uint16_t* base, uint32_t elems) {
@@ -704,9 +706,10 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
           const uint16_t* base = which == 0 ? p.Kg : which == 1 ? p.Qg : p.Kglo;
           pf[m] = ld16(base + cid * kL * K + 8 * (i0 - which * (kL * K / 8)), 8u * tid);
         } else {
-          const int row = tid / (K / 8) + (i0 - which * (kL * K / 8)) / (K / 8);
-          const uint32_t off = uint32_t(min(row, rl - 1) * HK + 8 * (tid % (K / 8)));
-          pf[m] = ld16((which ? p.q : p.k) + row0 * K, off);
+          // Row tid/(K/8) + rowc, clamped through its (monotonic) offset.
+          const uint32_t rowc = uint32_t((i0 - which * (kL * K / 8)) / (K / 8));
+          const uint32_t klast = uint32_t((rl - 1) * HK) + kcol;
+          pf[m] = ld16((which ? p.q : p.k) + row0 * K, min(koff + rowc * uint32_t(HK), klast));
         }
       } else if (i0 < (NKQ * kL * K + 3 * kL * kL) / 8) {
         const int ii0 = i0 - NKQ * kL * K / 8;
@@ -783,18 +786,23 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
     }
   };
   // v[t][jl] for this lane's 16 tokens (4 row blocks × 4), as bf16 pairs.
+  // Offsets grow with the token, so clamping the token to the chunk's last
+  // row is clamping the offset: min(t·HV + jl, (rl−1)·HV + jl), where
+  // t·HV + jl = vlane + (16·tb + r)·HV with a per-lane vlane.
   uint32_t vA[4][2];
   const int HV = p.H * p.V;
+  const uint32_t vlane = uint32_t(4 * q4 * HV + jl);
   auto load_v = [&](int n) {
     const int rl = min(kL, p.S - n * kL);
     const uint16_t* vb = p.v + (bh_row0 + size_t(n) * kL * tokstride) * p.V;
+    const uint32_t vlast = uint32_t((rl - 1) * HV) + uint32_t(jl);
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
       for (int r2 = 0; r2 < 2; ++r2) {
-        const int t0 = 16 * tb + 4 * q4 + 2 * r2;
-        const uint32_t o0 = uint32_t(min(t0, rl - 1) * HV + jl);
-        const uint32_t o1 = uint32_t(min(t0 + 1, rl - 1) * HV + jl);
+        const uint32_t t0 = uint32_t(16 * tb + 2 * r2);
+        const uint32_t o0 = min(vlane + t0 * uint32_t(HV), vlast);
+        const uint32_t o1 = min(vlane + (t0 + 1) * uint32_t(HV), vlast);
         const uint32_t x0 = *reinterpret_cast<const uint16_t*>(
             reinterpret_cast<const char*>(vb) + 2u * o0);
         const uint32_t x1 = *reinterpret_cast<const uint16_t*>(
@@ -1518,7 +1526,8 @@ MfmaTiles mfma_bwd_tiles(const Dims& d, void* ws) {
 size_t mfma_bwd_workspace(const Dims& d) {
   const size_t G = size_t(d.B) * d.N * d.H, K = size_t(d.K);
   return mfma_fwd_workspace(d) + 3 * region(G * kL * kL * 2) + region(G * kL * K * 2) +
-         2 * region(G * K * kL * 2) + region(G * K * 4);
+         2 * region(G * K * kL * 2) + region(G * K * 4) +
+         region(size_t(d.B) * d.H * K * d.V * 4);  // the recompute's final state (unused)
 }
 
 hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
@@ -1526,21 +1535,26 @@ hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
                           const float* erase, const float* write, const float* g,
                           const float* state_in, float* states, float* ds_after, float* dstate,
                           void* ws, hipStream_t stream) {
-  const size_t G = size_t(d.B) * d.N * d.H;
-  // The forward recompute in states mode: its final state lands in dstate,
-  // which the reverse scan overwrites.
-  MfmaParams p = make_params(d, q, k, v, erase, write, g, state_in, nullptr, dstate, ws);
+  const size_t G = size_t(d.B) * d.N * d.H, K = size_t(d.K);
+  // The forward recompute (states mode) and the reverse scan need nothing
+  // from each other: after the intra kernel, the reverse scan and its tiles
+  // run on the device's second stream, overlapping the recompute (each scan
+  // alone fills few CUs when batch × heads is small). The recompute's final
+  // state goes to a scratch region of the workspace.
+  const BwdTiles bt = carve_bwd_tiles(d, ws);
+  float* s_scratch = reinterpret_cast<float*>(reinterpret_cast<char*>(bt.egl) + region(G * K * 4));
+  MfmaParams p = make_params(d, q, k, v, erase, write, g, state_in, nullptr, s_scratch, ws);
   p.states = states;
   hipError_t e = launch_intra(p, d, stream);
   if (e != hipSuccess) return e;
-  if ((e = launch_scan<true>(p, d, false, stream)) != hipSuccess) return e;
-  const BwdTiles bt = carve_bwd_tiles(d, ws);
+  hipStream_t side = nullptr;
+  if ((e = side_fork(stream, &side)) != hipSuccess) return e;
   const bool pc = per_channel(d);
   {
-    ProfScope ps("dn_mfma_bwd_tiles", stream);
+    ProfScope ps("dn_mfma_bwd_tiles", side);
 #define DN_TILES(KD, PCV)                                                                   \
   hipLaunchKernelGGL((mfma_bwd_tiles_kernel<KD, PCV>), dim3(unsigned(G)), dim3(kThreads), 0, \
-                     stream, p, bt)
+                     side, p, bt)
     if (d.K == 128) {
       if (pc) DN_TILES(128, true); else DN_TILES(128, false);
     } else {
@@ -1552,9 +1566,10 @@ hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
   RevParams rp{d.B, d.S, d.H, d.V, d.N, dy, dstate_final, ds_after, dstate, bt};
   const int waves = scan_waves(d);
   const unsigned blocks = unsigned(((d.B * d.H + 7) / 8) * 8 * (d.V / (16 * waves)));
-  ProfScope ps("dn_mfma_rev_scan", stream);
+  {
+  ProfScope ps("dn_mfma_rev_scan", side);
 #define DN_REV(KD, TG, W) \
-  hipLaunchKernelGGL((mfma_rev_scan_kernel<KD, TG, W>), dim3(blocks), dim3(64 * W), 0, stream, rp)
+  hipLaunchKernelGGL((mfma_rev_scan_kernel<KD, TG, W>), dim3(blocks), dim3(64 * W), 0, side, rp)
 #define DN_REV_W(KD, TG) \
   do { if (waves == 8) DN_REV(KD, TG, 8); else if (waves == 4) DN_REV(KD, TG, 4); else DN_REV(KD, TG, 2); } while (0)
   if (d.K == 128) {
@@ -1564,7 +1579,10 @@ hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
   }
 #undef DN_REV_W
 #undef DN_REV
-  return hipGetLastError();
+  }
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  if ((e = launch_scan<true>(p, d, false, stream)) != hipSuccess) return e;
+  return side_join(stream);
 }
 
 }  // namespace dn

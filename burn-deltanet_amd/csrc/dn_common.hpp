@@ -128,6 +128,12 @@ struct ProfScope {
 // Compute units of the current device (cached per device; 256 on MI355X).
 int device_cu_count();
 
+// Fork / join with the current device's second stream: work launched on
+// *side after side_fork(main, side) runs after what `main` already holds and
+// may overlap what `main` gets next; side_join(main) makes `main` wait for it.
+hipError_t side_fork(hipStream_t main, hipStream_t* side);
+hipError_t side_join(hipStream_t main);
+
 // NaN/Inf guard: sets *flag (device int) to 1 if any element is not finite.
 hipError_t launch_nonfinite_scan(const void* p, size_t n, int dtype, int* flag,
                                  hipStream_t stream);

@@ -2,6 +2,7 @@
 // src/delta/path.rs:198-207, compiled in by its check-nan/check-inf features).
 
 #include <atomic>
+#include <mutex>
 
 #include "dn_common.hpp"
 
@@ -19,6 +20,48 @@ __global__ __launch_bounds__(256) void nonfinite_kernel(const T* p, size_t n, in
 }
 
 }  // namespace
+
+namespace {
+// One second stream per device (default priority, non-blocking) and its
+// fork / join events, created on first use and kept until the process ends.
+struct Side {
+  hipStream_t s = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+constexpr int kMaxSides = 64;
+std::mutex side_mu;
+Side sides[kMaxSides];
+}  // namespace
+
+hipError_t side_fork(hipStream_t main, hipStream_t* side) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxSides) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(side_mu);
+  Side& sd = sides[dev];
+  if (!sd.s) {
+    if ((e = hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking)) != hipSuccess) return e;
+    if ((e = hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming)) != hipSuccess) return e;
+    if ((e = hipEventCreateWithFlags(&sd.join, hipEventDisableTiming)) != hipSuccess) return e;
+  }
+  if ((e = hipEventRecord(sd.fork, main)) != hipSuccess) return e;
+  if ((e = hipStreamWaitEvent(sd.s, sd.fork, 0)) != hipSuccess) return e;
+  *side = sd.s;
+  return hipSuccess;
+}
+
+hipError_t side_join(hipStream_t main) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxSides) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(side_mu);
+  Side& sd = sides[dev];
+  if (!sd.s) return hipErrorInvalidHandle;
+  if ((e = hipEventRecord(sd.join, sd.s)) != hipSuccess) return e;
+  return hipStreamWaitEvent(main, sd.join, 0);
+}
 
 int device_cu_count() {
   constexpr int kMaxDevices = 64;
