@@ -151,6 +151,40 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   // Row of the value reduce16 leaves in this lane (index 4·ib + r).
   const int red_row = 16 * (r16 >> 2) + 4 * g4 + (r16 & 3);
 
+  // ---- phase A's global operands, in flight together with the staging -----
+  const bool vwave = wave < V / 16;
+  const int col = 16 * wave + r16;  // this lane's value column in phase A
+  float pS[K / 32][8], pD[K / 32][8], vv[4][4], wv[4][4], dyv[2][8];
+  if (vwave) {
+    // S₀ and dS rows 32·s + 8·(lane/16) + t of this lane's column (B operands
+    // of kg·S₀ and kc·dS).
+#pragma unroll
+    for (int s = 0; s < K / 32; ++s)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        pS[s][t] = S0[size_t(32 * s + k8 + t) * V + col];
+        pD[s][t] = dSa[size_t(32 * s + k8 + t) * V + col];
+      }
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = rowi(ib, r);
+        const bool ok = i < valid;
+        vv[ib][r] = ok ? bf16_to_f32(p.v[row_of(i) * V + col]) : 0.f;
+        wv[ib][r] = (ok && p.ww != 1) ? p.write[row_of(i) * V + col] : 0.f;
+      }
+    // dY in the permuted token order of the attnᵀ fragments: token 4q+e /
+    // 16+4q+e of each 32-token step at position 8q+e / 8q+4+e.
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int t = 32 * kk + (e < 4 ? 4 * g4 + e : 16 + 4 * g4 + e - 4);
+        dyv[kk][e] = t < valid ? ld(dy, row_of(t) * V + col) : 0.f;
+      }
+  }
+
   // ---- staging -----------------------------------------------------------
   if (tid < kL) {
     const int t = tid;
@@ -211,30 +245,20 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   __syncthreads();
 
   // ---- phase A: value columns ---------------------------------------------
-  const bool vwave = wave < V / 16;
-  const int col = 16 * wave + r16;
   f32x4 X[4], dV[4], Vn[4], dW[4];
   if (vwave) {
-    float vv[4][4], wv[4][4];
+    if (p.ww == 1)
 #pragma unroll
-    for (int ib = 0; ib < 4; ++ib)
+      for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = rowi(ib, r);
-        const bool ok = i < valid;
-        vv[ib][r] = ok ? bf16_to_f32(p.v[row_of(i) * V + col]) : 0.f;
-        wv[ib][r] = p.ww == 1 ? wr_s[i] : (ok ? p.write[row_of(i) * V + col] : 0.f);
-      }
+        for (int r = 0; r < 4; ++r) wv[ib][r] = wr_s[rowi(ib, r)];
     // X = w⊙V − kg·S₀ (S₀ as hi + lo parts; per-head: k exact, e·e^G per row).
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib) X[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < K / 32; ++s) {
-      float sv[8];
-#pragma unroll
-      for (int t = 0; t < 8; ++t) sv[t] = S0[size_t(32 * s + k8 + t) * V + col];
       uint4 sh, sl;
-      split8(sv, sh, sl);
+      split8(pS[s], sh, sl);
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib) {
         const int at = tile_at<K>(16 * ib + r16, 32 * s + k8);
@@ -272,15 +296,7 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
     // 32-token step at position 8q+e / 8q+4+e, the permuted order).
     uint4 yh[2], yl[2];
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      float f[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int t = 32 * kk + (e < 4 ? 4 * g4 + e : 16 + 4 * g4 + e - 4);
-        f[e] = t < valid ? ld(dy, row_of(t) * V + col) : 0.f;
-      }
-      split8(f, yh[kk], yl[kk]);
-    }
+    for (int kk = 0; kk < 2; ++kk) split8(dyv[kk], yh[kk], yl[kk]);
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib) {
       dV[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -297,11 +313,8 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
       for (int ib = 0; ib < 4; ++ib) kd[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < K / 32; ++s) {
-        float dv8[8];
-#pragma unroll
-        for (int t = 0; t < 8; ++t) dv8[t] = dSa[size_t(32 * s + k8 + t) * V + col];
         uint4 dh, dl;
-        split8(dv8, dh, dl);
+        split8(pD[s], dh, dl);
 #pragma unroll
         for (int ib = 0; ib < 4; ++ib) {
           const uint4 a = ld8u(&R[oKc + tile_at<K>(16 * ib + r16, 32 * s + k8)]);
@@ -344,6 +357,54 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
       }
     if (p.ww == 1) atomicAdd(&racc[0][red_row], reduce16(rs, lane));
   }
+  // dY rows for LDS, then phase B's global operands: S₀ and dS rows of this
+  // lane's key channel.
+  constexpr int NY = kL * V / 8 / kNT;  // 16-byte chunks of dY rows per thread
+  static_assert(NY * kNT * 8 == kL * V, "dY staging assumes whole rounds");
+  float ydat[NY][8];
+#pragma unroll
+  for (int m = 0; m < NY; ++m) {
+    const int idx = tid + kNT * m, i = idx / (V / 8), c8 = idx % (V / 8);
+    if constexpr (F32DY) {
+      float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b2 = a;
+      if (i < valid) {
+        const float4* src = reinterpret_cast<const float4*>(dy + row_of(i) * V + 8 * c8);
+        a = src[0];
+        b2 = src[1];
+      }
+      ydat[m][0] = a.x; ydat[m][1] = a.y; ydat[m][2] = a.z; ydat[m][3] = a.w;
+      ydat[m][4] = b2.x; ydat[m][5] = b2.y; ydat[m][6] = b2.z; ydat[m][7] = b2.w;
+    } else {
+      uint4 v = make_uint4(0u, 0u, 0u, 0u);
+      if (i < valid)
+        v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(dy) +
+                                            row_of(i) * V + 8 * c8);
+      unpack8(v, ydat[m]);
+    }
+  }
+  const bool kwave = wave < K / 16;
+  const int c = 16 * wave + r16;  // this lane's key channel in phases B and D
+  float bS[V / 32][8], bD[V / 32][8], eA[4][4];
+  if (kwave) {
+#pragma unroll
+    for (int s = 0; s < V / 32; ++s) {
+      const float4* s0r = reinterpret_cast<const float4*>(S0 + size_t(c) * V + 32 * s + k8);
+      const float4* dsr = reinterpret_cast<const float4*>(dSa + size_t(c) * V + 32 * s + k8);
+      *reinterpret_cast<float4*>(bS[s]) = s0r[0];
+      *reinterpret_cast<float4*>(bS[s] + 4) = s0r[1];
+      *reinterpret_cast<float4*>(bD[s]) = dsr[0];
+      *reinterpret_cast<float4*>(bD[s] + 4) = dsr[1];
+    }
+    // Per-channel erase gate at the lane's positions (kept for phase D).
+    if (PC && p.ew != 1)
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = rowi(ib, r);
+          eA[ib][r] = i < valid ? p.erase[row_of(i) * K + c] : 0.f;
+        }
+  }
   __syncthreads();
 
   // ---- V', dVw and dY rows into LDS ---------------------------------------
@@ -360,55 +421,32 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
         R[oWl + at] = bf_bits(dW[ib][r] - bf16_to_f32(wh));
       }
   }
-  for (int idx = tid; idx < kL * V / 8; idx += kNT) {
-    const int i = idx / (V / 8), c8 = idx % (V / 8);
+#pragma unroll
+  for (int m = 0; m < NY; ++m) {
+    const int idx = tid + kNT * m, i = idx / (V / 8), c8 = idx % (V / 8);
     const int at = tile_at<V>(i, 8 * c8);
-    if constexpr (F32DY) {
-      float f[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      if (i < valid) {
-        const float4* src = reinterpret_cast<const float4*>(dy + row_of(i) * V + 8 * c8);
-        *reinterpret_cast<float4*>(f) = src[0];
-        *reinterpret_cast<float4*>(f + 4) = src[1];
-      }
-      uint4 hh, ll;
-      split8(f, hh, ll);
-      *reinterpret_cast<uint4*>(&R[oYh + at]) = hh;
-      *reinterpret_cast<uint4*>(&R[oYl + at]) = ll;
-    } else {
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (i < valid)
-        v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(dy) +
-                                            row_of(i) * V + 8 * c8);
-      *reinterpret_cast<uint4*>(&R[oYh + at]) = v;
-    }
+    uint4 hh, ll;
+    split8(ydat[m], hh, ll);
+    *reinterpret_cast<uint4*>(&R[oYh + at]) = hh;
+    if constexpr (F32DY) *reinterpret_cast<uint4*>(&R[oYl + at]) = ll;
   }
   __syncthreads();
 
   // ---- phase B: key channels; contractions over the value axis ------------
-  const bool kwave = wave < K / 16;
-  const int c = 16 * wave + r16;  // this lane's key channel in phases B and D
   f32x4 dkA[4], dqA[4], dkeA[4];
-  float dgA[4][4], eA[4][4];
+  float dgA[4][4], degl = 0.f;
   if (kwave) {
     f32x4 aKc[4], aQr[4], aKg[4];
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib)
       aKc[ib] = aQr[ib] = aKg[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float degl = 0.f;
 #pragma unroll
     for (int s = 0; s < V / 32; ++s) {
-      float sv[8], dv8[8];
-      const float4* s0r = reinterpret_cast<const float4*>(S0 + size_t(c) * V + 32 * s + k8);
-      const float4* dsr = reinterpret_cast<const float4*>(dSa + size_t(c) * V + 32 * s + k8);
-      *reinterpret_cast<float4*>(sv) = s0r[0];
-      *reinterpret_cast<float4*>(sv + 4) = s0r[1];
-      *reinterpret_cast<float4*>(dv8) = dsr[0];
-      *reinterpret_cast<float4*>(dv8 + 4) = dsr[1];
 #pragma unroll
-      for (int t = 0; t < 8; ++t) degl += sv[t] * dv8[t];
+      for (int t = 0; t < 8; ++t) degl += bS[s][t] * bD[s][t];
       uint4 sh, sl, dh, dl;
-      split8(sv, sh, sl);
-      split8(dv8, dh, dl);
+      split8(bS[s], sh, sl);
+      split8(bD[s], dh, dl);
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib) {
         const int at = tile_at<V>(16 * ib + r16, 32 * s + k8);
@@ -429,55 +467,28 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
     degl += __shfl_xor(degl, 16);
     degl += __shfl_xor(degl, 32);
     // The scan's cotangents through the gates (combined_backward.rs:284-313):
-    // d_k = d_kc⊙e^{G_last−G}, d_q = d_qr⊙e^G, d_ke = d_kg⊙e^G, and the
-    // pieces of d_G: −d_carry + (d_qr⊙qs + d_kg⊙ke)⊙e^G, plus d(G_last).
+    // d_k = d_kc⊙e^{G_last−G}, d_q = d_qr⊙e^G, d_ke = d_kg⊙e^G (their d_G
+    // pieces follow in phase D, where K and Q are staged).
     const float gl_c = PC ? Gc[(kL - 1) * GP + c] : 0.f;
-    float carry = 0.f, rowv[16];
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = rowi(ib, r);
-        const bool ok = i < valid;
-        float eg, ec, e;
+        float eg, ec;
         if constexpr (PC) {
           const float gci = Gc[i * GP + c];
           eg = __expf(gci);
           ec = __expf(gl_c - gci);
-          e = p.ew == 1 ? er_s[i] : (ok ? p.erase[row_of(i) * K + c] : 0.f);
-          eA[ib][r] = e;
+          if (p.ew == 1) eA[ib][r] = er_s[i];
         } else {
           eg = eg_s[i];
           ec = ec_s[i];
-          e = er_s[i];
         }
         dkA[ib][r] = aKc[ib][r] * ec;
         dqA[ib][r] = aQr[ib][r] * eg;
         dkeA[ib][r] = -aKg[ib][r] * eg;
-        float val = 0.f;
-        if (gated) {
-          const float kv = ok ? bf16_to_f32(p.k[row_of(i) * K + c]) : 0.f;
-          const float qv = ok ? bf16_to_f32(p.q[row_of(i) * K + c]) : 0.f;
-          const float dcarry = aKc[ib][r] * kv * ec;
-          const float deg = aQr[ib][r] * qv * p.scale - aKg[ib][r] * kv * e;
-          carry += dcarry;
-          val = -dcarry + deg * eg;
-        }
-        if constexpr (PC) dgA[ib][r] = val;
-        rowv[4 * ib + r] = val;
       }
-    if constexpr (PC) {
-      carry += __shfl_xor(carry, 16);
-      carry += __shfl_xor(carry, 32);
-      if (g4 == 0) cacc[c] = carry + degl * __expf(gl_c);
-    } else if (gated) {
-      atomicAdd(&racc[2][red_row], reduce16(rowv, lane));
-      // d(G_last) of the whole head: Σ d_carry + Σ_channels (dS⊙S₀)·e^{G_last}.
-      float tot = carry + (g4 == 0 ? degl * eg_s[kL - 1] : 0.f);
-#pragma unroll
-      for (int m = 32; m >= 1; m >>= 1) tot += __shfl_xor(tot, m);
-      if (lane == 0) atomicAdd(&racc[2][kL - 1], tot);
-    }
   }
   // dattn = dY·V'ᵀ on the lower tiles.
   f32x4 dat[2];
@@ -676,6 +687,40 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
 
   // ---- phase D: score backward, gates, stores -----------------------------
   if (kwave) {
+    // d_G of the scan (combined_backward.rs:284-313): −d_carry + (d_qr⊙qs +
+    // d_kg⊙ke)⊙e^G = −dkA⊙k + dqA⊙q·scale + dkeA⊙k⊙e with phase B's
+    // accumulators, and d(G_last) = Σ_i d_carry + (Σ_v dS⊙S₀)·e^{G_last}.
+    if (gated) {
+      float carry = 0.f, rowv[16];
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) {
+        const uint2 k4 = *reinterpret_cast<const uint2*>(&R[oKC + tile_at<kL>(c, 16 * ib + 4 * g4)]);
+        const uint2 q4 = *reinterpret_cast<const uint2*>(&R[oQC + tile_at<kL>(c, 16 * ib + 4 * g4)]);
+        const float kv[4] = {lo_f(k4.x), hi_f(k4.x), lo_f(k4.y), hi_f(k4.y)};
+        const float qv[4] = {lo_f(q4.x), hi_f(q4.x), lo_f(q4.y), hi_f(q4.y)};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float e = PC ? eA[ib][r] : er_s[rowi(ib, r)];
+          const float dcarry = dkA[ib][r] * kv[r];
+          const float val = -dcarry + dqA[ib][r] * qv[r] * p.scale + dkeA[ib][r] * kv[r] * e;
+          carry += dcarry;
+          if constexpr (PC) dgA[ib][r] = val;
+          rowv[4 * ib + r] = val;
+        }
+      }
+      if constexpr (PC) {
+        carry += __shfl_xor(carry, 16);
+        carry += __shfl_xor(carry, 32);
+        if (g4 == 0) cacc[c] = carry + degl * __expf(Gc[(kL - 1) * GP + c]);
+      } else {
+        atomicAdd(&racc[2][red_row], reduce16(rowv, lane));
+        // d(G_last) of the whole head: Σ d_carry + Σ_channels (dS⊙S₀)·e^{G_last}.
+        float tot = carry + (g4 == 0 ? degl * eg_s[kL - 1] : 0.f);
+#pragma unroll
+        for (int m = 32; m >= 1; m >>= 1) tot += __shfl_xor(tot, m);
+        if (lane == 0) atomicAdd(&racc[2][kL - 1], tot);
+      }
+    }
     if constexpr (!PC) {
       // head_scores_backward (combined_backward.rs:376-416) with drkk = dAkk⊙M,
       // drqk = dAqk⊙M: d_ke += drkk·K, d_qs += drqk·K, d_k += drkkᵀ·ke +
@@ -732,8 +777,23 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
       // channel_scores_backward (combined_backward.rs:421-513): per row block
       // pb with reference row r = 16·pb + 8, row factors e^{min(G[i]−G[r], 48)}
       // and column factors k[j]·e^{min(G[r]−G[j], 48)} (zero past block pb).
+      // The row factors' gate (erase for the dAkk half of the lanes, the
+      // readout scale for the dAqk half), loaded one row block ahead.
+      auto gate8 = [&](int pb, float* e8) {
+        const int i0 = 16 * pb + (k8 & 15);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const int i = i0 + t;
+          e8[t] = g4 >= 2 ? p.scale
+                          : (p.ew == 1 ? er_s[i] : (i < valid ? p.erase[row_of(i) * K + c] : 0.f));
+        }
+      };
+      float ecur[8];
+      gate8(0, ecur);
 #pragma unroll
       for (int pb = 0; pb < 4; ++pb) {
+        float enext[8];
+        if (pb < 3) gate8(pb + 1, enext);
         const float gref = Gc[(16 * pb + 8) * GP + c];
         // d(ke⊙rf), d(qs⊙rf) of the block's rows = dAkk, dAqk rows · colb.
         f32x4 drke = {0.f, 0.f, 0.f, 0.f}, drq = {0.f, 0.f, 0.f, 0.f};
@@ -770,10 +830,7 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
           for (int t = 0; t < 8; ++t) {
             const int i = i0 + t;
             const float rf = __expf(fminf(Gc[i * GP + c] - gref, kMaxExp));
-            const float e = isq ? p.scale
-                                : (p.ew == 1 ? er_s[i]
-                                             : (i < valid ? p.erase[row_of(i) * K + c] : 0.f));
-            rv[t] = xf[t] * e * rf;
+            rv[t] = xf[t] * ecur[t] * rf;
           }
           split8(rv, rh, rl);
         }
@@ -835,6 +892,9 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
         tot += __shfl_xor(tot, 16);
         tot += __shfl_xor(tot, 32);
         if (g4 == 2) dgA[pb][0] += tot;
+        if (pb < 3)
+#pragma unroll
+          for (int t = 0; t < 8; ++t) ecur[t] = enext[t];
       }
     }
     // Front end (combined_backward.rs:153-188) and the stores.
@@ -860,28 +920,48 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
     }
     if (p.ew == 1) atomicAdd(&racc[1][red_row], reduce16(rde, lane));
   }
-  __syncthreads();
   if constexpr (PC) {
-    // d_G per channel: (i = L−1 also takes d(G_last)), then the reverse
-    // cumulative sum over the chunk (the cotangent of g from that of G).
-    if (kwave)
+    // d_g = the reverse cumulative sum over the chunk of d_G (row L−1 also
+    // takes d(G_last)): within the lane's 4 rows, across the 4 lanes of its
+    // column, then across the 16-row blocks.
+    if (kwave) {
+      float tot[4], after[4];
 #pragma unroll
-      for (int ib = 0; ib < 4; ++ib)
+      for (int ib = 0; ib < 4; ++ib) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Gc[rowi(ib, r) * GP + c] = dgA[ib][r];
-    __syncthreads();
-    for (int cc = tid; cc < K; cc += kNT) {
-      float acc = cacc[cc];
-      for (int i = kL - 1; i >= 0; --i) {
-        acc += Gc[i * GP + cc];
-        if (i < valid) p.dg[row_of(i) * K + cc] = acc;
+        for (int r = 2; r >= 0; --r) dgA[ib][r] += dgA[ib][r + 1];
+        tot[ib] = dgA[ib][0];
+      }
+      float blk[4];
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) {
+        const float t0 = __shfl(tot[ib], r16), t1 = __shfl(tot[ib], r16 + 16),
+                    t2 = __shfl(tot[ib], r16 + 32), t3 = __shfl(tot[ib], r16 + 48);
+        after[ib] = (g4 < 1 ? t1 : 0.f) + (g4 < 2 ? t2 : 0.f) + (g4 < 3 ? t3 : 0.f);
+        blk[ib] = t0 + t1 + t2 + t3;
+      }
+      float carry = cacc[c];
+#pragma unroll
+      for (int ib = 3; ib >= 0; --ib) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = rowi(ib, r);
+          if (i < valid) p.dg[row_of(i) * K + c] = dgA[ib][r] + after[ib] + carry;
+        }
+        carry += blk[ib];
       }
     }
-  } else if (gated && tid == 0) {
-    float acc = 0.f;
-    for (int i = kL - 1; i >= 0; --i) {
-      acc += racc[2][i];
-      if (i < valid) p.dg[row_of(i)] = acc;
+    __syncthreads();
+  } else {
+    __syncthreads();
+    if (gated && wave == 0) {
+      float v = racc[2][lane];
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float t = __shfl_down(v, off);
+        if (lane + off < 64) v += t;
+      }
+      if (lane < valid) p.dg[row_of(lane)] = v;
     }
   }
   if (tid < valid) {
