@@ -261,6 +261,19 @@ def bench_config5(torch, pkg, steps, warmup):
     # gate gradients and dS0.
     b_bytes = rows * (2 * K + 2 * V) * 2 + rows * (2 * K + V) * 4 + st + \
         rows * (2 * K + V) * 2 + rows * (2 * K + V) * 4 + st
+    # The fused chunk-local backward kernel, per chunk-head (L = 64): q, k, v,
+    # dO (bf16), the three gates (fp32), S0 and dS leaving the chunk (fp32),
+    # T / Tlo / Tᵀ / Tᵀlo / attnᵀ (bf16), kg hi/lo and kc (bf16) in; dq, dk,
+    # dv (bf16) and the three gate gradients (fp32) out.
+    L, G = 64, B * H * (T // 64)
+    cb_unit = (L * (2 * K + V) * 2 + L * V * 2 + L * (2 * K + V) * 4 + 2 * K * V * 4 +
+               5 * L * L * 2 + 3 * L * K * 2 + L * (2 * K + V) * 2 + L * (2 * K + V) * 4)
+    cb = bk.get("dn_mfma_chunk_bwd")
+    cb_roof = None
+    if cb:
+        cb_roof = _hbm(cb_unit * G, cb["avg_us"] / 1e3)
+        cb_roof.update({"kernel": "dn_mfma_chunk_bwd", "bytes_per_chunk_head": cb_unit,
+                        "chunk_heads": G})
     name = {1: "generic", 2: "mfma"}
     return {"workload": "config 5: GDN-2 per-channel gates, forward + custom backward",
             "batch": B, "seq_len": T, "nheads": H, "head_k_dim": K, "head_v_dim": V,
@@ -268,7 +281,7 @@ def bench_config5(torch, pkg, steps, warmup):
             "fwd_ms": round(fms, 3), "bwd_ms": round(bms, 3),
             "tokens_per_s_fwd_bwd": round(B * T / ((fms + bms) / 1e3), 1),
             "roofline_fwd": _hbm(f_bytes, fms), "roofline_bwd": _hbm(b_bytes, bms),
-            "kernels_fwd": fk, "kernels_bwd": bk}
+            "roofline_chunk_bwd": cb_roof, "kernels_fwd": fk, "kernels_bwd": bk}
 
 
 def cpu_baseline(torch):
@@ -324,7 +337,8 @@ def main():
                     help="timed calls for configs 4 and 5 (after one warmup)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="short run for rocprofv3 --pmc: a 1 GiB copy (calibration), then 2 "
-                         "forward and 2 decode launches; prints no JSON")
+                         "forward and 2 decode launches and one config-5 forward + "
+                         "backward; prints no JSON")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -344,6 +358,7 @@ def main():
         torch.cuda.synchronize()
         bench_chunk_fwd(torch, pkg, 2, 0, algo)
         bench_decode(torch, pkg, 2, 0)
+        bench_config5(torch, pkg, 1, 0)
         torch.cuda.synchronize()
         print("[bench] profile pass done", file=sys.stderr, flush=True)
         return
