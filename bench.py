@@ -9,7 +9,9 @@ dk128) at 1 GPU; % roofline"):
   and state, bf16 y). One step = one dn_chunk_fwd over the whole batch, inputs
   already resident in HBM.
 * decode = config 3 (batch 256, H16, dk128, dv256, fp32 state ≈ 537 MB):
-  µs per dn_step over consecutive steps, and its HBM roofline.
+  µs per dn_step over consecutive steps, and its HBM roofline; product_u2 =
+  DeltaProduct decode (2 micro-steps per token) at the same shape as one
+  dn_recurrent call per token.
 * roofline = the dominant kernel of the forward, timed with HIP events on its
   own stream by the library's profiler (dn_profile_*), against algorithmic
   bytes per launch (DESIGN.md lists the per-unit figures).
@@ -152,6 +154,52 @@ def bench_decode(torch, pkg, steps, warmup):
     name = max(prof, key=lambda n: prof[n][0]) if prof else None
     k_us = prof[name][0] * 1e3 / prof[name][1] if name else us
     return dict(us=us, kernel_us=k_us, bytes=step_bytes, prof=prof, kernel=name)
+
+
+def bench_product_decode(torch, pkg, steps, warmup, u=2):
+    """DeltaProduct decode at the config-3 shape (B=256, H=16, dk=128,
+    dv=256, fp32 state): one decode token = u Householder micro-steps
+    (delta_product.rs:270-305), folded into a u-token sequence as in
+    config 4 (q on the last micro-step, the forget gate on the first,
+    β = 2σ(N)) and run as one dn_recurrent call, which reads and writes
+    the state once per token instead of once per micro-step."""
+    B, H, K, V = 256, 16, 128, 256
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20260831)
+    S = torch.randn((B, H, K, V), generator=gen, device=dev) * 0.02
+    n_in = min(steps, 32)  # distinct input sets, cycled
+    l2 = lambda x: x / torch.sqrt((x * x).sum(-1, keepdim=True) + 1e-6)
+    q = torch.zeros((n_in, B, u, H, K), device=dev)
+    q[:, :, u - 1] = l2(torch.randn((n_in, B, H, K), generator=gen, device=dev))
+    k = l2(torch.randn((n_in, B, u, H, K), generator=gen, device=dev))
+    v = torch.randn((n_in, B, u, H, V), generator=gen, device=dev)
+    beta = 2 * torch.sigmoid(torch.randn((n_in, B, u, H, 1), generator=gen, device=dev))
+    g = torch.zeros((n_in, B, u, H, 1), device=dev)
+    g[:, :, 0] = -torch.nn.functional.softplus(
+        torch.randn((n_in, B, H, 1), generator=gen, device=dev)) * 0.05
+    y = torch.empty((B, u, H, V), dtype=torch.float32, device=dev)
+    abi = pkg.abi
+    argv = [abi.recurrent_args(q[t], k[t], v[t], beta[t], beta[t], g[t], S, y, S, None)
+            for t in range(n_in)]
+    import ctypes
+    lib, stream = abi.lib(), abi.stream_handle()
+    refs = [ctypes.byref(a) for a in argv]
+    it = iter(range(1 << 62))
+
+    def run():
+        rc = lib.dn_recurrent(refs[next(it) % n_in], stream)
+        if rc:
+            abi.check(rc)
+    ms, kern = _timed(torch, abi, run, steps, warmup)
+    nbytes = 2 * B * H * K * V * 4 + u * B * H * (2 * K + 2 * V + 2) * 4
+    name = max(kern, key=lambda n: kern[n]["avg_us"]) if kern else None
+    k_us = kern[name]["avg_us"] if name else ms * 1e3
+    return {"workload": f"DeltaProduct decode, u={u} micro-steps per token, config-3 shape",
+            "entry_point": "dn_recurrent", "calls": steps, "us_per_token": round(ms * 1e3, 2),
+            "kernel_us": k_us, "bytes_per_token": nbytes,
+            "roofline": _hbm(nbytes, k_us / 1e3) | {"kernel": name,
+                                                     "traffic": traffic_from_profiles(name)}}
 
 
 def _timed(torch, abi, fn, steps, warmup):
@@ -337,8 +385,8 @@ def main():
                     help="timed calls for configs 4 and 5 (after one warmup)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="short run for rocprofv3 --pmc: a 1 GiB copy (calibration), then 2 "
-                         "forward and 2 decode launches and one config-5 forward + "
-                         "backward; prints no JSON")
+                         "forward, 2 decode and 2 DeltaProduct-decode launches and one "
+                         "config-5 forward + backward; prints no JSON")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -358,6 +406,7 @@ def main():
         torch.cuda.synchronize()
         bench_chunk_fwd(torch, pkg, 2, 0, algo)
         bench_decode(torch, pkg, 2, 0)
+        bench_product_decode(torch, pkg, 2, 0)
         bench_config5(torch, pkg, 1, 0)
         torch.cuda.synchronize()
         print("[bench] profile pass done", file=sys.stderr, flush=True)
@@ -397,6 +446,10 @@ def main():
                                "frac": round(gbs / HBM_PEAK_GBS, 4),
                                "traffic": traffic_from_profiles(dc["kernel"])}}
         print(f"[bench] decode {decode}", file=sys.stderr, flush=True)
+        pd = bench_product_decode(torch, pkg, max(args.decode_steps // 5, 1), 5)
+        pd["u_dn_step_kernel_us"] = round(2 * dc["kernel_us"], 2)  # the same token as 2 ticks
+        decode["product_u2"] = pd
+        print(f"[bench] DeltaProduct decode {pd}", file=sys.stderr, flush=True)
 
     extra = {}
     if not args.no_extra:

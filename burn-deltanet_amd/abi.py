@@ -19,6 +19,7 @@ LIB_PATH = _HERE / "libdeltanet_core.so"
 
 DN_F32, DN_BF16 = 0, 1
 DN_ALGO_AUTO, DN_ALGO_GENERIC, DN_ALGO_MFMA = 0, 1, 2
+RECURRENT_MAX_K = 256  # dn_recurrent's head_k_dim limit (deltanet_core.h)
 
 STATUS = {
     0: "DN_OK",
@@ -35,7 +36,7 @@ STATUS = {
 }
 
 EXPORTS = [
-    "dn_chunk_fwd", "dn_chunk_bwd", "dn_step", "dn_chunk_fwd_workspace_bytes",
+    "dn_chunk_fwd", "dn_chunk_bwd", "dn_step", "dn_recurrent", "dn_chunk_fwd_workspace_bytes",
     "dn_chunk_bwd_workspace_bytes", "dn_chunk_fwd_algo", "dn_chunk_bwd_algo",
     "dn_last_error", "dn_version", "dn_profile_enable", "dn_profile_read",
 ]
@@ -80,6 +81,17 @@ class StepArgs(ctypes.Structure):
     ]
 
 
+class RecurrentArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i64), ("sequence", _i64), ("nheads", _i64), ("head_k_dim", _i64),
+        ("head_v_dim", _i64), ("erase_width", _i64), ("write_width", _i64),
+        ("decay_width", _i64), ("has_gate", _i32), ("scale", _f64), ("qkv_dtype", _i32),
+        ("y_dtype", _i32), ("check_finite", _i32),
+        ("q", _vp), ("k", _vp), ("v", _vp), ("erase", _vp), ("write", _vp), ("g", _vp),
+        ("state_in", _vp), ("y", _vp), ("state_out", _vp),
+    ]
+
+
 _LIB = None
 
 
@@ -98,6 +110,8 @@ def lib() -> ctypes.CDLL:
         L.dn_chunk_bwd.restype = ctypes.c_int
         L.dn_step.argtypes = [ctypes.POINTER(StepArgs), _vp]
         L.dn_step.restype = ctypes.c_int
+        L.dn_recurrent.argtypes = [ctypes.POINTER(RecurrentArgs), _vp]
+        L.dn_recurrent.restype = ctypes.c_int
         L.dn_chunk_fwd_workspace_bytes.argtypes = [ctypes.POINTER(ChunkFwdArgs)]
         L.dn_chunk_fwd_workspace_bytes.restype = _sz
         L.dn_chunk_bwd_workspace_bytes.argtypes = [ctypes.POINTER(ChunkBwdArgs)]
@@ -200,6 +214,30 @@ def step_args(q, k, v, erase, write, g, state, y, state_out, scale, check_finite
 
 def run_step(args: StepArgs) -> None:
     check(lib().dn_step(ctypes.byref(args), stream_handle()))
+
+
+def recurrent_args(q, k, v, erase, write, g, state, y, state_out, scale, check_finite=False):
+    """dn_recurrent over [batch, sequence, nheads, ·] inputs."""
+    B, S, H, K = q.shape
+    V = v.shape[3]
+    a = RecurrentArgs()
+    a.batch, a.sequence, a.nheads, a.head_k_dim, a.head_v_dim = B, S, H, K, V
+    a.erase_width, a.write_width = erase.shape[3], write.shape[3]
+    a.decay_width = 0 if g is None else g.shape[3]
+    a.has_gate = 0 if g is None else 1
+    a.scale = nan_scale(scale)
+    a.qkv_dtype = dtype_tag(q.dtype)
+    a.y_dtype = dtype_tag(y.dtype)
+    a.check_finite = int(bool(check_finite))
+    a.q, a.k, a.v = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    a.erase, a.write = erase.data_ptr(), write.data_ptr()
+    a.g = None if g is None else g.data_ptr()
+    a.state_in, a.y, a.state_out = state.data_ptr(), y.data_ptr(), state_out.data_ptr()
+    return a
+
+
+def run_recurrent(args: RecurrentArgs) -> None:
+    check(lib().dn_recurrent(ctypes.byref(args), stream_handle()))
 
 
 def chunk_bwd_args(dy, dstate, q, k, v, erase, write, g, state, grads, chunk_len, scale,

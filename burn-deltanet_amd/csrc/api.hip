@@ -402,4 +402,41 @@ int dn_step(const dn_step_args* a, hipStream_t stream) {
   return DN_OK;
 }
 
+int dn_recurrent(const dn_recurrent_args* a, hipStream_t stream) {
+  g_last_error.clear();
+  if (!a) return fail(DN_ERR_NULL, "args is NULL");
+  if (int rc = check_common(a->batch, a->sequence, a->nheads, a->head_k_dim, a->head_v_dim,
+                            a->erase_width, a->write_width, a->decay_width, a->has_gate))
+    return rc;
+  if (!valid_dtype(a->qkv_dtype) || !valid_dtype(a->y_dtype))
+    return fail(DN_ERR_DTYPE, "dtype must be DN_F32 or DN_BF16");
+  if (!a->q || !a->k || !a->v || !a->erase || !a->write || !a->state_in || !a->y ||
+      !a->state_out || (a->has_gate && !a->g))
+    return fail(DN_ERR_NULL, "a required tensor pointer is NULL");
+  if (!recurrent_supported(*a))
+    return fail(DN_ERR_UNSUPPORTED, "dn_recurrent supports head_k_dim up to " +
+                                        std::to_string(kRecMaxK) +
+                                        "; run dn_step per token for larger heads");
+  const size_t nq = size_t(a->batch) * a->sequence * a->nheads;
+  const size_t ns = size_t(a->batch) * a->nheads * a->head_k_dim * a->head_v_dim;
+  if (a->check_finite) {
+    std::vector<Guarded> in = {{a->q, nq * a->head_k_dim, a->qkv_dtype},
+                               {a->k, nq * a->head_k_dim, a->qkv_dtype},
+                               {a->v, nq * a->head_v_dim, a->qkv_dtype},
+                               {a->erase, nq * a->erase_width, DN_F32},
+                               {a->write, nq * a->write_width, DN_F32},
+                               {a->has_gate ? a->g : nullptr, nq * a->decay_width, DN_F32},
+                               {a->state_in, ns, DN_F32}};
+    if (int rc = nonfinite_check(in, stream, "inputs")) return rc;
+  }
+  hipError_t e = launch_recurrent(*a, resolve_scale(a->scale, a->head_k_dim), stream);
+  if (e != hipSuccess) return hip_fail(e, "dn_recurrent launch");
+  if (a->check_finite) {
+    std::vector<Guarded> out = {{a->y, nq * a->head_v_dim, a->y_dtype},
+                                {a->state_out, ns, DN_F32}};
+    if (int rc = nonfinite_check(out, stream, "outputs")) return rc;
+  }
+  return DN_OK;
+}
+
 }  // extern "C"

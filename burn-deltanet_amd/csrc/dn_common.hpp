@@ -67,6 +67,11 @@ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 // Launch helpers (defined in the per-path translation units).
 hipError_t launch_step(const dn_step_args& a, float scale, hipStream_t stream);
+// dn_recurrent: the whole sequence in one pass over the state (head_k_dim up
+// to kRecMaxK).
+constexpr int64_t kRecMaxK = DN_RECURRENT_MAX_K;
+bool recurrent_supported(const dn_recurrent_args& a);
+hipError_t launch_recurrent(const dn_recurrent_args& a, float scale, hipStream_t stream);
 
 struct GenericFwdPlan {
   size_t ws_bytes;

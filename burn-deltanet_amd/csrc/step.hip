@@ -19,6 +19,7 @@ namespace {
 
 struct StepParams {
   int B, H, K, V, ew, ww, dw;
+  int S;  // tokens (dn_recurrent; 1 for dn_step)
   float scale;
   const void *q, *k, *v;
   const float *erase, *write, *g;
@@ -263,6 +264,176 @@ __global__ __launch_bounds__(kRowThreads) void step_row_kernel(StepParams p) {
   }
 }
 
+// dn_recurrent: delta_step over a whole sequence (recurrent.rs:107-142) with
+// the state held in registers from the first token to the last, so one call
+// reads and writes S once. Same work split as step_row_kernel: a workgroup
+// of 8 waves owns 64·C columns of one (head, batch) and all K rows; a lane
+// owns C columns of RPT rows. Per token the two key-axis reductions cross
+// the waves through LDS: two barriers per token, no traffic to S.
+//
+// Token vectors are staged into LDS TB tokens at a time, every load of a
+// block issued before the first LDS write, and the next block is staged
+// during the first token of the current one (a short sequence, such as a
+// DeltaProduct decode token's micro-steps, is staged whole beside the state
+// load). The staged vectors are padded to KP = 8·RPT rows with zeros (decay
+// 0 included), so rows past K hold zeros throughout and every LDS read of a
+// row is one base register plus an immediate offset.
+template <class TQ, class TY, int RPT, int C>
+__global__ __launch_bounds__(kRowThreads) void recurrent_row_kernel(StepParams p) {
+  constexpr int W = 64 * C;
+  constexpr int KP = kRowWaves * RPT;          // padded rows
+  constexpr int TB = 4;                        // tokens per staged block
+  constexpr int KI = (TB * KP + kRowThreads - 1) / kRowThreads;  // (token, row) pairs per thread
+  constexpr int VI = (TB * W + kRowThreads - 1) / kRowThreads;
+  using vec = ntv<C>;
+  const int nblk = (p.V + W - 1) / W;
+  const int cb = blockIdx.x % nblk, bh_id = blockIdx.x / nblk;
+  const int h = bh_id % p.H, b = bh_id / p.H;
+  const int tid = threadIdx.x, lane = tid & 63, rg = tid >> 6;
+  const int K = p.K, V = p.V, S = p.S;
+  const int jb = cb * W, j0 = jb + C * lane;
+  const size_t bh = size_t(b) * p.H + h;
+
+  __shared__ float tok[2][TB][4][KP];  // k, k⊙erase, scale·q, α per token
+  __shared__ float vw[2][TB][W];       // v⊙write on the block's columns
+  __shared__ float red_r[kRowWaves][W];
+  __shared__ float red_q[kRowWaves][W];
+  __shared__ float s_u[W];
+  __shared__ float s_kq;
+
+  const TQ* qp = static_cast<const TQ*>(p.q);
+  const TQ* kp = static_cast<const TQ*>(p.k);
+  const TQ* vp = static_cast<const TQ*>(p.v);
+  // Tokens t0 .. t0+TB−1 into buffer `buf` (inputs laid out [B, S, H, ·]).
+  // Indexes past the sequence or the head clamp to its last element, and
+  // the values staged for them are zeros (rows) or never read (tokens).
+  auto stage = [&](int t0, int buf) {
+    float kv[KI], ev[KI], qv[KI], gv[KI], vv[VI], wv[VI];
+#pragma unroll
+    for (int x = 0; x < KI; ++x) {
+      const int idx = min(tid + x * kRowThreads, TB * KP - 1), tt = idx / KP, i = idx % KP;
+      const int t = min(t0 + tt, S - 1), ic = min(i, K - 1);
+      const size_t row = (size_t(b) * S + t) * p.H + h;
+      kv[x] = ld(kp, row * K + ic);
+      qv[x] = ld(qp, row * K + ic);
+      ev[x] = p.erase[row * p.ew + (p.ew == 1 ? 0 : ic)];
+      gv[x] = p.dw ? p.g[row * p.dw + (p.dw == 1 ? 0 : ic)] : 0.f;
+    }
+#pragma unroll
+    for (int x = 0; x < VI; ++x) {
+      const int idx = min(tid + x * kRowThreads, TB * W - 1), tt = idx / W;
+      const int t = min(t0 + tt, S - 1), jc = min(jb + idx % W, V - 1);
+      const size_t row = (size_t(b) * S + t) * p.H + h;
+      vv[x] = ld(vp, row * V + jc);
+      wv[x] = p.write[row * p.ww + (p.ww == 1 ? 0 : jc)];
+    }
+#pragma unroll
+    for (int x = 0; x < KI; ++x) {
+      const int idx = tid + x * kRowThreads, tt = idx / KP, i = idx % KP;
+      if (idx < TB * KP) {
+        const bool ok = i < K;
+        tok[buf][tt][0][i] = ok ? kv[x] : 0.f;
+        tok[buf][tt][1][i] = ok ? kv[x] * ev[x] : 0.f;
+        tok[buf][tt][2][i] = ok ? p.scale * qv[x] : 0.f;
+        tok[buf][tt][3][i] = ok ? (p.dw ? expf(gv[x]) : 1.0f) : 0.f;
+      }
+    }
+#pragma unroll
+    for (int x = 0; x < VI; ++x) {
+      const int idx = tid + x * kRowThreads;
+      if (idx < TB * W) vw[buf][idx / W][idx % W] = jb + idx % W < V ? vv[x] * wv[x] : 0.f;
+    }
+  };
+
+  const bool colok = j0 + C - 1 < V;
+  const float* sin = p.s_in + bh * size_t(K) * V + j0;
+  vec s[RPT];
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg + kRowWaves * r;
+    s[r] = (i < K && colok) ? *reinterpret_cast<const vec*>(sin + size_t(i) * V) : vec(0.f);
+  }
+  stage(0, 0);
+  __syncthreads();
+  TY* y = static_cast<TY*>(p.y);
+  const int nblocks = (S + TB - 1) / TB;
+#pragma unroll 1
+  for (int blk = 0; blk < nblocks; ++blk) {
+    const int buf = blk & 1, t0 = blk * TB, tn = min(TB, S - t0);
+#pragma unroll 1
+    for (int tt = 0; tt < tn; ++tt) {
+      const float(*d)[KP] = tok[buf][tt];
+      if (tid < 64) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = tid; i < KP; i += 64) acc += d[0][i] * d[2][i];
+        acc = wave_sum(acc);
+        if (tid == 0) s_kq = acc;
+      }
+      // S⁻ = α⊙S, and the lane's partial sums of S⁻ᵀ(k⊙erase) and S⁻ᵀq'.
+      vec pr = vec(0.f), pq = vec(0.f);
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) {
+        const int i = rg + kRowWaves * r;
+        s[r] *= d[3][i];
+        pr += s[r] * d[1][i];
+        pq += s[r] * d[2][i];
+      }
+      *reinterpret_cast<vec*>(&red_r[rg][C * lane]) = pr;
+      *reinterpret_cast<vec*>(&red_q[rg][C * lane]) = pq;
+      __syncthreads();
+      // u = v⊙write − S⁻ᵀ(k⊙erase), y = S⁻ᵀq' + u·(kᵀq') per column.
+      if (tid < W) {
+        const int j = jb + tid;
+        float rr = 0.f, qs = 0.f;
+#pragma unroll
+        for (int x = 0; x < kRowWaves; ++x) {
+          rr += red_r[x][tid];
+          qs += red_q[x][tid];
+        }
+        const float u = vw[buf][tt][tid] - rr;
+        if (j < V) st(y, ((size_t(b) * S + t0 + tt) * p.H + h) * V + j, qs + u * s_kq);
+        s_u[tid] = u;
+      }
+      if (tt == 0 && blk + 1 < nblocks) stage(t0 + TB, buf ^ 1);
+      __syncthreads();
+      // S = S⁻ + k uᵀ.
+      const vec uv = *reinterpret_cast<const vec*>(&s_u[C * lane]);
+#pragma unroll
+      for (int r = 0; r < RPT; ++r) s[r] += d[0][rg + kRowWaves * r] * uv;
+    }
+  }
+  float* sout = p.s_out + bh * size_t(K) * V + j0;
+#pragma unroll
+  for (int r = 0; r < RPT; ++r) {
+    const int i = rg + kRowWaves * r;
+    if (i < K && colok) *reinterpret_cast<vec*>(sout + size_t(i) * V) = s[r];
+  }
+}
+
+template <class TQ, class TY, int C>
+hipError_t launch_recurrent_c(const StepParams& p, hipStream_t stream) {
+  constexpr int W = 64 * C;
+  const dim3 grid(unsigned(p.B * p.H * ((p.V + W - 1) / W)));
+  ProfScope ps("dn_recurrent_row", stream);
+#define DN_REC(RPT) \
+  hipLaunchKernelGGL((recurrent_row_kernel<TQ, TY, RPT, C>), grid, dim3(kRowThreads), 0, stream, p)
+  if (p.K <= 64) DN_REC(8);
+  else if (p.K <= 128) DN_REC(16);
+  else DN_REC(32);
+#undef DN_REC
+  return hipGetLastError();
+}
+
+template <class TQ, class TY>
+hipError_t launch_recurrent_typed(const StepParams& p, hipStream_t stream) {
+  // Two columns per lane (8-byte state accesses) when the rows allow it.
+  const bool c2 = p.V >= 128 && p.V % 2 == 0 &&
+                  ((reinterpret_cast<uintptr_t>(p.s_in) | reinterpret_cast<uintptr_t>(p.s_out)) %
+                   8) == 0;
+  return c2 ? launch_recurrent_c<TQ, TY, 2>(p, stream) : launch_recurrent_c<TQ, TY, 1>(p, stream);
+}
+
 // Fallback for head_k_dim > 512: one workgroup per (head, batch), two passes
 // over S (one lane per column).
 template <class TQ, class TY>
@@ -347,6 +518,7 @@ hipError_t launch_typed(const StepParams& p, hipStream_t stream) {
 
 hipError_t launch_step(const dn_step_args& a, float scale, hipStream_t stream) {
   StepParams p;
+  p.S = 1;
   p.B = int(a.batch);
   p.H = int(a.nheads);
   p.K = int(a.head_k_dim);
@@ -369,6 +541,39 @@ hipError_t launch_step(const dn_step_args& a, float scale, hipStream_t stream) {
   if (qb) return launch_typed<bf16, float>(p, stream);
   if (yb) return launch_typed<float, bf16>(p, stream);
   return launch_typed<float, float>(p, stream);
+}
+
+}  // namespace dn
+
+namespace dn {
+
+bool recurrent_supported(const dn_recurrent_args& a) { return a.head_k_dim <= kRecMaxK; }
+
+hipError_t launch_recurrent(const dn_recurrent_args& a, float scale, hipStream_t stream) {
+  StepParams p;
+  p.B = int(a.batch);
+  p.S = int(a.sequence);
+  p.H = int(a.nheads);
+  p.K = int(a.head_k_dim);
+  p.V = int(a.head_v_dim);
+  p.ew = int(a.erase_width);
+  p.ww = int(a.write_width);
+  p.dw = a.has_gate ? int(a.decay_width) : 0;
+  p.scale = scale;
+  p.q = a.q;
+  p.k = a.k;
+  p.v = a.v;
+  p.erase = a.erase;
+  p.write = a.write;
+  p.g = a.g;
+  p.s_in = a.state_in;
+  p.y = a.y;
+  p.s_out = a.state_out;
+  const bool qb = a.qkv_dtype == DN_BF16, yb = a.y_dtype == DN_BF16;
+  if (qb && yb) return launch_recurrent_typed<bf16, bf16>(p, stream);
+  if (qb) return launch_recurrent_typed<bf16, float>(p, stream);
+  if (yb) return launch_recurrent_typed<float, bf16>(p, stream);
+  return launch_recurrent_typed<float, float>(p, stream);
 }
 
 }  // namespace dn

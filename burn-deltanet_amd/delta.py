@@ -120,9 +120,22 @@ class DeltaInput:
         return self.delta_chunk_recalculated(chunk_len, check_finite)
 
     def delta_recurrent(self, check_finite: bool = False):
-        """recurrent.rs:107-142: delta_step unrolled over the sequence."""
+        """recurrent.rs:107-142: delta_step unrolled over the sequence — one
+        dn_recurrent call (the state stays on chip across the tokens), or
+        dn_step per token for head_k_dim above dn_recurrent's limit."""
         batch, sequence, nheads, head_k_dim, head_v_dim = self.dims()
         scale = self.resolved_scale()
+        if head_k_dim <= abi.RECURRENT_MAX_K:
+            c = lambda x: None if x is None else x.contiguous()
+            q, k, v = c(self.q_bshk), c(self.k_bshk), c(self.v_bshv)
+            e, w, g = c(self.erase_bshK), c(self.write_bshV), c(self.g_bshK)
+            state = self.state_bhkv.float().contiguous()
+            y = torch.empty((batch, sequence, nheads, head_v_dim), dtype=q.dtype,
+                            device=q.device)
+            s_out = torch.empty_like(state)
+            abi.run_recurrent(abi.recurrent_args(q, k, v, e, w, g, state, y, s_out, scale,
+                                                 check_finite))
+            return y, s_out
         state = self.state_bhkv.float().contiguous().clone()
         ys = []
         at = lambda x, t: None if x is None else x[:, t].contiguous()

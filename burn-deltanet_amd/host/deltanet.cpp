@@ -217,11 +217,41 @@ std::pair<Tensor, Tensor> DeltaInput::delta_recurrent(hipStream_t stream,
   const Dims d = dims();
   const DType dt = q_bshk.dtype();
   const double sc = resolved_scale();
+  Tensor y = Tensor::empty({d.batch, d.sequence, d.nheads, d.head_v_dim}, dt);
+  if (d.head_k_dim <= DN_RECURRENT_MAX_K) {
+    // One dn_recurrent call: the state stays on chip across the tokens.
+    Tensor s = Tensor::empty(state_bhkv.dims(), DType::F32);
+    dn_recurrent_args a{};
+    a.batch = d.batch;
+    a.sequence = d.sequence;
+    a.nheads = d.nheads;
+    a.head_k_dim = d.head_k_dim;
+    a.head_v_dim = d.head_v_dim;
+    a.erase_width = erase_bshK.dim(3);
+    a.write_width = write_bshV.dim(3);
+    a.decay_width = g_bshK ? g_bshK->dim(3) : 0;
+    a.has_gate = g_bshK ? 1 : 0;
+    a.scale = sc;
+    a.qkv_dtype = int32_t(dt);
+    a.y_dtype = int32_t(dt);
+    a.check_finite = check_finite ? 1 : 0;
+    a.q = q_bshk.data();
+    a.k = k_bshk.data();
+    a.v = v_bshv.data();
+    a.erase = static_cast<const float*>(erase_bshK.data());
+    a.write = static_cast<const float*>(write_bshV.data());
+    a.g = g_bshK ? static_cast<const float*>(g_bshK->data()) : nullptr;
+    a.state_in = static_cast<const float*>(state_bhkv.data());
+    a.y = y.data();
+    a.state_out = static_cast<float*>(s.data());
+    check(dn_recurrent(&a, stream));
+    return {y, s};
+  }
+  // head_k_dim above dn_recurrent's limit: dn_step per token, in place.
   Tensor state = Tensor::empty(state_bhkv.dims(), DType::F32);
   check_hip(hipMemcpyAsync(state.data(), state_bhkv.data(), state.bytes(),
                            hipMemcpyDeviceToDevice, stream),
             "hipMemcpyAsync");
-  Tensor y = Tensor::empty({d.batch, d.sequence, d.nheads, d.head_v_dim}, dt);
   // Per-token slices [batch, nheads, ·] of the [batch, sequence, nheads, ·]
   // inputs: rows of nheads·width elements, sequence·nheads·width apart.
   auto slice_buf = [&](const Tensor& x) {

@@ -138,6 +138,24 @@ typedef struct {
   float *state_out;             /* may alias state_in */
 } dn_step_args;
 
+/* delta_step over a whole sequence (recurrent.rs:107-142): the same gates and
+ * layouts as dn_chunk_fwd, evaluated token by token like the reference's
+ * DeltaPath::Recurrent. */
+typedef struct {
+  int64_t batch, sequence, nheads, head_k_dim, head_v_dim;
+  int64_t erase_width, write_width, decay_width;
+  int32_t has_gate;
+  double scale;          /* NaN => 1/sqrt(head_k_dim) */
+  int32_t qkv_dtype;
+  int32_t y_dtype;
+  int32_t check_finite;
+  const void *q, *k, *v;        /* [batch, sequence, nheads, head_k_dim | head_v_dim] */
+  const float *erase, *write, *g; /* [batch, sequence, nheads, width] */
+  const float *state_in;        /* [batch, nheads, head_k_dim, head_v_dim] */
+  void *y;                      /* [batch, sequence, nheads, head_v_dim] */
+  float *state_out;             /* may alias state_in */
+} dn_recurrent_args;
+
 /* Replaces DeltaChunkBackendExt::delta_chunk_recalculated
  * (src/delta/chunk_recalculated/chunk_recalculated.rs:110-151). */
 int dn_chunk_fwd(const dn_chunk_fwd_args *args, hipStream_t stream);
@@ -148,6 +166,17 @@ int dn_chunk_bwd(const dn_chunk_bwd_args *args, hipStream_t stream);
 
 /* Replaces delta_step (src/delta/recurrent.rs:41-50). */
 int dn_step(const dn_step_args *args, hipStream_t stream);
+
+/* Replaces DeltaInput::delta_recurrent (src/delta/recurrent.rs:107-142), the
+ * DeltaPath::Recurrent arm of DeltaInput::run (path.rs:215-231): delta_step
+ * unrolled over the sequence, with the state kept on chip from the first
+ * token to the last (one read and one write of it per call instead of one
+ * of each per token). DeltaProduct's decode folds its u Householder
+ * micro-steps into a u-token sequence and runs it this way
+ * (delta_product.rs:270-305). head_k_dim up to 256; larger returns
+ * DN_ERR_UNSUPPORTED (delta_step per token covers it). */
+#define DN_RECURRENT_MAX_K 256
+int dn_recurrent(const dn_recurrent_args *args, hipStream_t stream);
 
 /* Bytes of device workspace dn_chunk_fwd / dn_chunk_bwd need for these
  * arguments (0 on invalid arguments). Has no counterpart in the reference,

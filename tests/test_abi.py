@@ -86,6 +86,34 @@ def test_step_rejects_invalid_arguments():
     assert lib.dn_step(ctypes.byref(a), None) == -6  # null pointers
 
 
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(sequence=0), -1, "sequence length must be at least 1"),
+    (dict(nheads=0), -2, "at least 1"),
+    (dict(erase_width=3), -3, "erase gate: last axis must be 1 or 4, got 3"),
+    (dict(write_width=5), -3, "write gate: last axis must be 1 or 6, got 5"),
+    (dict(decay_width=2), -3, "forget gate: last axis must be 1 or 4, got 2"),
+    (dict(y_dtype=3), -7, "dtype"),
+    (dict(state_out=None), -6, "NULL"),
+    (dict(head_k_dim=abi.RECURRENT_MAX_K + 1, erase_width=1, decay_width=1), -9,
+     f"head_k_dim up to {abi.RECURRENT_MAX_K}"),
+])
+def test_recurrent_rejects_invalid_arguments(over, code, msg):
+    """dn_recurrent takes dn_chunk_fwd's shape rules (no chunk_len) and
+    refuses heads above its limit before touching any pointer."""
+    lib = abi.lib()
+    a = abi.RecurrentArgs()
+    a.batch, a.sequence, a.nheads, a.head_k_dim, a.head_v_dim = 1, 8, 1, 4, 6
+    a.erase_width, a.write_width, a.decay_width, a.has_gate = 1, 1, 1, 1
+    a.scale = float("nan")
+    a.qkv_dtype = a.y_dtype = abi.DN_F32
+    for f in ["q", "k", "v", "erase", "write", "g", "state_in", "y", "state_out"]:
+        setattr(a, f, 0x1000)  # never dereferenced: every case fails its checks first
+    for k, v in over.items():
+        setattr(a, k, v)
+    assert lib.dn_recurrent(ctypes.byref(a), None) == code
+    assert msg in lib.dn_last_error().decode()
+
+
 def test_bwd_rejects_missing_d_g():
     lib = abi.lib()
     a = abi.ChunkBwdArgs()
