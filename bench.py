@@ -18,6 +18,8 @@ dk128) at 1 GPU; % roofline"):
 * config4 / config5 = BASELINE configs 4 (DeltaProduct u=2, folded core
   forward) and 5 (GDN-2 per-channel gates, forward + custom backward), each
   with its own HBM roofline; not part of `value`.
+* frontend = dn_frontend (the projection front-end) at the config-2 shape,
+  with its HBM roofline; not part of `value`.
 * cpu_baseline = the CPU oracle (a C++ restatement of the reference algorithm,
   incl. its 24·L³ ladder) on a bounded sample of config 2, all host threads.
 
@@ -200,6 +202,43 @@ def bench_product_decode(torch, pkg, steps, warmup, u=2):
             "kernel_us": k_us, "bytes_per_token": nbytes,
             "roofline": _hbm(nbytes, k_us / 1e3) | {"kernel": name,
                                                      "traffic": traffic_from_profiles(name)}}
+
+
+def bench_frontend(torch, pkg, steps, warmup):
+    """The projection front-end (dn_frontend: QkvProjection::forward after its
+    in_proj, qkv.rs:373-449) at the config-2 shape: B=8, T=4096, H=16,
+    dk=128, dv=256, u=1, short conv of 4 with SiLU, L2 q/k norm, scalar β;
+    bf16 projection in, bf16 q/k/v out, fp32 β."""
+    B, S, H, K, V, KC = 8, 4096, 16, 128, 256, 4
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20260832)
+    conv_dim = H * K * 2 + H * V
+    width = conv_dim + H
+    proj = torch.randn((B, S, width), generator=gen, device=dev).to(torch.bfloat16)
+    weight = torch.randn((conv_dim, KC), generator=gen, device=dev) * 0.5
+    win = torch.randn((B, conv_dim, KC), generator=gen, device=dev).to(torch.bfloat16)
+    wout = torch.empty_like(win)
+    q = torch.empty((B, S, H, K), dtype=torch.bfloat16, device=dev)
+    k, v = torch.empty_like(q), torch.empty((B, S, H, V), dtype=torch.bfloat16, device=dev)
+    beta = torch.empty((B, S, H, 1), device=dev)
+    abi = pkg.abi
+    args = abi.frontend_args(proj, weight, None, win, wout, q, k, v, beta, beta, nheads=H,
+                             head_k_dim=K, head_v_dim=V, n_householder=1,
+                             conv_activation=abi.DN_ACT_SILU, qk_activation=abi.DN_ACT_SILU,
+                             qk_norm=abi.DN_QKNORM_L2, write_gate=abi.DN_WRITE_SCALAR,
+                             allow_neg_eigval=False)
+    ms, kern = _timed(torch, abi, lambda: abi.run_frontend(args), steps, warmup)
+    # Read the conv and β columns (bf16), write q, k, v (bf16) and β (fp32);
+    # the windows (read + write) are B·conv_dim·KC each.
+    nbytes = B * S * (width * 2 + conv_dim * 2 + H * 4) + 2 * B * conv_dim * KC * 2
+    k_ms = kern["dn_frontend"]["avg_us"] / 1e3 if "dn_frontend" in kern else ms
+    return {"workload": "dn_frontend at the config-2 shape (B=8 T=4096 H=16 dk=128 dv=256, "
+                        "conv 4, SiLU, L2, scalar beta; bf16)",
+            "ms_per_call": round(ms, 4), "tokens_per_s": round(B * S / (ms / 1e3), 1),
+            "roofline": _hbm(nbytes, k_ms) | {"kernel": "dn_frontend",
+                                               "traffic": traffic_from_profiles("dn_frontend")},
+            "kernels": kern}
 
 
 def _timed(torch, abi, fn, steps, warmup):
@@ -385,8 +424,8 @@ def main():
                     help="timed calls for configs 4 and 5 (after one warmup)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="short run for rocprofv3 --pmc: a 1 GiB copy (calibration), then 2 "
-                         "forward, 2 decode and 2 DeltaProduct-decode launches and one "
-                         "config-5 forward + backward; prints no JSON")
+                         "forward, 2 decode, 2 DeltaProduct-decode and 2 front-end calls and "
+                         "one config-5 forward + backward; prints no JSON")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -407,6 +446,7 @@ def main():
         bench_chunk_fwd(torch, pkg, 2, 0, algo)
         bench_decode(torch, pkg, 2, 0)
         bench_product_decode(torch, pkg, 2, 0)
+        bench_frontend(torch, pkg, 2, 0)
         bench_config5(torch, pkg, 1, 0)
         torch.cuda.synchronize()
         print("[bench] profile pass done", file=sys.stderr, flush=True)
@@ -460,6 +500,10 @@ def main():
         print("[bench] config 5 (GDN-2 forward + backward)", file=sys.stderr, flush=True)
         extra["config5"] = bench_config5(torch, pkg, args.extra_steps, 1)
         print(f"[bench] config5 {extra['config5']}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+        print("[bench] projection front-end (dn_frontend)", file=sys.stderr, flush=True)
+        extra["frontend"] = bench_frontend(torch, pkg, max(args.extra_steps, 10), 2)
+        print(f"[bench] frontend {extra['frontend']}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
 
     cpu = None

@@ -20,6 +20,10 @@ LIB_PATH = _HERE / "libdeltanet_core.so"
 DN_F32, DN_BF16 = 0, 1
 DN_ALGO_AUTO, DN_ALGO_GENERIC, DN_ALGO_MFMA = 0, 1, 2
 RECURRENT_MAX_K = 256  # dn_recurrent's head_k_dim limit (deltanet_core.h)
+DN_ACT_IDENTITY, DN_ACT_SILU, DN_ACT_RELU, DN_ACT_ELU_PLUS_ONE = 0, 1, 2, 3
+DN_QKNORM_NONE, DN_QKNORM_L2, DN_QKNORM_SUM = 0, 1, 2
+DN_WRITE_FIXED, DN_WRITE_SCALAR, DN_WRITE_CHANNEL = 0, 1, 2
+FRONTEND_MAX_HEAD_DIM, FRONTEND_MAX_KERNEL = 256, 8
 
 STATUS = {
     0: "DN_OK",
@@ -36,7 +40,8 @@ STATUS = {
 }
 
 EXPORTS = [
-    "dn_chunk_fwd", "dn_chunk_bwd", "dn_step", "dn_recurrent", "dn_chunk_fwd_workspace_bytes",
+    "dn_chunk_fwd", "dn_chunk_bwd", "dn_step", "dn_recurrent", "dn_frontend",
+    "dn_chunk_fwd_workspace_bytes",
     "dn_chunk_bwd_workspace_bytes", "dn_chunk_fwd_algo", "dn_chunk_bwd_algo",
     "dn_last_error", "dn_version", "dn_profile_enable", "dn_profile_read",
 ]
@@ -92,6 +97,19 @@ class RecurrentArgs(ctypes.Structure):
     ]
 
 
+class FrontendArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i64), ("sequence", _i64), ("nheads", _i64), ("head_k_dim", _i64),
+        ("head_v_dim", _i64), ("n_householder", _i64), ("conv_kernel", _i64),
+        ("proj_stride", _i64), ("conv_activation", _i32), ("qk_activation", _i32),
+        ("qk_norm", _i32), ("write_gate", _i32), ("allow_neg_eigval", _i32),
+        ("in_dtype", _i32), ("out_dtype", _i32),
+        ("projected", _vp), ("conv_weight", _vp), ("conv_bias", _vp), ("window_in", _vp),
+        ("window_out", _vp), ("q", _vp), ("k", _vp), ("v", _vp), ("erase", _vp),
+        ("write", _vp),
+    ]
+
+
 _LIB = None
 
 
@@ -112,6 +130,8 @@ def lib() -> ctypes.CDLL:
         L.dn_step.restype = ctypes.c_int
         L.dn_recurrent.argtypes = [ctypes.POINTER(RecurrentArgs), _vp]
         L.dn_recurrent.restype = ctypes.c_int
+        L.dn_frontend.argtypes = [ctypes.POINTER(FrontendArgs), _vp]
+        L.dn_frontend.restype = ctypes.c_int
         L.dn_chunk_fwd_workspace_bytes.argtypes = [ctypes.POINTER(ChunkFwdArgs)]
         L.dn_chunk_fwd_workspace_bytes.restype = _sz
         L.dn_chunk_bwd_workspace_bytes.argtypes = [ctypes.POINTER(ChunkBwdArgs)]
@@ -238,6 +258,36 @@ def recurrent_args(q, k, v, erase, write, g, state, y, state_out, scale, check_f
 
 def run_recurrent(args: RecurrentArgs) -> None:
     check(lib().dn_recurrent(ctypes.byref(args), stream_handle()))
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def frontend_args(projected, conv_weight, conv_bias, window_in, window_out, q, k, v, erase,
+                  write, *, nheads, head_k_dim, head_v_dim, n_householder, conv_activation,
+                  qk_activation, qk_norm, write_gate, allow_neg_eigval):
+    """dn_frontend over `projected` [batch, sequence, proj_stride] (contiguous
+    rows; the stride is its last axis)."""
+    B, S, W = projected.shape
+    a = FrontendArgs()
+    a.batch, a.sequence, a.nheads = B, S, nheads
+    a.head_k_dim, a.head_v_dim, a.n_householder = head_k_dim, head_v_dim, n_householder
+    a.conv_kernel = 0 if conv_weight is None else conv_weight.shape[-1]
+    a.proj_stride = W
+    a.conv_activation, a.qk_activation = int(conv_activation), int(qk_activation)
+    a.qk_norm, a.write_gate = int(qk_norm), int(write_gate)
+    a.allow_neg_eigval = int(bool(allow_neg_eigval))
+    a.in_dtype, a.out_dtype = dtype_tag(projected.dtype), dtype_tag(q.dtype)
+    a.projected, a.conv_weight, a.conv_bias = (_ptr(projected), _ptr(conv_weight),
+                                               _ptr(conv_bias))
+    a.window_in, a.window_out = _ptr(window_in), _ptr(window_out)
+    a.q, a.k, a.v, a.erase, a.write = (_ptr(q), _ptr(k), _ptr(v), _ptr(erase), _ptr(write))
+    return a
+
+
+def run_frontend(args: FrontendArgs) -> None:
+    check(lib().dn_frontend(ctypes.byref(args), stream_handle()))
 
 
 def chunk_bwd_args(dy, dstate, q, k, v, erase, write, g, state, grads, chunk_len, scale,

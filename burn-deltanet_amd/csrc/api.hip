@@ -402,6 +402,60 @@ int dn_step(const dn_step_args* a, hipStream_t stream) {
   return DN_OK;
 }
 
+int dn_frontend(const dn_frontend_args* a, hipStream_t stream) {
+  g_last_error.clear();
+  if (!a) return fail(DN_ERR_NULL, "args is NULL");
+  // conv.rs:88-90 and qkv.rs:397-401
+  if (a->sequence < 1) return fail(DN_ERR_SEQUENCE, "sequence length must be at least 1");
+  if (a->batch < 1 || a->nheads < 1 || a->head_k_dim < 1 || a->head_v_dim < 1 ||
+      a->n_householder < 1 || a->conv_kernel < 0)
+    return fail(DN_ERR_SHAPE, "batch, nheads, head_k_dim, head_v_dim and n_householder must be "
+                              "at least 1, conv_kernel at least 0");
+  if (a->head_k_dim > DN_FRONTEND_MAX_HEAD_DIM || a->head_v_dim > DN_FRONTEND_MAX_HEAD_DIM)
+    return fail(DN_ERR_UNSUPPORTED, "dn_frontend supports head dims up to " +
+                                        std::to_string(DN_FRONTEND_MAX_HEAD_DIM));
+  if (a->conv_kernel > DN_FRONTEND_MAX_KERNEL)
+    return fail(DN_ERR_UNSUPPORTED, "dn_frontend supports conv_kernel up to " +
+                                        std::to_string(DN_FRONTEND_MAX_KERNEL));
+  if (!valid_dtype(a->in_dtype) || !valid_dtype(a->out_dtype))
+    return fail(DN_ERR_DTYPE, "dtype must be DN_F32 or DN_BF16");
+  if (a->qk_norm == DN_QKNORM_SUM)
+    return fail(DN_ERR_UNSUPPORTED, "QkNorm::Sum is not offered (its epsilon is burn_stack's)");
+  if (a->qk_norm != DN_QKNORM_L2 && a->qk_norm != DN_QKNORM_NONE)
+    return fail(DN_ERR_SHAPE, "unknown qk_norm");
+  if (a->qk_activation < DN_ACT_IDENTITY || a->qk_activation > DN_ACT_ELU_PLUS_ONE)
+    return fail(DN_ERR_SHAPE, "unknown qk_activation");
+  if (a->conv_activation != DN_ACT_IDENTITY && a->conv_activation != DN_ACT_SILU)
+    return fail(DN_ERR_SHAPE, "conv_activation must be DN_ACT_SILU or DN_ACT_IDENTITY");
+  if (a->write_gate < DN_WRITE_FIXED || a->write_gate > DN_WRITE_CHANNEL)
+    return fail(DN_ERR_SHAPE, "unknown write_gate");
+  const bool has_conv = a->conv_kernel > 0;
+  if (has_conv != (a->window_in != nullptr) || has_conv != (a->window_out != nullptr))
+    return fail(DN_ERR_SHAPE, "convolution window presence must match the block's convolution");
+  const int64_t H = a->nheads, u = a->n_householder;
+  const int64_t key_dim = H * a->head_k_dim, value_dim = H * a->head_v_dim;
+  const int64_t conv_dim = key_dim + u * (key_dim + value_dim);
+  const int64_t gate_w = a->write_gate == DN_WRITE_FIXED    ? 0
+                         : a->write_gate == DN_WRITE_SCALAR ? u * H
+                                                            : u * (key_dim + value_dim);
+  if (a->proj_stride < conv_dim + gate_w)
+    return fail(DN_ERR_SHAPE, "proj_stride " + std::to_string(a->proj_stride) +
+                                  " is narrower than the conv and write-gate columns (" +
+                                  std::to_string(conv_dim + gate_w) + ")");
+  if (a->batch * a->sequence >= (int64_t(1) << 31) || conv_dim >= (int64_t(1) << 31) ||
+      a->batch * a->sequence * a->proj_stride >= (int64_t(1) << 40) ||
+      a->batch * a->sequence * (gate_w > u * H ? gate_w : u * H) >= (int64_t(1) << 32))
+    return fail(DN_ERR_SHAPE, "tensor too large");
+  if (!a->projected || !a->q || !a->k || !a->v || !a->erase || !a->write ||
+      (has_conv && !a->conv_weight))
+    return fail(DN_ERR_NULL, "a required tensor pointer is NULL");
+  if (a->write_gate == DN_WRITE_CHANNEL && a->write == a->erase)
+    return fail(DN_ERR_SHAPE, "per-channel erase and write gates need separate buffers");
+  hipError_t e = launch_frontend(*a, stream);
+  if (e != hipSuccess) return hip_fail(e, "dn_frontend launch");
+  return DN_OK;
+}
+
 int dn_recurrent(const dn_recurrent_args* a, hipStream_t stream) {
   g_last_error.clear();
   if (!a) return fail(DN_ERR_NULL, "args is NULL");

@@ -72,6 +72,8 @@ hipError_t launch_step(const dn_step_args& a, float scale, hipStream_t stream);
 constexpr int64_t kRecMaxK = DN_RECURRENT_MAX_K;
 bool recurrent_supported(const dn_recurrent_args& a);
 hipError_t launch_recurrent(const dn_recurrent_args& a, float scale, hipStream_t stream);
+// dn_frontend: the projection front-end (frontend.hip).
+hipError_t launch_frontend(const dn_frontend_args& a, hipStream_t stream);
 
 struct GenericFwdPlan {
   size_t ws_bytes;

@@ -1,0 +1,252 @@
+"""Host-side mirror of the reference's projection front-end
+(src/common/qkv.rs, conv.rs, norm.rs) over dn_frontend.
+
+`QkvProjection` keeps the reference's fields and methods (`key_dim`,
+`value_dim`, `conv_dim`, `write_gate_width`, `d_in_proj`, `segments`,
+`zero_conv_window`, `forward`, `step`). The in-projection is a plain library
+GEMM (torch.matmul, i.e. hipBLASLt); everything after it, up to the delta
+rule's inputs, is one dn_frontend call. Grouped values (n_value_heads ≠
+nheads) and QkNorm.SUM are not offered: both depend on burn_stack code the
+reference does not vendor.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from enum import IntEnum
+from typing import List, Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from . import abi
+from .abi import DeltaError
+
+
+class QkActivation(IntEnum):
+    """norm.rs:22-34."""
+    IDENTITY = abi.DN_ACT_IDENTITY
+    SILU = abi.DN_ACT_SILU
+    RELU = abi.DN_ACT_RELU
+    ELU_PLUS_ONE = abi.DN_ACT_ELU_PLUS_ONE
+
+
+class ConvActivation(IntEnum):
+    """conv.rs:29-35."""
+    SILU = abi.DN_ACT_SILU
+    IDENTITY = abi.DN_ACT_IDENTITY
+
+
+class QkNorm(IntEnum):
+    """norm.rs:56-65 (SUM is declared for completeness and refused)."""
+    L2 = abi.DN_QKNORM_L2
+    SUM = abi.DN_QKNORM_SUM
+    NONE = abi.DN_QKNORM_NONE
+
+
+class WriteGate(IntEnum):
+    """qkv.rs:45-54."""
+    FIXED = abi.DN_WRITE_FIXED
+    SCALAR = abi.DN_WRITE_SCALAR
+    CHANNEL = abi.DN_WRITE_CHANNEL
+
+
+@dataclass
+class ShortConv:
+    """conv.rs:49-83: the depthwise weight [conv_dim, conv_kernel] (Conv1d's
+    [conv_dim, 1, kernel] without its unit axis), an optional bias, and the
+    fused activation."""
+
+    weight: Tensor
+    bias: Optional[Tensor] = None
+    activation: ConvActivation = ConvActivation.SILU
+
+    def conv_dim(self) -> int:
+        return self.weight.shape[0]
+
+    def conv_kernel(self) -> int:
+        return self.weight.shape[-1]
+
+    def zero_window(self, batch: int, device, dtype=torch.float32) -> Tensor:
+        return torch.zeros((batch, self.conv_dim(), self.conv_kernel()), dtype=dtype,
+                           device=device)
+
+
+@dataclass
+class Qkv:
+    """qkv.rs:76-97 (k, v and the gates with the micro-steps folded into the
+    sequence)."""
+
+    q_bshk: Tensor
+    k_bShk: Tensor
+    v_bShv: Tensor
+    erase_bShK: Tensor
+    write_bShV: Tensor
+    gate_bshv: Optional[Tensor]
+    extra_bsx: Optional[Tensor]
+
+
+@dataclass
+class QkvStep:
+    """qkv.rs:99-116."""
+
+    q_bhk: Tensor
+    k_buhk: Tensor
+    v_buhv: Tensor
+    erase_buhK: Tensor
+    write_buhV: Tensor
+    gate_bhv: Optional[Tensor]
+    extra_bx: Optional[Tensor]
+
+
+@dataclass
+class QkvProjection:
+    """qkv.rs:118-155, n_value_heads = nheads. `in_proj` is the weight
+    [d_model, d_in_proj] (applied as x @ in_proj) or None when the caller
+    supplies the projection itself (`forward_projected` / `step_projected`)."""
+
+    nheads: int
+    head_k_dim: int
+    head_v_dim: int
+    n_householder: int = 1
+    conv: Optional[ShortConv] = None
+    qk_activation: QkActivation = QkActivation.SILU
+    qk_norm: QkNorm = QkNorm.L2
+    write_gate: WriteGate = WriteGate.SCALAR
+    has_gate: bool = False
+    allow_neg_eigval: bool = False
+    extra_channels: int = 0
+    in_proj: Optional[Tensor] = None
+    in_proj_bias: Optional[Tensor] = None  # QkvProjectionConfig::has_proj_bias
+
+    def key_dim(self) -> int:
+        return self.nheads * self.head_k_dim
+
+    def value_dim(self) -> int:
+        return self.nheads * self.head_v_dim
+
+    def conv_dim(self) -> int:
+        """qkv.rs:180-182."""
+        return self.key_dim() + self.n_householder * (self.key_dim() + self.value_dim())
+
+    def write_gate_width(self) -> int:
+        """qkv.rs:189-197."""
+        per = {WriteGate.FIXED: 0, WriteGate.SCALAR: self.nheads,
+               WriteGate.CHANNEL: self.key_dim() + self.value_dim()}[self.write_gate]
+        return self.n_householder * per
+
+    def d_in_proj(self) -> int:
+        """qkv.rs:199-205."""
+        return (self.conv_dim() + self.write_gate_width()
+                + (self.value_dim() if self.has_gate else 0) + self.extra_channels)
+
+    def conv_kernel(self) -> int:
+        return 0 if self.conv is None else self.conv.conv_kernel()
+
+    def zero_conv_window(self, batch: int, device, dtype=torch.float32) -> Optional[Tensor]:
+        return None if self.conv is None else self.conv.zero_window(batch, device, dtype)
+
+    def segments(self) -> List[Tuple[str, int]]:
+        """qkv.rs:237-262."""
+        u = self.n_householder
+        seg = [("q", self.key_dim()), ("k", u * self.key_dim()), ("v", u * self.value_dim())]
+        if self.write_gate == WriteGate.SCALAR:
+            seg.append(("beta", u * self.nheads))
+        elif self.write_gate == WriteGate.CHANNEL:
+            seg += [("erase", u * self.key_dim()), ("write", u * self.value_dim())]
+        if self.has_gate:
+            seg.append(("gate", self.value_dim()))
+        if self.extra_channels > 0:
+            seg.append(("extra", self.extra_channels))
+        return seg
+
+    # -- forward ---------------------------------------------------------------
+
+    def forward(self, x_bsd: Tensor, conv_window_bwc: Optional[Tensor],
+                out_dtype=None) -> Tuple[Qkv, Optional[Tensor]]:
+        """qkv.rs:373-449: in_proj, then dn_frontend."""
+        if self.in_proj is None:
+            raise DeltaError(-6, "QkvProjection.forward needs in_proj; use forward_projected")
+        return self.forward_projected(self._in_proj(x_bsd), conv_window_bwc, out_dtype)
+
+    def step(self, x_bd: Tensor, conv_window_bwc: Optional[Tensor],
+             out_dtype=None) -> Tuple[QkvStep, Optional[Tensor]]:
+        """qkv.rs:454-516: the single-token form."""
+        if self.in_proj is None:
+            raise DeltaError(-6, "QkvProjection.step needs in_proj; use step_projected")
+        return self.step_projected(self._in_proj(x_bd), conv_window_bwc, out_dtype)
+
+    def forward_projected(self, projected_bsw: Tensor, conv_window_bwc: Optional[Tensor],
+                          out_dtype=None) -> Tuple[Qkv, Optional[Tensor]]:
+        B, S, W = projected_bsw.shape
+        if W != self.d_in_proj():
+            raise DeltaError(-2, f"projection width {W} != d_in_proj {self.d_in_proj()}")
+        outs, window = self._run(projected_bsw, conv_window_bwc, out_dtype)
+        gate, extra = self._tail_views(projected_bsw)
+        return Qkv(*outs, gate_bshv=gate, extra_bsx=extra), window
+
+    def step_projected(self, projected_bw: Tensor, conv_window_bwc: Optional[Tensor],
+                       out_dtype=None) -> Tuple[QkvStep, Optional[Tensor]]:
+        B, W = projected_bw.shape
+        if W != self.d_in_proj():
+            raise DeltaError(-2, f"projection width {W} != d_in_proj {self.d_in_proj()}")
+        outs, window = self._run(projected_bw.reshape(B, 1, W), conv_window_bwc, out_dtype)
+        q, k, v, e, w = outs
+        gate, extra = self._tail_views(projected_bw.reshape(B, 1, W))
+        return QkvStep(q[:, 0], k, v, e, w,
+                       gate_bhv=None if gate is None else gate[:, 0],
+                       extra_bx=None if extra is None else extra[:, 0]), window
+
+    # -- internals ---------------------------------------------------------------
+
+    def _in_proj(self, x: Tensor) -> Tensor:
+        y = torch.matmul(x, self.in_proj)
+        return y if self.in_proj_bias is None else y + self.in_proj_bias
+
+    def _tail_views(self, p: Tensor):
+        """The output gate and the extra channels: views of the projection,
+        as the reference's split + reshape give (qkv.rs:267-300, 429)."""
+        B, S, _ = p.shape
+        c = self.conv_dim() + self.write_gate_width()
+        gate = None
+        if self.has_gate:
+            gate = p[:, :, c:c + self.value_dim()].unflatten(2, (self.nheads, self.head_v_dim))
+            c += self.value_dim()
+        extra = p[:, :, c:c + self.extra_channels] if self.extra_channels > 0 else None
+        return gate, extra
+
+    def _run(self, p: Tensor, window: Optional[Tensor], out_dtype):
+        if (self.conv is None) != (window is None):
+            raise DeltaError(-2, "convolution window presence must match the block's "
+                                 "convolution")  # qkv.rs:397-401
+        if not p.is_cuda:
+            raise DeltaError(-6, "tensors must live on the GPU (no CPU fallback)")
+        p = p.contiguous()
+        B, S, _ = p.shape
+        H, dk, dv, u = self.nheads, self.head_k_dim, self.head_v_dim, self.n_householder
+        od = p.dtype if out_dtype is None else out_dtype
+        dev = p.device
+        q = torch.empty((B, S, H, dk), dtype=od, device=dev)
+        k = torch.empty((B, S * u, H, dk), dtype=od, device=dev)
+        v = torch.empty((B, S * u, H, dv), dtype=od, device=dev)
+        if self.write_gate == WriteGate.CHANNEL:
+            erase = torch.empty((B, S * u, H, dk), dtype=torch.float32, device=dev)
+            write = torch.empty((B, S * u, H, dv), dtype=torch.float32, device=dev)
+        else:
+            # One tensor for both halves, as the reference's (beta.clone(), beta).
+            erase = torch.empty((B, S * u, H, 1), dtype=torch.float32, device=dev)
+            write = erase
+        win_in = win_out = weight = bias = None
+        act = ConvActivation.IDENTITY
+        if self.conv is not None:
+            weight = self.conv.weight.reshape(self.conv_dim(), -1).float().contiguous()
+            bias = None if self.conv.bias is None else self.conv.bias.float().contiguous()
+            act = self.conv.activation
+            win_in = window.to(p.dtype).contiguous()
+            win_out = torch.empty_like(win_in)
+        abi.run_frontend(abi.frontend_args(
+            p, weight, bias, win_in, win_out, q, k, v, erase, write, nheads=H, head_k_dim=dk,
+            head_v_dim=dv, n_householder=u, conv_activation=act,
+            qk_activation=self.qk_activation, qk_norm=self.qk_norm,
+            write_gate=self.write_gate, allow_neg_eigval=self.allow_neg_eigval))
+        return (q, k, v, erase, write), win_out

@@ -436,4 +436,129 @@ DeltaChunkGrads combined_backward(const Tensor& d_y_bshv,
   return g;
 }
 
+// ---------------------------------------------------------------------------
+// The projection front-end (qkv.rs:373-516) over dn_frontend.
+// ---------------------------------------------------------------------------
+
+Tensor ShortConv::zero_window(int64_t batch, DType dtype, hipStream_t stream) const {
+  Tensor w = Tensor::empty({batch, conv_dim(), conv_kernel()}, dtype);
+  check_hip(hipMemsetAsync(w.data(), 0, w.bytes(), stream), "hipMemsetAsync");
+  return w;
+}
+
+int64_t QkvProjection::conv_dim() const {
+  return key_dim() + n_householder * (key_dim() + value_dim());
+}
+
+int64_t QkvProjection::write_gate_width() const {
+  switch (write_gate) {
+    case WriteGate::Fixed: return 0;
+    case WriteGate::Scalar: return n_householder * nheads;
+    default: return n_householder * (key_dim() + value_dim());
+  }
+}
+
+int64_t QkvProjection::d_in_proj() const {
+  return conv_dim() + write_gate_width() + (has_gate ? value_dim() : 0) + extra_channels;
+}
+
+std::optional<Tensor> QkvProjection::zero_conv_window(int64_t batch, DType dtype,
+                                                      hipStream_t stream) const {
+  if (!conv) return std::nullopt;
+  return conv->zero_window(batch, dtype, stream);
+}
+
+namespace {
+
+struct FrontOut {
+  Tensor q, k, v, erase, write;
+  std::optional<Tensor> window;
+};
+
+FrontOut run_frontend(const QkvProjection& pr, const Tensor& projected, int64_t batch,
+                      int64_t sequence, const std::optional<Tensor>& window,
+                      std::optional<DType> out_dtype, hipStream_t stream) {
+  require_defined(projected, "projection");
+  if (projected.dim(projected.rank() - 1) != pr.d_in_proj())
+    throw Error(DN_ERR_SHAPE, "projection: last axis must be d_in_proj = " +
+                                  std::to_string(pr.d_in_proj()) + ", got " +
+                                  std::to_string(projected.dim(projected.rank() - 1)));
+  if (pr.conv.has_value() != window.has_value())  // qkv.rs:397-401
+    throw Error(DN_ERR_SHAPE, "convolution window presence must match the block's convolution");
+  const int64_t H = pr.nheads, dk = pr.head_k_dim, dv = pr.head_v_dim, u = pr.n_householder;
+  const DType od = out_dtype.value_or(projected.dtype());
+  FrontOut o;
+  o.q = Tensor::empty({batch, sequence, H, dk}, od);
+  o.k = Tensor::empty({batch, sequence * u, H, dk}, od);
+  o.v = Tensor::empty({batch, sequence * u, H, dv}, od);
+  if (pr.write_gate == WriteGate::Channel) {
+    o.erase = Tensor::empty({batch, sequence * u, H, dk}, DType::F32);
+    o.write = Tensor::empty({batch, sequence * u, H, dv}, DType::F32);
+  } else {
+    // One tensor for both halves, as the reference's (beta.clone(), beta).
+    o.erase = Tensor::empty({batch, sequence * u, H, 1}, DType::F32);
+    o.write = o.erase;
+  }
+  dn_frontend_args a{};
+  a.batch = batch;
+  a.sequence = sequence;
+  a.nheads = H;
+  a.head_k_dim = dk;
+  a.head_v_dim = dv;
+  a.n_householder = u;
+  a.conv_kernel = pr.conv_kernel();
+  a.proj_stride = pr.d_in_proj();
+  a.conv_activation = pr.conv ? int32_t(pr.conv->activation) : DN_ACT_IDENTITY;
+  a.qk_activation = int32_t(pr.qk_activation);
+  a.qk_norm = int32_t(pr.qk_norm);
+  a.write_gate = int32_t(pr.write_gate);
+  a.allow_neg_eigval = pr.allow_neg_eigval ? 1 : 0;
+  a.in_dtype = int32_t(projected.dtype());
+  a.out_dtype = int32_t(od);
+  a.projected = projected.data();
+  if (pr.conv) {
+    require_f32(pr.conv->weight, "conv weight");
+    expect_shape(*window, {batch, pr.conv_dim(), pr.conv_kernel()}, "conv window");
+    if (window->dtype() != projected.dtype())
+      throw Error(DN_ERR_DTYPE, "conv window: dtype must be the projection's");
+    a.conv_weight = static_cast<const float*>(pr.conv->weight.data());
+    if (pr.conv->bias) {
+      require_f32(*pr.conv->bias, "conv bias");
+      a.conv_bias = static_cast<const float*>(pr.conv->bias->data());
+    }
+    o.window = Tensor::empty(window->dims(), window->dtype());
+    a.window_in = window->data();
+    a.window_out = o.window->data();
+  }
+  a.q = o.q.data();
+  a.k = o.k.data();
+  a.v = o.v.data();
+  a.erase = static_cast<float*>(o.erase.data());
+  a.write = static_cast<float*>(o.write.data());
+  check(dn_frontend(&a, stream));
+  return o;
+}
+
+}  // namespace
+
+std::pair<Qkv, std::optional<Tensor>> QkvProjection::forward_projected(
+    const Tensor& projected_bsw, const std::optional<Tensor>& conv_window_bwc,
+    hipStream_t stream, std::optional<DType> out_dtype) const {
+  if (projected_bsw.rank() != 3)
+    throw Error(DN_ERR_SHAPE, "projection: expected [batch, sequence, d_in_proj]");
+  FrontOut o = run_frontend(*this, projected_bsw, projected_bsw.dim(0), projected_bsw.dim(1),
+                            conv_window_bwc, out_dtype, stream);
+  return {Qkv{o.q, o.k, o.v, o.erase, o.write}, o.window};
+}
+
+std::pair<QkvStep, std::optional<Tensor>> QkvProjection::step_projected(
+    const Tensor& projected_bw, const std::optional<Tensor>& conv_window_bwc,
+    hipStream_t stream, std::optional<DType> out_dtype) const {
+  if (projected_bw.rank() != 2)
+    throw Error(DN_ERR_SHAPE, "projection: expected [batch, d_in_proj]");
+  const int64_t B = projected_bw.dim(0);
+  FrontOut o = run_frontend(*this, projected_bw, B, 1, conv_window_bwc, out_dtype, stream);
+  return {QkvStep{o.q.reshape({B, nheads, head_k_dim}), o.k, o.v, o.erase, o.write}, o.window};
+}
+
 }  // namespace deltanet

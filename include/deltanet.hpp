@@ -173,6 +173,84 @@ DeltaChunkGrads combined_backward(const Tensor& d_y_bshv,
                                   int64_t chunk_len, double scale, hipStream_t stream = nullptr,
                                   bool check_finite = false);
 
+// ---------------------------------------------------------------------------
+// The projection front-end (src/common/qkv.rs, conv.rs, norm.rs) over
+// dn_frontend: everything QkvProjection does after its in_proj GEMM, which
+// stays with the caller (the reference's Burn Linear). n_value_heads =
+// nheads; QkNorm::Sum is refused (both depend on burn_stack code the
+// reference does not vendor).
+// ---------------------------------------------------------------------------
+
+enum class QkActivation : int32_t {  // norm.rs:22-34
+  Identity = DN_ACT_IDENTITY,
+  Silu = DN_ACT_SILU,
+  Relu = DN_ACT_RELU,
+  EluPlusOne = DN_ACT_ELU_PLUS_ONE
+};
+enum class ConvActivation : int32_t { Silu = DN_ACT_SILU, Identity = DN_ACT_IDENTITY };  // conv.rs:29-35
+enum class QkNorm : int32_t { L2 = DN_QKNORM_L2, Sum = DN_QKNORM_SUM, None = DN_QKNORM_NONE };
+enum class WriteGate : int32_t {  // qkv.rs:45-54
+  Fixed = DN_WRITE_FIXED,
+  Scalar = DN_WRITE_SCALAR,
+  Channel = DN_WRITE_CHANNEL
+};
+
+// conv.rs:49-83: the depthwise weight [conv_dim, conv_kernel] (Conv1d's
+// [conv_dim, 1, kernel] without its unit axis), float32.
+struct ShortConv {
+  Tensor weight;
+  std::optional<Tensor> bias;  // [conv_dim], float32
+  ConvActivation activation = ConvActivation::Silu;
+
+  int64_t conv_dim() const { return weight.dim(0); }
+  int64_t conv_kernel() const { return weight.dim(weight.rank() - 1); }
+  // A zero rolling window [batch, conv_dim, conv_kernel] ("no previous tokens").
+  Tensor zero_window(int64_t batch, DType dtype, hipStream_t stream = nullptr) const;
+};
+
+// qkv.rs:76-97. The output gate and the extra channels are column ranges of
+// the projection (qkv.rs:267-300), left to the caller.
+struct Qkv {
+  Tensor q_bshk, k_bShk, v_bShv, erase_bShK, write_bShV;
+};
+// qkv.rs:99-116.
+struct QkvStep {
+  Tensor q_bhk, k_buhk, v_buhv, erase_buhK, write_buhV;
+};
+
+// qkv.rs:118-155.
+struct QkvProjection {
+  int64_t nheads = 1, head_k_dim = 1, head_v_dim = 1, n_householder = 1;
+  std::optional<ShortConv> conv;
+  QkActivation qk_activation = QkActivation::Silu;
+  QkNorm qk_norm = QkNorm::L2;
+  WriteGate write_gate = WriteGate::Scalar;
+  bool has_gate = false;
+  bool allow_neg_eigval = false;
+  int64_t extra_channels = 0;
+
+  int64_t key_dim() const { return nheads * head_k_dim; }
+  int64_t value_dim() const { return nheads * head_v_dim; }
+  int64_t conv_dim() const;          // qkv.rs:180-182
+  int64_t write_gate_width() const;  // qkv.rs:189-197
+  int64_t d_in_proj() const;         // qkv.rs:199-205
+  int64_t conv_kernel() const { return conv ? conv->conv_kernel() : 0; }
+  std::optional<Tensor> zero_conv_window(int64_t batch, DType dtype,
+                                         hipStream_t stream = nullptr) const;
+
+  // QkvProjection::forward after in_proj (qkv.rs:373-449): projected
+  // [batch, sequence, d_in_proj] → the delta rule's inputs and the next
+  // window. q, k, v take `out_dtype` (default: the projection's dtype).
+  std::pair<Qkv, std::optional<Tensor>> forward_projected(
+      const Tensor& projected_bsw, const std::optional<Tensor>& conv_window_bwc,
+      hipStream_t stream = nullptr, std::optional<DType> out_dtype = std::nullopt) const;
+  // QkvProjection::step after in_proj (qkv.rs:454-516): projected
+  // [batch, d_in_proj].
+  std::pair<QkvStep, std::optional<Tensor>> step_projected(
+      const Tensor& projected_bw, const std::optional<Tensor>& conv_window_bwc,
+      hipStream_t stream = nullptr, std::optional<DType> out_dtype = std::nullopt) const;
+};
+
 }  // namespace deltanet
 
 #endif  // DELTANET_HPP

@@ -178,6 +178,65 @@ int dn_step(const dn_step_args *args, hipStream_t stream);
 #define DN_RECURRENT_MAX_K 256
 int dn_recurrent(const dn_recurrent_args *args, hipStream_t stream);
 
+/* The projection front-end: everything QkvProjection::forward does after its
+ * in_proj GEMM (src/common/qkv.rs:373-449), and QkvProjection::step's
+ * single-token form (:454-516) as sequence = 1. From the projection output
+ * [q | k (u copies) | v (u copies) | beta or (erase | write)] (qkv.rs:237-262)
+ * it produces the delta rule's inputs in one pass: the causal depthwise short
+ * convolution with its rolling window and fused activation (ShortConv,
+ * src/common/conv.rs:85-158), the q/k activation, the q/k L2 norm
+ * (norm.rs:36-97), v's SiLU, the head split with the n_householder micro-steps
+ * folded into the sequence, and the squashed write gates (squash_write,
+ * qkv.rs:332-369). The reference runs these as separate passes over the
+ * projection. n_value_heads = nheads only (grouped values replicate heads in
+ * burn_stack code the reference does not vendor), and QkNorm::Sum is not
+ * offered (its epsilon lives there too): both return DN_ERR_UNSUPPORTED. */
+typedef enum {
+  DN_ACT_IDENTITY = 0,
+  DN_ACT_SILU = 1,
+  DN_ACT_RELU = 2,          /* q/k activation only */
+  DN_ACT_ELU_PLUS_ONE = 3   /* q/k activation only */
+} dn_activation;
+
+typedef enum { DN_QKNORM_NONE = 0, DN_QKNORM_L2 = 1, DN_QKNORM_SUM = 2 } dn_qk_norm;
+
+typedef enum { DN_WRITE_FIXED = 0, DN_WRITE_SCALAR = 1, DN_WRITE_CHANNEL = 2 } dn_write_gate;
+
+typedef struct {
+  int64_t batch, sequence;      /* tokens per call; 1 for QkvProjection::step */
+  int64_t nheads, head_k_dim, head_v_dim;  /* head dims up to DN_FRONTEND_MAX_HEAD_DIM */
+  int64_t n_householder;        /* u >= 1 micro-steps per token (DeltaProduct) */
+  int64_t conv_kernel;          /* 0: no short convolution; else 1..DN_FRONTEND_MAX_KERNEL */
+  int64_t proj_stride;          /* elements from one token's projection row to the next */
+  int32_t conv_activation;      /* DN_ACT_SILU or DN_ACT_IDENTITY */
+  int32_t qk_activation;        /* dn_activation */
+  int32_t qk_norm;              /* DN_QKNORM_L2 or DN_QKNORM_NONE */
+  int32_t write_gate;           /* dn_write_gate */
+  int32_t allow_neg_eigval;     /* doubles the erase gate (and the scalar beta) */
+  int32_t in_dtype;             /* projected and the windows: DN_F32 or DN_BF16 */
+  int32_t out_dtype;            /* q, k, v: DN_F32 or DN_BF16 */
+  const void *projected;        /* [batch, sequence, proj_stride] */
+  const float *conv_weight;     /* [conv_dim, conv_kernel] (Conv1d's [conv_dim, 1, kernel]) */
+  const float *conv_bias;       /* [conv_dim] or NULL */
+  const void *window_in;        /* [batch, conv_dim, conv_kernel], newest column last */
+  void *window_out;             /* same shape; may alias window_in */
+  void *q;                      /* [batch, sequence, nheads, head_k_dim] */
+  void *k;                      /* [batch, sequence * u, nheads, head_k_dim] */
+  void *v;                      /* [batch, sequence * u, nheads, head_v_dim] */
+  float *erase;                 /* [batch, sequence * u, nheads, 1 | head_k_dim] */
+  float *write;                 /* [batch, sequence * u, nheads, 1 | head_v_dim]; may equal erase
+                                   for DN_WRITE_FIXED / DN_WRITE_SCALAR, where they are one tensor */
+} dn_frontend_args;
+
+#define DN_FRONTEND_MAX_HEAD_DIM 256
+#define DN_FRONTEND_MAX_KERNEL 8
+
+/* Replaces QkvProjection::forward / ::step after in_proj
+ * (src/common/qkv.rs:373-449, 454-516). conv_dim = nheads*head_k_dim +
+ * u*nheads*(head_k_dim + head_v_dim) (qkv.rs:180-182); the write-gate columns
+ * follow at conv_dim (qkv.rs:267-300). */
+int dn_frontend(const dn_frontend_args *args, hipStream_t stream);
+
 /* Bytes of device workspace dn_chunk_fwd / dn_chunk_bwd need for these
  * arguments (0 on invalid arguments). Has no counterpart in the reference,
  * whose tensors are allocated by Burn; it lets a caller own the memory. */

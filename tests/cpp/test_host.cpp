@@ -294,6 +294,37 @@ void host_cases() {
       fail("beta_gates");
     ok("beta_gates");
   }
+  // The projection front-end's own checks (qkv.rs:397-401), before any device work.
+  {
+    QkvProjection pr;
+    pr.nheads = 2;
+    pr.head_k_dim = 4;
+    pr.head_v_dim = 6;
+    if (pr.conv_dim() != 2 * 4 + 2 * (4 + 6) || pr.write_gate_width() != 2 ||
+        pr.d_in_proj() != 30)
+      fail("qkv_projection widths");
+    pr.write_gate = WriteGate::Channel;
+    pr.n_householder = 2;
+    pr.has_gate = true;
+    pr.extra_channels = 3;
+    if (pr.write_gate_width() != 2 * (8 + 12) || pr.d_in_proj() != 8 + 2 * 20 + 40 + 12 + 3)
+      fail("qkv_projection widths (channel, u = 2)");
+    ok("qkv_projection_widths");
+    QkvProjection plain;
+    plain.nheads = 2;
+    plain.head_k_dim = 4;
+    plain.head_v_dim = 6;
+    expect_error("frontend_window_presence", DN_ERR_SHAPE,
+                 "convolution window presence must match the block's convolution", [&] {
+                   plain.forward_projected(Tensor::view(fake, {1, 3, 30}, DType::F32),
+                                           Tensor::view(fake, {1, 28, 4}, DType::F32));
+                 });
+    expect_error("frontend_projection_width", DN_ERR_SHAPE,
+                 "projection: last axis must be d_in_proj = 30, got 31", [&] {
+                   plain.forward_projected(Tensor::view(fake, {1, 3, 31}, DType::F32),
+                                           std::nullopt);
+                 });
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -430,6 +461,92 @@ void gpu_cases() {
     expect_close("bf16_y", download(y), y0, 2e-2);
     expect_close("bf16_state", download(s), s0, 2e-2);
     ok("bf16_mfma_path");
+  }
+  // The projection front-end. With the newest conv tap 1 and the others 0,
+  // identity activations and no norm, q and k are the raw columns, v their
+  // SiLU (qkv.rs:413-421), erase 2σ and write σ of theirs (qkv.rs:356-366),
+  // and the next window the last 4 raw inputs (conv.rs:108-111).
+  {
+    const int64_t B = 2, S = 5, H = 2, dk = 16, dv = 32, u = 2, KC = 4;
+    QkvProjection pr;
+    pr.nheads = H;
+    pr.head_k_dim = dk;
+    pr.head_v_dim = dv;
+    pr.n_householder = u;
+    pr.qk_activation = QkActivation::Identity;
+    pr.qk_norm = QkNorm::None;
+    pr.write_gate = WriteGate::Channel;
+    pr.allow_neg_eigval = true;
+    const int64_t cd = pr.conv_dim(), W = pr.d_in_proj(), key = H * dk, val = H * dv;
+    Vec wt(size_t(cd * KC), 0.0);
+    for (int64_t c = 0; c < cd; ++c) wt[size_t(c * KC + KC - 1)] = 1.0;
+    pr.conv = ShortConv{upload(wt, {cd, KC}, DType::F32), std::nullopt, ConvActivation::Identity};
+    Rng r(5);
+    Vec raw = r.normals(size_t(B * S * W)), win = r.normals(size_t(B * cd * KC));
+    Tensor tp = upload(raw, {B, S, W}, DType::F32), tw = upload(win, {B, cd, KC}, DType::F32);
+    auto [o, next] = pr.forward_projected(tp, tw);
+    const Vec q = download(o.q_bshk), k = download(o.k_bShk), v = download(o.v_bShv);
+    const Vec e = download(o.erase_bShK), w = download(o.write_bShV), nw = download(*next);
+    auto sig = [](double x) { return 1.0 / (1.0 + std::exp(-x)); };
+    double err = 0.0;
+    for (int64_t b = 0; b < B; ++b)
+      for (int64_t t = 0; t < S; ++t) {
+        const double* row = &raw[size_t((b * S + t) * W)];
+        for (int64_t c = 0; c < key; ++c)
+          err = std::max(err, std::fabs(q[size_t((b * S + t) * key + c)] - row[c]));
+        for (int64_t c = 0; c < u * key; ++c)  // [t, m, h, :] = channel key + m·key + h·dk + :
+          err = std::max(err, std::fabs(k[size_t((b * S + t) * u * key + c)] - row[key + c]));
+        for (int64_t c = 0; c < u * val; ++c) {
+          const double x = row[key * (1 + u) + c];
+          err = std::max(err, std::fabs(v[size_t((b * S + t) * u * val + c)] - x * sig(x)));
+        }
+        for (int64_t c = 0; c < u * key; ++c)
+          err = std::max(err, std::fabs(e[size_t((b * S + t) * u * key + c)] -
+                                        2.0 * sig(row[cd + c])));
+        for (int64_t c = 0; c < u * val; ++c)
+          err = std::max(err, std::fabs(w[size_t((b * S + t) * u * val + c)] -
+                                        sig(row[cd + u * key + c])));
+      }
+    for (int64_t b = 0; b < B; ++b)
+      for (int64_t c = 0; c < cd; ++c)
+        for (int64_t j = 0; j < KC; ++j)
+          err = std::max(err, std::fabs(nw[size_t((b * cd + c) * KC + j)] -
+                                        raw[size_t((b * S + S - KC + j) * W + c)]));
+    if (err > 1e-5) fail("frontend closed form: max error " + std::to_string(err));
+    ok("frontend_closed_form");
+    // L2 norm on (qkv.rs:425-426): unit rows of q and k; and a step chain,
+    // carrying the window, equals the forward.
+    pr.qk_norm = QkNorm::L2;
+    Vec wt2 = r.normals(size_t(cd * KC), 0.5);
+    pr.conv->weight = upload(wt2, {cd, KC}, DType::F32);
+    pr.conv->activation = ConvActivation::Silu;
+    pr.qk_activation = QkActivation::Silu;
+    auto [f, fnext] = pr.forward_projected(tp, tw);
+    const Vec fq = download(f.q_bshk), fk = download(f.k_bShk);
+    for (size_t row = 0; row < fq.size() / size_t(dk); ++row) {
+      double n2 = 0.0;
+      for (int64_t c = 0; c < dk; ++c) n2 += fq[row * size_t(dk) + size_t(c)] * fq[row * size_t(dk) + size_t(c)];
+      if (std::fabs(std::sqrt(n2) - 1.0) > 1e-4) fail("frontend: q row not unit norm");
+    }
+    std::optional<Tensor> wcur = tw;
+    for (int64_t t = 0; t < S; ++t) {
+      Vec rowv(size_t(B * W));
+      for (int64_t b = 0; b < B; ++b)
+        for (int64_t c = 0; c < W; ++c) rowv[size_t(b * W + c)] = raw[size_t((b * S + t) * W + c)];
+      auto [st, wn] = pr.step_projected(upload(rowv, {B, W}, DType::F32), wcur);
+      wcur = wn;
+      const Vec sq = download(st.q_bhk), sk = download(st.k_buhk);
+      for (int64_t b = 0; b < B; ++b) {
+        for (int64_t c = 0; c < key; ++c)
+          if (std::fabs(sq[size_t(b * key + c)] - fq[size_t((b * S + t) * key + c)]) > 1e-6)
+            fail("frontend: step q differs from forward");
+        for (int64_t c = 0; c < u * key; ++c)
+          if (std::fabs(sk[size_t(b * u * key + c)] - fk[size_t((b * S + t) * u * key + c)]) > 1e-6)
+            fail("frontend: step k differs from forward");
+      }
+    }
+    if (rel_err(download(*wcur), download(*fnext)) != 0.0) fail("frontend: step window");
+    ok("frontend_step_chain");
   }
 }
 

@@ -154,3 +154,42 @@ def test_delta_path_mirrors_the_reference():
     assert P.default().resolved_chunk_len() == 64
     assert P.recurrent().resolved_chunk_len() == 1
     assert P.with_chunk_len(16).resolved_chunk_len() == 16
+
+
+def frontend_args(**over):
+    a = abi.FrontendArgs()
+    a.batch, a.sequence, a.nheads, a.head_k_dim, a.head_v_dim = 1, 8, 2, 4, 6
+    a.n_householder, a.conv_kernel = 1, 4
+    a.proj_stride = 2 * 4 + 2 * (4 + 6) + 2  # conv_dim + scalar β columns
+    a.conv_activation, a.qk_activation = abi.DN_ACT_SILU, abi.DN_ACT_SILU
+    a.qk_norm, a.write_gate = abi.DN_QKNORM_L2, abi.DN_WRITE_SCALAR
+    a.in_dtype = a.out_dtype = abi.DN_F32
+    for f in ["projected", "conv_weight", "window_in", "window_out", "q", "k", "v", "erase",
+              "write"]:
+        setattr(a, f, 0x1000)  # never dereferenced: every case fails its checks first
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(sequence=0), -1, "sequence length must be at least 1"),
+    (dict(n_householder=0), -2, "at least 1"),
+    (dict(window_in=None), -2, "convolution window presence must match"),
+    (dict(conv_kernel=0), -2, "convolution window presence must match"),
+    (dict(qk_norm=abi.DN_QKNORM_SUM), -9, "QkNorm::Sum"),
+    (dict(head_k_dim=257, proj_stride=10 ** 5), -9, "head dims up to 256"),
+    (dict(conv_kernel=9), -9, "conv_kernel up to 8"),
+    (dict(proj_stride=29), -2, "narrower than the conv and write-gate columns (30)"),
+    (dict(conv_activation=abi.DN_ACT_RELU), -2, "conv_activation"),
+    (dict(out_dtype=5), -7, "dtype"),
+    (dict(q=None), -6, "NULL"),
+    (dict(write_gate=abi.DN_WRITE_CHANNEL, proj_stride=100), -2, "separate buffers"),
+])
+def test_frontend_rejects_invalid_arguments(over, code, msg):
+    """dn_frontend mirrors ShortConv's and QkvProjection's asserts
+    (conv.rs:88-90, qkv.rs:397-401) and refuses what it does not offer."""
+    lib = abi.lib()
+    a = frontend_args(**over)
+    assert lib.dn_frontend(ctypes.byref(a), None) == code
+    assert msg in lib.dn_last_error().decode()

@@ -1,0 +1,179 @@
+"""GPU parity of dn_frontend (the projection front-end, qkv.rs:373-516) with
+the CPU oracle (oracle/frontend.py), through the C ABI and its Python mirror
+QkvProjection.
+
+Bars: normwise relative error 1e-5 for fp32 in and out (the arithmetic is a
+handful of fp32 operations per element); 1e-2 where q, k, v are written in
+bf16 (one rounding: 2⁻⁹ relative) — below the 2e-2 of BASELINE.json's
+north_star for bf16 inputs. Gates are fp32 at 1e-5 in every case. The next
+conv window is compared exactly (it is a copy of inputs)."""
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_err
+from gpu_util import DEV, announce, np_of, pkg
+from oracle import frontend as F
+
+pytestmark = pytest.mark.gpu
+
+abi = pkg.abi
+
+CASES = [
+    # B, S, H, dk, dv, u, K, conv_act, qk_act, qk_norm, gate, neg, bias, in, out, extra
+    (2, 37, 4, 128, 256, 1, 4, F.ACT_SILU, F.ACT_SILU, F.QKNORM_L2, F.WRITE_SCALAR, False,
+     False, torch.bfloat16, torch.bfloat16, 0),
+    (2, 40, 2, 64, 64, 1, 4, F.ACT_SILU, F.ACT_SILU, F.QKNORM_L2, F.WRITE_SCALAR, False,
+     True, torch.float32, torch.float32, 0),
+    (1, 33, 2, 128, 128, 2, 4, F.ACT_SILU, F.ACT_SILU, F.QKNORM_L2, F.WRITE_CHANNEL, True,
+     False, torch.float32, torch.float32, 5),
+    (2, 19, 3, 32, 48, 1, 3, F.ACT_IDENTITY, F.ACT_RELU, F.QKNORM_L2, F.WRITE_FIXED, True,
+     True, torch.float32, torch.float32, 0),
+    (1, 21, 2, 16, 16, 1, 0, F.ACT_SILU, F.ACT_ELU_PLUS_ONE, F.QKNORM_NONE, F.WRITE_SCALAR,
+     True, False, torch.float32, torch.float32, 3),
+    (2, 18, 2, 100, 36, 1, 4, F.ACT_SILU, F.ACT_SILU, F.QKNORM_L2, F.WRITE_CHANNEL, False,
+     True, torch.float32, torch.float32, 0),
+    (1, 25, 2, 64, 64, 1, 6, F.ACT_SILU, F.ACT_SILU, F.QKNORM_L2, F.WRITE_SCALAR, False,
+     True, torch.float32, torch.float32, 0),
+    (1, 9, 2, 64, 64, 1, 1, F.ACT_SILU, F.ACT_IDENTITY, F.QKNORM_L2, F.WRITE_SCALAR, False,
+     False, torch.float32, torch.float32, 0),
+    (2, 5, 1, 4, 6, 3, 4, F.ACT_SILU, F.ACT_SILU, F.QKNORM_L2, F.WRITE_CHANNEL, True,
+     True, torch.float32, torch.float32, 0),
+    (2, 30, 2, 256, 128, 1, 4, F.ACT_SILU, F.ACT_SILU, F.QKNORM_L2, F.WRITE_SCALAR, False,
+     False, torch.bfloat16, torch.float32, 0),
+    (2, 2, 2, 64, 64, 1, 4, F.ACT_SILU, F.ACT_SILU, F.QKNORM_L2, F.WRITE_SCALAR, False,
+     False, torch.float32, torch.float32, 0),
+]
+
+
+def make_case(rng, case):
+    (B, S, H, dk, dv, u, K, cact, qact, qn, gate, neg, bias, din, dout, extra) = case
+    cd = F.conv_dim(H, dk, dv, u)
+    width = cd + F.gate_width(H, dk, dv, u, gate) + extra
+    # The oracle sees the values the GPU sees: inputs rounded to their dtype.
+    rd = lambda a, d: torch.tensor(a, dtype=torch.float32).to(d).double().numpy()
+    p = rd(rng.standard_normal((B, S, width)), din)
+    conv = None
+    if K:
+        w = rd(rng.standard_normal((cd, K)) * 0.5, torch.float32)
+        window = rd(rng.standard_normal((B, cd, K)), din)
+        conv = dict(weight=w, bias=rd(rng.standard_normal(cd) * 0.1, torch.float32)
+                    if bias else None, window=window, activation=cact)
+    return p, conv
+
+
+def oracle_of(p, conv, case):
+    (B, S, H, dk, dv, u, K, cact, qact, qn, gate, neg, *_rest) = case
+    return F.frontend(p, nheads=H, head_k_dim=dk, head_v_dim=dv, n_householder=u, conv=conv,
+                      qk_activation=qact, qk_norm_kind=qn, write_gate=gate,
+                      allow_neg_eigval=neg)
+
+
+def run_abi(p, conv, case, alias_window=False):
+    (B, S, H, dk, dv, u, K, cact, qact, qn, gate, neg, bias, din, dout, extra) = case
+    t = lambda a, d=torch.float32: torch.tensor(a, dtype=torch.float32, device=DEV).to(d)
+    gp = t(p, din)
+    q = torch.empty((B, S, H, dk), dtype=dout, device=DEV)
+    k = torch.empty((B, S * u, H, dk), dtype=dout, device=DEV)
+    v = torch.empty((B, S * u, H, dv), dtype=dout, device=DEV)
+    if gate == F.WRITE_CHANNEL:
+        e = torch.empty((B, S * u, H, dk), device=DEV)
+        w = torch.empty((B, S * u, H, dv), device=DEV)
+    else:
+        e = torch.empty((B, S * u, H, 1), device=DEV)
+        w = torch.empty_like(e)
+    weight = bias_t = win_in = win_out = None
+    if conv is not None:
+        weight = t(conv["weight"])
+        bias_t = None if conv["bias"] is None else t(conv["bias"])
+        win_in = t(conv["window"], din)
+        win_out = win_in if alias_window else torch.empty_like(win_in)
+    abi.run_frontend(abi.frontend_args(
+        gp, weight, bias_t, win_in, win_out, q, k, v, e, w, nheads=H, head_k_dim=dk,
+        head_v_dim=dv, n_householder=u, conv_activation=cact if K else F.ACT_IDENTITY,
+        qk_activation=qact, qk_norm=qn, write_gate=gate, allow_neg_eigval=neg))
+    torch.cuda.synchronize()
+    return dict(q=q, k=k, v=v, erase=e, write=w, window=win_out)
+
+
+def check(got, want, dout):
+    tol = 1e-5 if dout == torch.float32 else 1e-2
+    for name in ["q", "k", "v"]:
+        err = rel_err(np_of(got[name]), want[name])
+        assert err < tol, f"{name}: rel err {err:.2e}"
+    for name in ["erase", "write"]:
+        err = rel_err(np_of(got[name]), want[name])
+        assert err < 1e-5, f"{name}: rel err {err:.2e}"
+    if want["window"] is not None:
+        assert np.array_equal(np_of(got["window"]).astype(np.float64), want["window"])
+
+
+@pytest.mark.parametrize("case", CASES)
+def test_frontend_matches_oracle(rng, case):
+    announce(f"dn_frontend {case[:12]}")
+    p, conv = make_case(rng, case)
+    check(run_abi(p, conv, case), oracle_of(p, conv, case), case[14])
+
+
+def test_frontend_window_in_place(rng):
+    """window_out aliasing window_in (the decode cache updated in place)."""
+    case = CASES[1]
+    announce("dn_frontend in-place window")
+    p, conv = make_case(rng, case)
+    want = oracle_of(p, conv, case)
+    check(run_abi(p, conv, case, alias_window=True), want, case[14])
+
+
+def test_step_chain_equals_forward(rng):
+    """QkvProjection.step token by token, carrying the window, equals one
+    forward over the sequence (the reference's forward/step parity)."""
+    announce("QkvProjection step chain")
+    B, S, H, dk, dv = 2, 6, 2, 64, 128
+    proj = pkg.QkvProjection(nheads=H, head_k_dim=dk, head_v_dim=dv, has_gate=True,
+                             extra_channels=4)
+    cd = proj.conv_dim()
+    proj.conv = pkg.ShortConv(torch.tensor(rng.standard_normal((cd, 4)) * 0.5,
+                                           dtype=torch.float32, device=DEV))
+    p = torch.tensor(rng.standard_normal((B, S, proj.d_in_proj())), dtype=torch.float32,
+                     device=DEV)
+    win0 = torch.tensor(rng.standard_normal((B, cd, 4)), dtype=torch.float32, device=DEV)
+    full, wfull = proj.forward_projected(p, win0)
+    win = win0
+    for t in range(S):
+        st, win = proj.step_projected(p[:, t].contiguous(), win)
+        assert rel_err(np_of(st.q_bhk), np_of(full.q_bshk[:, t])) < 1e-6
+        assert rel_err(np_of(st.k_buhk[:, 0]), np_of(full.k_bShk[:, t])) < 1e-6
+        assert rel_err(np_of(st.v_buhv[:, 0]), np_of(full.v_bShv[:, t])) < 1e-6
+        assert torch.equal(st.erase_buhK[:, 0], full.erase_bShK[:, t])
+        assert torch.equal(st.gate_bhv, full.gate_bshv[:, t])
+    torch.cuda.synchronize()
+    assert torch.equal(win, wfull)
+    # The mirror's gate and extra views are the projection's own columns.
+    c = cd + proj.write_gate_width()
+    assert torch.equal(full.gate_bshv.reshape(B, S, -1), p[:, :, c:c + H * dv])
+    assert torch.equal(full.extra_bsx, p[:, :, c + H * dv:])
+
+
+def test_projection_forward_runs_in_proj(rng):
+    """QkvProjection.forward = in_proj (a library GEMM) + dn_frontend."""
+    announce("QkvProjection forward with in_proj")
+    B, S, D, H, dk, dv = 2, 8, 48, 2, 32, 32
+    proj = pkg.QkvProjection(nheads=H, head_k_dim=dk, head_v_dim=dv)
+    cd = proj.conv_dim()
+    wproj = rng.standard_normal((D, proj.d_in_proj())) * 0.2
+    wconv = rng.standard_normal((cd, 4)) * 0.5
+    proj.in_proj = torch.tensor(wproj, dtype=torch.float32, device=DEV)
+    proj.conv = pkg.ShortConv(torch.tensor(wconv, dtype=torch.float32, device=DEV))
+    x = rng.standard_normal((B, S, D))
+    qkv, win = proj.forward(torch.tensor(x, dtype=torch.float32, device=DEV),
+                            proj.zero_conv_window(B, DEV))
+    want = F.frontend(x @ wproj, nheads=H, head_k_dim=dk, head_v_dim=dv,
+                      conv=dict(weight=wconv, bias=None, window=np.zeros((B, cd, 4)),
+                                activation=F.ACT_SILU))
+    # The GEMM runs in fp32 on the GPU (rocBLAS/hipBLASLt order): 1e-4.
+    assert rel_err(np_of(qkv.q_bshk), want["q"]) < 1e-4
+    assert rel_err(np_of(qkv.k_bShk), want["k"]) < 1e-4
+    assert rel_err(np_of(qkv.v_bShv), want["v"]) < 1e-4
+    assert rel_err(np_of(qkv.erase_bShK), want["erase"]) < 1e-4
+    assert qkv.write_bShV.data_ptr() == qkv.erase_bShK.data_ptr()
