@@ -18,8 +18,9 @@ dk128) at 1 GPU; % roofline"):
 * config4 / config5 = BASELINE configs 4 (DeltaProduct u=2, folded core
   forward) and 5 (GDN-2 per-channel gates, forward + custom backward), each
   with its own HBM roofline; not part of `value`.
-* frontend = dn_frontend (the projection front-end) at the config-2 shape,
-  with its HBM roofline; not part of `value`.
+* frontend / out_norm = dn_frontend (the projection front-end) and
+  dn_out_norm (the gated output norm) at the config-2 shape, each with its
+  HBM roofline; not part of `value`.
 * cpu_baseline = the CPU oracle (a C++ restatement of the reference algorithm,
   incl. its 24·L³ ladder) on a bounded sample of config 2, all host threads.
 
@@ -241,6 +242,30 @@ def bench_frontend(torch, pkg, steps, warmup):
             "kernels": kern}
 
 
+def bench_out_norm(torch, pkg, steps, warmup):
+    """The gated output norm (dn_out_norm: OutNorm::forward, norm.rs:106-144)
+    on config 2's delta-rule output: y [8, 4096, 16, 256] bf16, the gate of
+    the same shape in bf16, bf16 out; ε = 1e-5."""
+    B, S, H, V = 8, 4096, 16, 256
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20260833)
+    x = torch.randn((B, S, H, V), generator=gen, device=dev).to(torch.bfloat16)
+    g = torch.randn((B, S, H, V), generator=gen, device=dev).to(torch.bfloat16)
+    w = torch.randn(V, generator=gen, device=dev)
+    out = torch.empty_like(x)
+    abi = pkg.abi
+    args = abi.out_norm_args(x, g, w, out, 1e-5)
+    ms, kern = _timed(torch, abi, lambda: abi.run_out_norm(args), steps, warmup)
+    nbytes = 3 * B * S * H * V * 2 + V * 4
+    k_ms = kern["dn_out_norm"]["avg_us"] / 1e3 if "dn_out_norm" in kern else ms
+    return {"workload": "dn_out_norm (gated RMSNorm per head) on config 2's output, bf16",
+            "ms_per_call": round(ms, 4), "tokens_per_s": round(B * S / (ms / 1e3), 1),
+            "roofline": _hbm(nbytes, k_ms) | {"kernel": "dn_out_norm",
+                                               "traffic": traffic_from_profiles("dn_out_norm")},
+            "kernels": kern}
+
+
 def _timed(torch, abi, fn, steps, warmup):
     """Mean ms per call of fn() over `steps` calls after `warmup`, with the
     library's per-kernel HIP-event profile of the timed calls."""
@@ -424,8 +449,8 @@ def main():
                     help="timed calls for configs 4 and 5 (after one warmup)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="short run for rocprofv3 --pmc: a 1 GiB copy (calibration), then 2 "
-                         "forward, 2 decode, 2 DeltaProduct-decode and 2 front-end calls and "
-                         "one config-5 forward + backward; prints no JSON")
+                         "forward, 2 decode, 2 DeltaProduct-decode, 2 front-end and 2 "
+                         "output-norm calls and one config-5 forward + backward; prints no JSON")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -447,6 +472,7 @@ def main():
         bench_decode(torch, pkg, 2, 0)
         bench_product_decode(torch, pkg, 2, 0)
         bench_frontend(torch, pkg, 2, 0)
+        bench_out_norm(torch, pkg, 2, 0)
         bench_config5(torch, pkg, 1, 0)
         torch.cuda.synchronize()
         print("[bench] profile pass done", file=sys.stderr, flush=True)
@@ -504,6 +530,10 @@ def main():
         print("[bench] projection front-end (dn_frontend)", file=sys.stderr, flush=True)
         extra["frontend"] = bench_frontend(torch, pkg, max(args.extra_steps, 10), 2)
         print(f"[bench] frontend {extra['frontend']}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+        print("[bench] output norm (dn_out_norm)", file=sys.stderr, flush=True)
+        extra["out_norm"] = bench_out_norm(torch, pkg, max(args.extra_steps, 10), 2)
+        print(f"[bench] out_norm {extra['out_norm']}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
 
     cpu = None

@@ -4,19 +4,20 @@ The product is libdeltanet_core.so (HIP kernels for gfx950 behind the C ABI
 in include/deltanet_core.h). This package is its Python host side: `abi`
 binds the C ABI, `delta` mirrors the reference's interface (DeltaInput,
 DeltaPath, delta_step, DeltaChunkBackendExt::delta_chunk_recalculated,
-combined_backward), `frontend` its projection front-end (QkvProjection).
+combined_backward), `frontend` its projection front-end (QkvProjection) and
+output norm (OutNorm).
 """
 
 from . import abi
 from .abi import DeltaError
 from .delta import (DeltaChunkFunction, DeltaChunkGrads, DeltaInput, DeltaPath, TriSolve,
                     beta_gates, combined_backward, delta_chunk_recalculated, delta_step)
-from .frontend import (ConvActivation, QkActivation, QkNorm, Qkv, QkvProjection, QkvStep,
-                       ShortConv, WriteGate)
+from .frontend import (ConvActivation, OutNorm, QkActivation, QkNorm, Qkv, QkvProjection,
+                       QkvStep, ShortConv, WriteGate)
 
 __all__ = [
     "abi", "DeltaError", "DeltaChunkFunction", "DeltaChunkGrads", "DeltaInput", "DeltaPath",
     "TriSolve", "beta_gates", "combined_backward", "delta_chunk_recalculated", "delta_step",
-    "ConvActivation", "QkActivation", "QkNorm", "Qkv", "QkvProjection", "QkvStep", "ShortConv",
-    "WriteGate",
+    "ConvActivation", "OutNorm", "QkActivation", "QkNorm", "Qkv", "QkvProjection", "QkvStep",
+    "ShortConv", "WriteGate",
 ]

@@ -24,6 +24,7 @@ DN_ACT_IDENTITY, DN_ACT_SILU, DN_ACT_RELU, DN_ACT_ELU_PLUS_ONE = 0, 1, 2, 3
 DN_QKNORM_NONE, DN_QKNORM_L2, DN_QKNORM_SUM = 0, 1, 2
 DN_WRITE_FIXED, DN_WRITE_SCALAR, DN_WRITE_CHANNEL = 0, 1, 2
 FRONTEND_MAX_HEAD_DIM, FRONTEND_MAX_KERNEL = 256, 8
+OUT_NORM_MAX_HEAD_DIM = 1024
 
 STATUS = {
     0: "DN_OK",
@@ -40,7 +41,7 @@ STATUS = {
 }
 
 EXPORTS = [
-    "dn_chunk_fwd", "dn_chunk_bwd", "dn_step", "dn_recurrent", "dn_frontend",
+    "dn_chunk_fwd", "dn_chunk_bwd", "dn_step", "dn_recurrent", "dn_frontend", "dn_out_norm",
     "dn_chunk_fwd_workspace_bytes",
     "dn_chunk_bwd_workspace_bytes", "dn_chunk_fwd_algo", "dn_chunk_bwd_algo",
     "dn_last_error", "dn_version", "dn_profile_enable", "dn_profile_read",
@@ -110,6 +111,14 @@ class FrontendArgs(ctypes.Structure):
     ]
 
 
+class OutNormArgs(ctypes.Structure):
+    _fields_ = [
+        ("tokens", _i64), ("nheads", _i64), ("head_v_dim", _i64), ("gate_stride", _i64),
+        ("eps", _f64), ("x_dtype", _i32), ("gate_dtype", _i32), ("out_dtype", _i32),
+        ("x", _vp), ("gate", _vp), ("weight", _vp), ("out", _vp),
+    ]
+
+
 _LIB = None
 
 
@@ -132,6 +141,8 @@ def lib() -> ctypes.CDLL:
         L.dn_recurrent.restype = ctypes.c_int
         L.dn_frontend.argtypes = [ctypes.POINTER(FrontendArgs), _vp]
         L.dn_frontend.restype = ctypes.c_int
+        L.dn_out_norm.argtypes = [ctypes.POINTER(OutNormArgs), _vp]
+        L.dn_out_norm.restype = ctypes.c_int
         L.dn_chunk_fwd_workspace_bytes.argtypes = [ctypes.POINTER(ChunkFwdArgs)]
         L.dn_chunk_fwd_workspace_bytes.restype = _sz
         L.dn_chunk_bwd_workspace_bytes.argtypes = [ctypes.POINTER(ChunkBwdArgs)]
@@ -288,6 +299,38 @@ def frontend_args(projected, conv_weight, conv_bias, window_in, window_out, q, k
 
 def run_frontend(args: FrontendArgs) -> None:
     check(lib().dn_frontend(ctypes.byref(args), stream_handle()))
+
+
+def out_norm_args(x, gate, weight, out, eps):
+    """dn_out_norm over x [.., nheads, head_v_dim] (contiguous). `gate` has
+    the same shape and may be a view whose heads are contiguous within a
+    token and whose tokens are evenly strided (a column range of the
+    projection)."""
+    H, D = x.shape[-2], x.shape[-1]
+    a = OutNormArgs()
+    a.tokens, a.nheads, a.head_v_dim = x.numel() // (H * D), H, D
+    if gate is not None:
+        if tuple(gate.shape) != tuple(x.shape):
+            raise DeltaError(-2, f"gate: expected shape {list(x.shape)}, got {list(gate.shape)}")
+        if gate.stride(-1) != 1 or gate.stride(-2) != D:
+            raise DeltaError(-2, "gate: heads must be contiguous within a token")
+        lead, strides = gate.shape[:-2], gate.stride()[:-2]
+        token_stride = strides[-1] if lead else H * D
+        want = token_stride  # the leading axes must flatten to one token stride
+        for n, st in zip(reversed(lead), reversed(strides)):
+            if n > 1 and st != want:
+                raise DeltaError(-2, "gate: tokens must be evenly strided")
+            want *= n
+        a.gate_stride = token_stride
+        a.gate_dtype = dtype_tag(gate.dtype)
+    a.eps = float(eps)
+    a.x_dtype, a.out_dtype = dtype_tag(x.dtype), dtype_tag(out.dtype)
+    a.x, a.gate, a.weight, a.out = _ptr(x), _ptr(gate), _ptr(weight), _ptr(out)
+    return a
+
+
+def run_out_norm(args: OutNormArgs) -> None:
+    check(lib().dn_out_norm(ctypes.byref(args), stream_handle()))
 
 
 def chunk_bwd_args(dy, dstate, q, k, v, erase, write, g, state, grads, chunk_len, scale,

@@ -456,6 +456,27 @@ int dn_frontend(const dn_frontend_args* a, hipStream_t stream) {
   return DN_OK;
 }
 
+int dn_out_norm(const dn_out_norm_args* a, hipStream_t stream) {
+  g_last_error.clear();
+  if (!a) return fail(DN_ERR_NULL, "args is NULL");
+  if (a->tokens < 1 || a->nheads < 1 || a->head_v_dim < 1)
+    return fail(DN_ERR_SHAPE, "tokens, nheads and head_v_dim must be at least 1");
+  if (a->head_v_dim > DN_OUT_NORM_MAX_HEAD_DIM)
+    return fail(DN_ERR_UNSUPPORTED, "dn_out_norm supports head_v_dim up to " +
+                                        std::to_string(DN_OUT_NORM_MAX_HEAD_DIM));
+  if (!valid_dtype(a->x_dtype) || !valid_dtype(a->out_dtype) ||
+      (a->gate && !valid_dtype(a->gate_dtype)))
+    return fail(DN_ERR_DTYPE, "dtype must be DN_F32 or DN_BF16");
+  if (!a->x || !a->weight || !a->out) return fail(DN_ERR_NULL, "a required tensor pointer is NULL");
+  if (a->gate && a->gate_stride < a->nheads * a->head_v_dim)
+    return fail(DN_ERR_SHAPE, "gate_stride is narrower than one token's gates");
+  if (!(a->eps >= 0.0)) return fail(DN_ERR_SHAPE, "eps must be a non-negative number");
+  if (a->tokens * a->nheads >= (int64_t(1) << 40)) return fail(DN_ERR_SHAPE, "tensor too large");
+  hipError_t e = launch_out_norm(*a, stream);
+  if (e != hipSuccess) return hip_fail(e, "dn_out_norm launch");
+  return DN_OK;
+}
+
 int dn_recurrent(const dn_recurrent_args* a, hipStream_t stream) {
   g_last_error.clear();
   if (!a) return fail(DN_ERR_NULL, "args is NULL");

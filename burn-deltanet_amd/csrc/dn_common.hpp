@@ -74,6 +74,8 @@ bool recurrent_supported(const dn_recurrent_args& a);
 hipError_t launch_recurrent(const dn_recurrent_args& a, float scale, hipStream_t stream);
 // dn_frontend: the projection front-end (frontend.hip).
 hipError_t launch_frontend(const dn_frontend_args& a, hipStream_t stream);
+// dn_out_norm: the per-head (gated) RMSNorm (out_norm.hip).
+hipError_t launch_out_norm(const dn_out_norm_args& a, hipStream_t stream);
 
 struct GenericFwdPlan {
   size_t ws_bytes;

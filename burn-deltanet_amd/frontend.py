@@ -1,5 +1,6 @@
 """Host-side mirror of the reference's projection front-end
-(src/common/qkv.rs, conv.rs, norm.rs) over dn_frontend.
+(src/common/qkv.rs, conv.rs, norm.rs) over dn_frontend, and of its output
+norm (OutNorm, norm.rs:106-144) over dn_out_norm.
 
 `QkvProjection` keeps the reference's fields and methods (`key_dim`,
 `value_dim`, `conv_dim`, `write_gate_width`, `d_in_proj`, `segments`,
@@ -250,3 +251,35 @@ class QkvProjection:
             qk_activation=self.qk_activation, qk_norm=self.qk_norm,
             write_gate=self.write_gate, allow_neg_eigval=self.allow_neg_eigval))
         return (q, k, v, erase, write), win_out
+
+
+@dataclass
+class OutNorm:
+    """OutNorm (norm.rs:106-144): RMSNorm over head_v_dim, per head, with
+    weight γ; gated, it multiplies by silu(gate) after the norm. `eps` is the
+    RmsNorm epsilon of burn_stack, which the reference does not vendor;
+    1e-5 (Burn's RmsNorm default) unless set."""
+
+    weight: Tensor
+    gated: bool = True
+    eps: float = 1e-5
+
+    @staticmethod
+    def init(head_v_dim: int, has_gate: bool, device) -> "OutNorm":
+        """norm.rs:137-143 (γ = 1)."""
+        return OutNorm(torch.ones(head_v_dim, device=device), gated=has_gate)
+
+    def forward(self, x: Tensor, gate: Optional[Tensor] = None, out_dtype=None) -> Tensor:
+        """norm.rs:127-134, over x [.., nheads, head_v_dim]."""
+        if self.gated and gate is None:
+            raise DeltaError(-6, "OutNorm::Gated needs an output gate")
+        if not self.gated and gate is not None:
+            raise DeltaError(-2, "OutNorm::Plain takes no output gate")
+        if not x.is_cuda:
+            raise DeltaError(-6, "tensors must live on the GPU (no CPU fallback)")
+        x = x.contiguous()
+        out = torch.empty(x.shape, dtype=x.dtype if out_dtype is None else out_dtype,
+                          device=x.device)
+        w = self.weight.float().contiguous()
+        abi.run_out_norm(abi.out_norm_args(x, gate, w, out, self.eps))
+        return out

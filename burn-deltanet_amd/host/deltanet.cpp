@@ -561,4 +561,34 @@ std::pair<QkvStep, std::optional<Tensor>> QkvProjection::step_projected(
   return {QkvStep{o.q.reshape({B, nheads, head_k_dim}), o.k, o.v, o.erase, o.write}, o.window};
 }
 
+Tensor OutNorm::forward(const Tensor& x, const std::optional<Tensor>& gate,
+                       int64_t gate_token_stride, hipStream_t stream,
+                       std::optional<DType> out_dtype) const {
+  // norm.rs:131-132
+  if (gated && !gate) throw Error(DN_ERR_NULL, "OutNorm::Gated needs an output gate");
+  if (!gated && gate) throw Error(DN_ERR_SHAPE, "OutNorm::Plain takes no output gate");
+  require_defined(x, "x");
+  require_f32(weight, "norm weight");
+  if (x.rank() < 2) throw Error(DN_ERR_SHAPE, "x: expected [.., nheads, head_v_dim]");
+  const int64_t H = x.dim(x.rank() - 2), D = x.dim(x.rank() - 1);
+  if (weight.numel() != size_t(D))
+    throw Error(DN_ERR_SHAPE, "norm weight: expected " + std::to_string(D) + " values");
+  Tensor out = Tensor::empty(x.dims(), out_dtype.value_or(x.dtype()));
+  dn_out_norm_args a{};
+  a.tokens = int64_t(x.numel()) / (H * D);
+  a.nheads = H;
+  a.head_v_dim = D;
+  a.gate_stride = gate ? (gate_token_stride ? gate_token_stride : H * D) : 0;
+  a.eps = eps;
+  a.x_dtype = int32_t(x.dtype());
+  a.gate_dtype = gate ? int32_t(gate->dtype()) : DN_F32;
+  a.out_dtype = int32_t(out.dtype());
+  a.x = x.data();
+  a.gate = gate ? gate->data() : nullptr;
+  a.weight = static_cast<const float*>(weight.data());
+  a.out = out.data();
+  check(dn_out_norm(&a, stream));
+  return out;
+}
+
 }  // namespace deltanet

@@ -251,6 +251,24 @@ struct QkvProjection {
       hipStream_t stream = nullptr, std::optional<DType> out_dtype = std::nullopt) const;
 };
 
+// OutNorm (src/common/norm.rs:106-144): RMSNorm over head_v_dim per head,
+// weight gamma [head_v_dim] (float32); gated, times silu(gate) after the norm.
+// eps is burn_stack's RmsNorm epsilon, which the reference does not vendor
+// (1e-5, Burn's RmsNorm default, unless set).
+struct OutNorm {
+  Tensor weight;
+  bool gated = true;
+  double eps = 1e-5;
+
+  // x [.., nheads, head_v_dim]. The gate, when gated, is nheads·head_v_dim
+  // values per token starting at gate.data(), tokens gate_token_stride
+  // elements apart (0: packed, as x) — a column range of the projection
+  // (qkv.rs:429) is passed as a view of its first element and d_in_proj.
+  Tensor forward(const Tensor& x, const std::optional<Tensor>& gate = std::nullopt,
+                 int64_t gate_token_stride = 0, hipStream_t stream = nullptr,
+                 std::optional<DType> out_dtype = std::nullopt) const;
+};
+
 }  // namespace deltanet
 
 #endif  // DELTANET_HPP

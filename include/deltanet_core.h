@@ -237,6 +237,32 @@ typedef struct {
  * follow at conv_dim (qkv.rs:267-300). */
 int dn_frontend(const dn_frontend_args *args, hipStream_t stream);
 
+/* The output norm after the delta rule: OutNorm::forward
+ * (src/common/norm.rs:106-144), per head over head_v_dim. Gated:
+ * out = x / sqrt(mean(x^2) + eps) * weight * silu(gate); plain (gate NULL):
+ * the same without the gate factor. Both RmsNorm forms live in burn_stack,
+ * which the reference does not vendor, so eps is the caller's (burn's RmsNorm
+ * default is 1e-5). The gate is read in place from the projection: row t's
+ * gate for head h starts at gate + t*gate_stride + h*head_v_dim. */
+typedef struct {
+  int64_t tokens;               /* batch * sequence (or batch for a decode step) */
+  int64_t nheads, head_v_dim;
+  int64_t gate_stride;          /* elements between consecutive tokens' gates */
+  double eps;
+  int32_t x_dtype, gate_dtype, out_dtype;   /* DN_F32 or DN_BF16 */
+  const void *x;                /* [tokens, nheads, head_v_dim] */
+  const void *gate;             /* NULL for OutNorm::Plain */
+  const float *weight;          /* gamma [head_v_dim] */
+  void *out;                    /* [tokens, nheads, head_v_dim]; may alias x */
+} dn_out_norm_args;
+
+#define DN_OUT_NORM_MAX_HEAD_DIM 1024
+
+/* Replaces OutNorm::forward (src/common/norm.rs:127-134) as called after the
+ * delta rule by every family (deltanet.rs:171, 219; gated_deltanet_1.rs:183, 234;
+ * gated_deltanet_2.rs:282, 367; delta_product.rs:230, 306). */
+int dn_out_norm(const dn_out_norm_args *args, hipStream_t stream);
+
 /* Bytes of device workspace dn_chunk_fwd / dn_chunk_bwd need for these
  * arguments (0 on invalid arguments). Has no counterpart in the reference,
  * whose tensors are allocated by Burn; it lets a caller own the memory. */

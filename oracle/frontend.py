@@ -9,6 +9,7 @@ reference runs between the fused in-projection and the delta rule:
     ShortConv::forward / ShortConv::step   (src/common/conv.rs:85-158)
     QkActivation / QkNorm / l2_normalize   (src/common/norm.rs:36-97)
     squash_write                           (src/common/qkv.rs:332-369)
+    OutNorm::forward                       (src/common/norm.rs:106-144)
 
 Layouts are the reference's: `projected` [B, S, ≥ conv_dim + gate width] with
 the segments [q | k (u copies) | v (u copies) | β or (erase | write)]
@@ -156,3 +157,15 @@ def gate_width(nheads, head_k_dim, head_v_dim, n_householder, write_gate):
 def conv_dim(nheads, head_k_dim, head_v_dim, n_householder):
     """QkvProjection::conv_dim (qkv.rs:180-182)."""
     return nheads * head_k_dim + n_householder * nheads * (head_k_dim + head_v_dim)
+
+
+def out_norm(x, gate, weight, eps):
+    """OutNorm::forward (norm.rs:106-144), per head over the last axis:
+    x / √(mean(x²) + ε) · γ, times silu(gate) when gated. ε is burn_stack's
+    RmsNorm(Gated) epsilon, which the reference does not vendor: parity in ε
+    is unpinned, so it is an argument here."""
+    x = np.asarray(x, np.float64)
+    y = x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * np.asarray(weight, np.float64)
+    if gate is not None:
+        y = y * silu(np.asarray(gate, np.float64))
+    return y

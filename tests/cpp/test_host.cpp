@@ -319,6 +319,9 @@ void host_cases() {
                    plain.forward_projected(Tensor::view(fake, {1, 3, 30}, DType::F32),
                                            Tensor::view(fake, {1, 28, 4}, DType::F32));
                  });
+    expect_error("out_norm_gate_presence", DN_ERR_NULL, "OutNorm::Gated needs an output gate",
+                 [&] { OutNorm{Tensor::view(fake, {6}, DType::F32)}.forward(
+                           Tensor::view(fake, {2, 3, 6}, DType::F32)); });
     expect_error("frontend_projection_width", DN_ERR_SHAPE,
                  "projection: last axis must be d_in_proj = 30, got 31", [&] {
                    plain.forward_projected(Tensor::view(fake, {1, 3, 31}, DType::F32),
@@ -547,6 +550,37 @@ void gpu_cases() {
     }
     if (rel_err(download(*wcur), download(*fnext)) != 0.0) fail("frontend: step window");
     ok("frontend_step_chain");
+  }
+  // OutNorm on constant rows: row c with gate g gives c/√(c² + ε)·γᵢ·silu(g)
+  // (norm.rs:106-113); the gate read in place from a wider projection row.
+  {
+    const int64_t T = 3, H = 2, D = 128, W = H * D + 10;
+    Vec x(static_cast<size_t>(T * H * D)), proj(static_cast<size_t>(T * W), 0.0);
+    Vec gm(static_cast<size_t>(D));
+    Rng r(8);
+    Vec cs = r.normals(size_t(T * H)), gs = r.normals(size_t(T * H));
+    for (int64_t i = 0; i < D; ++i) gm[size_t(i)] = 0.5 + 0.01 * double(i);
+    for (int64_t t = 0; t < T; ++t)
+      for (int64_t h = 0; h < H; ++h)
+        for (int64_t i = 0; i < D; ++i) {
+          x[size_t((t * H + h) * D + i)] = cs[size_t(t * H + h)];
+          proj[size_t(t * W + 3 + h * D + i)] = gs[size_t(t * H + h)];
+        }
+    Tensor tx = upload(x, {T, H, D}, DType::F32), tp = upload(proj, {T, W}, DType::F32);
+    OutNorm norm{upload(gm, {D}, DType::F32), true, 1e-5};
+    Tensor gview = Tensor::view(static_cast<float*>(tp.data()) + 3, {T, H, D}, DType::F32);
+    const Vec y = download(norm.forward(tx, gview, W));
+    double err = 0.0;
+    for (int64_t t = 0; t < T; ++t)
+      for (int64_t h = 0; h < H; ++h) {
+        const double c = cs[size_t(t * H + h)], g = gs[size_t(t * H + h)];
+        for (int64_t i = 0; i < D; ++i) {
+          const double want = c / std::sqrt(c * c + 1e-5) * gm[size_t(i)] * g / (1.0 + std::exp(-g));
+          err = std::max(err, std::fabs(y[size_t((t * H + h) * D + i)] - want));
+        }
+      }
+    if (err > 1e-5) fail("out_norm closed form: max error " + std::to_string(err));
+    ok("out_norm_closed_form");
   }
 }
 

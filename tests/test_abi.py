@@ -193,3 +193,24 @@ def test_frontend_rejects_invalid_arguments(over, code, msg):
     a = frontend_args(**over)
     assert lib.dn_frontend(ctypes.byref(a), None) == code
     assert msg in lib.dn_last_error().decode()
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(tokens=0), -2, "at least 1"),
+    (dict(head_v_dim=abi.OUT_NORM_MAX_HEAD_DIM + 1, gate_stride=10 ** 6), -9, "up to 1024"),
+    (dict(gate_stride=15), -2, "gate_stride is narrower"),
+    (dict(eps=-1.0), -2, "eps"),
+    (dict(out_dtype=4), -7, "dtype"),
+    (dict(weight=None), -6, "NULL"),
+])
+def test_out_norm_rejects_invalid_arguments(over, code, msg):
+    lib = abi.lib()
+    a = abi.OutNormArgs()
+    a.tokens, a.nheads, a.head_v_dim, a.gate_stride, a.eps = 4, 2, 8, 16, 1e-5
+    a.x_dtype = a.gate_dtype = a.out_dtype = abi.DN_F32
+    for f in ["x", "gate", "weight", "out"]:
+        setattr(a, f, 0x1000)  # never dereferenced: every case fails its checks first
+    for k, v in over.items():
+        setattr(a, k, v)
+    assert lib.dn_out_norm(ctypes.byref(a), None) == code
+    assert msg in lib.dn_last_error().decode()

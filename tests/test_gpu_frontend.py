@@ -177,3 +177,69 @@ def test_projection_forward_runs_in_proj(rng):
     assert rel_err(np_of(qkv.v_bShv), want["v"]) < 1e-4
     assert rel_err(np_of(qkv.erase_bShK), want["erase"]) < 1e-4
     assert qkv.write_bShV.data_ptr() == qkv.erase_bShK.data_ptr()
+
+
+# ---------------------------------------------------------------------------
+# dn_out_norm: OutNorm::forward (norm.rs:106-144)
+# ---------------------------------------------------------------------------
+
+NORM_CASES = [
+    # tokens shape, H, D, gated, x dtype, out dtype, gate as a projection view
+    ((2, 33), 4, 256, True, torch.bfloat16, torch.bfloat16, True),
+    ((2, 17), 3, 128, True, torch.float32, torch.float32, False),
+    ((5,), 16, 256, True, torch.float32, torch.bfloat16, True),
+    ((3, 9), 2, 128, False, torch.float32, torch.float32, False),
+    ((2, 7), 2, 100, True, torch.float32, torch.float32, True),
+    ((1, 6), 3, 6, True, torch.float32, torch.float32, False),
+    ((2, 4), 2, 512, True, torch.bfloat16, torch.float32, False),
+]
+
+
+@pytest.mark.parametrize("case", NORM_CASES)
+def test_out_norm_matches_oracle(rng, case):
+    lead, H, D, gated, dx, do, view = case
+    announce(f"dn_out_norm {case}")
+    rd = lambda a, d: torch.tensor(a, dtype=torch.float32).to(d).double().numpy()
+    x = rd(rng.standard_normal((*lead, H, D)) * 2.0, dx)
+    w = rd(rng.standard_normal(D), torch.float32)
+    gx = torch.tensor(x, dtype=torch.float32, device=DEV).to(dx)
+    gate = g_np = None
+    if gated:
+        g_np = rd(rng.standard_normal((*lead, H, D)), dx)
+        if view:  # the gate as the projection's column range (qkv.rs:429)
+            W = H * D + 37
+            proj = torch.zeros((*lead, W), dtype=dx, device=DEV)
+            proj[..., 5:5 + H * D] = torch.tensor(g_np, dtype=torch.float32,
+                                                  device=DEV).to(dx).reshape(*lead, H * D)
+            gate = proj[..., 5:5 + H * D].unflatten(-1, (H, D))
+        else:
+            gate = torch.tensor(g_np, dtype=torch.float32, device=DEV).to(dx)
+    norm = pkg.OutNorm(torch.tensor(w, dtype=torch.float32, device=DEV), gated=gated, eps=1e-5)
+    y = norm.forward(gx, gate, out_dtype=do)
+    torch.cuda.synchronize()
+    want = F.out_norm(x, g_np, w, 1e-5)
+    tol = 1e-5 if do == torch.float32 else 1e-2
+    assert rel_err(np_of(y), want) < tol
+
+
+def test_out_norm_in_place(rng):
+    """out may alias x."""
+    announce("dn_out_norm in place")
+    H, D = 4, 128
+    x = rng.standard_normal((6, H, D))
+    w = rng.standard_normal(D)
+    g = rng.standard_normal((6, H, D))
+    t = lambda a: torch.tensor(a, dtype=torch.float32, device=DEV)
+    gx, gg, gw = t(x), t(g), t(w)
+    abi.run_out_norm(abi.out_norm_args(gx, gg, gw, gx, 1e-5))
+    torch.cuda.synchronize()
+    assert rel_err(np_of(gx), F.out_norm(x, g, w, 1e-5)) < 1e-5
+
+
+def test_out_norm_gate_presence_mirrors_the_reference(rng):
+    """norm.rs:131-132: a gated norm without a gate, or the reverse, panics."""
+    x = torch.zeros((2, 2, 8), device=DEV)
+    with pytest.raises(pkg.DeltaError, match="needs an output gate"):
+        pkg.OutNorm.init(8, True, DEV).forward(x)
+    with pytest.raises(pkg.DeltaError, match="takes no output gate"):
+        pkg.OutNorm.init(8, False, DEV).forward(x, x)

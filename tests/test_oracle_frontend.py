@@ -146,3 +146,23 @@ def test_activations_at_special_points():
     e = F.activation(x, F.ACT_ELU_PLUS_ONE)
     assert np.allclose(e, [np.exp(-50), np.exp(-1), 1.0, 2.0, 51.0]) and np.all(e > 0)
     assert F.sigmoid(np.array(0.0)) == 0.5
+
+
+def test_out_norm_is_torch_rms_norm_times_silu_gate(rng):
+    """OutNorm's plain form against torch's rms_norm (a library routine:
+    the mean of squares over the last axis, ε inside the root); the gated
+    form multiplies by silu(gate) after the norm (norm.rs:106-113)."""
+    x = rng.standard_normal((3, 5, 4, 16))
+    w = rng.standard_normal(16)
+    g = rng.standard_normal(x.shape)
+    for eps in [1e-5, 1e-2]:
+        ref = torch.nn.functional.rms_norm(torch.tensor(x), (16,), torch.tensor(w), eps).numpy()
+        assert np.abs(F.out_norm(x, None, w, eps) - ref).max() < 1e-12
+        assert np.abs(F.out_norm(x, g, w, eps) - ref * F.silu(g)).max() < 1e-12
+
+
+def test_out_norm_closed_forms():
+    c = np.full((1, 8), -3.0)
+    assert np.allclose(F.out_norm(c, None, np.ones(8), 0.0), -1.0)       # a constant row → ±1
+    assert np.allclose(F.out_norm(c, np.zeros((1, 8)), np.ones(8), 1e-5), 0.0)  # silu(0) = 0
+    assert np.allclose(F.out_norm(np.zeros((1, 8)), None, np.ones(8), 1e-5), 0.0)
