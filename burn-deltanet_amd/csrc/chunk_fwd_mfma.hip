@@ -841,6 +841,13 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
     const int nn = n + 1 < p.N ? n + 1 : n;  // the last chunk prefetches itself again
     const uint16_t* tl = tiles[cur];
     const float egl = PC ? 1.f : gegl[cur];
+    // The next chunk's tiles are fetched at the top, so the loads have all
+    // three phases to land before stage() writes them to LDS (config 2 scan
+    // 392 → 376 µs, config 5's per-channel scan 1165 → 870 µs). The
+    // per-channel states mode (the backward's recompute) measured slower so
+    // (1055 → 1105 µs): its fetch stays after phase 1.
+    constexpr bool kFetchTop = !(PC && ST);
+    if constexpr (kFetchTop) fetch(nn);
     if constexpr (ST) {
       float* sdst = p.states + chunk_of(n) * K * p.V + jl;
 #pragma unroll
@@ -885,7 +892,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
         }
       }
     }
-    fetch(nn);
+    if constexpr (!kFetchTop) fetch(nn);
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
 #pragma unroll
