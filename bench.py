@@ -14,7 +14,7 @@ dk128) at 1 GPU; % roofline"):
   dn_recurrent call per token.
 * roofline = the dominant kernel of the forward, timed with HIP events on its
   own stream by the library's profiler (dn_profile_*), against algorithmic
-  bytes per launch (DESIGN.md lists the per-unit figures).
+  bytes per launch (the per-unit figures are in bench_chunk_fwd).
 * config4 / config5 = BASELINE configs 4 (DeltaProduct u=2, folded core
   forward) and 5 (GDN-2 per-channel gates, forward + custom backward), each
   with its own HBM roofline; not part of `value`.
@@ -94,7 +94,8 @@ def bench_chunk_fwd(torch, pkg, steps, warmup, algo):
     ms = start.elapsed_time(stop) / steps
     tokens = B * T
     G = B * (T // L) * H
-    # Algorithmic bytes per launch of each forward kernel.
+    # Algorithmic bytes per launch of each forward kernel: every tensor it
+    # must move once.
     qk = 2 * B * T * H * K * 2          # q and k, bf16
     vb = B * T * H * V * 2              # v, bf16
     yb = B * T * H * V * 2              # y, bf16
@@ -455,7 +456,7 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one GPU only: the delta-rule core shards over (batch, "
-              "head) with no communication (DESIGN.md), and this build runs no "
+              "head) with no communication, and this build runs no "
               "multi-GPU path. Use --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
