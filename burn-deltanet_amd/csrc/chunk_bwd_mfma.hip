@@ -80,6 +80,25 @@ __device__ inline float reduce16(const float (&v)[16], int lane) {
   return (u1 ? c[1] : c[0]) + __shfl_xor(u1 ? c[0] : c[1], 1);
 }
 
+// Materialises x in a register at this point: keeps the compiler from sinking
+// an accumulation chain into the guarded store that consumes it, which would
+// hold every partial term live until then.
+__device__ inline void pin(float& x) { asm volatile("" : "+v"(x)); }
+__device__ inline void pin(f32x4& x) { asm volatile("" : "+v"(x)); }
+
+// v[0..3] summed over the 16 lanes that share lane/16; lane l receives the
+// total of index l%4.
+__device__ inline float reduce4(const float (&v)[4], int lane) {
+  const bool u2 = lane & 2, u1 = lane & 1;
+  float a[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    a[j] = (u2 ? v[2 + j] : v[j]) + __shfl_xor(u2 ? v[j] : v[2 + j], 2);
+  float c = (u1 ? a[1] : a[0]) + __shfl_xor(u1 ? a[0] : a[1], 1);
+  c += __shfl_xor(c, 4);
+  return c + __shfl_xor(c, 8);
+}
+
 // 64 rows of C bf16 (global, row pitch C) → LDS tile, natural order.
 template <int C>
 __device__ inline void stage_rows(uint16_t* R, int dst, const uint16_t* src, int tid) {
@@ -395,15 +414,6 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
       *reinterpret_cast<float4*>(bD[s]) = dsr[0];
       *reinterpret_cast<float4*>(bD[s] + 4) = dsr[1];
     }
-    // Per-channel erase gate at the lane's positions (kept for phase D).
-    if (PC && p.ew != 1)
-#pragma unroll
-      for (int ib = 0; ib < 4; ++ib)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int i = rowi(ib, r);
-          eA[ib][r] = i < valid ? p.erase[row_of(i) * K + c] : 0.f;
-        }
   }
   __syncthreads();
 
@@ -480,7 +490,6 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
           const float gci = Gc[i * GP + c];
           eg = __expf(gci);
           ec = __expf(gl_c - gci);
-          if (p.ew == 1) eA[ib][r] = er_s[i];
         } else {
           eg = eg_s[i];
           ec = ec_s[i];
@@ -510,6 +519,16 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
     }
   }
   __syncthreads();
+  // Per-channel erase gate at the lane's rows, for phase D: loaded here so
+  // that phase B does not hold it, its latency covered by phase C.
+  if (PC && kwave)
+#pragma unroll
+    for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = rowi(ib, r);
+        eA[ib][r] = p.ew == 1 ? er_s[i] : (i < valid ? p.erase[row_of(i) * K + c] : 0.f);
+      }
 
   // ---- X, dV' rows and the dAqk layouts into LDS --------------------------
   if (vwave) {
@@ -687,6 +706,8 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
 
   // ---- phase D: score backward, gates, stores -----------------------------
   if (kwave) {
+    TG* gq = static_cast<TG*>(p.dq);
+    TG* gk = static_cast<TG*>(p.dk);
     // d_G of the scan (combined_backward.rs:284-313): −d_carry + (d_qr⊙qs +
     // d_kg⊙ke)⊙e^G = −dkA⊙k + dqA⊙q·scale + dkeA⊙k⊙e with phase B's
     // accumulators, and d(G_last) = Σ_i d_carry + (Σ_v dS⊙S₀)·e^{G_last}.
@@ -892,33 +913,68 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
         tot += __shfl_xor(tot, 16);
         tot += __shfl_xor(tot, 32);
         if (g4 == 2) dgA[pb][0] += tot;
+        // Only this iteration adds to row block pb's d_q and d_ke: store d_q,
+        // fold d_ke⊙e into d_k and emit d_erase now, which frees their
+        // registers for the blocks that follow.
+        {
+          const uint2 k4 = *reinterpret_cast<const uint2*>(&R[oKC + tile_at<kL>(c, 16 * pb + 4 * g4)]);
+          const float kv[4] = {lo_f(k4.x), hi_f(k4.x), lo_f(k4.y), hi_f(k4.y)};
+          float rde[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int i = rowi(pb, r);
+            const bool ok = i < valid;
+            if (ok) st(gq, row_of(i) * K + c, dqA[pb][r] * p.scale);
+            dkA[pb][r] += dkeA[pb][r] * eA[pb][r];
+            rde[r] = dkeA[pb][r] * kv[r];
+            if (p.ew != 1 && ok) p.derase[row_of(i) * K + c] = rde[r];
+          }
+          if (p.ew == 1) {
+            const float tot4 = reduce4(rde, lane);
+            if ((lane & 12) == 0) atomicAdd(&racc[1][rowi(pb, lane & 3)], tot4);
+          }
+        }
+#pragma unroll
+        for (int jb = 0; jb < 4; ++jb) {
+          pin(dkA[jb]);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) pin(dgA[jb][r]);
+        }
         if (pb < 3)
 #pragma unroll
           for (int t = 0; t < 8; ++t) ecur[t] = enext[t];
       }
     }
-    // Front end (combined_backward.rs:153-188) and the stores.
-    TG* gq = static_cast<TG*>(p.dq);
-    TG* gk = static_cast<TG*>(p.dk);
-    float rde[16];
+    // Front end (combined_backward.rs:153-188) and the stores (the
+    // per-channel branch has stored d_q and d_erase block by block).
+    if constexpr (PC) {
 #pragma unroll
-    for (int ib = 0; ib < 4; ++ib) {
-      const uint2 k4 = *reinterpret_cast<const uint2*>(&R[oKC + tile_at<kL>(c, 16 * ib + 4 * g4)]);
-      const float kv[4] = {lo_f(k4.x), hi_f(k4.x), lo_f(k4.y), hi_f(k4.y)};
+      for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int i = rowi(ib, r);
-        const bool ok = i < valid;
-        const float e = PC ? eA[ib][r] : er_s[i];
-        if (ok) {
-          st(gq, row_of(i) * K + c, dqA[ib][r] * p.scale);
-          st(gk, row_of(i) * K + c, dkA[ib][r] + dkeA[ib][r] * e);
+        for (int r = 0; r < 4; ++r) {
+          const int i = rowi(ib, r);
+          if (i < valid) st(gk, row_of(i) * K + c, dkA[ib][r]);
         }
-        rde[4 * ib + r] = dkeA[ib][r] * kv[r];
-        if (p.ew != 1 && ok) p.derase[row_of(i) * K + c] = rde[4 * ib + r];
+    } else {
+      float rde[16];
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib) {
+        const uint2 k4 = *reinterpret_cast<const uint2*>(&R[oKC + tile_at<kL>(c, 16 * ib + 4 * g4)]);
+        const float kv[4] = {lo_f(k4.x), hi_f(k4.x), lo_f(k4.y), hi_f(k4.y)};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = rowi(ib, r);
+          const bool ok = i < valid;
+          if (ok) {
+            st(gq, row_of(i) * K + c, dqA[ib][r] * p.scale);
+            st(gk, row_of(i) * K + c, dkA[ib][r] + dkeA[ib][r] * er_s[i]);
+          }
+          rde[4 * ib + r] = dkeA[ib][r] * kv[r];
+          if (p.ew != 1 && ok) p.derase[row_of(i) * K + c] = rde[4 * ib + r];
+        }
       }
+      if (p.ew == 1) atomicAdd(&racc[1][red_row], reduce16(rde, lane));
     }
-    if (p.ew == 1) atomicAdd(&racc[1][red_row], reduce16(rde, lane));
   }
   if constexpr (PC) {
     // d_g = the reverse cumulative sum over the chunk of d_G (row L−1 also

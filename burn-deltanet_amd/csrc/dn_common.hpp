@@ -30,6 +30,11 @@ __host__ __device__ inline uint16_t f32_to_bf16(float f) {
   return uint16_t(u >> 16);
 }
 
+// The same rounding in one v_cvt_pk_bf16_f32 (device code).
+__device__ inline uint16_t f32_to_bf16_dev(float f) {
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+
 template <class T>
 __device__ inline float ld(const T* p, size_t i);
 template <>
@@ -49,7 +54,7 @@ __device__ inline void st<float>(float* p, size_t i, float v) {
 }
 template <>
 __device__ inline void st<bf16>(bf16* p, size_t i, float v) {
-  p[i].bits = f32_to_bf16(v);
+  p[i].bits = f32_to_bf16_dev(v);
 }
 
 // ---------------------------------------------------------------------------

@@ -156,7 +156,7 @@ __device__ inline void store_n(T* p, const float (&v)[N], int valid) {
   if constexpr (VEC) {
     if constexpr (sizeof(T) == 2) {
       if constexpr (N == 1) {
-        *reinterpret_cast<uint16_t*>(p) = f32_to_bf16(v[0]);
+        *reinterpret_cast<uint16_t*>(p) = f32_to_bf16_dev(v[0]);
       } else {
         uint32_t w[N / 2];
 #pragma unroll
