@@ -377,32 +377,41 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
 // r = 16·(i div 16) + 8,
 //   Akk[i][j] = Σ_d (k⊙e)[i][d]·e^{min(G[i][d]−G[r][d], 48)} · k[j][d]·e^{min(G[r][d]−G[j][d], 48)}
 // (j < i; Aqk likewise with scale·q and j ≤ i). The row factors are formed
-// once per chunk as bf16 tiles (hi + lo for Akk, which feeds the inverse);
-// the column factors, which depend on the row block, are formed per MFMA
-// fragment in registers. Besides T/attn/Kcᵀ the kernel writes what the scan
+// one 16-row block at a time as bf16 tiles (hi + lo for Akk, which feeds the
+// inverse); the column factors, which depend on the row block, are formed per
+// MFMA fragment in registers. Besides T/attn/Kcᵀ the kernel writes what the scan
 // needs in place of K, Q and the scalar gates: kg = e⊙e^G⊙K (hi + lo),
 // qg = scale·e^G⊙Q and e^{G_last} per channel. One workgroup per chunk-head.
 template <int K>
 __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p) {
-  constexpr int KP = K + 8;  // bf16 row pitch
   constexpr int GP = K + 4;  // fp32 row pitch of G
   constexpr int KS8 = K / 8;
   constexpr int NLD = kL * KS8 / kThreads;
-  constexpr int kTile = kL * KP * 2;
+  constexpr int NIT = 16 * KS8;  // items (one row, 8 channels) of a 16-row block
+  static_assert(NIT <= kThreads, "one item per thread per row block");
+  constexpr int kGBytes = kL * GP * 4;
   constexpr int kSolveBytes = (kL * (kL + 1) + (kL / 2) * (kL / 2 + 1)) * 4;
   constexpr float kMaxExp = 48.f;  // MAX_EXPONENT, decay.rs:49
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kL * KP];
-  __shared__ __attribute__((aligned(16))) float Gc[kL * GP];
-  // Row-factor tiles; T and the merge scratch reuse their space afterwards.
+  // K rows and the row-factor tiles are unpadded: a row's 16-byte segments
+  // are permuted by its row index, so the 16 rows an MFMA operand read spans
+  // cover 16 distinct 16-byte bank slots (rows of 128 bytes pair up per 256
+  // bytes, hence the shift when K = 64).
+  constexpr int kSwz = KS8 >= 16 ? 0 : 1;
+  auto sw = [](int row, int col) {
+    return row * K + ((((col >> 3) ^ (row >> kSwz)) & (KS8 - 1)) << 3) + (col & 7);
+  };
+  // 79 KB at K = 128, which keeps two workgroups per CU: the row-factor
+  // tiles hold one 16-row block at a time, attn goes to memory straight from
+  // the accumulators, and T with the merge scratch takes G's place once Kcᵀ
+  // is written.
+  __shared__ __attribute__((aligned(16))) uint16_t Ks[kL * K];
   __shared__ __attribute__((aligned(16)))
-  unsigned char rows[3 * kTile > kSolveBytes ? 3 * kTile : kSolveBytes];
-  uint16_t* AKh = reinterpret_cast<uint16_t*>(rows);
-  uint16_t* AKl = AKh + kL * KP;
-  uint16_t* AQ = AKl + kL * KP;
-  float(*Tm)[kL + 1] = reinterpret_cast<float(*)[kL + 1]>(rows);
-  float(*Xs)[kL / 2 + 1] = reinterpret_cast<float(*)[kL / 2 + 1]>(rows + kL * (kL + 1) * 4);
-  __shared__ float A[kL][kL + 1];
-  __shared__ __attribute__((aligned(16))) uint16_t At[kL * (kL + 8)];
+  unsigned char gsolve[kGBytes > kSolveBytes ? kGBytes : kSolveBytes];
+  __shared__ __attribute__((aligned(16))) uint16_t RT[3][16 * K];  // (k⊙e)·rf hi, lo; scale·q·rf
+  __shared__ float A[kL][kL + 1];  // strict-lower Akk, fp32 (upper blocks never read)
+  float* Gc = reinterpret_cast<float*>(gsolve);
+  float(*Tm)[kL + 1] = reinterpret_cast<float(*)[kL + 1]>(gsolve);
+  float(*Xs)[kL / 2 + 1] = reinterpret_cast<float(*)[kL / 2 + 1]>(gsolve + kL * (kL + 1) * 4);
 
   const int cid = blockIdx.x;
   const int h = cid % p.H, n = (cid / p.H) % p.N, b = cid / (p.H * p.N);
@@ -415,23 +424,39 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p) {
     f[4] = lo_f(u.z); f[5] = hi_f(u.z); f[6] = lo_f(u.w); f[7] = hi_f(u.w);
   };
 
-  for (int idx = tid; idx < kL * kL; idx += kThreads) {
-    const int i = idx / kL, j = idx % kL;
-    if (j / 16 > i / 16) At[i * (kL + 8) + j] = 0;
-  }
-  // K tile to LDS, Q rows to registers (zero past the sequence end).
-  uint4 qr[NLD];
+  // K tile to LDS (zero past the sequence end).
 #pragma unroll
   for (int m = 0; m < NLD; ++m) {
     const int idx = tid + kThreads * m, row = idx / KS8, c8 = idx % KS8;
     uint4 kv = make_uint4(0u, 0u, 0u, 0u);
-    qr[m] = kv;
-    if (tok0 + row < p.S) {
-      const size_t off = row_of(row) * K + 8 * c8;
-      kv = *reinterpret_cast<const uint4*>(p.k + off);
-      qr[m] = *reinterpret_cast<const uint4*>(p.q + off);
+    if (tok0 + row < p.S) kv = *reinterpret_cast<const uint4*>(p.k + row_of(row) * K + 8 * c8);
+    *reinterpret_cast<uint4*>(&Ks[sw(row, 8 * c8)]) = kv;
+  }
+  // This thread's item of each row block rb is row 16·rb + irow, channels
+  // d0i…d0i+7: its Q segment and erase gate, in registers.
+  const bool item = tid < NIT;
+  const int irow = tid / KS8, d0i = 8 * (tid % KS8);
+  uint4 qr[4];
+  float ef[4][8];
+#pragma unroll
+  for (int rb = 0; rb < 4; ++rb) {
+    const int i = 16 * rb + irow;
+    const bool ok = item && tok0 + i < p.S;
+    qr[rb] = ok ? *reinterpret_cast<const uint4*>(p.q + row_of(i) * K + d0i)
+                : make_uint4(0u, 0u, 0u, 0u);
+    if (p.ew == 1) {
+      const float e = ok ? p.erase[row_of(i)] : 0.f;
+#pragma unroll
+      for (int x = 0; x < 8; ++x) ef[rb][x] = e;
+    } else if (ok) {
+      *reinterpret_cast<float4*>(ef[rb]) =
+          *reinterpret_cast<const float4*>(p.erase + row_of(i) * K + d0i);
+      *reinterpret_cast<float4*>(ef[rb] + 4) =
+          *reinterpret_cast<const float4*>(p.erase + row_of(i) * K + d0i + 4);
+    } else {
+#pragma unroll
+      for (int x = 0; x < 8; ++x) ef[rb][x] = 0.f;
     }
-    *reinterpret_cast<uint4*>(&Ks[row * KP + 8 * c8]) = kv;
   }
   // G = in-chunk cumulative sum of g per channel: KPART lanes per channel,
   // each summing a run of tokens, then the runs' totals are carried over.
@@ -460,140 +485,133 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p) {
   }
   __syncthreads();
 
-  // Row factors e^{min(G[i]−G[r], 48)} into the A-operand tiles, and the
-  // scan's kg / qg (e^G ≤ 1: G ≤ 0).
+  const int r16 = lane & 15, q4 = lane >> 4, k8 = 8 * q4;
 #pragma unroll
-  for (int m = 0; m < NLD; ++m) {
-    const int idx = tid + kThreads * m, i = idx / KS8, d0 = 8 * (idx % KS8);
-    const int r = 16 * (i / 16) + 8;
-    const bool ok = tok0 + i < p.S;
-    float gi[8], gr[8], kf[8], qf[8], ef[8];
-    *reinterpret_cast<float4*>(gi) = *reinterpret_cast<const float4*>(&Gc[i * GP + d0]);
-    *reinterpret_cast<float4*>(gi + 4) = *reinterpret_cast<const float4*>(&Gc[i * GP + d0 + 4]);
-    *reinterpret_cast<float4*>(gr) = *reinterpret_cast<const float4*>(&Gc[r * GP + d0]);
-    *reinterpret_cast<float4*>(gr + 4) = *reinterpret_cast<const float4*>(&Gc[r * GP + d0 + 4]);
-    f8(*reinterpret_cast<const uint4*>(&Ks[i * KP + d0]), kf);
-    f8(qr[m], qf);
-    if (p.ew == 1) {
-      const float e = ok ? p.erase[row_of(i)] : 0.f;
+  for (int rb = 0; rb < 4; ++rb) {
+    const int r = 16 * rb + 8;  // the block's reference row
+    // Row factors e^{min(G[i]−G[r], 48)} of block rb into the A-operand
+    // tiles, and the scan's kg / qg (e^G ≤ 1: G ≤ 0).
+    if (item) {
+      const int i = 16 * rb + irow;
+      float gi[8], gr[8], kf[8], qf[8];
+      *reinterpret_cast<float4*>(gi) = *reinterpret_cast<const float4*>(&Gc[i * GP + d0i]);
+      *reinterpret_cast<float4*>(gi + 4) = *reinterpret_cast<const float4*>(&Gc[i * GP + d0i + 4]);
+      *reinterpret_cast<float4*>(gr) = *reinterpret_cast<const float4*>(&Gc[r * GP + d0i]);
+      *reinterpret_cast<float4*>(gr + 4) = *reinterpret_cast<const float4*>(&Gc[r * GP + d0i + 4]);
+      f8(*reinterpret_cast<const uint4*>(&Ks[sw(i, d0i)]), kf);
+      f8(qr[rb], qf);
+      float ak[8], aq[8], kg[8], qg[8];
 #pragma unroll
-      for (int x = 0; x < 8; ++x) ef[x] = e;
-    } else if (ok) {
-      *reinterpret_cast<float4*>(ef) =
-          *reinterpret_cast<const float4*>(p.erase + row_of(i) * K + d0);
-      *reinterpret_cast<float4*>(ef + 4) =
-          *reinterpret_cast<const float4*>(p.erase + row_of(i) * K + d0 + 4);
-    } else {
+      for (int x = 0; x < 8; ++x) {
+        const float rf = __expf(fminf(gi[x] - gr[x], kMaxExp));
+        const float eg = __expf(gi[x]);
+        const float ke = kf[x] * ef[rb][x], qs = qf[x] * p.scale;
+        ak[x] = ke * rf;
+        aq[x] = qs * rf;
+        kg[x] = ke * eg;
+        qg[x] = qs * eg;
+      }
+      uint32_t ah[4], al[4], qh[4], gh[4], gl[4], qq[4];
 #pragma unroll
-      for (int x = 0; x < 8; ++x) ef[x] = 0.f;
+      for (int x = 0; x < 4; ++x) {
+        ah[x] = pk_bf16(ak[2 * x], ak[2 * x + 1]);
+        al[x] = pk_bf16(ak[2 * x] - lo_f(ah[x]), ak[2 * x + 1] - hi_f(ah[x]));
+        qh[x] = pk_bf16(aq[2 * x], aq[2 * x + 1]);
+        gh[x] = pk_bf16(kg[2 * x], kg[2 * x + 1]);
+        gl[x] = pk_bf16(kg[2 * x] - lo_f(gh[x]), kg[2 * x + 1] - hi_f(gh[x]));
+        qq[x] = pk_bf16(qg[2 * x], qg[2 * x + 1]);
+      }
+      const int at = sw(irow, d0i);
+      *reinterpret_cast<uint4*>(&RT[0][at]) = make_uint4(ah[0], ah[1], ah[2], ah[3]);
+      *reinterpret_cast<uint4*>(&RT[1][at]) = make_uint4(al[0], al[1], al[2], al[3]);
+      *reinterpret_cast<uint4*>(&RT[2][at]) = make_uint4(qh[0], qh[1], qh[2], qh[3]);
+      const size_t go = (size_t(cid) * kL + i) * K + d0i;
+      *reinterpret_cast<uint4*>(p.Kg + go) = make_uint4(gh[0], gh[1], gh[2], gh[3]);
+      *reinterpret_cast<uint4*>(p.Kglo + go) = make_uint4(gl[0], gl[1], gl[2], gl[3]);
+      *reinterpret_cast<uint4*>(p.Qg + go) = make_uint4(qq[0], qq[1], qq[2], qq[3]);
     }
-    float ak[8], aq[8], kg[8], qg[8];
+    __syncthreads();
+    // Scores of block row rb: wave w ≤ rb forms block (rb, w); a wave past
+    // the diagonal writes attn's zero block (rb, w). attn row i, column j:
+    // the 16 lanes of one q4 store 16 consecutive columns.
+    {
+      const int cb = wave, j = 16 * cb + r16;
+      uint16_t* adst = p.attn + size_t(cid) * kL * kL + size_t(16 * rb + 4 * q4) * kL + j;
+      if (cb <= rb) {
+        f32x4 acck = {0.f, 0.f, 0.f, 0.f}, accq = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int x = 0; x < 8; ++x) {
-      const float rf = __expf(fminf(gi[x] - gr[x], kMaxExp));
-      const float eg = __expf(gi[x]);
-      const float ke = kf[x] * ef[x], qs = qf[x] * p.scale;
-      ak[x] = ke * rf;
-      aq[x] = qs * rf;
-      kg[x] = ke * eg;
-      qg[x] = qs * eg;
-    }
-    uint32_t ah[4], al[4], qh[4], gh[4], gl[4], qq[4];
+        for (int kk = 0; kk < K / 32; ++kk) {
+          const int d0 = 32 * kk + k8;
+          float kf[8], gj[8], gr[8];
+          f8(*reinterpret_cast<const uint4*>(&Ks[sw(j, d0)]), kf);
+          *reinterpret_cast<float4*>(gj) = *reinterpret_cast<const float4*>(&Gc[j * GP + d0]);
+          *reinterpret_cast<float4*>(gj + 4) = *reinterpret_cast<const float4*>(&Gc[j * GP + d0 + 4]);
+          *reinterpret_cast<float4*>(gr) = *reinterpret_cast<const float4*>(&Gc[r * GP + d0]);
+          *reinterpret_cast<float4*>(gr + 4) = *reinterpret_cast<const float4*>(&Gc[r * GP + d0 + 4]);
+          float c[8];
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      ah[x] = pk_bf16(ak[2 * x], ak[2 * x + 1]);
-      al[x] = pk_bf16(ak[2 * x] - lo_f(ah[x]), ak[2 * x + 1] - hi_f(ah[x]));
-      qh[x] = pk_bf16(aq[2 * x], aq[2 * x + 1]);
-      gh[x] = pk_bf16(kg[2 * x], kg[2 * x + 1]);
-      gl[x] = pk_bf16(kg[2 * x] - lo_f(gh[x]), kg[2 * x + 1] - hi_f(gh[x]));
-      qq[x] = pk_bf16(qg[2 * x], qg[2 * x + 1]);
+          for (int x = 0; x < 8; ++x) c[x] = kf[x] * __expf(fminf(gr[x] - gj[x], kMaxExp));
+          uint4 bh, bl;
+          bh.x = pk_bf16(c[0], c[1]);
+          bh.y = pk_bf16(c[2], c[3]);
+          bh.z = pk_bf16(c[4], c[5]);
+          bh.w = pk_bf16(c[6], c[7]);
+          bl.x = pk_bf16(c[0] - lo_f(bh.x), c[1] - hi_f(bh.x));
+          bl.y = pk_bf16(c[2] - lo_f(bh.y), c[3] - hi_f(bh.y));
+          bl.z = pk_bf16(c[4] - lo_f(bh.z), c[5] - hi_f(bh.z));
+          bl.w = pk_bf16(c[6] - lo_f(bh.w), c[7] - hi_f(bh.w));
+          const bf16x8 b_h = __builtin_bit_cast(bf16x8, bh), b_l = __builtin_bit_cast(bf16x8, bl);
+          const int at = sw(r16, d0);
+          const bf16x8 a_h = ld8(&RT[0][at]);
+          acck = mfma16(a_h, b_h, acck);
+          acck = mfma16(ld8(&RT[1][at]), b_h, acck);
+          acck = mfma16(a_h, b_l, acck);
+          accq = mfma16(ld8(&RT[2][at]), b_h, accq);
+        }
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int i = 16 * rb + 4 * q4 + rr;
+          A[i][j] = (j < i) ? acck[rr] : 0.f;
+          adst[rr * kL] = uint16_t(pk_bf16((j <= i) ? accq[rr] : 0.f, 0.f));
+        }
+      } else {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) adst[rr * kL] = 0;
+      }
     }
-    *reinterpret_cast<uint4*>(&AKh[i * KP + d0]) = make_uint4(ah[0], ah[1], ah[2], ah[3]);
-    *reinterpret_cast<uint4*>(&AKl[i * KP + d0]) = make_uint4(al[0], al[1], al[2], al[3]);
-    *reinterpret_cast<uint4*>(&AQ[i * KP + d0]) = make_uint4(qh[0], qh[1], qh[2], qh[3]);
-    const size_t go = (size_t(cid) * kL + i) * K + d0;
-    *reinterpret_cast<uint4*>(p.Kg + go) = make_uint4(gh[0], gh[1], gh[2], gh[3]);
-    *reinterpret_cast<uint4*>(p.Kglo + go) = make_uint4(gl[0], gl[1], gl[2], gl[3]);
-    *reinterpret_cast<uint4*>(p.Qg + go) = make_uint4(qq[0], qq[1], qq[2], qq[3]);
+    if (rb < 3) __syncthreads();  // the next block rewrites RT
   }
-  __syncthreads();
 
-  // Scores: the ten lower 16×16 block pairs (rb ≥ cb), dealt 3/3/2/2.
-  {
-    const int r16 = lane & 15, q4 = lane >> 4, k8 = 8 * q4;
+  // Kcᵀ = (e^{G_last−G}⊙K)ᵀ, two channels per item; e^{G_last}.
+  for (int it = tid; it < K * 2; it += kThreads) {
+    const int d = 2 * (it % (K / 2)), t0 = 16 * (it / (K / 2));
+    const float gl0 = Gc[(kL - 1) * GP + d], gl1 = Gc[(kL - 1) * GP + d + 1];
+    uint32_t w0[8], w1[8];
 #pragma unroll
-    for (int pi = wave; pi < 10; pi += 4) {
-      const int rb = pi < 1 ? 0 : pi < 3 ? 1 : pi < 6 ? 2 : 3;
-      const int cb = pi - rb * (rb + 1) / 2;
-      const int r = 16 * rb + 8, j = 16 * cb + r16, ia = 16 * rb + r16;
-      f32x4 acck = {0.f, 0.f, 0.f, 0.f}, accq = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < K / 32; ++kk) {
-        const int d0 = 32 * kk + k8;
-        float kf[8], gj[8], gr[8];
-        f8(*reinterpret_cast<const uint4*>(&Ks[j * KP + d0]), kf);
-        *reinterpret_cast<float4*>(gj) = *reinterpret_cast<const float4*>(&Gc[j * GP + d0]);
-        *reinterpret_cast<float4*>(gj + 4) = *reinterpret_cast<const float4*>(&Gc[j * GP + d0 + 4]);
-        *reinterpret_cast<float4*>(gr) = *reinterpret_cast<const float4*>(&Gc[r * GP + d0]);
-        *reinterpret_cast<float4*>(gr + 4) = *reinterpret_cast<const float4*>(&Gc[r * GP + d0 + 4]);
-        float c[8];
-#pragma unroll
-        for (int x = 0; x < 8; ++x) c[x] = kf[x] * __expf(fminf(gr[x] - gj[x], kMaxExp));
-        uint4 bh, bl;
-        bh.x = pk_bf16(c[0], c[1]);
-        bh.y = pk_bf16(c[2], c[3]);
-        bh.z = pk_bf16(c[4], c[5]);
-        bh.w = pk_bf16(c[6], c[7]);
-        bl.x = pk_bf16(c[0] - lo_f(bh.x), c[1] - hi_f(bh.x));
-        bl.y = pk_bf16(c[2] - lo_f(bh.y), c[3] - hi_f(bh.y));
-        bl.z = pk_bf16(c[4] - lo_f(bh.z), c[5] - hi_f(bh.z));
-        bl.w = pk_bf16(c[6] - lo_f(bh.w), c[7] - hi_f(bh.w));
-        const bf16x8 b_h = __builtin_bit_cast(bf16x8, bh), b_l = __builtin_bit_cast(bf16x8, bl);
-        const bf16x8 a_h = ld8(&AKh[ia * KP + d0]);
-        acck = mfma16(a_h, b_h, acck);
-        acck = mfma16(ld8(&AKl[ia * KP + d0]), b_h, acck);
-        acck = mfma16(a_h, b_l, acck);
-        accq = mfma16(ld8(&AQ[ia * KP + d0]), b_h, accq);
-      }
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int i = 16 * rb + 4 * q4 + rr;
-        A[i][j] = (j < i) ? acck[rr] : 0.f;
-        At[i * (kL + 8) + j] = uint16_t(pk_bf16((j <= i) ? accq[rr] : 0.f, 0.f));
-      }
+    for (int e = 0; e < 8; ++e) {
+      const int t = t0 + 2 * e;
+      const uint32_t a = *reinterpret_cast<const uint32_t*>(&Ks[sw(t, d)]);
+      const uint32_t c = *reinterpret_cast<const uint32_t*>(&Ks[sw(t + 1, d)]);
+      const float2 ga = *reinterpret_cast<const float2*>(&Gc[t * GP + d]);
+      const float2 gb = *reinterpret_cast<const float2*>(&Gc[(t + 1) * GP + d]);
+      w0[e] = pk_bf16(lo_f(a) * __expf(gl0 - ga.x), lo_f(c) * __expf(gl0 - gb.x));
+      w1[e] = pk_bf16(hi_f(a) * __expf(gl1 - ga.y), hi_f(c) * __expf(gl1 - gb.y));
     }
+    uint4* dst0 = reinterpret_cast<uint4*>(p.KcT + (size_t(cid) * K + d) * kL + t0);
+    uint4* dst1 = reinterpret_cast<uint4*>(p.KcT + (size_t(cid) * K + d + 1) * kL + t0);
+    dst0[0] = make_uint4(w0[0], w0[1], w0[2], w0[3]);
+    dst0[1] = make_uint4(w0[4], w0[5], w0[6], w0[7]);
+    dst1[0] = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+    dst1[1] = make_uint4(w1[4], w1[5], w1[6], w1[7]);
   }
-  __syncthreads();
+  for (int d = tid; d < K; d += kThreads) p.egl[size_t(cid) * K + d] = __expf(Gc[(kL - 1) * GP + d]);
+  __syncthreads();  // G is dead: T and the merge scratch take its space
 
   diag_inverse(A, Tm, wave, lane);
-  {
-    // Kcᵀ = (e^{G_last−G}⊙K)ᵀ, two channels per item; e^{G_last}.
-    for (int it = tid; it < K * 2; it += kThreads) {
-      const int d = 2 * (it % (K / 2)), t0 = 16 * (it / (K / 2));
-      const float gl0 = Gc[(kL - 1) * GP + d], gl1 = Gc[(kL - 1) * GP + d + 1];
-      uint32_t w0[8], w1[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int t = t0 + 2 * e;
-        const uint32_t a = *reinterpret_cast<const uint32_t*>(&Ks[t * KP + d]);
-        const uint32_t c = *reinterpret_cast<const uint32_t*>(&Ks[(t + 1) * KP + d]);
-        const float2 ga = *reinterpret_cast<const float2*>(&Gc[t * GP + d]);
-        const float2 gb = *reinterpret_cast<const float2*>(&Gc[(t + 1) * GP + d]);
-        w0[e] = pk_bf16(lo_f(a) * __expf(gl0 - ga.x), lo_f(c) * __expf(gl0 - gb.x));
-        w1[e] = pk_bf16(hi_f(a) * __expf(gl1 - ga.y), hi_f(c) * __expf(gl1 - gb.y));
-      }
-      uint4* dst0 = reinterpret_cast<uint4*>(p.KcT + (size_t(cid) * K + d) * kL + t0);
-      uint4* dst1 = reinterpret_cast<uint4*>(p.KcT + (size_t(cid) * K + d + 1) * kL + t0);
-      dst0[0] = make_uint4(w0[0], w0[1], w0[2], w0[3]);
-      dst0[1] = make_uint4(w0[4], w0[5], w0[6], w0[7]);
-      dst1[0] = make_uint4(w1[0], w1[1], w1[2], w1[3]);
-      dst1[1] = make_uint4(w1[4], w1[5], w1[6], w1[7]);
-    }
-    for (int d = tid; d < K; d += kThreads) p.egl[size_t(cid) * K + d] = __expf(Gc[(kL - 1) * GP + d]);
-    for (int idx = tid; idx < kL * kL; idx += kThreads) {
-      const int i = idx / kL, j = idx % kL;
-      if (j / 16 > i / 16) Tm[i][j] = 0.f;
-    }
+  // Zero T above the block diagonal (the merges never write there).
+  for (int idx = tid; idx < kL * kL; idx += kThreads) {
+    const int i = idx / kL, j = idx % kL;
+    if (j / 16 > i / 16) Tm[i][j] = 0.f;
   }
   __syncthreads();
   merge_T(A, Tm, Xs, wave, lane);
@@ -609,13 +627,10 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p) {
     }
     uint4* tdst = reinterpret_cast<uint4*>(p.T + off);
     uint4* ldst = reinterpret_cast<uint4*>(p.Tlo + off);
-    uint4* adst = reinterpret_cast<uint4*>(p.attn + off);
     tdst[0] = make_uint4(tv[0], tv[1], tv[2], tv[3]);
     tdst[1] = make_uint4(tv[4], tv[5], tv[6], tv[7]);
     ldst[0] = make_uint4(tl[0], tl[1], tl[2], tl[3]);
     ldst[1] = make_uint4(tl[4], tl[5], tl[6], tl[7]);
-    adst[0] = *reinterpret_cast<const uint4*>(&At[row * (kL + 8) + c0]);
-    adst[1] = *reinterpret_cast<const uint4*>(&At[row * (kL + 8) + c0 + 8]);
   }
 }
 
