@@ -87,6 +87,15 @@ struct MfmaParams {
   float* states;   // [G][K][V] fp32 state entering each chunk (states mode of the scan)
 };
 
+// The backward's transposed tiles (the reverse scan contracts over a chunk's
+// tokens where the forward contracts over its rows).
+struct BwdTiles {
+  uint16_t *Tt, *Ttl, *AtT;  // [G][64][64]
+  uint16_t* Kc;              // [G][64][K]
+  uint16_t *QgT, *KgT;       // [G][K][64]
+  float* egl;                // [G][K] e^{G_last} per key channel
+};
+
 // ---------------------------------------------------------------------------
 // intra
 // ---------------------------------------------------------------------------
@@ -382,8 +391,11 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
 // MFMA fragment in registers. Besides T/attn/Kcᵀ the kernel writes what the scan
 // needs in place of K, Q and the scalar gates: kg = e⊙e^G⊙K (hi + lo),
 // qg = scale·e^G⊙Q and e^{G_last} per channel. One workgroup per chunk-head.
-template <int K>
-__global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p) {
+// BT (the backward's recompute): the kernel also writes the reverse scan's
+// transposed tiles (Tᵀ hi/lo, attnᵀ, Kc, Qgᵀ, Kgᵀ, e^{G_last}), the same
+// values the transposing pass of the per-head backward produces.
+template <int K, bool BT>
+__global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p, BwdTiles bt) {
   constexpr int GP = K + 4;  // fp32 row pitch of G
   constexpr int KS8 = K / 8;
   constexpr int NLD = kL * KS8 / kThreads;
@@ -529,6 +541,46 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p) {
       *reinterpret_cast<uint4*>(p.Kg + go) = make_uint4(gh[0], gh[1], gh[2], gh[3]);
       *reinterpret_cast<uint4*>(p.Kglo + go) = make_uint4(gl[0], gl[1], gl[2], gl[3]);
       *reinterpret_cast<uint4*>(p.Qg + go) = make_uint4(qq[0], qq[1], qq[2], qq[3]);
+      if constexpr (BT) {
+        // Qgᵀ and Kgᵀ: the four lanes holding rows i0…i0+3 of the same eight
+        // channels trade channel-pair words, so that lane q ends with channels
+        // d0i + 2q and d0i + 2q + 1 of all four rows and stores 8 bytes for
+        // each. Round s receives row (q + s) mod 4.
+        const int q = (lane / KS8) & 3, lbase = lane - q * KS8;
+        const int i0 = 16 * rb + (irow & ~3);
+        uint32_t rq[4], rk[4];
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+          const int sel = (q - s4) & 3;
+          const uint32_t sq = sel == 0 ? qq[0] : sel == 1 ? qq[1] : sel == 2 ? qq[2] : qq[3];
+          const uint32_t sk = sel == 0 ? gh[0] : sel == 1 ? gh[1] : sel == 2 ? gh[2] : gh[3];
+          const int src = lbase + KS8 * ((q + s4) & 3);
+          rq[s4] = uint32_t(__shfl(int(sq), src, 64));
+          rk[s4] = uint32_t(__shfl(int(sk), src, 64));
+        }
+        // Rotate so that index t holds row t (t = (q + s) mod 4).
+        auto rot = [&](uint32_t (&r)[4]) {
+          if (q & 1) {
+            const uint32_t t = r[3];
+            r[3] = r[2]; r[2] = r[1]; r[1] = r[0]; r[0] = t;
+          }
+          if (q & 2) {
+            uint32_t t = r[0]; r[0] = r[2]; r[2] = t;
+            t = r[1]; r[1] = r[3]; r[3] = t;
+          }
+        };
+        rot(rq);
+        rot(rk);
+        auto put = [&](uint16_t* dst, const uint32_t (&r)[4]) {
+          const size_t o = (size_t(cid) * K + d0i + 2 * q) * kL + i0;
+          *reinterpret_cast<uint2*>(dst + o) =
+              make_uint2((r[0] & 0xffffu) | (r[1] << 16), (r[2] & 0xffffu) | (r[3] << 16));
+          *reinterpret_cast<uint2*>(dst + o + kL) =
+              make_uint2((r[0] >> 16) | (r[1] & 0xffff0000u), (r[2] >> 16) | (r[3] & 0xffff0000u));
+        };
+        put(bt.QgT, rq);
+        put(bt.KgT, rk);
+      }
     }
     __syncthreads();
     // Scores of block row rb: wave w ≤ rb forms block (rb, w); a wave past
@@ -568,15 +620,24 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p) {
           acck = mfma16(a_h, b_l, acck);
           accq = mfma16(ld8(&RT[2][at]), b_h, accq);
         }
+        uint32_t av[4];
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int i = 16 * rb + 4 * q4 + rr;
           A[i][j] = (j < i) ? acck[rr] : 0.f;
-          adst[rr * kL] = uint16_t(pk_bf16((j <= i) ? accq[rr] : 0.f, 0.f));
+          av[rr] = pk_bf16((j <= i) ? accq[rr] : 0.f, 0.f);
+          adst[rr * kL] = uint16_t(av[rr]);
         }
+        if constexpr (BT)  // attnᵀ row j, columns 16·rb + 4·q4 … +3
+          *reinterpret_cast<uint2*>(bt.AtT + size_t(cid) * kL * kL + size_t(j) * kL + 16 * rb +
+                                    4 * q4) =
+              make_uint2(av[0] | (av[1] << 16), av[2] | (av[3] << 16));
       } else {
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) adst[rr * kL] = 0;
+        if constexpr (BT)
+          *reinterpret_cast<uint2*>(bt.AtT + size_t(cid) * kL * kL + size_t(j) * kL + 16 * rb +
+                                    4 * q4) = make_uint2(0u, 0u);
       }
     }
     if (rb < 3) __syncthreads();  // the next block rewrites RT
@@ -604,7 +665,30 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p) {
     dst1[0] = make_uint4(w1[0], w1[1], w1[2], w1[3]);
     dst1[1] = make_uint4(w1[4], w1[5], w1[6], w1[7]);
   }
-  for (int d = tid; d < K; d += kThreads) p.egl[size_t(cid) * K + d] = __expf(Gc[(kL - 1) * GP + d]);
+  for (int d = tid; d < K; d += kThreads) {
+    const float e = __expf(Gc[(kL - 1) * GP + d]);
+    p.egl[size_t(cid) * K + d] = e;
+    if constexpr (BT) bt.egl[size_t(cid) * K + d] = e;
+  }
+  if constexpr (BT) {
+    // Kc = e^{G_last−G}⊙K row-major (the same products as Kcᵀ).
+#pragma unroll
+    for (int m = 0; m < NLD; ++m) {
+      const int idx = tid + kThreads * m, t = idx / KS8, d0 = 8 * (idx % KS8);
+      float kf[8], gt[8], gl[8], c[8];
+      f8(*reinterpret_cast<const uint4*>(&Ks[sw(t, d0)]), kf);
+      *reinterpret_cast<float4*>(gt) = *reinterpret_cast<const float4*>(&Gc[t * GP + d0]);
+      *reinterpret_cast<float4*>(gt + 4) = *reinterpret_cast<const float4*>(&Gc[t * GP + d0 + 4]);
+      *reinterpret_cast<float4*>(gl) = *reinterpret_cast<const float4*>(&Gc[(kL - 1) * GP + d0]);
+      *reinterpret_cast<float4*>(gl + 4) =
+          *reinterpret_cast<const float4*>(&Gc[(kL - 1) * GP + d0 + 4]);
+#pragma unroll
+      for (int x = 0; x < 8; ++x) c[x] = kf[x] * __expf(gl[x] - gt[x]);
+      *reinterpret_cast<uint4*>(bt.Kc + (size_t(cid) * kL + t) * K + d0) =
+          make_uint4(pk_bf16(c[0], c[1]), pk_bf16(c[2], c[3]), pk_bf16(c[4], c[5]),
+                     pk_bf16(c[6], c[7]));
+    }
+  }
   __syncthreads();  // G is dead: T and the merge scratch take its space
 
   diag_inverse(A, Tm, wave, lane);
@@ -631,6 +715,21 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p) {
     tdst[1] = make_uint4(tv[4], tv[5], tv[6], tv[7]);
     ldst[0] = make_uint4(tl[0], tl[1], tl[2], tl[3]);
     ldst[1] = make_uint4(tl[4], tl[5], tl[6], tl[7]);
+    if constexpr (BT) {
+      // Tᵀ row `row` = T's column `row`.
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const float x0 = Tm[c0 + 2 * c][row], x1 = Tm[c0 + 2 * c + 1][row];
+        tv[c] = pk_bf16(x0, x1);
+        tl[c] = pk_bf16(x0 - lo_f(tv[c]), x1 - hi_f(tv[c]));
+      }
+      uint4* ttd = reinterpret_cast<uint4*>(bt.Tt + off);
+      uint4* tld = reinterpret_cast<uint4*>(bt.Ttl + off);
+      ttd[0] = make_uint4(tv[0], tv[1], tv[2], tv[3]);
+      ttd[1] = make_uint4(tv[4], tv[5], tv[6], tv[7]);
+      tld[0] = make_uint4(tl[0], tl[1], tl[2], tl[3]);
+      tld[1] = make_uint4(tl[4], tl[5], tl[6], tl[7]);
+    }
   }
 }
 
@@ -1029,15 +1128,9 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
 // tiles: Tᵀ (hi, lo), attnᵀ, Kc = (Kcᵀ)ᵀ, and Qgᵀ = (scale·e^G⊙Q)ᵀ,
 // Kgᵀ = (e⊙e^G⊙K)ᵀ (combined_backward.rs:272-282: the state cotangent picks
 // up qrᵀ·dy and Wᵀ·dV' = kgᵀ·(Tᵀ·dV')). One workgroup per chunk-head; tiles
-// are transposed through LDS.
-struct BwdTiles {
-  uint16_t *Tt, *Ttl, *AtT;  // [G][64][64]
-  uint16_t* Kc;              // [G][64][K]
-  uint16_t *QgT, *KgT;       // [G][K][64]
-  float* egl;                // [G][K] e^{G_last} per key channel
-};
-
-template <int K, bool PC>
+// are transposed through LDS. Per-head gates only: with per-channel gates the
+// intra kernel writes these tiles itself (mfma_intra_pc_kernel<K, true>).
+template <int K>
 __global__ __launch_bounds__(kThreads) void mfma_bwd_tiles_kernel(MfmaParams p, BwdTiles bt) {
   constexpr int RP = (K > kL ? K : kL) + 2;  // LDS row pitch (elements) of the staged tile
   __shared__ __attribute__((aligned(16))) uint16_t buf[(K > kL ? K : kL) * RP];
@@ -1082,13 +1175,9 @@ __global__ __launch_bounds__(kThreads) void mfma_bwd_tiles_kernel(MfmaParams p, 
   transpose(p.Tlo + o64, bt.Ttl + o64, kL, kL);
   transpose(p.attn + o64, bt.AtT + o64, kL, kL);
   transpose(p.KcT + oK, bt.Kc + oK, K, kL);
-  if constexpr (PC) {
-    transpose(p.Qg + oK, bt.QgT + oK, kL, K);
-    transpose(p.Kg + oK, bt.KgT + oK, kL, K);
-    for (int d = tid; d < K; d += kThreads) bt.egl[size_t(cid) * K + d] = p.egl[size_t(cid) * K + d];
-  } else {
-    // Per-head gates: Qg = scale·e^G·q and Kg = e·e^G·k row by row (zero
-    // past the sequence end).
+  {
+    // Qg = scale·e^G·q and Kg = e·e^G·k row by row (zero past the sequence
+    // end).
     for (int which = 0; which < 2; ++which) {
       if (tid < kL) {
         const int t = tid;
@@ -1443,16 +1532,21 @@ BwdTiles carve_bwd_tiles(const Dims& d, void* ws) {
   return bt;
 }
 
-hipError_t launch_intra(const MfmaParams& p, const Dims& d, hipStream_t stream) {
+// bt (per-channel gates only): also write the backward's transposed tiles.
+hipError_t launch_intra(const MfmaParams& p, const Dims& d, hipStream_t stream,
+                        const BwdTiles* bt = nullptr) {
   const size_t G = size_t(d.B) * d.N * d.H;
   if (per_channel(d)) {
-    ProfScope ps("dn_mfma_intra_pc", stream);
-    if (d.K == 128)
-      hipLaunchKernelGGL(mfma_intra_pc_kernel<128>, dim3(unsigned(G)), dim3(kThreads), 0, stream,
-                         p);
-    else
-      hipLaunchKernelGGL(mfma_intra_pc_kernel<64>, dim3(unsigned(G)), dim3(kThreads), 0, stream,
-                         p);
+    ProfScope ps(bt ? "dn_mfma_intra_pc_bwd" : "dn_mfma_intra_pc", stream);
+#define DN_IPC(KD, BTV)                                                                     \
+  hipLaunchKernelGGL((mfma_intra_pc_kernel<KD, BTV>), dim3(unsigned(G)), dim3(kThreads), 0, \
+                     stream, p, bt ? *bt : BwdTiles{})
+    if (d.K == 128) {
+      if (bt) DN_IPC(128, true); else DN_IPC(128, false);
+    } else {
+      if (bt) DN_IPC(64, true); else DN_IPC(64, false);
+    }
+#undef DN_IPC
   } else {
     // Two resident workgroups per CU (LDS-bound) walk all chunk-heads.
     const int grid = int(std::min<size_t>(G, size_t(2) * device_cu_count()));
@@ -1569,22 +1663,20 @@ hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
   float* s_scratch = reinterpret_cast<float*>(reinterpret_cast<char*>(bt.egl) + region(G * K * 4));
   MfmaParams p = make_params(d, q, k, v, erase, write, g, state_in, nullptr, s_scratch, ws);
   p.states = states;
-  hipError_t e = launch_intra(p, d, stream);
+  const bool pc = per_channel(d);
+  // Per-channel gates: the intra kernel writes the transposed tiles itself.
+  hipError_t e = launch_intra(p, d, stream, pc ? &bt : nullptr);
   if (e != hipSuccess) return e;
   hipStream_t side = nullptr;
   if ((e = side_fork(stream, &side)) != hipSuccess) return e;
-  const bool pc = per_channel(d);
-  {
+  if (!pc) {
     ProfScope ps("dn_mfma_bwd_tiles", side);
-#define DN_TILES(KD, PCV)                                                                   \
-  hipLaunchKernelGGL((mfma_bwd_tiles_kernel<KD, PCV>), dim3(unsigned(G)), dim3(kThreads), 0, \
-                     side, p, bt)
-    if (d.K == 128) {
-      if (pc) DN_TILES(128, true); else DN_TILES(128, false);
-    } else {
-      if (pc) DN_TILES(64, true); else DN_TILES(64, false);
-    }
-#undef DN_TILES
+    if (d.K == 128)
+      hipLaunchKernelGGL(mfma_bwd_tiles_kernel<128>, dim3(unsigned(G)), dim3(kThreads), 0, side,
+                         p, bt);
+    else
+      hipLaunchKernelGGL(mfma_bwd_tiles_kernel<64>, dim3(unsigned(G)), dim3(kThreads), 0, side,
+                         p, bt);
   }
   if ((e = hipGetLastError()) != hipSuccess) return e;
   RevParams rp{d.B, d.S, d.H, d.V, d.N, dy, dstate_final, ds_after, dstate, bt};
