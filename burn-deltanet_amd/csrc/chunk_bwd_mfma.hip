@@ -99,24 +99,19 @@ __device__ inline float reduce4(const float (&v)[4], int lane) {
   return c + __shfl_xor(c, 8);
 }
 
-// 64 rows of C bf16 (global, row pitch C) → LDS tile, natural order.
-template <int C>
-__device__ inline void stage_rows(uint16_t* R, int dst, const uint16_t* src, int tid) {
-#pragma unroll
-  for (int idx = tid; idx < kL * C / 8; idx += kNT) {
-    const int row = idx / (C / 8), c8 = idx % (C / 8);
-    *reinterpret_cast<uint4*>(&R[dst + tile_at<C>(row, 8 * c8)]) =
-        *reinterpret_cast<const uint4*>(src + size_t(row) * C + 8 * c8);
-  }
+// A 64×64 bf16 tile (global, row-major) → LDS with the permuted column order:
+// thread tid loads 16-byte chunk tid (512 threads, one each), then stores it.
+__device__ inline uint4 load_perm(const uint16_t* src, int tid) {
+  return *reinterpret_cast<const uint4*>(src + (tid >> 3) * kL + 8 * (tid & 7));
 }
-
-// A 64×64 bf16 tile (global, row-major) → LDS with the permuted column order.
-__device__ inline void stage_perm(uint16_t* R, int dst, const uint16_t* src, int tid) {
-  const int row = tid >> 3, c8 = tid & 7;  // 512 threads: one 16-byte chunk each
-  const uint4 v = *reinterpret_cast<const uint4*>(src + row * kL + 8 * c8);
+__device__ inline void store_perm(uint16_t* R, int dst, const uint4& v, int tid) {
+  const int row = tid >> 3, c8 = tid & 7;
   *reinterpret_cast<uint2*>(&R[dst + tile_at<kL>(row, perm_pos(8 * c8))]) = make_uint2(v.x, v.y);
   *reinterpret_cast<uint2*>(&R[dst + tile_at<kL>(row, perm_pos(8 * c8 + 4))]) =
       make_uint2(v.z, v.w);
+}
+__device__ inline void stage_perm(uint16_t* R, int dst, const uint16_t* src, int tid) {
+  store_perm(R, dst, load_perm(src, tid), tid);
 }
 
 // The 16 lower-or-diagonal and upper 16×16 tiles of a 64×64 matrix, two per
@@ -161,6 +156,11 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   const int valid = min(kL, p.S - tok0);
   const size_t row0 = size_t(b) * p.S * p.H + h + size_t(tok0) * p.H;
   auto row_of = [&](int t) { return row0 + size_t(t) * p.H; };
+  // Global reads are unconditional: a row past the sequence end reads the
+  // chunk's last row (valid ≥ 1) and the value is then dropped. A load under
+  // a lane guard becomes a branch of its own with a full wait on every load
+  // in flight, which serialised the staging.
+  auto rowc = [&](int t) { return row_of(min(t, valid - 1)); };
   const size_t o64 = size_t(cid) * kL * kL, oLK = size_t(cid) * kL * K;
   const float* S0 = p.states + size_t(cid) * K * V;
   const float* dSa = p.ds_after + size_t(cid) * K * V;
@@ -170,7 +170,85 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   // Row of the value reduce16 leaves in this lane (index 4·ib + r).
   const int red_row = 16 * (r16 >> 2) + 4 * g4 + (r16 & 3);
 
-  // ---- phase A's global operands, in flight together with the staging -----
+  // ---- staging -----------------------------------------------------------
+  // The gate and tile loads are issued together and written to LDS (one
+  // round trip); phase A's operand loads follow, in flight across the
+  // cumulative sum and the barriers. Loads complete in order, so issuing the
+  // phase-A loads first would make every LDS write wait for them too.
+  float e0 = 0.f, w0 = 0.f, gct = 0.f, gl = 0.f;
+  if (tid < kL) {
+    // Index rowc(t) is in bounds at either gate width.
+    e0 = p.erase[rowc(tid)];
+    w0 = p.write[rowc(tid)];
+    if constexpr (!PC) {
+      if (gated) {
+        gct = p.gc[size_t(cid) * kL + tid];
+        gl = p.gc[size_t(cid) * kL + kL - 1];
+      }
+    }
+  }
+  constexpr int KPART = kNT / K, RUN = kL / KPART;  // per-channel cumulative sum
+  float vals[PC ? RUN : 1];
+  if constexpr (PC) {
+    const int d = tid % K, part = tid / K;
+#pragma unroll
+    for (int t = 0; t < RUN; ++t) {
+      const int tt = part * RUN + t;
+      const float x = p.g[rowc(tt) * K + d];
+      vals[t] = tt < valid ? x : 0.f;
+    }
+  }
+
+  constexpr int NKR = kL * K / 8 / kNT;  // 16-byte chunks per thread of a [64][K] tile
+  static_assert(NKR * kNT * 8 == kL * K, "K-wide staging assumes whole rounds");
+  uint4 tp[5], tk[PC ? 3 : 1][NKR];
+  tp[0] = load_perm(p.T + o64, tid);
+  tp[1] = load_perm(p.Tlo + o64, tid);
+  tp[2] = load_perm(p.Tt + o64, tid);
+  tp[3] = load_perm(p.Ttl + o64, tid);
+  tp[4] = load_perm(p.AtT + o64, tid);
+#pragma unroll
+  for (int m = 0; m < NKR; ++m) {
+    const int idx = tid + kNT * m, row = idx / (K / 8), c8 = idx % (K / 8);
+    if constexpr (PC) {
+      const size_t o = oLK + size_t(row) * K + 8 * c8;
+      tk[0][m] = *reinterpret_cast<const uint4*>(p.Kg + o);
+      tk[1][m] = *reinterpret_cast<const uint4*>(p.Kglo + o);
+      tk[2][m] = *reinterpret_cast<const uint4*>(p.Kc + o);
+    } else {
+      const uint4 x = *reinterpret_cast<const uint4*>(p.k + rowc(row) * K + 8 * c8);
+      tk[0][m] = row < valid ? x : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  if (tid < kL) {
+    const int t = tid;
+    const bool ok = t < valid;
+    er_s[t] = (ok && p.ew == 1) ? e0 : 0.f;
+    wr_s[t] = (ok && p.ww == 1) ? w0 : 0.f;
+    if constexpr (!PC) {
+      Gc[t] = gct;
+      eg_s[t] = gated ? __expf(gct) : 1.f;
+      ec_s[t] = gated ? __expf(gl - gct) : 1.f;
+    }
+    racc[0][t] = racc[1][t] = racc[2][t] = 0.f;
+  }
+  store_perm(R, oTh, tp[0], tid);
+  store_perm(R, oTl, tp[1], tid);
+  store_perm(R, oTth, tp[2], tid);
+  store_perm(R, oTtl, tp[3], tid);
+  store_perm(R, oAt, tp[4], tid);
+#pragma unroll
+  for (int m = 0; m < NKR; ++m) {
+    const int idx = tid + kNT * m, row = idx / (K / 8), c8 = idx % (K / 8);
+    const int at = tile_at<K>(row, 8 * c8);
+    *reinterpret_cast<uint4*>(&R[oKop + at]) = tk[0][m];
+    if constexpr (PC) {
+      *reinterpret_cast<uint4*>(&R[oKgl + at]) = tk[1][m];
+      *reinterpret_cast<uint4*>(&R[oKc + at]) = tk[2][m];
+    }
+  }
+
+  // ---- phase A's global operands -------------------------------------------
   const bool vwave = wave < V / 16;
   const int col = 16 * wave + r16;  // this lane's value column in phase A
   float pS[K / 32][8], pD[K / 32][8], vv[4][4], wv[4][4], dyv[2][8];
@@ -189,10 +267,24 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = rowi(ib, r);
-        const bool ok = i < valid;
-        vv[ib][r] = ok ? bf16_to_f32(p.v[row_of(i) * V + col]) : 0.f;
-        wv[ib][r] = (ok && p.ww != 1) ? p.write[row_of(i) * V + col] : 0.f;
+        const float x = bf16_to_f32(p.v[rowc(i) * V + col]);
+        vv[ib][r] = i < valid ? x : 0.f;
       }
+    if (p.ww != 1) {
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int i = rowi(ib, r);
+          const float x = p.write[rowc(i) * V + col];
+          wv[ib][r] = i < valid ? x : 0.f;
+        }
+    } else {
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wv[ib][r] = 0.f;
+    }
     // dY in the permuted token order of the attnᵀ fragments: token 4q+e /
     // 16+4q+e of each 32-token step at position 8q+e / 8q+4+e.
 #pragma unroll
@@ -200,36 +292,14 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int t = 32 * kk + (e < 4 ? 4 * g4 + e : 16 + 4 * g4 + e - 4);
-        dyv[kk][e] = t < valid ? ld(dy, row_of(t) * V + col) : 0.f;
+        const float x = ld(dy, rowc(t) * V + col);
+        dyv[kk][e] = t < valid ? x : 0.f;
       }
-  }
-
-  // ---- staging -----------------------------------------------------------
-  if (tid < kL) {
-    const int t = tid;
-    const bool ok = t < valid;
-    er_s[t] = (ok && p.ew == 1) ? p.erase[row_of(t)] : 0.f;
-    wr_s[t] = (ok && p.ww == 1) ? p.write[row_of(t)] : 0.f;
-    if constexpr (!PC) {
-      const float gct = gated ? p.gc[size_t(cid) * kL + t] : 0.f;
-      const float gl = gated ? p.gc[size_t(cid) * kL + kL - 1] : 0.f;
-      Gc[t] = gct;
-      eg_s[t] = gated ? __expf(gct) : 1.f;
-      ec_s[t] = gated ? __expf(gl - gct) : 1.f;
-    }
-    racc[0][t] = racc[1][t] = racc[2][t] = 0.f;
   }
   for (int c = tid; c < K; c += kNT) cacc[c] = 0.f;
   if constexpr (PC) {
     // G = in-chunk cumulative sum of g per channel (KPART lanes per channel).
-    constexpr int KPART = kNT / K, RUN = kL / KPART;
     const int d = tid % K, part = tid / K;
-    float vals[RUN];
-#pragma unroll
-    for (int t = 0; t < RUN; ++t) {
-      const int tt = part * RUN + t;
-      vals[t] = tt < valid ? p.g[row_of(tt) * K + d] : 0.f;
-    }
     float acc = 0.f;
 #pragma unroll
     for (int t = 0; t < RUN; ++t) {
@@ -243,23 +313,6 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
     __syncthreads();
 #pragma unroll
     for (int t = 0; t < RUN; ++t) Gc[(part * RUN + t) * GP + d] = vals[t] + carry;
-  }
-  stage_perm(R, oTh, p.T + o64, tid);
-  stage_perm(R, oTl, p.Tlo + o64, tid);
-  stage_perm(R, oTth, p.Tt + o64, tid);
-  stage_perm(R, oTtl, p.Ttl + o64, tid);
-  stage_perm(R, oAt, p.AtT + o64, tid);
-  if constexpr (PC) {
-    stage_rows<K>(R, oKop, p.Kg + oLK, tid);
-    stage_rows<K>(R, oKgl, p.Kglo + oLK, tid);
-    stage_rows<K>(R, oKc, p.Kc + oLK, tid);
-  } else {
-    for (int idx = tid; idx < kL * K / 8; idx += kNT) {
-      const int row = idx / (K / 8), c8 = idx % (K / 8);
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (row < valid) v = *reinterpret_cast<const uint4*>(p.k + row_of(row) * K + 8 * c8);
-      *reinterpret_cast<uint4*>(&R[oKop + tile_at<K>(row, 8 * c8)]) = v;
-    }
   }
   __syncthreads();
 
@@ -385,19 +438,15 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   for (int m = 0; m < NY; ++m) {
     const int idx = tid + kNT * m, i = idx / (V / 8), c8 = idx % (V / 8);
     if constexpr (F32DY) {
-      float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b2 = a;
-      if (i < valid) {
-        const float4* src = reinterpret_cast<const float4*>(dy + row_of(i) * V + 8 * c8);
-        a = src[0];
-        b2 = src[1];
-      }
+      const float4* src = reinterpret_cast<const float4*>(dy + rowc(i) * V + 8 * c8);
+      float4 a = src[0], b2 = src[1];
+      if (i >= valid) a = b2 = make_float4(0.f, 0.f, 0.f, 0.f);
       ydat[m][0] = a.x; ydat[m][1] = a.y; ydat[m][2] = a.z; ydat[m][3] = a.w;
       ydat[m][4] = b2.x; ydat[m][5] = b2.y; ydat[m][6] = b2.z; ydat[m][7] = b2.w;
     } else {
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if (i < valid)
-        v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(dy) +
-                                            row_of(i) * V + 8 * c8);
+      uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(dy) +
+                                                rowc(i) * V + 8 * c8);
+      if (i >= valid) v = make_uint4(0u, 0u, 0u, 0u);
       unpack8(v, ydat[m]);
     }
   }
@@ -520,14 +569,17 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   }
   __syncthreads();
   // Per-channel erase gate at the lane's rows, for phase D: loaded here so
-  // that phase B does not hold it, its latency covered by phase C.
+  // that phase B does not hold it, its latency covered by phase C. One load
+  // whose index depends on the gate width (a load inside a branch would be
+  // waited for where the branch joins).
   if (PC && kwave)
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = rowi(ib, r);
-        eA[ib][r] = p.ew == 1 ? er_s[i] : (i < valid ? p.erase[row_of(i) * K + c] : 0.f);
+        const float x = p.erase[p.ew == 1 ? rowc(i) : rowc(i) * K + c];
+        eA[ib][r] = i < valid ? x : 0.f;
       }
 
   // ---- X, dV' rows and the dAqk layouts into LDS --------------------------
@@ -689,11 +741,9 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   }
   for (int idx = tid; idx < kL * K / 8; idx += kNT) {
     const int i = idx / (K / 8), c8 = idx % (K / 8);
-    uint4 kv = make_uint4(0u, 0u, 0u, 0u), qv = kv;
-    if (i < valid) {
-      kv = *reinterpret_cast<const uint4*>(p.k + row_of(i) * K + 8 * c8);
-      qv = *reinterpret_cast<const uint4*>(p.q + row_of(i) * K + 8 * c8);
-    }
+    uint4 kv = *reinterpret_cast<const uint4*>(p.k + rowc(i) * K + 8 * c8);
+    uint4 qv = *reinterpret_cast<const uint4*>(p.q + rowc(i) * K + 8 * c8);
+    if (i >= valid) kv = qv = make_uint4(0u, 0u, 0u, 0u);
     const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, qw[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -805,8 +855,8 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) {
           const int i = i0 + t;
-          e8[t] = g4 >= 2 ? p.scale
-                          : (p.ew == 1 ? er_s[i] : (i < valid ? p.erase[row_of(i) * K + c] : 0.f));
+          const float x = p.erase[p.ew == 1 ? rowc(i) : rowc(i) * K + c];
+          e8[t] = g4 >= 2 ? p.scale : (i < valid ? x : 0.f);
         }
       };
       float ecur[8];
