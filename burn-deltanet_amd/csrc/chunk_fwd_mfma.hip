@@ -393,8 +393,9 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
 // qg = scale·e^G⊙Q and e^{G_last} per channel. One workgroup per chunk-head.
 // BT (the backward's recompute): the kernel also writes the reverse scan's
 // transposed tiles (Tᵀ hi/lo, attnᵀ, Kc, Qgᵀ, Kgᵀ, e^{G_last}), the same
-// values the transposing pass of the per-head backward produces.
-template <int K, bool BT>
+// values the transposing pass of the per-head backward produces. EW1: the
+// erase gate has width 1 (else K).
+template <int K, bool BT, bool EW1>
 __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p, BwdTiles bt) {
   constexpr int GP = K + 4;  // fp32 row pitch of G
   constexpr int KS8 = K / 8;
@@ -430,19 +431,24 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p, B
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tok0 = n * kL;
   const size_t row0 = size_t(b) * p.S * p.H + h + size_t(tok0) * p.H;
+  const int valid = min(kL, p.S - tok0);
   auto row_of = [&](int t) { return row0 + size_t(t) * p.H; };
+  // Global reads are unconditional: a row past the sequence end reads the
+  // chunk's last row and the value is dropped (a load under a lane guard
+  // becomes a branch with a full wait, which serialises the loads).
+  auto rowc = [&](int t) { return row_of(min(t, valid - 1)); };
   auto f8 = [](const uint4& u, float* f) {
     f[0] = lo_f(u.x); f[1] = hi_f(u.x); f[2] = lo_f(u.y); f[3] = hi_f(u.y);
     f[4] = lo_f(u.z); f[5] = hi_f(u.z); f[6] = lo_f(u.w); f[7] = hi_f(u.w);
   };
 
-  // K tile to LDS (zero past the sequence end).
+  // K tile to LDS (zero past the sequence end): all loads first, then the
+  // stores.
+  uint4 kx[NLD];
 #pragma unroll
   for (int m = 0; m < NLD; ++m) {
     const int idx = tid + kThreads * m, row = idx / KS8, c8 = idx % KS8;
-    uint4 kv = make_uint4(0u, 0u, 0u, 0u);
-    if (tok0 + row < p.S) kv = *reinterpret_cast<const uint4*>(p.k + row_of(row) * K + 8 * c8);
-    *reinterpret_cast<uint4*>(&Ks[sw(row, 8 * c8)]) = kv;
+    kx[m] = *reinterpret_cast<const uint4*>(p.k + rowc(row) * K + 8 * c8);
   }
   // This thread's item of each row block rb is row 16·rb + irow, channels
   // d0i…d0i+7: its Q segment and erase gate, in registers.
@@ -453,34 +459,44 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p, B
 #pragma unroll
   for (int rb = 0; rb < 4; ++rb) {
     const int i = 16 * rb + irow;
-    const bool ok = item && tok0 + i < p.S;
-    qr[rb] = ok ? *reinterpret_cast<const uint4*>(p.q + row_of(i) * K + d0i)
-                : make_uint4(0u, 0u, 0u, 0u);
-    if (p.ew == 1) {
-      const float e = ok ? p.erase[row_of(i)] : 0.f;
+    const bool ok = item && i < valid;
+    const uint4 qx = *reinterpret_cast<const uint4*>(p.q + rowc(i) * K + d0i);
+    qr[rb] = ok ? qx : make_uint4(0u, 0u, 0u, 0u);
+    if constexpr (EW1) {
+      const float e = p.erase[rowc(i)];
 #pragma unroll
-      for (int x = 0; x < 8; ++x) ef[rb][x] = e;
-    } else if (ok) {
-      *reinterpret_cast<float4*>(ef[rb]) =
-          *reinterpret_cast<const float4*>(p.erase + row_of(i) * K + d0i);
-      *reinterpret_cast<float4*>(ef[rb] + 4) =
-          *reinterpret_cast<const float4*>(p.erase + row_of(i) * K + d0i + 4);
+      for (int x = 0; x < 8; ++x) ef[rb][x] = ok ? e : 0.f;
     } else {
+      float e8[8];
+      *reinterpret_cast<float4*>(e8) = *reinterpret_cast<const float4*>(p.erase + rowc(i) * K + d0i);
+      *reinterpret_cast<float4*>(e8 + 4) =
+          *reinterpret_cast<const float4*>(p.erase + rowc(i) * K + d0i + 4);
 #pragma unroll
-      for (int x = 0; x < 8; ++x) ef[rb][x] = 0.f;
+      for (int x = 0; x < 8; ++x) ef[rb][x] = ok ? e8[x] : 0.f;
     }
   }
   // G = in-chunk cumulative sum of g per channel: KPART lanes per channel,
   // each summing a run of tokens, then the runs' totals are carried over.
+  // Its loads go out with the others, before the K tile's stores.
+  constexpr int KPART = kThreads / K, RUN = kL / KPART;
+  float vals[RUN];
   {
-    constexpr int KPART = kThreads / K, RUN = kL / KPART;
     const int d = tid % K, part = tid / K;
-    float vals[RUN];
 #pragma unroll
     for (int t = 0; t < RUN; ++t) {
       const int tt = part * RUN + t;
-      vals[t] = tok0 + tt < p.S ? p.g[row_of(tt) * K + d] : 0.f;
+      const float x = p.g[rowc(tt) * K + d];
+      vals[t] = tt < valid ? x : 0.f;
     }
+  }
+#pragma unroll
+  for (int m = 0; m < NLD; ++m) {
+    const int idx = tid + kThreads * m, row = idx / KS8, c8 = idx % KS8;
+    *reinterpret_cast<uint4*>(&Ks[sw(row, 8 * c8)]) =
+        row < valid ? kx[m] : make_uint4(0u, 0u, 0u, 0u);
+  }
+  {
+    const int d = tid % K, part = tid / K;
     float acc = 0.f;
 #pragma unroll
     for (int t = 0; t < RUN; ++t) {
@@ -1262,14 +1278,19 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_rev_scan_kernel(RevParams p) 
   const size_t bh_row0 = size_t(b) * p.S * p.H + h;
   auto chunk_of = [&](int n) { return (size_t(b) * p.N + n) * p.H + h; };
 
+  // One test of dstate_final around all the loads (a test per element made
+  // each load a branch of its own, waited for before the next).
   f32x4 dS[RBK];
+  if (p.dstate_final) {
 #pragma unroll
-  for (int rb = 0; rb < RBK; ++rb)
+    for (int rb = 0; rb < RBK; ++rb)
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      dS[rb][r] = p.dstate_final
-                      ? p.dstate_final[(size_t(bh) * K + 16 * rb + 4 * q4 + r) * p.V + jl]
-                      : 0.f;
+      for (int r = 0; r < 4; ++r)
+        dS[rb][r] = p.dstate_final[(size_t(bh) * K + 16 * rb + 4 * q4 + r) * p.V + jl];
+  } else {
+#pragma unroll
+    for (int rb = 0; rb < RBK; ++rb) dS[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
 
   uint4 pf[NPF];
   float pch;
@@ -1538,14 +1559,20 @@ hipError_t launch_intra(const MfmaParams& p, const Dims& d, hipStream_t stream,
   const size_t G = size_t(d.B) * d.N * d.H;
   if (per_channel(d)) {
     ProfScope ps(bt ? "dn_mfma_intra_pc_bwd" : "dn_mfma_intra_pc", stream);
-#define DN_IPC(KD, BTV)                                                                     \
-  hipLaunchKernelGGL((mfma_intra_pc_kernel<KD, BTV>), dim3(unsigned(G)), dim3(kThreads), 0, \
+#define DN_IPC(KD, BTV, EW)                                                                     \
+  hipLaunchKernelGGL((mfma_intra_pc_kernel<KD, BTV, EW>), dim3(unsigned(G)), dim3(kThreads), 0, \
                      stream, p, bt ? *bt : BwdTiles{})
+#define DN_IPC_E(KD, BTV)                         \
+  do {                                            \
+    if (d.ew == 1) DN_IPC(KD, BTV, true);         \
+    else DN_IPC(KD, BTV, false);                  \
+  } while (0)
     if (d.K == 128) {
-      if (bt) DN_IPC(128, true); else DN_IPC(128, false);
+      if (bt) DN_IPC_E(128, true); else DN_IPC_E(128, false);
     } else {
-      if (bt) DN_IPC(64, true); else DN_IPC(64, false);
+      if (bt) DN_IPC_E(64, true); else DN_IPC_E(64, false);
     }
+#undef DN_IPC_E
 #undef DN_IPC
   } else {
     // Two resident workgroups per CU (LDS-bound) walk all chunk-heads.
