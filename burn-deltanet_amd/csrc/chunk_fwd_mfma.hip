@@ -1155,6 +1155,7 @@ __global__ __launch_bounds__(kThreads) void mfma_bwd_tiles_kernel(MfmaParams p, 
   const int h = cid % p.H, n = (cid / p.H) % p.N, b = cid / (p.H * p.N);
   const int tid = threadIdx.x;
   const int tok0 = n * kL;
+  const int valid = min(kL, p.S - tok0);  // rows of this chunk; reads clamp to them
   const size_t row0 = size_t(b) * p.S * p.H + h + size_t(tok0) * p.H;
 
   // dst[C][R] = src[R][C]ᵀ for a tile already in `buf` ([R][C], pitch RP).
@@ -1199,14 +1200,15 @@ __global__ __launch_bounds__(kThreads) void mfma_bwd_tiles_kernel(MfmaParams p, 
         const int t = tid;
         const bool ok = tok0 + t < p.S;
         const float eg = p.gated ? __expf(p.gc[size_t(cid) * kL + t]) : 1.f;
-        rowsc[t] = !ok ? 0.f : which == 0 ? p.scale * eg : p.erase[row0 + size_t(t) * p.H] * eg;
+        const float e = p.erase[row0 + size_t(min(t, valid - 1)) * p.H];
+        rowsc[t] = !ok ? 0.f : which == 0 ? p.scale * eg : e * eg;
       }
       __syncthreads();
       const uint16_t* src = which == 0 ? p.q : p.k;
       for (int idx = tid; idx < kL * K / 8; idx += kThreads) {
         const int r = idx / (K / 8), c8 = 8 * (idx % (K / 8));
-        uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (tok0 + r < p.S) v = *reinterpret_cast<const uint4*>(src + (row0 + size_t(r) * p.H) * K + c8);
+        uint4 v = *reinterpret_cast<const uint4*>(src + (row0 + size_t(min(r, valid - 1)) * p.H) * K + c8);
+        if (r >= valid) v = make_uint4(0u, 0u, 0u, 0u);
         const float sc = rowsc[r];
         uint32_t* d = reinterpret_cast<uint32_t*>(&buf[r * RP + c8]);
         d[0] = pk_bf16(lo_f(v.x) * sc, hi_f(v.x) * sc);
