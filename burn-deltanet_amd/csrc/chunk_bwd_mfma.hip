@@ -86,6 +86,14 @@ __device__ inline float reduce16(const float (&v)[16], int lane) {
 __device__ inline void pin(float& x) { asm volatile("" : "+v"(x)); }
 __device__ inline void pin(f32x4& x) { asm volatile("" : "+v"(x)); }
 
+// Lanes 32…63 take b, lanes 0…31 keep a: one DPP move with a row mask. A
+// per-lane select whose operand is a load let the compiler move the load into
+// a branch for the lanes that use it, with a wait of its own.
+__device__ inline float upper_half_take(float a, float b) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(a), __float_as_int(b), 0xE4, 0xC, 0xF, false));
+}
+
 // v[0..3] summed over the 16 lanes that share lane/16; lane l receives the
 // total of index l%4.
 __device__ inline float reduce4(const float (&v)[4], int lane) {
@@ -856,7 +864,7 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
         for (int t = 0; t < 8; ++t) {
           const int i = i0 + t;
           const float x = p.erase[p.ew == 1 ? rowc(i) : rowc(i) * K + c];
-          e8[t] = g4 >= 2 ? p.scale : (i < valid ? x : 0.f);
+          e8[t] = upper_half_take(i < valid ? x : 0.f, p.scale);  // g4 ≥ 2: the readout scale
         }
       };
       float ecur[8];
