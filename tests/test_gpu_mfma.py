@@ -145,6 +145,7 @@ PC_CASES = [
     (1, 200, 2, 128, 128, 128, 1, 0.02, 0.05),
     (1, 256, 2, 128, 128, 128, 128, 0.02, 1.0),
     (2, 130, 2, 64, 64, 64, 64, 0.05, 0.1),
+    (1, 100, 2, 64, 64, 1, 1, 0.02, 0.05),
 ]
 
 
@@ -194,6 +195,7 @@ BWD_CASES = [
     (1, 256, 2, 128, 128, (128, 128)),
     (1, 130, 2, 128, 64, (1, 64)),
     (2, 128, 2, 64, 64, (64, 1)),
+    (1, 100, 2, 64, 128, (1, 128)),
     # a repeated key in every chunk (the retrieval cancels), β ∈ (0, 2)
     (1, 256, 2, 128, 128, "head", {"const_keys": True}),
     (1, 256, 2, 128, 128, (128, 128), {"const_keys": True}),
