@@ -15,6 +15,10 @@ kernels at small sizes in the other GPU tests):
 - config 4 (DeltaProduct u = 2 fold) and config 5 (GDN-2 per-channel gates):
   the MFMA forward, and for config 5 the MFMA backward, agree with the
   generic fp32 kernels, which share no code with them.
+- the projection front-end at the config-2 shape: a sequence split in two,
+  with the conv window carried across (conv.rs:14-20), gives the same bits
+  as one call. The output norm at config 2's output shape agrees with its
+  formula restated in torch fp32 (norm.rs:106-144).
 
 Bars: bit-exact where the arithmetic is the same, 1e-4 relative between fp32
 paths and for the affine identity, and 2e-2 (the bf16-input bar) across the
@@ -201,3 +205,55 @@ def test_config5_mfma_forward_and_backward_agree_with_generic():
         err = rel_err(m, gn)
         print(f"  backward {name} rel err {err:.2e}", flush=True)
         assert err < TOL_BF16, name
+
+
+def test_frontend_split_with_carried_window_is_bit_exact():
+    announce("dn_frontend at the config-2 shape: two halves with the window carried vs one call")
+    abi = pkg.abi
+    B, T, H, K, V, KC = 8, 4096, 16, 128, 256, 4
+    gr = gen(8)
+    conv_dim = H * K * 2 + H * V
+    width = conv_dim + H
+    proj = torch.randn((B, T, width), generator=gr, device=DEV).to(torch.bfloat16)
+    weight = torch.randn((conv_dim, KC), generator=gr, device=DEV) * 0.5
+    win0 = torch.randn((B, conv_dim, KC), generator=gr, device=DEV).to(torch.bfloat16)
+
+    def run(p, win):
+        S = p.shape[1]
+        q = torch.empty((B, S, H, K), dtype=torch.bfloat16, device=DEV)
+        k, v = torch.empty_like(q), torch.empty((B, S, H, V), dtype=torch.bfloat16, device=DEV)
+        beta = torch.empty((B, S, H, 1), device=DEV)
+        wout = torch.empty_like(win)
+        abi.run_frontend(abi.frontend_args(
+            p, weight, None, win, wout, q, k, v, beta, beta, nheads=H, head_k_dim=K,
+            head_v_dim=V, n_householder=1, conv_activation=abi.DN_ACT_SILU,
+            qk_activation=abi.DN_ACT_SILU, qk_norm=abi.DN_QKNORM_L2,
+            write_gate=abi.DN_WRITE_SCALAR, allow_neg_eigval=False))
+        return (q, k, v, beta), wout
+
+    full, wfull = run(proj, win0)
+    half = T // 2
+    a, wa = run(proj[:, :half].contiguous(), win0)
+    b, wb = run(proj[:, half:].contiguous(), wa)
+    torch.cuda.synchronize()
+    for f, x, y in zip(full, a, b):
+        assert torch.equal(f, torch.cat([x, y], 1))
+    assert torch.equal(wfull, wb)
+
+
+def test_out_norm_agrees_with_its_formula_in_fp32():
+    announce("dn_out_norm at config 2's output shape vs torch fp32")
+    abi = pkg.abi
+    B, T, H, V = 8, 4096, 16, 256
+    gr = gen(9)
+    x = torch.randn((B, T, H, V), generator=gr, device=DEV).to(torch.bfloat16)
+    gate = torch.randn((B, T, H, V), generator=gr, device=DEV).to(torch.bfloat16)
+    w = 1.0 + 0.1 * torch.randn((V,), generator=gr, device=DEV)
+    out = torch.empty_like(x)
+    abi.run_out_norm(abi.out_norm_args(x, gate, w, out, 1e-5))
+    xf, gf = x.float(), gate.float()
+    want = xf * torch.rsqrt((xf * xf).mean(-1, keepdim=True) + 1e-5) * w * (gf * torch.sigmoid(gf))
+    torch.cuda.synchronize()
+    err = rel_err(out, want)
+    print(f"  rel err {err:.2e}", flush=True)
+    assert err < 1e-2  # bf16 output: a rounding of 2^-9 relative per element
