@@ -397,9 +397,24 @@ def bench_config5(torch, pkg, steps, warmup):
             "roofline_chunk_bwd": cb_roof, "kernels_fwd": fk, "kernels_bwd": bk}
 
 
+def _host_cpu():
+    """nproc and the CPU model name of this host."""
+    model = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "cpu": model}
+
+
 def cpu_baseline(torch):
     """The oracle on the whole config-2 workload (B=8, H=16, T=4096: 32768
-    tokens), fp32, all available host threads (OMP_NUM_THREADS)."""
+    tokens), fp32, on all available host threads (OMP_NUM_THREADS), repeated
+    until 10 s have passed; beside it, one thread on one sequence (B=1), and
+    the host's nproc and CPU model."""
     import numpy as np
     sys.path.insert(0, str(ROOT))
     from oracle import oracle as O
@@ -415,12 +430,27 @@ def cpu_baseline(torch):
     threads = O.max_threads()
     O.chunk_fwd(q[:, :64], k[:, :64], v[:, :64], beta[:, :64], beta[:, :64], g[:, :64], s0,
                 chunk_len=L, dtype=np.float32)
-    t0 = time.perf_counter()
-    O.chunk_fwd(q, k, v, beta, beta, g, s0, chunk_len=L, dtype=np.float32)
-    dt = time.perf_counter() - t0
+    reps, t0 = 0, time.perf_counter()
+    while reps == 0 or time.perf_counter() - t0 < 10.0:
+        O.chunk_fwd(q, k, v, beta, beta, g, s0, chunk_len=L, dtype=np.float32)
+        reps += 1
+    dt = (time.perf_counter() - t0) / reps
+    # One thread, one sequence of the same workload (B=1: 4096 tokens).
+    O.set_threads(1)
+    try:
+        t1 = time.perf_counter()
+        O.chunk_fwd(q[:1], k[:1], v[:1], beta[:1], beta[:1], g[:1], s0[:1], chunk_len=L,
+                    dtype=np.float32)
+        d1 = time.perf_counter() - t1
+    finally:
+        O.set_threads(threads)
     return dict(value=B * T / dt, unit="tokens/s", cores=threads, kind="port",
                 sample=f"full config 2 (B=8 H=16 T=4096 dk=128 dv=256, 32768 tokens), "
-                       f"fp32, {threads} OpenMP threads, {dt:.2f} s")
+                       f"fp32, {threads} OpenMP threads, {reps} runs of {dt:.2f} s",
+                single_thread={"value": round(T / d1, 1), "unit": "tokens/s", "cores": 1,
+                               "sample": f"one sequence of config 2 (B=1, 4096 tokens), "
+                                         f"fp32, 1 thread, {d1:.2f} s"},
+                host=_host_cpu())
 
 
 def traffic_from_profiles(kernel):
