@@ -77,21 +77,9 @@ def bench_chunk_fwd(torch, pkg, steps, warmup, algo):
     args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
     chosen = abi.lib().dn_chunk_fwd_algo(args)
     run = lambda: abi.run_chunk_fwd(args)
-    for _ in range(warmup):
-        run()
-    torch.cuda.synchronize()
-    abi.profile_enable(True)
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
-    start.record()
-    for _ in range(steps):
-        run()
-    stop.record()
-    torch.cuda.synchronize()
+    ms, prof = _timed_raw(torch, abi, run, steps, warmup)
     wall = time.perf_counter() - t0
-    prof = abi.profile_read()
-    abi.profile_enable(False)
-    ms = start.elapsed_time(stop) / steps
     tokens = B * T
     G = B * (T // L) * H
     # Algorithmic bytes per launch of each forward kernel: every tensor it
@@ -104,14 +92,19 @@ def bench_chunk_fwd(torch, pkg, steps, warmup, algo):
     tri = 3 * G * L * L * 2             # T (hi, lo) and attn, bf16
     gcb = G * L * 4                     # in-chunk cumulative gate, fp32
     kct = G * K * L * 2                 # (e^{G_last-G} k)^T, bf16
+    # The bytes each kernel moves by its own design (intermediates included),
+    # beside the path's algorithmic bytes.
     kernel_bytes = {
         "dn_mfma_intra": qk + gates + tri + gcb + kct,
         "dn_mfma_scan": qk + vb + yb + gates + tri + gcb + kct + 2 * st,
+        "dn_mfma_fused": qk + vb + yb + gates + 2 * st,
     }
     flops_unit = 6 * L * L * K + 4 * L * L * V + 6 * L * K * V + L ** 3 / 3
+    # The path's algorithmic bytes (every tensor crossing the C ABI once):
+    # 102,912 B per chunk-head at this shape, 843,055,104 B per launch.
     path_bytes = qk + vb + yb + gates + 2 * st
     return dict(ms=ms, wall_ms=wall * 1e3 / steps, tokens=tokens, prof=prof,
-                kernel_bytes=kernel_bytes, path_bytes=path_bytes,
+                kernel_bytes=kernel_bytes, path_bytes=path_bytes, chunk_heads=G,
                 path_flops=G * flops_unit, algo=chosen, ws_bytes=ws_bytes)
 
 
@@ -137,23 +130,14 @@ def bench_decode(torch, pkg, steps, warmup):
     import ctypes
     stream = abi.stream_handle()
     refs = [ctypes.byref(a) for a in argv]
-    def run(t):
-        rc = lib.dn_step(refs[t % n_tok], stream)
+    it = iter(range(1 << 62))
+
+    def run():
+        rc = lib.dn_step(refs[next(it) % n_tok], stream)
         if rc:
             abi.check(rc)
-    for t in range(warmup):
-        run(t)
-    torch.cuda.synchronize()
-    abi.profile_enable(True)
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for t in range(steps):
-        run(t)
-    stop.record()
-    torch.cuda.synchronize()
-    prof = abi.profile_read()
-    abi.profile_enable(False)
-    us = start.elapsed_time(stop) * 1e3 / steps
+    ms, prof = _timed_raw(torch, abi, run, steps, warmup)
+    us = ms * 1e3
     step_bytes = 2 * B * H * K * V * 4 + B * H * (2 * K + 2 * V + 2) * 4
     name = max(prof, key=lambda n: prof[n][0]) if prof else None
     k_us = prof[name][0] * 1e3 / prof[name][1] if name else us
@@ -267,23 +251,44 @@ def bench_out_norm(torch, pkg, steps, warmup):
             "kernels": kern}
 
 
-def _timed(torch, abi, fn, steps, warmup):
-    """Mean ms per call of fn() over `steps` calls after `warmup`, with the
-    library's per-kernel HIP-event profile of the timed calls."""
+MIN_STEPS, MIN_WARMUP = 20, 2  # timed calls and warm-ups of every line
+_EXACT = {"on": False}  # --profile-pass: run exactly the calls asked for, no profiler pass
+
+
+def _timed_raw(torch, abi, fn, steps, warmup):
+    """Mean ms per call of fn() over max(steps, 20) calls after max(warmup, 2),
+    timed with HIP events on torch's current stream (the stream the library
+    launches on) and nothing else recorded inside the timed region; then a
+    separate pass with the library's per-kernel HIP-event profiler on, which
+    gives {kernel: (total_ms, launches)}."""
+    if not _EXACT["on"]:
+        steps, warmup = max(steps, MIN_STEPS), max(warmup, MIN_WARMUP)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
-    abi.profile_enable(True)
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(steps):
         fn()
     stop.record()
     torch.cuda.synchronize()
+    ms = start.elapsed_time(stop) / steps
+    if _EXACT["on"]:
+        return ms, {}
+    abi.profile_enable(True)
+    for _ in range(min(steps, 10)):
+        fn()
+    torch.cuda.synchronize()
     prof = abi.profile_read()
     abi.profile_enable(False)
+    return ms, prof
+
+
+def _timed(torch, abi, fn, steps, warmup):
+    """_timed_raw with the profile as {kernel: {avg_us, launches}}."""
+    ms, prof = _timed_raw(torch, abi, fn, steps, warmup)
     kern = {n: {"avg_us": round(v[0] / v[1] * 1e3, 2), "launches": v[1]} for n, v in prof.items()}
-    return start.elapsed_time(stop) / steps, kern
+    return ms, kern
 
 
 def _hbm(nbytes, ms):
@@ -453,6 +458,18 @@ def cpu_baseline(torch):
                 host=_host_cpu())
 
 
+def mfma_from_profiles(kernel):
+    """MFMA work the matrix cores executed per launch, from the committed
+    rocprofv3 --pmc summary (MfmaFlopsBF16, MfmaFlopsF32, MfmaUtil), if any."""
+    path = ROOT / "profiles" / "mfma.json"
+    if not path.exists():
+        return None
+    try:
+        return json.loads(path.read_text()).get(kernel)
+    except (ValueError, OSError):
+        return None
+
+
 def traffic_from_profiles(kernel):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary, if any."""
     path = ROOT / "profiles" / "traffic.json"
@@ -476,8 +493,9 @@ def main():
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the config 4 and config 5 measurements")
-    ap.add_argument("--extra-steps", type=int, default=3,
-                    help="timed calls for configs 4 and 5 (after one warmup)")
+    ap.add_argument("--extra-steps", type=int, default=MIN_STEPS,
+                    help="timed calls for configs 4 and 5, the front-end and the output norm "
+                         f"(at least {MIN_STEPS}, after at least {MIN_WARMUP} warm-ups)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="short run for rocprofv3 --pmc: a 1 GiB copy (calibration), then 2 "
                          "forward, 2 decode, 2 DeltaProduct-decode, 2 front-end and 2 "
@@ -494,6 +512,7 @@ def main():
     pkg = load_package()
     algo = {"auto": 0, "generic": 1, "mfma": 2}[args.algo]
     if args.profile_pass:
+        _EXACT["on"] = True
         # Calibration: a plain device copy of exactly 1 GiB read + 1 GiB written.
         src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
@@ -516,15 +535,32 @@ def main():
     dom = max(prof, key=lambda n: prof[n][0]) if prof else None
     roof = None
     if dom:
-        avg_s = prof[dom][0] / prof[dom][1] / 1e3
-        nbytes = fw["kernel_bytes"].get(dom)
-        if nbytes:
-            ach = nbytes / avg_s / 1e9
-            roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1),
-                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                    "traffic": traffic_from_profiles(dom),
-                    "avg_launch_us": round(avg_s * 1e6, 2),
-                    "algorithmic_bytes": nbytes}
+        # The dominant kernel's launch duration: with one kernel per step the
+        # timed region's per-step time (HIP events on the launch stream,
+        # launch gaps included); otherwise that kernel's average from the
+        # separate profile pass (HIP events around each launch on its stream).
+        one_kernel = len(prof) == 1 and prof[dom][1] > 0
+        prof_s = prof[dom][0] / prof[dom][1] / 1e3
+        avg_s = fw["ms"] / 1e3 if one_kernel else prof_s
+        # Algorithmic bytes per launch: the path's (every tensor crossing the
+        # C ABI once), however many intermediates the kernel itself moves.
+        nbytes = fw["path_bytes"]
+        ach = nbytes / avg_s / 1e9
+        roof = {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1),
+                "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
+                "traffic": traffic_from_profiles(dom),
+                "avg_launch_us": round(avg_s * 1e6, 2),
+                "avg_launch_source": "timed region" if one_kernel else "profile pass",
+                "profile_pass_avg_us": round(prof_s * 1e6, 2),
+                "algorithmic_bytes": nbytes,
+                "algorithmic_bytes_per_chunk_head": nbytes // fw["chunk_heads"],
+                "design_bytes": fw["kernel_bytes"].get(dom)}
+        mf = mfma_from_profiles(dom)
+        if mf:
+            roof["mfma"] = mf | {
+                "executed_bf16_TFLOPs": round(mf["bf16_flop_per_launch"] / avg_s / 1e12, 1),
+                "executed_frac_of_bf16_peak": round(
+                    mf["bf16_flop_per_launch"] / avg_s / 1e12 / BF16_PEAK_TFLOPS, 4)}
     per_kernel = {n: {"avg_us": round(v[0] / v[1] * 1e3, 2), "launches": v[1]}
                   for n, v in prof.items()}
     print(f"[bench] forward {fw['ms']:.3f} ms/step, {tok_s:.3e} tokens/s, kernels "
@@ -551,19 +587,19 @@ def main():
     extra = {}
     if not args.no_extra:
         print("[bench] config 4 (DeltaProduct fold)", file=sys.stderr, flush=True)
-        extra["config4"] = bench_config4(torch, pkg, args.extra_steps, 1)
+        extra["config4"] = bench_config4(torch, pkg, args.extra_steps, MIN_WARMUP)
         print(f"[bench] config4 {extra['config4']}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
         print("[bench] config 5 (GDN-2 forward + backward)", file=sys.stderr, flush=True)
-        extra["config5"] = bench_config5(torch, pkg, args.extra_steps, 1)
+        extra["config5"] = bench_config5(torch, pkg, args.extra_steps, MIN_WARMUP)
         print(f"[bench] config5 {extra['config5']}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
         print("[bench] projection front-end (dn_frontend)", file=sys.stderr, flush=True)
-        extra["frontend"] = bench_frontend(torch, pkg, max(args.extra_steps, 10), 2)
+        extra["frontend"] = bench_frontend(torch, pkg, args.extra_steps, MIN_WARMUP)
         print(f"[bench] frontend {extra['frontend']}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
         print("[bench] output norm (dn_out_norm)", file=sys.stderr, flush=True)
-        extra["out_norm"] = bench_out_norm(torch, pkg, max(args.extra_steps, 10), 2)
+        extra["out_norm"] = bench_out_norm(torch, pkg, args.extra_steps, MIN_WARMUP)
         print(f"[bench] out_norm {extra['out_norm']}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
 

@@ -36,7 +36,13 @@ struct Pool {
 };
 Pool g_pool;
 
-hipError_t pool_get(size_t bytes, void** out) {
+// The pool is one buffer per device: calls that use it on two streams at once
+// share it (they race), and growing it frees the old buffer after a device
+// synchronisation, which a stream under HIP graph capture must not see (a
+// captured graph would keep the freed pointer). Growth is therefore refused
+// during capture (hipErrorStreamCaptureUnsupported); callers that capture or
+// run several streams pass their own workspace.
+hipError_t pool_get(size_t bytes, void** out, hipStream_t stream) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
@@ -46,6 +52,9 @@ hipError_t pool_get(size_t bytes, void** out) {
     g_pool.size.resize(size_t(dev) + 1, 0);
   }
   if (g_pool.size[size_t(dev)] < bytes) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if ((e = hipStreamIsCapturing(stream, &cap)) != hipSuccess) return e;
+    if (cap != hipStreamCaptureStatusNone) return hipErrorStreamCaptureUnsupported;
     // Callers on this device may still be using the old buffer on their
     // streams; drain the device before it is replaced.
     if (g_pool.ptr[size_t(dev)]) {
@@ -263,7 +272,7 @@ int dn_chunk_fwd(const dn_chunk_fwd_args* a, hipStream_t stream) {
       return fail(DN_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) +
                                         " bytes");
   } else if (need) {
-    hipError_t e = pool_get(need, &ws);
+    hipError_t e = pool_get(need, &ws, stream);
     if (e != hipSuccess) return hip_fail(e, "workspace allocation");
   }
   const size_t nq = size_t(d.B) * d.S * d.H, ns = size_t(d.B) * d.H * d.K * d.V;
@@ -319,7 +328,7 @@ int dn_chunk_bwd(const dn_chunk_bwd_args* a, hipStream_t stream) {
       return fail(DN_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) +
                                         " bytes");
   } else {
-    hipError_t e = pool_get(need, &ws);
+    hipError_t e = pool_get(need, &ws, stream);
     if (e != hipSuccess) return hip_fail(e, "workspace allocation");
   }
   const size_t nq = size_t(d.B) * d.S * d.H, ns = size_t(d.B) * d.H * d.K * d.V;

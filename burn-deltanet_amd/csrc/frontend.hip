@@ -340,13 +340,15 @@ struct GateParams {
   int fixed;           // 1: no raw columns, every output is `scale`
 };
 
-// One thread per gate value (rows·width < 2³² is checked on the host).
+// One thread per gate value (rows·width < 2³² is checked on the host). The
+// grid-stride index is 64-bit: with a 32-bit one, i + stride could wrap past
+// 2³² for n close to it and the loop would never end.
 template <class TI>
 __global__ __launch_bounds__(kFrontThreads) void frontend_gate_kernel(GateParams p) {
-  const uint32_t n = uint32_t(p.rows) * uint32_t(p.width);
-  for (uint32_t i = blockIdx.x * kFrontThreads + threadIdx.x; i < n;
-       i += gridDim.x * kFrontThreads) {
-    const uint32_t row = i / uint32_t(p.width), c = i - row * uint32_t(p.width);
+  const uint64_t n = uint64_t(p.rows) * uint64_t(p.width);
+  for (uint64_t i = uint64_t(blockIdx.x) * kFrontThreads + threadIdx.x; i < n;
+       i += uint64_t(gridDim.x) * kFrontThreads) {
+    const uint32_t row = uint32_t(i / uint32_t(p.width)), c = uint32_t(i - uint64_t(row) * p.width);
     const float g = p.fixed ? p.scale
                             : p.scale * sigmoidf_(ld(static_cast<const TI*>(p.proj),
                                                      size_t(row) * p.stride + p.c0 + c));

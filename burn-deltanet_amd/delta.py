@@ -126,12 +126,15 @@ class DeltaInput:
         batch, sequence, nheads, head_k_dim, head_v_dim = self.dims()
         scale = self.resolved_scale()
         if head_k_dim <= abi.RECURRENT_MAX_K:
-            c = lambda x: None if x is None else x.contiguous()
-            q, k, v = c(self.q_bshk), c(self.k_bshk), c(self.v_bshv)
-            e, w, g = c(self.erase_bshK), c(self.write_bshV), c(self.g_bshK)
-            state = self.state_bhkv.float().contiguous()
-            y = torch.empty((batch, sequence, nheads, head_v_dim), dtype=q.dtype,
-                            device=q.device)
+            # The same dtype and device rules as the chunk and step paths: one
+            # q/k/v dtype, every tensor on the GPU, gates and state as fp32.
+            dt = _qkv_dtype(self.q_bshk, self.k_bshk, self.v_bshv)
+            q, k, v = _dev(self.q_bshk), _dev(self.k_bshk), _dev(self.v_bshv)
+            e = _dev(self.erase_bshK, torch.float32)
+            w = _dev(self.write_bshV, torch.float32)
+            g = _dev(self.g_bshK, torch.float32)
+            state = _dev(self.state_bhkv, torch.float32)
+            y = torch.empty((batch, sequence, nheads, head_v_dim), dtype=dt, device=q.device)
             s_out = torch.empty_like(state)
             abi.run_recurrent(abi.recurrent_args(q, k, v, e, w, g, state, y, s_out, scale,
                                                  check_finite))
@@ -198,9 +201,23 @@ def delta_chunk_recalculated(q_bshk, k_bshk, v_bshv, erase_bshK, write_bshV, g_b
     V = v.shape[3]
     y = torch.empty((B, S, H, V), dtype=y_dtype or dt, device=q.device)
     s_out = torch.empty((B, H, K, V), dtype=torch.float32, device=q.device)
-    abi.run_chunk_fwd(abi.chunk_fwd_args(q, k, v, e, w, g, s, y, s_out, chunk_len, scale,
-                                         algo=algo, check_finite=check_finite))
+    args = abi.chunk_fwd_args(q, k, v, e, w, g, s, y, s_out, chunk_len, scale, algo=algo,
+                              check_finite=check_finite)
+    _own_workspace(args, abi.lib().dn_chunk_fwd_workspace_bytes(args), q.device)
+    abi.run_chunk_fwd(args)
     return y, s_out
+
+
+def _own_workspace(args, nbytes: int, device) -> None:
+    """Give the call a workspace from torch's caching allocator, so that the
+    library never allocates (or synchronises the device) inside the call and
+    concurrent calls on different streams never share scratch memory. The
+    tensor lives as long as torch's stream-ordered allocator keeps it for the
+    call's stream."""
+    if nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+        args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
+        args._workspace_tensor = ws  # keep it alive with the arguments
 
 
 def delta_step(q_bhk, k_bhk, v_bhv, erase_bhK, write_bhV, g_bhK, state_bhkv, scale,
@@ -255,8 +272,10 @@ def combined_backward(d_y_bshv, d_final_state_bhkv, q_bshk, k_bshk, v_bshv, eras
              torch.empty(w.shape, dtype=torch.float32, device=q.device),
              None if g is None else torch.empty(g.shape, dtype=torch.float32, device=q.device),
              torch.empty(s.shape, dtype=torch.float32, device=q.device))
-    abi.run_chunk_bwd(abi.chunk_bwd_args(dy, ds, q, k, v, e, w, g, s, grads, chunk_len, scale,
-                                         algo=algo, check_finite=check_finite))
+    args = abi.chunk_bwd_args(dy, ds, q, k, v, e, w, g, s, grads, chunk_len, scale, algo=algo,
+                              check_finite=check_finite)
+    _own_workspace(args, abi.lib().dn_chunk_bwd_workspace_bytes(args), q.device)
+    abi.run_chunk_bwd(args)
     return DeltaChunkGrads(*grads)
 
 

@@ -92,7 +92,7 @@ typedef struct {
   const float *state_in;
   void *y;
   float *state_out;
-  void *workspace;         /* NULL => library-managed workspace */
+  void *workspace;         /* NULL => library-managed workspace (see below) */
   size_t workspace_bytes;
 } dn_chunk_fwd_args;
 
@@ -265,7 +265,16 @@ int dn_out_norm(const dn_out_norm_args *args, hipStream_t stream);
 
 /* Bytes of device workspace dn_chunk_fwd / dn_chunk_bwd need for these
  * arguments (0 on invalid arguments). Has no counterpart in the reference,
- * whose tensors are allocated by Burn; it lets a caller own the memory. */
+ * whose tensors are allocated by Burn; it lets a caller own the memory.
+ *
+ * A caller that passes workspace = NULL gets the library-managed workspace:
+ * one grow-only buffer per device. It is meant for a single stream: calls on
+ * two streams of one device at once share it and race. Growing it allocates
+ * with hipMalloc and drains the device first (hipDeviceSynchronize), so the
+ * first call at a new largest size is not asynchronous; under HIP graph
+ * capture growth is refused (DN_ERR_HIP, hipErrorStreamCaptureUnsupported).
+ * Callers that capture graphs, use several streams, or must not allocate in
+ * the call pass their own workspace of at least these many bytes. */
 size_t dn_chunk_fwd_workspace_bytes(const dn_chunk_fwd_args *args);
 size_t dn_chunk_bwd_workspace_bytes(const dn_chunk_bwd_args *args);
 

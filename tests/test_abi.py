@@ -14,6 +14,13 @@ from conftest import ROOT, load_package
 pkg = load_package()
 abi = pkg.abi
 
+# The argument-check cases below pass a fake device address (0x1000) that a
+# correct check never lets through. They run only where no GPU is visible, so
+# that a regression in a check can never launch a kernel on that address.
+fake_pointers = pytest.mark.skipif(
+    torch.cuda.is_available(),
+    reason="fake-pointer argument checks run on CPU-only hosts (no kernel can launch there)")
+
 
 def header_symbols():
     text = (ROOT / "include" / "deltanet_core.h").read_text()
@@ -59,6 +66,7 @@ def fwd_args(**over):
     (dict(qkv_dtype=7), -7, "dtype"),
     (dict(q=None), -6, "NULL"),
 ])
+@fake_pointers
 def test_chunk_fwd_rejects_invalid_arguments(over, code, msg):
     lib = abi.lib()
     a = fwd_args(**over)
@@ -68,6 +76,7 @@ def test_chunk_fwd_rejects_invalid_arguments(over, code, msg):
     assert lib.dn_chunk_fwd_workspace_bytes(ctypes.byref(a)) == 0
 
 
+@fake_pointers
 def test_ungated_call_ignores_the_gate_width():
     """has_gate = 0 is the reference's placeholder gate (chunk_recalculated.rs:50-56):
     its width is never checked."""
@@ -75,6 +84,7 @@ def test_ungated_call_ignores_the_gate_width():
     assert abi.lib().dn_chunk_fwd(ctypes.byref(a), None) == -4
 
 
+@fake_pointers
 def test_step_rejects_invalid_arguments():
     lib = abi.lib()
     a = abi.StepArgs()
@@ -97,6 +107,7 @@ def test_step_rejects_invalid_arguments():
     (dict(head_k_dim=abi.RECURRENT_MAX_K + 1, erase_width=1, decay_width=1), -9,
      f"head_k_dim up to {abi.RECURRENT_MAX_K}"),
 ])
+@fake_pointers
 def test_recurrent_rejects_invalid_arguments(over, code, msg):
     """dn_recurrent takes dn_chunk_fwd's shape rules (no chunk_len) and
     refuses heads above its limit before touching any pointer."""
@@ -114,6 +125,7 @@ def test_recurrent_rejects_invalid_arguments(over, code, msg):
     assert msg in lib.dn_last_error().decode()
 
 
+@fake_pointers
 def test_bwd_rejects_missing_d_g():
     lib = abi.lib()
     a = abi.ChunkBwdArgs()
@@ -146,6 +158,21 @@ def test_host_mirror_sanity_mirrors_the_reference_asserts():
         pkg.DeltaInput(**{**good, "q_bshk": z(1, 0, 2, 4)}).sanity()
     with pytest.raises(pkg.DeltaError, match="chunk_len must be at least 1"):
         pkg.DeltaInput(**good).run(pkg.DeltaPath.with_chunk_len(0))
+
+
+def test_recurrent_path_applies_the_chunk_paths_dtype_and_device_rules():
+    """DeltaPath::Recurrent (path.rs:215-231) through DeltaInput.delta_recurrent
+    refuses what the chunk and step paths refuse, before any device work:
+    tensors off the GPU (no CPU fallback) and q/k/v of different dtypes."""
+    z = lambda *s, dt=torch.float32: torch.zeros(*s, dtype=dt)
+    good = dict(q_bshk=z(1, 3, 2, 4), k_bshk=z(1, 3, 2, 4), v_bshv=z(1, 3, 2, 6),
+                erase_bshK=z(1, 3, 2, 1), write_bshV=z(1, 3, 2, 1), g_bshK=z(1, 3, 2, 1),
+                state_bhkv=z(1, 2, 4, 6))
+    with pytest.raises(pkg.DeltaError, match="GPU"):
+        pkg.DeltaInput(**good).run(pkg.DeltaPath.recurrent())
+    mixed = {**good, "k_bshk": z(1, 3, 2, 4, dt=torch.bfloat16)}
+    with pytest.raises(pkg.DeltaError, match="one dtype"):
+        pkg.DeltaInput(**mixed).run(pkg.DeltaPath.recurrent())
 
 
 def test_delta_path_mirrors_the_reference():
@@ -186,6 +213,7 @@ def frontend_args(**over):
     (dict(q=None), -6, "NULL"),
     (dict(write_gate=abi.DN_WRITE_CHANNEL, proj_stride=100), -2, "separate buffers"),
 ])
+@fake_pointers
 def test_frontend_rejects_invalid_arguments(over, code, msg):
     """dn_frontend mirrors ShortConv's and QkvProjection's asserts
     (conv.rs:88-90, qkv.rs:397-401) and refuses what it does not offer."""
@@ -203,6 +231,7 @@ def test_frontend_rejects_invalid_arguments(over, code, msg):
     (dict(out_dtype=4), -7, "dtype"),
     (dict(weight=None), -6, "NULL"),
 ])
+@fake_pointers
 def test_out_norm_rejects_invalid_arguments(over, code, msg):
     lib = abi.lib()
     a = abi.OutNormArgs()

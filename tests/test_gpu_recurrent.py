@@ -140,3 +140,21 @@ def test_wide_heads_fall_back_to_the_step_loop(rng):
     torch.cuda.synchronize()
     y0, s0 = O.recurrent(q, k, v, e, w, g, s)
     assert rel_err(np_of(yr), y0) < 1e-4 and rel_err(np_of(sr), s0) < 1e-4
+
+
+def test_recurrent_path_reads_bf16_gates_as_their_fp32_values():
+    """DeltaPath::Recurrent with gates and state in bf16 (a Burn backend whose
+    float dtype is bf16 hands them over so) gives the result of the same
+    values upcast to fp32: the host mirror converts them before the call."""
+    announce("dn_recurrent through DeltaPath.recurrent(): bf16 gates and state")
+    rng = np.random.default_rng(31)
+    q, k, v, e, w, g, s = inputs(rng, 2, 9, 3, 16, 24, 16, 1, 16)
+    gq, gk, gv, ge, gw, gg, gs = on_gpu(q, k, v, e, w, g, s, torch.float32)
+    b = lambda t: t.to(torch.bfloat16)
+    y_b, s_b = pkg.DeltaInput(gq, gk, gv, b(ge), b(gw), b(gg), b(gs)).run(
+        pkg.DeltaPath.recurrent())
+    up = lambda t: b(t).float()
+    y_f, s_f = pkg.DeltaInput(gq, gk, gv, up(ge), up(gw), up(gg), up(gs)).run(
+        pkg.DeltaPath.recurrent())
+    torch.cuda.synchronize()
+    assert torch.equal(y_b, y_f) and torch.equal(s_b, s_f)
