@@ -45,7 +45,9 @@ EXPORTS = [
     "dn_chunk_fwd_workspace_bytes",
     "dn_chunk_bwd_workspace_bytes", "dn_chunk_fwd_algo", "dn_chunk_bwd_algo",
     "dn_last_error", "dn_version", "dn_profile_enable", "dn_profile_read",
+    "dn_chunk_fwd_noalloc",
 ]
+NOALLOC_SCRATCH_BYTES = 64 << 20  # DN_NOALLOC_SCRATCH_BYTES (deltanet_core.h)
 
 _i64, _i32, _f64, _vp, _sz = (ctypes.c_int64, ctypes.c_int32, ctypes.c_double,
                               ctypes.c_void_p, ctypes.c_size_t)
@@ -133,6 +135,8 @@ def lib() -> ctypes.CDLL:
         L = ctypes.CDLL(str(LIB_PATH))
         L.dn_chunk_fwd.argtypes = [ctypes.POINTER(ChunkFwdArgs), _vp]
         L.dn_chunk_fwd.restype = ctypes.c_int
+        L.dn_chunk_fwd_noalloc.argtypes = [ctypes.POINTER(ChunkFwdArgs), _vp]
+        L.dn_chunk_fwd_noalloc.restype = ctypes.c_int
         L.dn_chunk_bwd.argtypes = [ctypes.POINTER(ChunkBwdArgs), _vp]
         L.dn_chunk_bwd.restype = ctypes.c_int
         L.dn_step.argtypes = [ctypes.POINTER(StepArgs), _vp]
@@ -222,6 +226,12 @@ def chunk_fwd_args(q, k, v, erase, write, g, state, y, state_out, chunk_len, sca
 
 def run_chunk_fwd(args: ChunkFwdArgs) -> None:
     check(lib().dn_chunk_fwd(ctypes.byref(args), stream_handle()))
+
+
+def run_chunk_fwd_noalloc(args: ChunkFwdArgs) -> None:
+    """dn_chunk_fwd_noalloc: the forward on the library's fixed scratch array
+    (no allocation in the call; `workspace` is ignored)."""
+    check(lib().dn_chunk_fwd_noalloc(ctypes.byref(args), stream_handle()))
 
 
 def step_args(q, k, v, erase, write, g, state, y, state_out, scale, check_finite=False):

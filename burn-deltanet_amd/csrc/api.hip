@@ -72,6 +72,32 @@ hipError_t pool_get(size_t bytes, void** out, hipStream_t stream) {
   return hipSuccess;
 }
 
+// Scratch of dn_chunk_fwd_noalloc: a file-scope device array, so that entry
+// point allocates nothing. Each device that loads the library holds its own
+// copy (DN_NOALLOC_SCRATCH_BYTES) until the process ends. In host code
+// `scratch` only stands in for the symbol; its device address, per device,
+// comes from hipGetSymbolAddress (scratch_ptr) and is what kernels receive.
+__device__ __align__(256) unsigned char scratch[DN_NOALLOC_SCRATCH_BYTES];
+
+// The calling thread's current device's address of `scratch`, looked up once
+// per device (with that device current) and kept.
+hipError_t scratch_ptr(void** out) {
+  static std::mutex mu;
+  static std::vector<void*> ptrs;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  if (size_t(dev) >= ptrs.size()) ptrs.resize(size_t(dev) + 1, nullptr);
+  if (!ptrs[size_t(dev)]) {
+    void* p = nullptr;
+    if ((e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch))) != hipSuccess) return e;
+    ptrs[size_t(dev)] = p;
+  }
+  *out = ptrs[size_t(dev)];
+  return hipSuccess;
+}
+
 bool valid_dtype(int t) { return t == DN_F32 || t == DN_BF16; }
 
 // The reference's shape/gate checks (path.rs:177-208, recurrent.rs:51-54).
@@ -298,6 +324,41 @@ int dn_chunk_fwd(const dn_chunk_fwd_args* a, hipStream_t stream) {
     std::vector<Guarded> out = {{a->y, nq * d.V, a->y_dtype}, {a->state_out, ns, DN_F32}};
     if (int rc = nonfinite_check(out, stream, "outputs")) return rc;
   }
+  return DN_OK;
+}
+
+int dn_chunk_fwd_noalloc(const dn_chunk_fwd_args* a, hipStream_t stream) {
+  g_last_error.clear();
+  if (int rc = check_fwd(a)) return rc;
+  if (a->check_finite)
+    return fail(DN_ERR_UNSUPPORTED,
+                "dn_chunk_fwd_noalloc does not run the NaN/Inf guard (its flag is allocated and "
+                "read back); use dn_chunk_fwd for check_finite");
+  Dims d = make_dims(a->batch, a->sequence, a->nheads, a->head_k_dim, a->head_v_dim,
+                     a->erase_width, a->write_width, a->decay_width, a->has_gate, a->chunk_len,
+                     a->scale);
+  const int algo = fwd_algo(a, d);
+  if (algo < 0)
+    return fail(DN_ERR_UNSUPPORTED, "DN_ALGO_MFMA does not cover this shape/dtype");
+  const size_t need = algo == DN_ALGO_MFMA ? mfma_fwd_workspace(d) : generic_fwd_workspace(d);
+  if (need > size_t(DN_NOALLOC_SCRATCH_BYTES))
+    return fail(DN_ERR_WORKSPACE,
+                "dn_chunk_fwd_noalloc: these arguments need " + std::to_string(need) +
+                    " bytes of scratch, above its maximum of " +
+                    std::to_string(size_t(DN_NOALLOC_SCRATCH_BYTES)) +
+                    "; call dn_chunk_fwd with a workspace instead");
+  void* ws = nullptr;
+  hipError_t e = scratch_ptr(&ws);
+  if (e != hipSuccess) return hip_fail(e, "scratch address");
+  // Every byte of scratch a forward kernel reads was written earlier in the
+  // same call (no counters or partial sums), so nothing is cleared first.
+  if (algo == DN_ALGO_MFMA)
+    e = mfma_fwd(d, a->y_dtype, a->q, a->k, a->v, a->erase, a->write,
+                 a->has_gate ? a->g : nullptr, a->state_in, a->y, a->state_out, ws, stream);
+  else
+    e = generic_fwd(d, a->qkv_dtype, a->y_dtype, a->q, a->k, a->v, a->erase, a->write,
+                    a->has_gate ? a->g : nullptr, a->state_in, a->y, a->state_out, ws, stream);
+  if (e != hipSuccess) return hip_fail(e, "dn_chunk_fwd_noalloc launch");
   return DN_OK;
 }
 

@@ -278,6 +278,27 @@ int dn_out_norm(const dn_out_norm_args *args, hipStream_t stream);
 size_t dn_chunk_fwd_workspace_bytes(const dn_chunk_fwd_args *args);
 size_t dn_chunk_bwd_workspace_bytes(const dn_chunk_bwd_args *args);
 
+/* dn_chunk_fwd for callers that cannot allocate: code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc. No counterpart in the
+ * reference, whose Burn backend allocates every tensor. It takes the same
+ * arguments and gives the same results as dn_chunk_fwd, but ignores
+ * `workspace` and runs on a fixed scratch array of DN_NOALLOC_SCRATCH_BYTES
+ * that the library holds on each device it runs on until the process ends
+ * (the array is part of the loaded code object). It calls no hipMalloc,
+ * hipFree or other allocating routine. Limits:
+ *   - arguments whose dn_chunk_fwd_workspace_bytes() exceeds
+ *     DN_NOALLOC_SCRATCH_BYTES return DN_ERR_WORKSPACE (the MFMA path needs
+ *     40.25 KiB per (batch, head, chunk of 64 tokens) at head_k_dim 128, so
+ *     64 MiB covers 1628 of them, e.g. batch 1 x 16 heads x 6500 tokens);
+ *   - check_finite is refused (DN_ERR_UNSUPPORTED): the guard allocates its
+ *     flag and synchronises;
+ *   - every call on one device shares that device's array, so calls that
+ *     overlap on one device (two streams, or two host threads) race; the
+ *     array keeps the last call's contents, and no kernel reads any of it
+ *     before writing it. */
+#define DN_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int dn_chunk_fwd_noalloc(const dn_chunk_fwd_args *args, hipStream_t stream);
+
 /* Which algorithm AUTO would pick (DN_ALGO_GENERIC or DN_ALGO_MFMA). */
 int dn_chunk_fwd_algo(const dn_chunk_fwd_args *args);
 int dn_chunk_bwd_algo(const dn_chunk_bwd_args *args);
