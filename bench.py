@@ -41,6 +41,7 @@ ROOT = Path(__file__).resolve().parent
 METRIC = "chunk fwd tokens/s + decode step µs (GDN H16 dk128) at 1 GPU; % roofline"
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+ALGO_NAMES = {1: "generic", 2: "mfma (intra + scan kernels)", 3: "mfma (fused kernel)"}
 
 
 def load_package():
@@ -333,7 +334,7 @@ def bench_config4(torch, pkg, steps, warmup):
     nbytes = rows * (2 * K + 2 * V) * 2 + rows * 3 * 4 + 2 * B * H * K * V * 4
     return {"workload": "config 4: DeltaProduct u=2 (allow_neg_eigval), folded core forward",
             "batch": B, "seq_len": T, "core_seq_len": S, "nheads": H, "head_k_dim": K,
-            "head_v_dim": V, "algo": {1: "generic", 2: "mfma"}.get(algo, algo),
+            "head_v_dim": V, "algo": ALGO_NAMES.get(algo, algo),
             "ms_per_step": round(ms, 4), "tokens_per_s": round(B * T / (ms / 1e3), 1),
             "roofline": _hbm(nbytes, ms), "kernels": kern}
 
@@ -486,9 +487,10 @@ def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--warmup", type=int, default=100,
+                    help="untimed steps first (about 50 ms of work: the clocks ramp up)")
     ap.add_argument("--decode-steps", type=int, default=1000)
-    ap.add_argument("--algo", choices=["auto", "generic", "mfma"], default="auto")
+    ap.add_argument("--algo", choices=["auto", "generic", "mfma", "fused"], default="auto")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true")
     ap.add_argument("--no-extra", action="store_true",
@@ -510,7 +512,7 @@ def main():
 
     import torch
     pkg = load_package()
-    algo = {"auto": 0, "generic": 1, "mfma": 2}[args.algo]
+    algo = {"auto": 0, "generic": 1, "mfma": 2, "fused": 3}[args.algo]
     if args.profile_pass:
         _EXACT["on"] = True
         # Calibration: a plain device copy of exactly 1 GiB read + 1 GiB written.
@@ -518,7 +520,8 @@ def main():
         dst = torch.empty_like(src)
         dst.copy_(src)
         torch.cuda.synchronize()
-        bench_chunk_fwd(torch, pkg, 2, 0, algo)
+        bench_chunk_fwd(torch, pkg, 2, 0, 2)  # the two-kernel MFMA forward
+        bench_chunk_fwd(torch, pkg, 2, 0, 3)  # the fused MFMA forward
         bench_decode(torch, pkg, 2, 0)
         bench_product_decode(torch, pkg, 2, 0)
         bench_frontend(torch, pkg, 2, 0)
@@ -585,6 +588,23 @@ def main():
         print(f"[bench] DeltaProduct decode {pd}", file=sys.stderr, flush=True)
 
     extra = {}
+    other = {2: 3, 3: 2}.get(fw["algo"])
+    if not args.no_extra and other:
+        # The same workload through the other MFMA forward: the two-kernel
+        # path (tiles through HBM) or the fused kernel (tiles in LDS).
+        print(f"[bench] config 2 forward, {ALGO_NAMES[other]}", file=sys.stderr, flush=True)
+        ff = bench_chunk_fwd(torch, pkg, args.extra_steps, MIN_WARMUP, other)
+        ff_gbs = ff["path_bytes"] / (ff["ms"] / 1e3) / 1e9
+        extra["other_mfma_forward"] = {
+            "algo": ALGO_NAMES[other],
+            "ms_per_step": round(ff["ms"], 4),
+            "tokens_per_s": round(ff["tokens"] / (ff["ms"] / 1e3), 1),
+            "kernels": {n: round(v[0] / v[1] * 1e3, 2) for n, v in ff["prof"].items()},
+            "path_frac_of_hbm": round(ff_gbs / HBM_PEAK_GBS, 4),
+            "traffic": {n: traffic_from_profiles(n) for n in ff["prof"]}}
+        print(f"[bench] other MFMA forward {extra['other_mfma_forward']}", file=sys.stderr,
+              flush=True)
+        torch.cuda.empty_cache()
     if not args.no_extra:
         print("[bench] config 4 (DeltaProduct fold)", file=sys.stderr, flush=True)
         extra["config4"] = bench_config4(torch, pkg, args.extra_steps, MIN_WARMUP)
@@ -626,7 +646,8 @@ def main():
         "config": {"workload": "config 2: Gated DeltaNet chunkwise prefill (core forward)",
                    "batch": 8, "seq_len": 4096, "nheads": 16, "head_k_dim": 128,
                    "head_v_dim": 256, "chunk_len": 64, "qkv": "bf16", "state": "fp32",
-                   "y": "bf16", "algo": {1: "generic", 2: "mfma"}.get(fw["algo"], fw["algo"])},
+                   "y": "bf16",
+                   "algo": ALGO_NAMES.get(fw["algo"], fw["algo"])},
         "roofline": roof,
         "path_roofline": {"bound": "hbm", "achieved": round(path_gbs, 1),
                           "peak": HBM_PEAK_GBS, "unit": "GB/s",

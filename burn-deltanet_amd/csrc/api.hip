@@ -215,11 +215,24 @@ int check_bwd(const dn_chunk_bwd_args* a) {
   return DN_OK;
 }
 
+bool mfma_requested(int algo) { return algo == DN_ALGO_MFMA || algo == DN_ALGO_MFMA_FUSED; }
+
+// The forward's kernels: DN_ALGO_GENERIC, DN_ALGO_MFMA (intra + scan) or,
+// on request only, DN_ALGO_MFMA_FUSED (one kernel; at BASELINE config 2 on
+// a warm MI355X 0.48 ms against the two kernels' 0.45 ms).
 int fwd_algo(const dn_chunk_fwd_args* a, const Dims& d) {
   if (a->algo == DN_ALGO_GENERIC) return DN_ALGO_GENERIC;
   const bool fits = mfma_fwd_supported(d, a->qkv_dtype, a->y_dtype);
+  if (a->algo == DN_ALGO_MFMA_FUSED)
+    return fits && fused_fwd_supported(d, a->qkv_dtype) ? DN_ALGO_MFMA_FUSED
+                                                         : DN_ERR_UNSUPPORTED;
   if (a->algo == DN_ALGO_MFMA) return fits ? DN_ALGO_MFMA : DN_ERR_UNSUPPORTED;
   return fits ? DN_ALGO_MFMA : DN_ALGO_GENERIC;
+}
+
+size_t fwd_workspace(const Dims& d, int algo) {
+  if (algo == DN_ALGO_GENERIC) return generic_fwd_workspace(d);
+  return mfma_fwd_workspace(d, algo == DN_ALGO_MFMA_FUSED);
 }
 
 Dims bwd_dims(const dn_chunk_bwd_args* a) {
@@ -234,7 +247,7 @@ Dims bwd_dims(const dn_chunk_bwd_args* a) {
 int bwd_algo(const dn_chunk_bwd_args* a, const Dims& d) {
   if (a->algo == DN_ALGO_GENERIC) return DN_ALGO_GENERIC;
   const bool fits = mfma_fwd_supported(d, a->qkv_dtype, DN_BF16);
-  if (a->algo == DN_ALGO_MFMA) return fits ? DN_ALGO_MFMA : DN_ERR_UNSUPPORTED;
+  if (mfma_requested(a->algo)) return fits ? DN_ALGO_MFMA : DN_ERR_UNSUPPORTED;
   return fits ? DN_ALGO_MFMA : DN_ALGO_GENERIC;
 }
 
@@ -277,9 +290,7 @@ size_t dn_chunk_fwd_workspace_bytes(const dn_chunk_fwd_args* a) {
                      a->erase_width, a->write_width, a->decay_width, a->has_gate, a->chunk_len,
                      a->scale);
   const int algo = fwd_algo(a, d);
-  if (algo == DN_ALGO_MFMA) return mfma_fwd_workspace(d);
-  if (algo == DN_ALGO_GENERIC) return generic_fwd_workspace(d);
-  return 0;
+  return algo < 0 ? 0 : fwd_workspace(d, algo);
 }
 
 int dn_chunk_fwd(const dn_chunk_fwd_args* a, hipStream_t stream) {
@@ -290,8 +301,8 @@ int dn_chunk_fwd(const dn_chunk_fwd_args* a, hipStream_t stream) {
                      a->scale);
   const int algo = fwd_algo(a, d);
   if (algo < 0)
-    return fail(DN_ERR_UNSUPPORTED, "DN_ALGO_MFMA does not cover this shape/dtype");
-  const size_t need = algo == DN_ALGO_MFMA ? mfma_fwd_workspace(d) : generic_fwd_workspace(d);
+    return fail(DN_ERR_UNSUPPORTED, "the requested MFMA path does not cover this shape/dtype");
+  const size_t need = fwd_workspace(d, algo);
   void* ws = a->workspace;
   if (ws) {
     if (a->workspace_bytes < need)
@@ -313,9 +324,10 @@ int dn_chunk_fwd(const dn_chunk_fwd_args* a, hipStream_t stream) {
     if (int rc = nonfinite_check(in, stream, "inputs")) return rc;
   }
   hipError_t e;
-  if (algo == DN_ALGO_MFMA)
+  if (algo != DN_ALGO_GENERIC)
     e = mfma_fwd(d, a->y_dtype, a->q, a->k, a->v, a->erase, a->write,
-                 a->has_gate ? a->g : nullptr, a->state_in, a->y, a->state_out, ws, stream);
+                 a->has_gate ? a->g : nullptr, a->state_in, a->y, a->state_out, ws, stream,
+                 algo == DN_ALGO_MFMA_FUSED);
   else
     e = generic_fwd(d, a->qkv_dtype, a->y_dtype, a->q, a->k, a->v, a->erase, a->write,
                     a->has_gate ? a->g : nullptr, a->state_in, a->y, a->state_out, ws, stream);
@@ -339,8 +351,8 @@ int dn_chunk_fwd_noalloc(const dn_chunk_fwd_args* a, hipStream_t stream) {
                      a->scale);
   const int algo = fwd_algo(a, d);
   if (algo < 0)
-    return fail(DN_ERR_UNSUPPORTED, "DN_ALGO_MFMA does not cover this shape/dtype");
-  const size_t need = algo == DN_ALGO_MFMA ? mfma_fwd_workspace(d) : generic_fwd_workspace(d);
+    return fail(DN_ERR_UNSUPPORTED, "the requested MFMA path does not cover this shape/dtype");
+  const size_t need = fwd_workspace(d, algo);
   if (need > size_t(DN_NOALLOC_SCRATCH_BYTES))
     return fail(DN_ERR_WORKSPACE,
                 "dn_chunk_fwd_noalloc: these arguments need " + std::to_string(need) +
@@ -352,9 +364,10 @@ int dn_chunk_fwd_noalloc(const dn_chunk_fwd_args* a, hipStream_t stream) {
   if (e != hipSuccess) return hip_fail(e, "scratch address");
   // Every byte of scratch a forward kernel reads was written earlier in the
   // same call (no counters or partial sums), so nothing is cleared first.
-  if (algo == DN_ALGO_MFMA)
+  if (algo != DN_ALGO_GENERIC)
     e = mfma_fwd(d, a->y_dtype, a->q, a->k, a->v, a->erase, a->write,
-                 a->has_gate ? a->g : nullptr, a->state_in, a->y, a->state_out, ws, stream);
+                 a->has_gate ? a->g : nullptr, a->state_in, a->y, a->state_out, ws, stream,
+                 algo == DN_ALGO_MFMA_FUSED);
   else
     e = generic_fwd(d, a->qkv_dtype, a->y_dtype, a->q, a->k, a->v, a->erase, a->write,
                     a->has_gate ? a->g : nullptr, a->state_in, a->y, a->state_out, ws, stream);

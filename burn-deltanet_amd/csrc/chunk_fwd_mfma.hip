@@ -37,6 +37,7 @@
 
 #include "dn_common.hpp"
 #include "mfma_util.hpp"
+#include "wy_inverse.hpp"
 
 namespace dn {
 namespace {
@@ -44,24 +45,6 @@ namespace {
 constexpr int kL = 64;        // chunk length
 constexpr int kThreads = 256;  // 4 waves
 constexpr int kBV = 64;       // head_v_dim granularity of the MFMA path
-
-// Value of lane `src` of each group of four lanes, to the whole group (DPP
-// quad_perm); `src` folds to a constant once the caller's loop is unrolled.
-template <int SRC>
-__device__ inline float quad_bcast_c(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v),
-                                                 SRC | (SRC << 2) | (SRC << 4) | (SRC << 6),
-                                                 0xf, 0xf, false));
-}
-__device__ inline float quad_bcast(float v, int src) {
-  switch (src) {
-    case 0: return quad_bcast_c<0>(v);
-    case 1: return quad_bcast_c<1>(v);
-    case 2: return quad_bcast_c<2>(v);
-    default: return quad_bcast_c<3>(v);
-  }
-}
-
 
 struct MfmaParams {
   int B, S, H, V, N;
@@ -99,90 +82,6 @@ struct BwdTiles {
 // ---------------------------------------------------------------------------
 // intra
 // ---------------------------------------------------------------------------
-// T's diagonal 16×16 block `wave` of T = (I + A)⁻¹ (A strict lower, fp32 in
-// LDS) by column elimination; one wave per block.
-__device__ inline void diag_inverse(const float (*A)[kL + 1], float (*Tm)[kL + 1], int wave,
-                                    int lane) {
-  // T's diagonal 16×16 block `wave` by column elimination: lane (c, g)
-  // holds rows g, g+4, g+8, g+12 of column c; step k₂ broadcasts x[k₂]
-  // inside the lane quad (DPP) and updates the rows below it.
-  const int base = 16 * wave, c = lane >> 2, g = lane & 3;
-  float x[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) x[j] = (4 * j + g == c) ? 1.f : 0.f;
-  // Multipliers A[i][k₂] for i > k₂ (zero otherwise), read up front.
-  float mul[15][4];
-#pragma unroll
-  for (int k2 = 0; k2 < 15; ++k2)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = 4 * j + g;
-      mul[k2][j] = (4 * j + 3 > k2 && i > k2) ? A[base + i][base + k2] : 0.f;
-    }
-#pragma unroll
-  for (int k2 = 0; k2 < 15; ++k2) {
-    const float xk = quad_bcast(x[k2 >> 2], k2 & 3);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (4 * j + 3 > k2) x[j] -= mul[k2][j] * xk;
-  }
-#pragma unroll
-  for (int j = 0; j < 4; ++j) Tm[base + 4 * j + g][base + c] = x[j];
-}
-
-// The two doubling merges that complete T from its diagonal blocks (all
-// four waves call it; it synchronises the workgroup).
-__device__ inline void merge_T(const float (*A)[kL + 1], float (*Tm)[kL + 1],
-                               float (*Xs)[kL / 2 + 1], int wave, int lane) {
-  // The merges run on fp32 MFMA (v_mfma_f32_16x16x4_f32: exact fp32
-  // products): lane l holds A[l%16][l/16] and B[l/16][l%16] of a
-  // 16×4 · 4×16 step, and D[4(l/16)+r][l%16]. Full-block sums are exact:
-  // the triangular factors hold zeros outside their triangles.
-  const int m16 = lane & 15, g4 = lane >> 4;
-  // 16 → 32: T₁₀ = −T₁₁ A₁₀ T₀₀ for the two 32-blocks (waves 0 and 1).
-  if (wave < 2) {
-    const int r0 = 32 * wave + 16, c0 = 32 * wave;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4)
-      acc = mfma_f32(A[r0 + m16][c0 + 4 * s4 + g4], Tm[c0 + 4 * s4 + g4][c0 + m16], acc);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) Xs[16 * wave + 4 * g4 + r][m16] = acc[r];
-  }
-  __syncthreads();
-  if (wave < 2) {
-    const int r0 = 32 * wave + 16, c0 = 32 * wave;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s4 = 0; s4 < 4; ++s4)
-      acc = mfma_f32(Tm[r0 + m16][r0 + 4 * s4 + g4], Xs[16 * wave + 4 * s4 + g4][m16], acc);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) Tm[r0 + 4 * g4 + r][c0 + m16] = -acc[r];
-  }
-  __syncthreads();
-  // 32 → 64: T[32:,:32] = −T[32:,32:] A[32:,:32] T[:32,:32]; wave w owns
-  // output tile (w/2, w%2) of the 32×32 block.
-  {
-    const int ti = wave >> 1, tj = wave & 1;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s4 = 0; s4 < 8; ++s4)
-      acc = mfma_f32(A[32 + 16 * ti + m16][4 * s4 + g4], Tm[4 * s4 + g4][16 * tj + m16], acc);
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < 4; ++r) Xs[16 * ti + 4 * g4 + r][16 * tj + m16] = acc[r];
-    __syncthreads();
-    acc = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s4 = 0; s4 < 8; ++s4)
-      acc = mfma_f32(Tm[32 + 16 * ti + m16][32 + 4 * s4 + g4], Xs[4 * s4 + g4][16 * tj + m16],
-                     acc);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) Tm[32 + 16 * ti + 4 * g4 + r][16 * tj + m16] = -acc[r];
-  }
-  __syncthreads();
-}
-
 template <int K, bool GATED>
 __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int G) {
   constexpr int KP = K + 8;                     // padded LDS row (bf16 elements)
@@ -353,7 +252,7 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
       }
     }
     __syncthreads();
-    merge_T(A, Tm, Xs, wave, lane);
+    merge_T(A, Tm, Xs, wave, lane, [] { __syncthreads(); });
 
     // T and attn of this chunk as bf16 rows, 16 values per lane.
     {
@@ -714,7 +613,7 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p, B
     if (j / 16 > i / 16) Tm[i][j] = 0.f;
   }
   __syncthreads();
-  merge_T(A, Tm, Xs, wave, lane);
+  merge_T(A, Tm, Xs, wave, lane, [] { __syncthreads(); });
   {
     const int row = tid / 4, c0 = 16 * (tid % 4);
     const size_t off = size_t(cid) * kL * kL + row * kL + c0;
@@ -1534,10 +1433,19 @@ MfmaParams make_params(const Dims& d, const void* q, const void* k, const void* 
   return p;
 }
 
-// The backward's transposed tiles, after the forward's workspace.
+// The two-kernel forward's tiles (make_params' layout).
+size_t tiles_workspace(const Dims& d) {
+  const size_t G = size_t(d.B) * d.N * d.H;
+  size_t bytes = 3 * region(G * kL * kL * 2) + region(G * kL * 4) +
+                 region(G * size_t(d.K) * kL * 2) + region(size_t(d.V) * 4);
+  if (per_channel(d)) bytes += 3 * region(G * kL * size_t(d.K) * 2) + region(G * size_t(d.K) * 4);
+  return bytes;
+}
+
+// The backward's transposed tiles, after the forward's tiles.
 BwdTiles carve_bwd_tiles(const Dims& d, void* ws) {
   const size_t G = size_t(d.B) * d.N * d.H, K = size_t(d.K);
-  char* base = static_cast<char*>(ws) + mfma_fwd_workspace(d);
+  char* base = static_cast<char*>(ws) + tiles_workspace(d);
   BwdTiles bt;
   bt.Tt = reinterpret_cast<uint16_t*>(base);
   base += region(G * kL * kL * 2);
@@ -1645,18 +1553,16 @@ bool mfma_fwd_supported(const Dims& d, int qkv_dtype, int y_dtype) {
   return d.ew == 1 && d.ww == 1 && d.dw <= 1;
 }
 
-size_t mfma_fwd_workspace(const Dims& d) {
-  const size_t G = size_t(d.B) * d.N * d.H;
-  size_t bytes = 3 * region(G * kL * kL * 2) + region(G * kL * 4) +
-                 region(G * size_t(d.K) * kL * 2) + region(size_t(d.V) * 4);
-  if (per_channel(d)) bytes += 3 * region(G * kL * size_t(d.K) * 2) + region(G * size_t(d.K) * 4);
-  return bytes;
+size_t mfma_fwd_workspace(const Dims& d, bool fused) {
+  return fused ? fused_fwd_workspace(d) : tiles_workspace(d);
 }
 
 hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, const void* v,
                     const float* erase, const float* write, const float* g,
                     const float* state_in, void* y, float* state_out, void* ws,
-                    hipStream_t stream) {
+                    hipStream_t stream, bool fused) {
+  if (fused)
+    return fused_fwd(d, y_dtype, q, k, v, erase, write, g, state_in, y, state_out, ws, stream);
   MfmaParams p = make_params(d, q, k, v, erase, write, g, state_in, y, state_out, ws);
   hipError_t e = launch_intra(p, d, stream);
   if (e != hipSuccess) return e;
@@ -1672,7 +1578,7 @@ MfmaTiles mfma_bwd_tiles(const Dims& d, void* ws) {
 
 size_t mfma_bwd_workspace(const Dims& d) {
   const size_t G = size_t(d.B) * d.N * d.H, K = size_t(d.K);
-  return mfma_fwd_workspace(d) + 3 * region(G * kL * kL * 2) + region(G * kL * K * 2) +
+  return tiles_workspace(d) + 3 * region(G * kL * kL * 2) + region(G * kL * K * 2) +
          2 * region(G * K * kL * 2) + region(G * K * 4) +
          region(size_t(d.B) * d.H * K * d.V * 4);  // the recompute's final state (unused)
 }

@@ -99,11 +99,22 @@ hipError_t generic_bwd(const Dims& d, int qkv_dtype, int grad_dtype, const void*
                        void* mfma_ws = nullptr);
 
 bool mfma_fwd_supported(const Dims& d, int qkv_dtype, int y_dtype);
-size_t mfma_fwd_workspace(const Dims& d);
+// The MFMA forward: the intra kernel and the scan as two launches with their
+// tiles in the workspace, or with `fused` (where fused_fwd_supported holds)
+// the one kernel of chunk_fwd_fused.hip.
+size_t mfma_fwd_workspace(const Dims& d, bool fused = false);
 hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, const void* v,
                     const float* erase, const float* write, const float* g,
                     const float* state_in, void* y, float* state_out, void* ws,
-                    hipStream_t stream);
+                    hipStream_t stream, bool fused = false);
+// The fused forward: per-head gates at head_k_dim 128, head_v_dim a multiple
+// of 128, bf16 q/k/v.
+bool fused_fwd_supported(const Dims& d, int qkv_dtype);
+size_t fused_fwd_workspace(const Dims& d);
+hipError_t fused_fwd(const Dims& d, int y_dtype, const void* q, const void* k, const void* v,
+                     const float* erase, const float* write, const float* g,
+                     const float* state_in, void* y, float* state_out, void* ws,
+                     hipStream_t stream);
 // The backward's two scans on MFMA (bf16 q/k/v, the shapes mfma_fwd_supported
 // accepts): the states entering each chunk and the state cotangents leaving
 // each chunk, fp32 [G][K][V], plus the initial state's cotangent.

@@ -54,11 +54,20 @@ typedef enum {
 } dn_dtype;
 
 /* Which kernels run dn_chunk_fwd / dn_chunk_bwd. AUTO picks the MFMA path
- * whenever the shape and dtypes allow it. */
+ * (DN_ALGO_MFMA) whenever the shape and dtypes allow it. */
 typedef enum {
   DN_ALGO_AUTO = 0,
   DN_ALGO_GENERIC = 1, /* fp32 arithmetic, any shape */
-  DN_ALGO_MFMA = 2,    /* bf16 MFMA tiles; DN_ERR_UNSUPPORTED if the shape does not fit */
+  DN_ALGO_MFMA = 2,    /* bf16 MFMA tiles; DN_ERR_UNSUPPORTED if the shape does not fit.
+                          The forward runs two kernels (intra-chunk tiles through the
+                          workspace, then the scan). */
+  DN_ALGO_MFMA_FUSED = 3, /* the MFMA forward as one kernel that builds each chunk's WY
+                             tiles in LDS beside the scan: q/k/v read once, no tile
+                             traffic, a 1 KB workspace instead of the two-kernel path's
+                             tiles (338 MB at BASELINE config 2), about 7% slower there.
+                             Per-head gates, head_k_dim 128, head_v_dim a multiple of 128,
+                             bf16 q/k/v; DN_ERR_UNSUPPORTED otherwise. Never chosen by AUTO;
+                             the backward treats it as DN_ALGO_MFMA. */
 } dn_algo;
 
 typedef enum {
@@ -299,7 +308,9 @@ size_t dn_chunk_bwd_workspace_bytes(const dn_chunk_bwd_args *args);
 #define DN_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
 int dn_chunk_fwd_noalloc(const dn_chunk_fwd_args *args, hipStream_t stream);
 
-/* Which algorithm AUTO would pick (DN_ALGO_GENERIC or DN_ALGO_MFMA). */
+/* The algorithm a call runs (DN_ALGO_GENERIC, DN_ALGO_MFMA or, for the
+ * forward, DN_ALGO_MFMA_FUSED), or DN_ERR_UNSUPPORTED for a requested MFMA
+ * path that does not cover the arguments. */
 int dn_chunk_fwd_algo(const dn_chunk_fwd_args *args);
 int dn_chunk_bwd_algo(const dn_chunk_bwd_args *args);
 

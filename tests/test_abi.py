@@ -126,6 +126,30 @@ def test_recurrent_rejects_invalid_arguments(over, code, msg):
 
 
 @fake_pointers
+def test_forward_algorithm_choice():
+    """AUTO runs the two-kernel MFMA forward; DN_ALGO_MFMA_FUSED, on request
+    only, the one-kernel forward, which needs only the sink row as workspace
+    and serves per-head gates at head_k_dim 128 and head_v_dim a multiple of
+    128."""
+    lib = abi.lib()
+    MFMA, FUSED = abi.DN_ALGO_MFMA, abi.DN_ALGO_MFMA_FUSED
+    base = dict(batch=8, sequence=4096, nheads=16, head_k_dim=128, head_v_dim=256,
+                qkv_dtype=abi.DN_BF16, y_dtype=abi.DN_BF16)
+    ws = {}
+    for algo, want in ((abi.DN_ALGO_AUTO, MFMA), (MFMA, MFMA), (FUSED, FUSED)):
+        a = fwd_args(**base, algo=algo)
+        assert lib.dn_chunk_fwd_algo(ctypes.byref(a)) == want
+        ws[algo] = lib.dn_chunk_fwd_workspace_bytes(ctypes.byref(a))
+    assert ws[FUSED] == 256 * 4  # one fp32-sized y row
+    assert ws[abi.DN_ALGO_AUTO] == ws[MFMA] > 100 * 2**20
+    for over in (dict(head_k_dim=64), dict(head_v_dim=192), dict(erase_width=128),
+                 dict(qkv_dtype=abi.DN_F32)):
+        a = fwd_args(**{**base, **over}, algo=FUSED)
+        assert lib.dn_chunk_fwd_algo(ctypes.byref(a)) == -9, over
+        assert lib.dn_chunk_fwd_workspace_bytes(ctypes.byref(a)) == 0
+
+
+@fake_pointers
 def test_bwd_rejects_missing_d_g():
     lib = abi.lib()
     a = abi.ChunkBwdArgs()
