@@ -68,6 +68,18 @@ struct MfmaParams {
   uint16_t* Qg;    // [G][64][K] bf16(scale·e^G⊙Q)
   float* egl;      // [G][K] e^{G_last} per key channel
   float* states;   // [G][K][V] fp32 state entering each chunk (states mode of the scan)
+  // Segmented scan: the sequence cut into seg_p segments of whole chunks,
+  // segment s of batch b scanned as batch b·seg_p + s of a seg_p times
+  // shorter sequence (the same token rows and chunk tiles). seg = 0: off;
+  // 1: each segment's transition M (the scan of K extra state columns that
+  // start at the identity and see no v) and offset H (the end state from
+  // S = 0); 2: outputs and states from the carried segment starts.
+  int seg, seg_p;
+  int vx;           // state columns the launch covers: V, or V + K when seg = 1
+  float* seg_m;     // [B·seg_p·H][K][K] M of each segment (seg = 1)
+  float* seg_h;     // [B·seg_p·H][K][V] H of each segment (seg = 1)
+  float* seg_start; // [B·seg_p·H][K][V] each segment's start state (the carry's output)
+  float* seg_final; // [B·H][K][V] the last segments' end states (seg = 2)
 };
 
 // The backward's transposed tiles (the reverse scan contracts over a chunk's
@@ -655,8 +667,9 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p, B
 // (mfma_util.hpp): S, X and V' accumulator tiles feed the MFMAs in place.
 
 // ST (states mode, for the backward's recompute): the fp32 state entering
-// each chunk is written to p.states and y is not written.
-template <int K, class TY, int WAVES, bool PC, bool ST = false>
+// each chunk is written to p.states and y is not written. SEG: the
+// segmented scan's mode (MfmaParams::seg), 0 for an unsegmented scan.
+template <int K, class TY, int WAVES, bool PC, bool ST = false, int SEG = 0>
 __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   constexpr int KK = K / 32;      // 32-deep k-steps over the key axis
   constexpr int RBK = K / 16;     // 16-row blocks of the state
@@ -678,7 +691,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   __shared__ float gxe[NBUF][kL], gwr[NBUF][kL], gys[NBUF][kL], gegl[NBUF];
   __shared__ float gch[PC ? K : 1];  // e^{G_last} per key channel (per-channel gates)
 
-  const int ntile = p.V / BW;
+  const int ntile = (SEG == 1 ? p.vx : p.V) / BW;
   const int BH = p.B * p.H;
   // XCD-aware: the `ntile` workgroups of one (b, h) get ids ≡ (mod 8).
   const int id = blockIdx.x;
@@ -690,10 +703,18 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   const int r16 = lane & 15, q4 = lane >> 4, k8 = 8 * q4;
   const int jw = tile * BW + 16 * wave;  // this wave's first value column
   const int jl = jw + r16;               // this lane's column (accumulator layout)
+  // A transition column (seg = 1): column jl − V of the identity, no v input.
+  const bool trans = SEG == 1 && jw >= p.V;
 
   // S[:, jw…jw+15] in accumulator layout: RBK row blocks of 16.
   f32x4 S[RBK];
-  {
+  if constexpr (SEG == 1) {
+#pragma unroll
+    for (int rb = 0; rb < RBK; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        S[rb][r] = trans && 16 * rb + 4 * q4 + r == jl - p.V ? 1.f : 0.f;
+  } else {
     const float* sin = p.s_in + size_t(bh) * K * p.V + jl;
 #pragma unroll
     for (int rb = 0; rb < RBK; ++rb)
@@ -820,11 +841,15 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   // t·HV + jl = vlane + (16·tb + r)·HV with a per-lane vlane.
   uint32_t vA[4][2];
   const int HV = p.H * p.V;
-  const uint32_t vlane = uint32_t(4 * q4 * HV + jl);
+  // A transition column reads column jl − V (< K ≤ V) and weighs it by zero:
+  // no branch around the loads, whose registers would be copied, and waited
+  // for, where the branches join.
+  const int jv = trans ? jl - p.V : jl;
+  const uint32_t vlane = uint32_t(4 * q4 * HV + jv);
   auto load_v = [&](int n) {
     const int rl = min(kL, p.S - n * kL);
     const uint16_t* vb = p.v + (bh_row0 + size_t(n) * kL * tokstride) * p.V;
-    const uint32_t vlast = uint32_t((rl - 1) * HV) + uint32_t(jl);
+    const uint32_t vlast = uint32_t((rl - 1) * HV) + uint32_t(jv);
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
@@ -846,7 +871,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
     if constexpr (PC) {
       const int rl = min(kL, p.S - n * kL);
       const float* wb = p.write + (bh_row0 + size_t(n) * kL * tokstride) * p.ww +
-                        (p.ww == 1 ? 0 : jl);
+                        (p.ww == 1 ? 0 : jv);
       const int hw = p.H * p.ww;
 #pragma unroll
       for (int tb = 0; tb < 4; ++tb)
@@ -929,7 +954,8 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
         const int t = 16 * tb + 4 * q4 + r;
         const float vv = (r & 1) ? hi_f(vA[tb][r >> 1]) : lo_f(vA[tb][r >> 1]);
         // Per-channel gates: e⊙e^G is inside kg, scale·e^G inside qg.
-        X[tb][r] = PC ? wA[tb][r] * vv - X[tb][r] : gwr[cur][t] * vv - gxe[cur][t] * X[tb][r];
+        const float wv = trans ? 0.f : (PC ? wA[tb][r] : gwr[cur][t]);
+        X[tb][r] = PC ? wv * vv - X[tb][r] : wv * vv - gxe[cur][t] * X[tb][r];
       }
       if constexpr (!PC) {
         const float ysc = gys[cur][16 * tb + r16];
@@ -1002,7 +1028,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
     }
     // y: lane (r16, q4) holds columns jw + 4q4 … +3 of token 16tb + r16;
     // rows past the sequence end go to the sink row.
-    if constexpr (!ST) {
+    if constexpr (!ST && SEG != 1) {
       TY* yb = static_cast<TY*>(p.y) + (bh_row0 + size_t(n) * kL * tokstride) * p.V;
       const int rl = p.S - n * kL;
 #pragma unroll
@@ -1029,10 +1055,112 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   }
 
   float* sout = p.s_out + size_t(bh) * K * p.V + jl;
+  int ld = p.V;
+  if constexpr (SEG == 1) {
+    sout = trans ? p.seg_m + size_t(bh) * K * K + (jl - p.V) : p.seg_h + size_t(bh) * K * p.V + jl;
+    ld = trans ? K : p.V;
+  } else if constexpr (SEG == 2) {
+    // only the last segment's end state leaves the call
+    if (b % p.seg_p != p.seg_p - 1) return;
+    sout = p.seg_final + (size_t(b / p.seg_p) * p.H + h) * K * p.V + jl;
+  }
 #pragma unroll
   for (int rb = 0; rb < RBK; ++rb)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sout[size_t(16 * rb + 4 * q4 + r) * p.V] = S[rb][r];
+    for (int r = 0; r < 4; ++r) sout[size_t(16 * rb + 4 * q4 + r) * ld] = S[rb][r];
+}
+
+// ---------------------------------------------------------------------------
+// Segmented scan: the carry between segments
+// ---------------------------------------------------------------------------
+// Over a segment the chunk update S ← A_n·S + B_n composes to S_end =
+// M·S_start + H (M = Π A_n, H the end state from S = 0), which the scan's
+// seg = 1 mode produces for every segment at once. Here one workgroup of
+// four waves per (b, h, 16 state columns) walks its segments in order:
+// start(0) = S_in, start(s+1) = M_s·start(s) + H_s, written to seg_start for
+// the seg = 2 scan. Wave w forms state rows 32w … 32w+31; the four waves
+// exchange the state through LDS once per step, and each holds its rows of
+// the next M and H in registers, loaded while the current step finishes.
+// The fp32 products run as bf16 MFMAs of hi + lo parts (Mh·Sh + Mh·Sl +
+// Ml·Sh, relative error about 2⁻¹⁶).
+template <int K>
+__global__ __launch_bounds__(256) void seg_carry_kernel(MfmaParams p) {
+  static_assert(K == 128, "four waves of 32 state rows");
+  constexpr int KK = K / 32;
+  __shared__ float Ss[K][17];  // the state's 16 columns
+  const int ncol = p.V / 16, P = p.seg_p;
+  const int bh = blockIdx.x / ncol, ct = blockIdx.x % ncol;
+  const int b = bh / p.H, h = bh % p.H;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, r16 = lane & 15, q4 = lane >> 4;
+  const int col = 16 * ct + r16, row0 = 32 * wave;
+  f32x4 S[2];  // rows row0 + 16j + 4q4 + r
+  {
+    const float* sin = p.s_in + size_t(bh) * K * p.V + col;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) S[j][r] = sin[size_t(row0 + 16 * j + 4 * q4 + r) * p.V];
+  }
+  // This wave's rows of M_s (channels 32kk + 4q4 + 0…3 and 32kk + 16 + 4q4 +
+  // 0…3, the B fragment's order) and of H_s.
+  float4 mA[2][KK][2];
+  f32x4 hA[2];
+  auto fetch = [&](int s) {
+    const size_t seg = size_t(b * P + s) * p.H + h;
+    const float* M = p.seg_m + seg * K * K;
+    const float* Hs = p.seg_h + seg * K * p.V + col;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const float* mr = M + size_t(row0 + 16 * j + r16) * K + 32 * kk + 4 * q4;
+        mA[j][kk][0] = *reinterpret_cast<const float4*>(mr);
+        mA[j][kk][1] = *reinterpret_cast<const float4*>(mr + 16);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) hA[j][r] = Hs[size_t(row0 + 16 * j + 4 * q4 + r) * p.V];
+    }
+  };
+  auto as8 = [](const uint4& x) { return __builtin_bit_cast(bf16x8, x); };
+  if (P > 1) fetch(0);
+  for (int s = 0; s < P; ++s) {
+    float* st = p.seg_start + (size_t(b * P + s) * p.H + h) * K * p.V + col;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        st[size_t(row0 + 16 * j + 4 * q4 + r) * p.V] = S[j][r];
+        Ss[row0 + 16 * j + 4 * q4 + r][r16] = S[j][r];
+      }
+    if (s + 1 == P) break;
+    __syncthreads();  // the whole state is in Ss
+    f32x4 acc[2] = {hA[0], hA[1]};
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      f32x4 s0, s1;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        s0[r] = Ss[32 * kk + 4 * q4 + r][r16];
+        s1[r] = Ss[32 * kk + 16 + 4 * q4 + r][r16];
+      }
+      const uint4 sh = frag_hi(s0, s1);
+      const uint4 sl = frag_lo(s0, s1, sh);
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float4 a0 = mA[j][kk][0], a1 = mA[j][kk][1];
+        const f32x4 m0 = {a0.x, a0.y, a0.z, a0.w}, m1 = {a1.x, a1.y, a1.z, a1.w};
+        const uint4 mh = frag_hi(m0, m1);
+        const uint4 ml = frag_lo(m0, m1, mh);
+        acc[j] = mfma16(as8(mh), as8(sh), acc[j]);
+        acc[j] = mfma16(as8(mh), as8(sl), acc[j]);
+        acc[j] = mfma16(as8(ml), as8(sh), acc[j]);
+      }
+    }
+    if (s + 2 < P) fetch(s + 1);
+    __syncthreads();  // every wave has read Ss
+    S[0] = acc[0];
+    S[1] = acc[1];
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1406,6 +1534,10 @@ MfmaParams make_params(const Dims& d, const void* q, const void* k, const void* 
   p.ew = int(d.ew);
   p.ww = int(d.ww);
   p.states = nullptr;
+  p.seg = 0;
+  p.seg_p = 1;
+  p.vx = d.V;
+  p.seg_m = p.seg_h = p.seg_start = p.seg_final = nullptr;
   char* base = static_cast<char*>(ws);
   p.T = reinterpret_cast<uint16_t*>(base);
   base += region(G * kL * kL * 2);
@@ -1513,9 +1645,80 @@ int scan_waves(const Dims& d) {
   return 2;
 }
 
+// Segments per sequence for the scans. A scan workgroup holds a CU's LDS,
+// and 8-wave workgroups do about twice the work per CU of the 2-wave ones
+// the unsegmented scan falls back to, while segmenting triples the scans'
+// work (the transitions cover K extra columns, then the outputs). So the
+// sequence is cut only when even 2-wave workgroups would leave half the
+// device idle, into enough segments to fill it with 8-wave workgroups, of
+// at least 16 whole chunks each (head_k_dim 128, head_v_dim a multiple of
+// 128, a sequence of whole chunks).
+int seg_parts(const Dims& d) {
+  if (d.K != 128 || d.V % 128 != 0 || size_t(d.S) != size_t(d.N) * d.L) return 1;
+  const size_t cus = size_t(device_cu_count());
+  if (size_t(d.B) * d.H * (d.V / 32) * 2 > cus) return 1;
+  const size_t wgs = size_t(d.B) * d.H * (d.V / 128);
+  int P = 1;
+  while (wgs * P * 2 <= cus && d.N % (P * 2) == 0 && d.N / (P * 2) >= 16) P *= 2;
+  return P;
+}
+
+// The segmented scan's buffers, after the tiles in the workspace.
+size_t seg_workspace(const Dims& d) {
+  const int P = seg_parts(d);
+  if (P == 1) return 0;
+  const size_t bh = size_t(d.B) * P * d.H, K = size_t(d.K);
+  return region(bh * K * K * 4) + 2 * region(bh * K * d.V * 4);
+}
+
+void carve_seg(MfmaParams& p, const Dims& d, void* seg_ws) {
+  const size_t bh = size_t(d.B) * seg_parts(d) * d.H, K = size_t(d.K);
+  char* base = static_cast<char*>(seg_ws);
+  p.seg_m = reinterpret_cast<float*>(base);
+  base += region(bh * K * K * 4);
+  p.seg_h = reinterpret_cast<float*>(base);
+  base += region(bh * K * d.V * 4);
+  p.seg_start = reinterpret_cast<float*>(base);
+}
+
+// The dims of the segmented scans: batch b·P + s runs segment s of batch b.
+Dims seg_dims(const Dims& d, int P) {
+  Dims s = d;
+  s.B = d.B * P;
+  s.S = d.S / P;
+  s.N = d.N / P;
+  return s;
+}
+
 template <bool ST>
 hipError_t launch_scan(const MfmaParams& p, const Dims& d, bool yb, hipStream_t stream) {
   const bool pc = per_channel(d);
+  if constexpr (!ST) {
+    if (p.seg) {
+      // The segmented scans: 8-wave workgroups, head_k_dim 128.
+      const unsigned blocks = unsigned(((d.B * d.H + 7) / 8) * 8 * (p.vx / 128));
+      ProfScope ps(p.seg == 1 ? (pc ? "dn_mfma_scan_pc_segs" : "dn_mfma_scan_segs")
+                              : (pc ? "dn_mfma_scan_pc" : "dn_mfma_scan"),
+                   stream);
+#define DN_SEG(TY, SG)                                                                           \
+  do {                                                                                           \
+    if (pc)                                                                                      \
+      hipLaunchKernelGGL((mfma_scan_kernel<128, TY, 8, true, false, SG>), dim3(blocks),          \
+                         dim3(512), 0, stream, p);                                               \
+    else                                                                                         \
+      hipLaunchKernelGGL((mfma_scan_kernel<128, TY, 8, false, false, SG>), dim3(blocks),         \
+                         dim3(512), 0, stream, p);                                               \
+  } while (0)
+      if (p.seg == 1)
+        DN_SEG(float, 1);  // no y
+      else if (yb)
+        DN_SEG(bf16, 2);
+      else
+        DN_SEG(float, 2);
+#undef DN_SEG
+      return hipGetLastError();
+    }
+  }
   const int waves = scan_waves(d);
   const unsigned blocks = unsigned(((d.B * d.H + 7) / 8) * 8 * (d.V / (16 * waves)));
   ProfScope ps(ST ? (pc ? "dn_mfma_scan_pc_states" : "dn_mfma_scan_states")
@@ -1554,7 +1757,7 @@ bool mfma_fwd_supported(const Dims& d, int qkv_dtype, int y_dtype) {
 }
 
 size_t mfma_fwd_workspace(const Dims& d, bool fused) {
-  return fused ? fused_fwd_workspace(d) : tiles_workspace(d);
+  return fused ? fused_fwd_workspace(d) : tiles_workspace(d) + seg_workspace(d);
 }
 
 hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, const void* v,
@@ -1566,7 +1769,35 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
   MfmaParams p = make_params(d, q, k, v, erase, write, g, state_in, y, state_out, ws);
   hipError_t e = launch_intra(p, d, stream);
   if (e != hipSuccess) return e;
-  return launch_scan<false>(p, d, y_dtype == DN_BF16, stream);
+  const int P = seg_parts(d);
+  if (P == 1) return launch_scan<false>(p, d, y_dtype == DN_BF16, stream);
+  // Segmented: the segments' transitions, the carry, then the outputs.
+  carve_seg(p, d, static_cast<char*>(ws) + tiles_workspace(d));
+  const Dims ds = seg_dims(d, P);
+  MfmaParams pa = p;
+  pa.B = ds.B;
+  pa.S = ds.S;
+  pa.N = ds.N;
+  pa.seg = 1;
+  pa.seg_p = P;
+  pa.vx = d.V + d.K;
+  pa.y = nullptr;
+  if ((e = launch_scan<false>(pa, ds, y_dtype == DN_BF16, stream)) != hipSuccess) return e;
+  {
+    ProfScope ps("dn_mfma_seg_carry", stream);
+    MfmaParams pb = p;
+    pb.seg_p = P;
+    hipLaunchKernelGGL(seg_carry_kernel<128>, dim3(unsigned(d.B * d.H * (d.V / 16))), dim3(256),
+                       0, stream, pb);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  MfmaParams pc = pa;
+  pc.seg = 2;
+  pc.vx = d.V;
+  pc.s_in = p.seg_start;
+  pc.y = y;
+  pc.seg_final = state_out;
+  return launch_scan<false>(pc, ds, y_dtype == DN_BF16, stream);
 }
 
 MfmaTiles mfma_bwd_tiles(const Dims& d, void* ws) {
