@@ -558,12 +558,20 @@ def main():
                 "algorithmic_bytes": nbytes,
                 "algorithmic_bytes_per_chunk_head": nbytes // fw["chunk_heads"],
                 "design_bytes": fw["kernel_bytes"].get(dom)}
-        mf = mfma_from_profiles(dom)
-        if mf:
-            roof["mfma"] = mf | {
-                "executed_bf16_TFLOPs": round(mf["bf16_flop_per_launch"] / avg_s / 1e12, 1),
-                "executed_frac_of_bf16_peak": round(
-                    mf["bf16_flop_per_launch"] / avg_s / 1e12 / BF16_PEAK_TFLOPS, 4)}
+        # What the matrix cores executed (rocprofv3 MfmaFlopsBF16/F32, bf16 hi/lo
+        # splits included) over each forward kernel's profile-pass duration.
+        mfma = {}
+        for name, (tot_ms, n) in prof.items():
+            mf = mfma_from_profiles(name)
+            if mf and n:
+                sec = tot_ms / n / 1e3
+                mfma[name] = mf | {
+                    "avg_launch_us": round(sec * 1e6, 2),
+                    "executed_bf16_TFLOPs": round(mf["bf16_flop_per_launch"] / sec / 1e12, 1),
+                    "executed_frac_of_bf16_peak": round(
+                        mf["bf16_flop_per_launch"] / sec / 1e12 / BF16_PEAK_TFLOPS, 4)}
+        if mfma:
+            roof["mfma"] = mfma
     per_kernel = {n: {"avg_us": round(v[0] / v[1] * 1e3, 2), "launches": v[1]}
                   for n, v in prof.items()}
     print(f"[bench] forward {fw['ms']:.3f} ms/step, {tok_s:.3e} tokens/s, kernels "
