@@ -403,6 +403,91 @@ def bench_config5(torch, pkg, steps, warmup):
             "roofline_chunk_bwd": cb_roof, "kernels_fwd": fk, "kernels_bwd": bk}
 
 
+def bench_config2_bwd(torch, pkg, steps, warmup):
+    """The custom backward (dn_chunk_bwd: combined_backward) at the config-2
+    shape: B=8, T=4096, H=16, dk=128, dv=256, per-head gates, bf16 q/k/v and
+    dO, fp32 state; the gradients of all seven inputs."""
+    B, T, H, K, V = 8, 4096, 16, 128, 256
+    dev = torch.device("cuda:0")
+    q, k, v, beta, g = gdn_inputs(torch, B, T, H, K, V, 0.05, 20260834, torch.bfloat16, dev)
+    s0 = torch.zeros((B, H, K, V), dtype=torch.float32, device=dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20260835)
+    dy = torch.randn((B, T, H, V), generator=gen, device=dev).to(torch.bfloat16)
+    grads = (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
+             torch.empty_like(beta), torch.empty_like(beta), torch.empty_like(g),
+             torch.empty_like(s0))
+    abi = pkg.abi
+    bargs = abi.chunk_bwd_args(dy, None, q, k, v, beta, beta, g, s0, grads, 64, None)
+    ws = torch.empty(max(abi.lib().dn_chunk_bwd_workspace_bytes(bargs), 1), dtype=torch.uint8,
+                     device=dev)
+    bargs.workspace, bargs.workspace_bytes = ws.data_ptr(), ws.numel()
+    algo = abi.lib().dn_chunk_bwd_algo(bargs)
+    ms, kern = _timed(torch, abi, lambda: abi.run_chunk_bwd(bargs), steps, warmup)
+    rows, st = B * T * H, B * H * K * V * 4
+    # reads q, k, v, dO (bf16), erase, write, g (fp32, width 1) and S0; writes
+    # dq, dk, dv (bf16), the three gate gradients (fp32) and dS0.
+    nbytes = rows * (2 * K + 2 * V) * 2 + rows * 3 * 4 + st + rows * (2 * K + V) * 2 + \
+        rows * 3 * 4 + st
+    return {"workload": "config-2 shape backward (dn_chunk_bwd), per-head gates, bf16",
+            "batch": B, "seq_len": T, "nheads": H, "head_k_dim": K, "head_v_dim": V,
+            "algo": ALGO_NAMES.get(algo, algo), "ms_per_call": round(ms, 4),
+            "tokens_per_s": round(B * T / (ms / 1e3), 1), "roofline": _hbm(nbytes, ms),
+            "kernels": kern}
+
+
+def bench_block_forward(torch, pkg, steps, warmup):
+    """A Gated DeltaNet block's forward after in_proj at the config-2 shape
+    (B=8, T=4096, H=16, dk=128, dv=256): dn_frontend (short conv of 4 with
+    SiLU, L2 q/k norm, scalar β), dn_chunk_fwd (with a synthetic decay of
+    config 2's distribution) and dn_out_norm (gated, bf16), as one step of
+    three calls, against the sum of the three timed one by one."""
+    B, S, H, K, V, KC = 8, 4096, 16, 128, 256, 4
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20260836)
+    conv_dim = H * K * 2 + H * V
+    width = conv_dim + H
+    proj = torch.randn((B, S, width), generator=gen, device=dev).to(torch.bfloat16)
+    weight = torch.randn((conv_dim, KC), generator=gen, device=dev) * 0.5
+    win = torch.zeros((B, conv_dim, KC), dtype=torch.bfloat16, device=dev)
+    wout = torch.empty_like(win)
+    q = torch.empty((B, S, H, K), dtype=torch.bfloat16, device=dev)
+    k, v = torch.empty_like(q), torch.empty((B, S, H, V), dtype=torch.bfloat16, device=dev)
+    beta = torch.empty((B, S, H, 1), device=dev)
+    g = -torch.nn.functional.softplus(torch.randn((B, S, H, 1), generator=gen, device=dev)) * 0.05
+    z = torch.randn((B, S, H, V), generator=gen, device=dev).to(torch.bfloat16)
+    gamma = torch.ones(V, device=dev)
+    s0 = torch.zeros((B, H, K, V), device=dev)
+    s1 = torch.empty_like(s0)
+    y = torch.empty((B, S, H, V), dtype=torch.bfloat16, device=dev)
+    out = torch.empty_like(y)
+    abi = pkg.abi
+    fe = abi.frontend_args(proj, weight, None, win, wout, q, k, v, beta, beta, nheads=H,
+                           head_k_dim=K, head_v_dim=V, n_householder=1,
+                           conv_activation=abi.DN_ACT_SILU, qk_activation=abi.DN_ACT_SILU,
+                           qk_norm=abi.DN_QKNORM_L2, write_gate=abi.DN_WRITE_SCALAR,
+                           allow_neg_eigval=False)
+    ca = abi.chunk_fwd_args(q, k, v, beta, beta, g, s0, y, s1, 64, None)
+    ws = torch.empty(max(abi.lib().dn_chunk_fwd_workspace_bytes(ca), 1), dtype=torch.uint8,
+                     device=dev)
+    ca.workspace, ca.workspace_bytes = ws.data_ptr(), ws.numel()
+    na = abi.out_norm_args(y, z, gamma, out, 1e-5)
+    calls = {"frontend": lambda: abi.run_frontend(fe), "core": lambda: abi.run_chunk_fwd(ca),
+             "out_norm": lambda: abi.run_out_norm(na)}
+
+    def block():
+        for f in calls.values():
+            f()
+    ms, kern = _timed(torch, abi, block, steps, warmup)
+    parts = {n: round(_timed(torch, abi, f, steps, warmup)[0], 4) for n, f in calls.items()}
+    return {"workload": "Gated DeltaNet block forward after in_proj at the config-2 shape: "
+                        "dn_frontend + dn_chunk_fwd + dn_out_norm, bf16",
+            "ms_per_step": round(ms, 4), "tokens_per_s": round(B * S / (ms / 1e3), 1),
+            "separate_ms": parts, "sum_of_separate_ms": round(sum(parts.values()), 4),
+            "kernels": kern}
+
+
 def _host_cpu():
     """nproc and the CPU model name of this host."""
     model = None
@@ -621,6 +706,15 @@ def main():
         print("[bench] config 5 (GDN-2 forward + backward)", file=sys.stderr, flush=True)
         extra["config5"] = bench_config5(torch, pkg, args.extra_steps, MIN_WARMUP)
         print(f"[bench] config5 {extra['config5']}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+        print("[bench] config-2 shape backward", file=sys.stderr, flush=True)
+        extra["config2_backward"] = bench_config2_bwd(torch, pkg, args.extra_steps, MIN_WARMUP)
+        print(f"[bench] config2_backward {extra['config2_backward']}", file=sys.stderr,
+              flush=True)
+        torch.cuda.empty_cache()
+        print("[bench] block forward (front-end + core + out norm)", file=sys.stderr, flush=True)
+        extra["block_forward"] = bench_block_forward(torch, pkg, args.extra_steps, MIN_WARMUP)
+        print(f"[bench] block_forward {extra['block_forward']}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
         print("[bench] projection front-end (dn_frontend)", file=sys.stderr, flush=True)
         extra["frontend"] = bench_frontend(torch, pkg, args.extra_steps, MIN_WARMUP)

@@ -261,7 +261,9 @@ size_t bwd_state_bytes(const Dims& d) {
 }
 
 size_t bwd_workspace(const Dims& d, int algo, int qkv_dtype) {
-  if (bwd_all_mfma(d, qkv_dtype, algo)) return 2 * bwd_state_bytes(d) + mfma_bwd_workspace(d);
+  if (bwd_all_mfma(d, qkv_dtype, algo))
+    return 2 * bwd_state_bytes(d) + align_up(mfma_bwd_workspace(d), 256) +
+           mfma_chunk_bwd_partials(d);
   return align_up(generic_bwd_workspace(d), 256) + (algo == DN_ALGO_MFMA ? mfma_bwd_workspace(d) : 0);
 }
 
@@ -428,9 +430,15 @@ int dn_chunk_bwd(const dn_chunk_bwd_args* a, hipStream_t stream) {
     e = mfma_bwd_scans(d, a->grad_dtype, a->d_y, a->d_state_final, a->q, a->k, a->v, a->erase,
                        a->write, g, a->state_in, states, ds_after, a->d_state, mws, stream);
     if (e == hipSuccess)
-      e = mfma_chunk_bwd(d, a->grad_dtype, a->d_y, a->q, a->k, a->v, a->erase, a->write, g,
-                         states, ds_after, a->d_q, a->d_k, a->d_v, a->d_erase, a->d_write,
-                         a->has_gate ? a->d_g : nullptr, mfma_bwd_tiles(d, mws), stream);
+      e = mfma_chunk_bwd(
+          d, a->grad_dtype, a->d_y, a->q, a->k, a->v, a->erase, a->write, g, states, ds_after,
+          a->d_q, a->d_k, a->d_v, a->d_erase, a->d_write, a->has_gate ? a->d_g : nullptr,
+          mfma_bwd_tiles(d, mws),
+          mfma_chunk_bwd_partials(d)
+              ? reinterpret_cast<float*>(static_cast<char*>(mws) +
+                                         align_up(mfma_bwd_workspace(d), 256))
+              : nullptr,
+          stream);
   } else {
     e = generic_bwd(d, a->qkv_dtype, a->grad_dtype, a->d_y, a->d_state_final, a->q, a->k, a->v,
                     a->erase, a->write, g, a->state_in, a->d_q, a->d_k, a->d_v, a->d_erase,

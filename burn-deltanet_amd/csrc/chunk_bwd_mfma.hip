@@ -52,7 +52,26 @@ struct CbParams {
   const float* ds_after;                     // [G][K][V]
   void *dq, *dk, *dv;
   float *derase, *dwrite, *dg;
+  // The value axis in passes of at most 128 columns: this pass covers
+  // columns voff … voff + V − 1 of rows vs wide (v, dO, the write gate, dv,
+  // S₀ and dS). pass 0: the only pass; 1: the first of several, whose
+  // value-summed outputs go to the fp32 partials; 2: a middle one, added to
+  // them; 3: the last, which adds them and stores.
+  int vs, voff, pass;
+  float *pq, *pk, *pe, *pg, *pw;  // partials of d_q, d_k, d_erase, d_g, width-1 d_write
 };
+
+// A value-summed output (d_q, d_k, d_erase, d_g, a width-1 d_write): a sum
+// over the value axis, so over the passes (CbParams::pass).
+template <class T>
+__device__ inline void st_sum(int pass, T* out, float* part, size_t i, float v) {
+  if (pass == 1)
+    part[i] = v;
+  else if (pass == 2)
+    part[i] += v;
+  else
+    st(out, i, pass == 3 ? v + part[i] : v);
+}
 
 __device__ inline uint16_t bf_bits(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
 
@@ -170,8 +189,9 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   // in flight, which serialised the staging.
   auto rowc = [&](int t) { return row_of(min(t, valid - 1)); };
   const size_t o64 = size_t(cid) * kL * kL, oLK = size_t(cid) * kL * K;
-  const float* S0 = p.states + size_t(cid) * K * V;
-  const float* dSa = p.ds_after + size_t(cid) * K * V;
+  const int VS = p.vs, vo = p.voff;  // row stride and first column of the value axis
+  const float* S0 = p.states + size_t(cid) * K * VS + vo;
+  const float* dSa = p.ds_after + size_t(cid) * K * VS + vo;
   const TG* dy = static_cast<const TG*>(p.dy);
   const bool gated = PC || p.gated;
   auto rowi = [&](int ib, int r) { return 16 * ib + 4 * g4 + r; };
@@ -267,15 +287,15 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
     for (int s = 0; s < K / 32; ++s)
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
-        pS[s][t] = S0[size_t(32 * s + k8 + t) * V + col];
-        pD[s][t] = dSa[size_t(32 * s + k8 + t) * V + col];
+        pS[s][t] = S0[size_t(32 * s + k8 + t) * VS + col];
+        pD[s][t] = dSa[size_t(32 * s + k8 + t) * VS + col];
       }
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = rowi(ib, r);
-        const float x = bf16_to_f32(p.v[rowc(i) * V + col]);
+        const float x = bf16_to_f32(p.v[rowc(i) * VS + vo + col]);
         vv[ib][r] = i < valid ? x : 0.f;
       }
     if (p.ww != 1) {
@@ -284,7 +304,7 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int i = rowi(ib, r);
-          const float x = p.write[rowc(i) * V + col];
+          const float x = p.write[rowc(i) * VS + vo + col];
           wv[ib][r] = i < valid ? x : 0.f;
         }
     } else {
@@ -300,7 +320,7 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int t = 32 * kk + (e < 4 ? 4 * g4 + e : 16 + 4 * g4 + e - 4);
-        const float x = ld(dy, rowc(t) * V + col);
+        const float x = ld(dy, rowc(t) * VS + vo + col);
         dyv[kk][e] = t < valid ? x : 0.f;
       }
   }
@@ -431,9 +451,9 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = rowi(ib, r);
-        if (i < valid) st(gv, row_of(i) * V + col, dW[ib][r] * wv[ib][r]);
+        if (i < valid) st(gv, row_of(i) * VS + vo + col, dW[ib][r] * wv[ib][r]);
         rs[4 * ib + r] = dW[ib][r] * vv[ib][r];
-        if (p.ww != 1 && i < valid) p.dwrite[row_of(i) * V + col] = rs[4 * ib + r];
+        if (p.ww != 1 && i < valid) p.dwrite[row_of(i) * VS + vo + col] = rs[4 * ib + r];
       }
     if (p.ww == 1) atomicAdd(&racc[0][red_row], reduce16(rs, lane));
   }
@@ -446,14 +466,14 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   for (int m = 0; m < NY; ++m) {
     const int idx = tid + kNT * m, i = idx / (V / 8), c8 = idx % (V / 8);
     if constexpr (F32DY) {
-      const float4* src = reinterpret_cast<const float4*>(dy + rowc(i) * V + 8 * c8);
+      const float4* src = reinterpret_cast<const float4*>(dy + rowc(i) * VS + vo + 8 * c8);
       float4 a = src[0], b2 = src[1];
       if (i >= valid) a = b2 = make_float4(0.f, 0.f, 0.f, 0.f);
       ydat[m][0] = a.x; ydat[m][1] = a.y; ydat[m][2] = a.z; ydat[m][3] = a.w;
       ydat[m][4] = b2.x; ydat[m][5] = b2.y; ydat[m][6] = b2.z; ydat[m][7] = b2.w;
     } else {
       uint4 v = *reinterpret_cast<const uint4*>(reinterpret_cast<const uint16_t*>(dy) +
-                                                rowc(i) * V + 8 * c8);
+                                                rowc(i) * VS + vo + 8 * c8);
       if (i >= valid) v = make_uint4(0u, 0u, 0u, 0u);
       unpack8(v, ydat[m]);
     }
@@ -464,8 +484,8 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   if (kwave) {
 #pragma unroll
     for (int s = 0; s < V / 32; ++s) {
-      const float4* s0r = reinterpret_cast<const float4*>(S0 + size_t(c) * V + 32 * s + k8);
-      const float4* dsr = reinterpret_cast<const float4*>(dSa + size_t(c) * V + 32 * s + k8);
+      const float4* s0r = reinterpret_cast<const float4*>(S0 + size_t(c) * VS + 32 * s + k8);
+      const float4* dsr = reinterpret_cast<const float4*>(dSa + size_t(c) * VS + 32 * s + k8);
       *reinterpret_cast<float4*>(bS[s]) = s0r[0];
       *reinterpret_cast<float4*>(bS[s] + 4) = s0r[1];
       *reinterpret_cast<float4*>(bD[s]) = dsr[0];
@@ -982,10 +1002,10 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
           for (int r = 0; r < 4; ++r) {
             const int i = rowi(pb, r);
             const bool ok = i < valid;
-            if (ok) st(gq, row_of(i) * K + c, dqA[pb][r] * p.scale);
+            if (ok) st_sum(p.pass, gq, p.pq, row_of(i) * K + c, dqA[pb][r] * p.scale);
             dkA[pb][r] += dkeA[pb][r] * eA[pb][r];
             rde[r] = dkeA[pb][r] * kv[r];
-            if (p.ew != 1 && ok) p.derase[row_of(i) * K + c] = rde[r];
+            if (p.ew != 1 && ok) st_sum(p.pass, p.derase, p.pe, row_of(i) * K + c, rde[r]);
           }
           if (p.ew == 1) {
             const float tot4 = reduce4(rde, lane);
@@ -1011,7 +1031,7 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int i = rowi(ib, r);
-          if (i < valid) st(gk, row_of(i) * K + c, dkA[ib][r]);
+          if (i < valid) st_sum(p.pass, gk, p.pk, row_of(i) * K + c, dkA[ib][r]);
         }
     } else {
       float rde[16];
@@ -1024,11 +1044,11 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
           const int i = rowi(ib, r);
           const bool ok = i < valid;
           if (ok) {
-            st(gq, row_of(i) * K + c, dqA[ib][r] * p.scale);
-            st(gk, row_of(i) * K + c, dkA[ib][r] + dkeA[ib][r] * er_s[i]);
+            st_sum(p.pass, gq, p.pq, row_of(i) * K + c, dqA[ib][r] * p.scale);
+            st_sum(p.pass, gk, p.pk, row_of(i) * K + c, dkA[ib][r] + dkeA[ib][r] * er_s[i]);
           }
           rde[4 * ib + r] = dkeA[ib][r] * kv[r];
-          if (p.ew != 1 && ok) p.derase[row_of(i) * K + c] = rde[4 * ib + r];
+          if (p.ew != 1 && ok) st_sum(p.pass, p.derase, p.pe, row_of(i) * K + c, rde[4 * ib + r]);
         }
       }
       if (p.ew == 1) atomicAdd(&racc[1][red_row], reduce16(rde, lane));
@@ -1060,7 +1080,8 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int i = rowi(ib, r);
-          if (i < valid) p.dg[row_of(i) * K + c] = dgA[ib][r] + after[ib] + carry;
+          if (i < valid)
+            st_sum(p.pass, p.dg, p.pg, row_of(i) * K + c, dgA[ib][r] + after[ib] + carry);
         }
         carry += blk[ib];
       }
@@ -1075,26 +1096,36 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
         const float t = __shfl_down(v, off);
         if (lane + off < 64) v += t;
       }
-      if (lane < valid) p.dg[row_of(lane)] = v;
+      if (lane < valid) st_sum(p.pass, p.dg, p.pg, row_of(lane), v);
     }
   }
   if (tid < valid) {
-    if (p.ww == 1) p.dwrite[row_of(tid)] = racc[0][tid];
-    if (p.ew == 1) p.derase[row_of(tid)] = racc[1][tid];
+    if (p.ww == 1) st_sum(p.pass, p.dwrite, p.pw, row_of(tid), racc[0][tid]);
+    if (p.ew == 1) st_sum(p.pass, p.derase, p.pe, row_of(tid), racc[1][tid]);
   }
 }
 
 }  // namespace
 
+// head_v_dim 64 or 128 in one pass; a multiple of 128 in passes of 128 columns.
 bool mfma_chunk_bwd_supported(const Dims& d, int qkv_dtype) {
-  return mfma_fwd_supported(d, qkv_dtype, DN_BF16) && (d.V == 64 || d.V == 128);
+  return mfma_fwd_supported(d, qkv_dtype, DN_BF16) && (d.V == 64 || d.V % 128 == 0);
+}
+
+// The fp32 partial sums of the value-summed gradients across the passes:
+// per (token, head) d_q, d_k (K each), d_erase (ew), d_g (dw) and d_write
+// (1 when its width is 1). None for a single pass.
+size_t mfma_chunk_bwd_partials(const Dims& d) {
+  if (d.V <= 128) return 0;
+  const size_t rows = size_t(d.B) * d.S * d.H;
+  return align_up(rows * (2 * d.K + d.ew + d.dw + (d.ww == 1 ? 1 : 0)) * sizeof(float), 256);
 }
 
 hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const void* q,
                           const void* k, const void* v, const float* erase, const float* write,
                           const float* g, const float* states, const float* ds_after, void* dq,
                           void* dk, void* dv, float* derase, float* dwrite, float* dg,
-                          const MfmaTiles& tiles, hipStream_t stream) {
+                          const MfmaTiles& tiles, float* partials, hipStream_t stream) {
   CbParams p;
   p.S = d.S;
   p.H = d.H;
@@ -1130,6 +1161,15 @@ hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const v
   const size_t G = size_t(d.B) * d.N * d.H;
   const bool pc = d.dw == d.K && d.K > 1;
   const bool f32 = grad_dtype == DN_F32;
+  // One pass for head_v_dim 64 or 128, else passes of 128 value columns.
+  const int vd = d.V <= 128 ? int(d.V) : 128, passes = int(d.V) / vd;
+  const size_t rows = size_t(d.B) * d.S * d.H;
+  p.vs = int(d.V);
+  p.pq = partials;
+  p.pk = p.pq ? p.pq + rows * d.K : nullptr;
+  p.pe = p.pk ? p.pk + rows * d.K : nullptr;
+  p.pg = p.pe ? p.pe + rows * d.ew : nullptr;
+  p.pw = p.pg ? p.pg + rows * d.dw : nullptr;
   ProfScope ps("dn_mfma_chunk_bwd", stream);
 #define DN_CB(KD, VD, PCV, TG)                                                                  \
   hipLaunchKernelGGL((mfma_chunk_bwd_kernel<KD, VD, PCV, TG>), dim3(unsigned(G)), dim3(kNT), 0, \
@@ -1144,10 +1184,16 @@ hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const v
     if (pc) DN_CB_T(KD, VD, true);        \
     else DN_CB_T(KD, VD, false);          \
   } while (0)
-  if (d.K == 128) {
-    if (d.V == 128) DN_CB_P(128, 128); else DN_CB_P(128, 64);
-  } else {
-    if (d.V == 128) DN_CB_P(64, 128); else DN_CB_P(64, 64);
+  for (int i = 0; i < passes; ++i) {
+    p.voff = vd * i;
+    p.pass = passes == 1 ? 0 : i == 0 ? 1 : i + 1 == passes ? 3 : 2;
+    if (d.K == 128) {
+      if (vd == 128) DN_CB_P(128, 128); else DN_CB_P(128, 64);
+    } else {
+      if (vd == 128) DN_CB_P(64, 128); else DN_CB_P(64, 64);
+    }
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
   }
 #undef DN_CB_P
 #undef DN_CB_T

@@ -132,14 +132,17 @@ struct MfmaTiles {
   const float* gc;
 };
 MfmaTiles mfma_bwd_tiles(const Dims& d, void* ws);
-// The chunk-local gradients on MFMA (head_v_dim 64 or 128 on top of the
-// shapes of mfma_fwd_supported), after mfma_bwd_scans.
+// The chunk-local gradients on MFMA (head_v_dim 64, or a multiple of 128 in
+// passes of 128 value columns, on top of the shapes of mfma_fwd_supported),
+// after mfma_bwd_scans. `partials`: mfma_chunk_bwd_partials(d) bytes of
+// workspace for the value-summed gradients between passes.
 bool mfma_chunk_bwd_supported(const Dims& d, int qkv_dtype);
+size_t mfma_chunk_bwd_partials(const Dims& d);
 hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const void* q,
                           const void* k, const void* v, const float* erase, const float* write,
                           const float* g, const float* states, const float* ds_after, void* dq,
                           void* dk, void* dv, float* derase, float* dwrite, float* dg,
-                          const MfmaTiles& tiles, hipStream_t stream);
+                          const MfmaTiles& tiles, float* partials, hipStream_t stream);
 
 // Per-kernel HIP-event timing (dn_profile_enable): a scope records a start
 // event on construction and a stop event on destruction, on `stream`.

@@ -200,8 +200,14 @@ BWD_CASES = [
     (1, 256, 2, 128, 128, "head", {"const_keys": True}),
     (1, 256, 2, 128, 128, (128, 128), {"const_keys": True}),
     (1, 192, 2, 128, 128, "head", {"beta_scale": 2.0}),
-    # head_v_dim 256: MFMA scans, chunk-local gradients on the generic kernel
+    # head_v_dim a multiple of 128 above 128: the chunk-local kernel in passes
+    # of 128 value columns, the value-summed gradients added across them
     (1, 128, 2, 128, 256, "head"),
+    (1, 200, 2, 128, 256, (128, 256)),
+    (1, 130, 2, 128, 256, (1, 1)),
+    (1, 192, 2, 128, 384, "head"),
+    (1, 128, 2, 128, 256, None),
+    (1, 256, 2, 128, 256, "head", {"const_keys": True}),
 ]
 
 
@@ -269,3 +275,21 @@ def test_mfma_bwd_is_chosen_and_matches_generic(rng):
                                          got.d_state_bhkv)]
     for m, gnr in zip(out[MFMA], out[pkg.abi.DN_ALGO_GENERIC]):
         assert rel_err(m, gnr) < TOL
+
+
+def test_mfma_chunk_local_backward_runs_in_value_passes(rng):
+    """head_v_dim 256 runs the MFMA chunk-local kernel (two 128-column passes
+    under one profiler scope), not the generic one."""
+    announce("mfma bwd, dv 256: kernels")
+    args, dy, ds = bwd_inputs(rng, 1, 128, 2, 128, 256, "head")
+    q, k, v, e, w, g, s = to_gpu(args, torch.bfloat16)
+    tdy = torch.tensor(dy, dtype=torch.float32, device=DEV).to(torch.bfloat16)
+    tds = torch.tensor(ds, dtype=torch.float32, device=DEV)
+    torch.cuda.synchronize()
+    pkg.abi.profile_enable(True)
+    pkg.combined_backward(tdy, tds, q, k, v, e, w, g, s, 64, 1.0 / np.sqrt(128))
+    torch.cuda.synchronize()
+    prof = pkg.abi.profile_read()
+    pkg.abi.profile_enable(False)
+    assert "dn_mfma_chunk_bwd" in prof, prof
+    assert not any(n.startswith("dn_generic") for n in prof), prof
