@@ -436,6 +436,33 @@ def bench_config2_bwd(torch, pkg, steps, warmup):
             "kernels": kern}
 
 
+def bench_generic_fallback(torch, pkg, steps, warmup):
+    """The fp32 kernels every shape the MFMA path does not cover falls back
+    to, at the config-2 workload: forced (DN_ALGO_GENERIC), and as AUTO picks
+    them for chunk_len 32."""
+    B, T, H, K, V = 8, 4096, 16, 128, 256
+    dev = torch.device("cuda:0")
+    q, k, v, beta, g = gdn_inputs(torch, B, T, H, K, V, 0.05, 20260837, torch.bfloat16, dev)
+    s0 = torch.zeros((B, H, K, V), dtype=torch.float32, device=dev)
+    y = torch.empty((B, T, H, V), dtype=torch.bfloat16, device=dev)
+    s1 = torch.empty_like(s0)
+    abi = pkg.abi
+    out = {"workload": "config 2 (B=8 T=4096 H=16 dk=128 dv=256, bf16 q/k/v) on the generic "
+                       "fp32 kernels"}
+    for name, L, algo in (("forced_chunk64", 64, 1), ("auto_chunk32", 32, 0)):
+        a = abi.chunk_fwd_args(q, k, v, beta, beta, g, s0, y, s1, L, None, algo=algo)
+        ws = torch.empty(max(abi.lib().dn_chunk_fwd_workspace_bytes(a), 1), dtype=torch.uint8,
+                         device=dev)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+        chosen = abi.lib().dn_chunk_fwd_algo(a)
+        ms, kern = _timed(torch, abi, lambda: abi.run_chunk_fwd(a), steps, warmup)
+        out[name] = {"chunk_len": L, "algo": ALGO_NAMES.get(chosen, chosen),
+                     "ms_per_step": round(ms, 3), "tokens_per_s": round(B * T / (ms / 1e3), 1),
+                     "kernels": kern}
+        del ws
+    return out
+
+
 def bench_block_forward(torch, pkg, steps, warmup):
     """A Gated DeltaNet block's forward after in_proj at the config-2 shape
     (B=8, T=4096, H=16, dk=128, dv=256): dn_frontend (short conv of 4 with
@@ -715,6 +742,11 @@ def main():
         print("[bench] block forward (front-end + core + out norm)", file=sys.stderr, flush=True)
         extra["block_forward"] = bench_block_forward(torch, pkg, args.extra_steps, MIN_WARMUP)
         print(f"[bench] block_forward {extra['block_forward']}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+        print("[bench] generic fallback", file=sys.stderr, flush=True)
+        extra["generic_fallback"] = bench_generic_fallback(torch, pkg, MIN_STEPS, MIN_WARMUP)
+        print(f"[bench] generic_fallback {extra['generic_fallback']}", file=sys.stderr,
+              flush=True)
         torch.cuda.empty_cache()
         print("[bench] projection front-end (dn_frontend)", file=sys.stderr, flush=True)
         extra["frontend"] = bench_frontend(torch, pkg, args.extra_steps, MIN_WARMUP)

@@ -82,8 +82,11 @@ struct MfmaParams {
   float* seg_final; // [B·H][K][V] the last segments' end states (seg = 2)
 };
 
-// The backward's transposed tiles (the reverse scan contracts over a chunk's
-// tokens where the forward contracts over its rows).
+// The backward's transposed tiles. The reverse scan contracts over a chunk's
+// tokens where the forward contracts over its rows, so it reads Tᵀ (hi, lo),
+// attnᵀ, Kc = (Kcᵀ)ᵀ, and Qgᵀ = (scale·e^G⊙Q)ᵀ, Kgᵀ = (e⊙e^G⊙K)ᵀ
+// (combined_backward.rs:272-282: the state cotangent picks up qrᵀ·dy and
+// Wᵀ·dV' = kgᵀ·(Tᵀ·dV')). The intra kernels write them in their BT mode.
 struct BwdTiles {
   uint16_t *Tt, *Ttl, *AtT;  // [G][64][64]
   uint16_t* Kc;              // [G][64][K]
@@ -94,8 +97,11 @@ struct BwdTiles {
 // ---------------------------------------------------------------------------
 // intra
 // ---------------------------------------------------------------------------
-template <int K, bool GATED>
-__global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int G) {
+// BT (the backward's recompute): the kernel also writes the reverse scan's
+// transposed tiles (Tᵀ hi/lo, attnᵀ, Kc, Qgᵀ, Kgᵀ, e^{G_last}) from the
+// tiles it holds in LDS, as the per-channel kernel does.
+template <int K, bool GATED, bool BT = false>
+__global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int G, BwdTiles bt) {
   constexpr int KP = K + 8;                     // padded LDS row (bf16 elements)
   constexpr int KS8 = K / 8;                    // 16-byte segments per key row
   constexpr int NLD = kL * KS8 / kThreads;      // 16-byte loads per lane per tile
@@ -167,6 +173,31 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
     adst[1] = pend[5];
   };
 
+  // dstᵀ[d][t] = bf16(X[t][d]·rowsc(t)) for a [64][K] tile X in LDS: an item
+  // is two key channels × 16 tokens, consecutive lanes taking consecutive
+  // channel pairs (conflict-free column reads, one 32-bit read per token).
+  auto scaled_t = [&](const uint16_t* X, uint16_t* dst, auto rowsc) {
+    for (int it = tid; it < K * 2; it += kThreads) {
+      const int d = 2 * (it % (K / 2)), t0 = 16 * (it / (K / 2));
+      uint32_t w0[8], w1[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int t = t0 + 2 * e;
+        const uint32_t a = *reinterpret_cast<const uint32_t*>(&X[t * KP + d]);
+        const uint32_t b = *reinterpret_cast<const uint32_t*>(&X[(t + 1) * KP + d]);
+        const float s0 = rowsc(t), s1 = rowsc(t + 1);
+        w0[e] = pk_bf16(lo_f(a) * s0, lo_f(b) * s1);
+        w1[e] = pk_bf16(hi_f(a) * s0, hi_f(b) * s1);
+      }
+      uint4* dst0 = reinterpret_cast<uint4*>(dst + size_t(d) * kL + t0);
+      uint4* dst1 = reinterpret_cast<uint4*>(dst + size_t(d + 1) * kL + t0);
+      dst0[0] = make_uint4(w0[0], w0[1], w0[2], w0[3]);
+      dst0[1] = make_uint4(w0[4], w0[5], w0[6], w0[7]);
+      dst1[0] = make_uint4(w1[0], w1[1], w1[2], w1[3]);
+      dst1[1] = make_uint4(w1[4], w1[5], w1[6], w1[7]);
+    }
+  };
+
   for (int cid = blockIdx.x; cid < G; cid += gridDim.x) {
 #pragma unroll
     for (int m = 0; m < NLD; ++m) {
@@ -228,34 +259,37 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
         }
       }
     }
+    // Qgᵀ = (scale·e^G⊙Q)ᵀ while Q is in LDS (T takes its space next); rows
+    // past the sequence end are zero in the tile.
+    if constexpr (BT)
+      scaled_t(Qs, bt.QgT + size_t(cid) * K * kL,
+               [&](int t) { return p.scale * (GATED ? __expf(gcs[t]) : 1.f); });
     __syncthreads();
 
     diag_inverse(A, Tm, wave, lane);
     {
       // Kcᵀ = (e^{G_last−G} ⊙ K)ᵀ for the scan's state update, while the K
-      // tile is in LDS: an item is one key channel × 16 tokens, consecutive
-      // lanes taking consecutive channels (conflict-free column reads).
+      // tile is in LDS.
       const float glast = gcs[kL - 1];
-      for (int it = tid; it < K * 2; it += kThreads) {
-        // Channels d, d+1 of 16 tokens: one 32-bit LDS read per token.
-        const int d = 2 * (it % (K / 2)), t0 = 16 * (it / (K / 2));
-        uint32_t w0[8], w1[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int t = t0 + 2 * e;
-          const uint32_t a = *reinterpret_cast<const uint32_t*>(&Ks[t * KP + d]);
-          const uint32_t b = *reinterpret_cast<const uint32_t*>(&Ks[(t + 1) * KP + d]);
-          const float s0 = GATED ? __expf(glast - gcs[t]) : 1.f;
-          const float s1 = GATED ? __expf(glast - gcs[t + 1]) : 1.f;
-          w0[e] = pk_bf16(lo_f(a) * s0, lo_f(b) * s1);
-          w1[e] = pk_bf16(hi_f(a) * s0, hi_f(b) * s1);
+      auto kcs = [&](int t) { return GATED ? __expf(glast - gcs[t]) : 1.f; };
+      scaled_t(Ks, p.KcT + size_t(cid) * K * kL, kcs);
+      if constexpr (BT) {
+        // Kgᵀ = (e⊙e^G⊙K)ᵀ, Kc = e^{G_last−G}⊙K row-major (the same products
+        // as Kcᵀ) and e^{G_last} per key channel.
+        scaled_t(Ks, bt.KgT + size_t(cid) * K * kL,
+                 [&](int t) { return ers[t] * (GATED ? __expf(gcs[t]) : 1.f); });
+        for (int idx = tid; idx < kL * KS8; idx += kThreads) {
+          const int t = idx / KS8, d0 = 8 * (idx % KS8);
+          const uint4 x = *reinterpret_cast<const uint4*>(&Ks[t * KP + d0]);
+          const float sc = kcs(t);
+          *reinterpret_cast<uint4*>(bt.Kc + (size_t(cid) * kL + t) * K + d0) =
+              make_uint4(pk_bf16(lo_f(x.x) * sc, hi_f(x.x) * sc),
+                         pk_bf16(lo_f(x.y) * sc, hi_f(x.y) * sc),
+                         pk_bf16(lo_f(x.z) * sc, hi_f(x.z) * sc),
+                         pk_bf16(lo_f(x.w) * sc, hi_f(x.w) * sc));
         }
-        uint4* dst0 = reinterpret_cast<uint4*>(p.KcT + (size_t(cid) * K + d) * kL + t0);
-        uint4* dst1 = reinterpret_cast<uint4*>(p.KcT + (size_t(cid) * K + d + 1) * kL + t0);
-        dst0[0] = make_uint4(w0[0], w0[1], w0[2], w0[3]);
-        dst0[1] = make_uint4(w0[4], w0[5], w0[6], w0[7]);
-        dst1[0] = make_uint4(w1[0], w1[1], w1[2], w1[3]);
-        dst1[1] = make_uint4(w1[4], w1[5], w1[6], w1[7]);
+        const float egl = GATED ? __expf(glast) : 1.f;
+        for (int d = tid; d < K; d += kThreads) bt.egl[size_t(cid) * K + d] = egl;
       }
       // Zero T above the block diagonal (the merges never write there).
       for (int idx = tid; idx < kL * kL; idx += kThreads) {
@@ -283,6 +317,28 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
       pend[4] = *reinterpret_cast<const uint4*>(&At[row * (kL + 8) + c0]);
       pend[5] = *reinterpret_cast<const uint4*>(&At[row * (kL + 8) + c0 + 8]);
       pend_cid = cid;
+      if constexpr (BT) {
+        // Tᵀ (hi, lo) and attnᵀ row `row` = column `row` of T and attn.
+        uint32_t av[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const int i0 = c0 + 2 * c;
+          const float x0 = Tm[i0][row], x1 = Tm[i0 + 1][row];
+          tv[c] = pk_bf16(x0, x1);
+          tl[c] = pk_bf16(x0 - lo_f(tv[c]), x1 - hi_f(tv[c]));
+          av[c] = uint32_t(At[i0 * (kL + 8) + row]) | (uint32_t(At[(i0 + 1) * (kL + 8) + row]) << 16);
+        }
+        const size_t off = size_t(cid) * kL * kL + row * kL + c0;
+        uint4* ttd = reinterpret_cast<uint4*>(bt.Tt + off);
+        uint4* tld = reinterpret_cast<uint4*>(bt.Ttl + off);
+        uint4* atd = reinterpret_cast<uint4*>(bt.AtT + off);
+        ttd[0] = make_uint4(tv[0], tv[1], tv[2], tv[3]);
+        ttd[1] = make_uint4(tv[4], tv[5], tv[6], tv[7]);
+        tld[0] = make_uint4(tl[0], tl[1], tl[2], tl[3]);
+        tld[1] = make_uint4(tl[4], tl[5], tl[6], tl[7]);
+        atd[0] = make_uint4(av[0], av[1], av[2], av[3]);
+        atd[1] = make_uint4(av[4], av[5], av[6], av[7]);
+      }
     }
     __syncthreads();  // LDS is restaged by the next chunk
   }
@@ -1164,95 +1220,6 @@ __global__ __launch_bounds__(256) void seg_carry_kernel(MfmaParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Backward: the reverse scan's operand tiles
-// ---------------------------------------------------------------------------
-// The reverse scan contracts over a chunk's tokens where the forward
-// contracts over its rows, so it reads the transposes of the forward's
-// tiles: Tᵀ (hi, lo), attnᵀ, Kc = (Kcᵀ)ᵀ, and Qgᵀ = (scale·e^G⊙Q)ᵀ,
-// Kgᵀ = (e⊙e^G⊙K)ᵀ (combined_backward.rs:272-282: the state cotangent picks
-// up qrᵀ·dy and Wᵀ·dV' = kgᵀ·(Tᵀ·dV')). One workgroup per chunk-head; tiles
-// are transposed through LDS. Per-head gates only: with per-channel gates the
-// intra kernel writes these tiles itself (mfma_intra_pc_kernel<K, true>).
-template <int K>
-__global__ __launch_bounds__(kThreads) void mfma_bwd_tiles_kernel(MfmaParams p, BwdTiles bt) {
-  constexpr int RP = (K > kL ? K : kL) + 2;  // LDS row pitch (elements) of the staged tile
-  __shared__ __attribute__((aligned(16))) uint16_t buf[(K > kL ? K : kL) * RP];
-  __shared__ float rowsc[kL];
-  const int cid = blockIdx.x;
-  const int h = cid % p.H, n = (cid / p.H) % p.N, b = cid / (p.H * p.N);
-  const int tid = threadIdx.x;
-  const int tok0 = n * kL;
-  const int valid = min(kL, p.S - tok0);  // rows of this chunk; reads clamp to them
-  const size_t row0 = size_t(b) * p.S * p.H + h + size_t(tok0) * p.H;
-
-  // dst[C][R] = src[R][C]ᵀ for a tile already in `buf` ([R][C], pitch RP).
-  auto write_t = [&](uint16_t* dst, int R, int C) {
-    for (int idx = tid; idx < C * R / 8; idx += kThreads) {
-      const int c = idx / (R / 8), r8 = 8 * (idx % (R / 8));
-      uint32_t w[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        w[e] = uint32_t(buf[(r8 + 2 * e) * RP + c]) | (uint32_t(buf[(r8 + 2 * e + 1) * RP + c]) << 16);
-      *reinterpret_cast<uint4*>(dst + size_t(c) * R + r8) = make_uint4(w[0], w[1], w[2], w[3]);
-    }
-  };
-  // buf ← src[R][C] (contiguous rows).
-  auto load = [&](const uint16_t* src, int R, int C) {
-    for (int idx = tid; idx < R * C / 8; idx += kThreads) {
-      const int r = idx / (C / 8), c8 = 8 * (idx % (C / 8));
-      const uint4 v = *reinterpret_cast<const uint4*>(src + size_t(r) * C + c8);
-      uint32_t* d = reinterpret_cast<uint32_t*>(&buf[r * RP + c8]);
-      d[0] = v.x;
-      d[1] = v.y;
-      d[2] = v.z;
-      d[3] = v.w;
-    }
-  };
-  auto transpose = [&](const uint16_t* src, uint16_t* dst, int R, int C) {
-    load(src, R, C);
-    __syncthreads();
-    write_t(dst, R, C);
-    __syncthreads();
-  };
-  const size_t o64 = size_t(cid) * kL * kL, oK = size_t(cid) * kL * K;
-  transpose(p.T + o64, bt.Tt + o64, kL, kL);
-  transpose(p.Tlo + o64, bt.Ttl + o64, kL, kL);
-  transpose(p.attn + o64, bt.AtT + o64, kL, kL);
-  transpose(p.KcT + oK, bt.Kc + oK, K, kL);
-  {
-    // Qg = scale·e^G·q and Kg = e·e^G·k row by row (zero past the sequence
-    // end).
-    for (int which = 0; which < 2; ++which) {
-      if (tid < kL) {
-        const int t = tid;
-        const bool ok = tok0 + t < p.S;
-        const float eg = p.gated ? __expf(p.gc[size_t(cid) * kL + t]) : 1.f;
-        const float e = p.erase[row0 + size_t(min(t, valid - 1)) * p.H];
-        rowsc[t] = !ok ? 0.f : which == 0 ? p.scale * eg : e * eg;
-      }
-      __syncthreads();
-      const uint16_t* src = which == 0 ? p.q : p.k;
-      for (int idx = tid; idx < kL * K / 8; idx += kThreads) {
-        const int r = idx / (K / 8), c8 = 8 * (idx % (K / 8));
-        uint4 v = *reinterpret_cast<const uint4*>(src + (row0 + size_t(min(r, valid - 1)) * p.H) * K + c8);
-        if (r >= valid) v = make_uint4(0u, 0u, 0u, 0u);
-        const float sc = rowsc[r];
-        uint32_t* d = reinterpret_cast<uint32_t*>(&buf[r * RP + c8]);
-        d[0] = pk_bf16(lo_f(v.x) * sc, hi_f(v.x) * sc);
-        d[1] = pk_bf16(lo_f(v.y) * sc, hi_f(v.y) * sc);
-        d[2] = pk_bf16(lo_f(v.z) * sc, hi_f(v.z) * sc);
-        d[3] = pk_bf16(lo_f(v.w) * sc, hi_f(v.w) * sc);
-      }
-      __syncthreads();
-      write_t(which == 0 ? bt.QgT + oK : bt.KgT + oK, kL, K);
-      __syncthreads();
-    }
-    const float egl = p.gated ? __expf(p.gc[size_t(cid) * kL + kL - 1]) : 1.f;
-    for (int d = tid; d < K; d += kThreads) bt.egl[size_t(cid) * K + d] = egl;
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Backward: the reverse scan carrying the state cotangent dS
 // ---------------------------------------------------------------------------
 // combined_backward.rs:240-319, the dS recurrence, walking the chunks in
@@ -1619,15 +1586,21 @@ hipError_t launch_intra(const MfmaParams& p, const Dims& d, hipStream_t stream,
   } else {
     // Two resident workgroups per CU (LDS-bound) walk all chunk-heads.
     const int grid = int(std::min<size_t>(G, size_t(2) * device_cu_count()));
-    ProfScope ps("dn_mfma_intra", stream);
-#define DN_INTRA(KD, GT)                                                                   \
-  hipLaunchKernelGGL((mfma_intra_kernel<KD, GT>), dim3(unsigned(grid)), dim3(kThreads), 0, \
-                     stream, p, int(G))
+    ProfScope ps(bt ? "dn_mfma_intra_bwd" : "dn_mfma_intra", stream);
+#define DN_INTRA(KD, GT, BTV)                                                                    \
+  hipLaunchKernelGGL((mfma_intra_kernel<KD, GT, BTV>), dim3(unsigned(grid)), dim3(kThreads), 0, \
+                     stream, p, int(G), bt ? *bt : BwdTiles{})
+#define DN_INTRA_G(KD, BTV)                              \
+  do {                                                   \
+    if (p.gated) DN_INTRA(KD, true, BTV);                \
+    else DN_INTRA(KD, false, BTV);                       \
+  } while (0)
     if (d.K == 128) {
-      if (p.gated) DN_INTRA(128, true); else DN_INTRA(128, false);
+      if (bt) DN_INTRA_G(128, true); else DN_INTRA_G(128, false);
     } else {
-      if (p.gated) DN_INTRA(64, true); else DN_INTRA(64, false);
+      if (bt) DN_INTRA_G(64, true); else DN_INTRA_G(64, false);
     }
+#undef DN_INTRA_G
 #undef DN_INTRA
   }
   return hipGetLastError();
@@ -1829,22 +1802,11 @@ hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
   float* s_scratch = reinterpret_cast<float*>(reinterpret_cast<char*>(bt.egl) + region(G * K * 4));
   MfmaParams p = make_params(d, q, k, v, erase, write, g, state_in, nullptr, s_scratch, ws);
   p.states = states;
-  const bool pc = per_channel(d);
-  // Per-channel gates: the intra kernel writes the transposed tiles itself.
-  hipError_t e = launch_intra(p, d, stream, pc ? &bt : nullptr);
+  // The intra kernel writes the reverse scan's transposed tiles too.
+  hipError_t e = launch_intra(p, d, stream, &bt);
   if (e != hipSuccess) return e;
   hipStream_t side = nullptr;
   if ((e = side_fork(stream, &side)) != hipSuccess) return e;
-  if (!pc) {
-    ProfScope ps("dn_mfma_bwd_tiles", side);
-    if (d.K == 128)
-      hipLaunchKernelGGL(mfma_bwd_tiles_kernel<128>, dim3(unsigned(G)), dim3(kThreads), 0, side,
-                         p, bt);
-    else
-      hipLaunchKernelGGL(mfma_bwd_tiles_kernel<64>, dim3(unsigned(G)), dim3(kThreads), 0, side,
-                         p, bt);
-  }
-  if ((e = hipGetLastError()) != hipSuccess) return e;
   RevParams rp{d.B, d.S, d.H, d.V, d.N, dy, dstate_final, ds_after, dstate, bt};
   const int waves = scan_waves(d);
   const unsigned blocks = unsigned(((d.B * d.H + 7) / 8) * 8 * (d.V / (16 * waves)));
