@@ -252,6 +252,26 @@ def bench_out_norm(torch, pkg, steps, warmup):
             "kernels": kern}
 
 
+def bench_unit_lower_inverse(torch, pkg, steps, warmup):
+    """The standalone unit_lower_inverse (dn_unit_lower_inverse, tri.rs:66-114,
+    TriSolve::Blocked) on a chunk path's batch: 8192 blocks of 64 (config 2's
+    chunk-heads), and 1024 blocks of 128; float32 in and out."""
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20260838)
+    abi = pkg.abi
+    out = {"workload": "dn_unit_lower_inverse (TriSolve::Blocked), float32"}
+    for name, G, L in (("blocks64", 8192, 64), ("blocks128", 1024, 128)):
+        n = torch.tril(torch.randn((G, L, L), generator=gen, device=dev) * 0.15, -1)
+        t = torch.empty_like(n)
+        args = abi.tri_args(n, t, abi.DN_TRI_BLOCKED)
+        ms, kern = _timed(torch, abi, lambda: abi.run_unit_lower_inverse(args), steps, warmup)
+        out[name] = {"matrices": G, "size": L, "ms_per_call": round(ms, 4),
+                     "roofline": _hbm(2 * G * L * L * 4, ms), "kernels": kern}
+        del n, t
+    return out
+
+
 MIN_STEPS, MIN_WARMUP = 20, 2  # timed calls and warm-ups of every line
 _EXACT = {"on": False}  # --profile-pass: run exactly the calls asked for, no profiler pass
 
@@ -755,6 +775,11 @@ def main():
         print("[bench] output norm (dn_out_norm)", file=sys.stderr, flush=True)
         extra["out_norm"] = bench_out_norm(torch, pkg, args.extra_steps, MIN_WARMUP)
         print(f"[bench] out_norm {extra['out_norm']}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+        print("[bench] unit_lower_inverse", file=sys.stderr, flush=True)
+        extra["unit_lower_inverse"] = bench_unit_lower_inverse(torch, pkg, MIN_STEPS, MIN_WARMUP)
+        print(f"[bench] unit_lower_inverse {extra['unit_lower_inverse']}", file=sys.stderr,
+              flush=True)
         torch.cuda.empty_cache()
 
     cpu = None

@@ -11,13 +11,15 @@ output norm (OutNorm).
 from . import abi
 from .abi import DeltaError
 from .delta import (DeltaChunkFunction, DeltaChunkGrads, DeltaInput, DeltaPath, TriSolve,
-                    beta_gates, combined_backward, delta_chunk_recalculated, delta_step)
+                    beta_gates, combined_backward, delta_chunk_recalculated, delta_step,
+                    unit_lower_inverse)
 from .frontend import (ConvActivation, OutNorm, QkActivation, QkNorm, Qkv, QkvProjection,
                        QkvStep, ShortConv, WriteGate)
 
 __all__ = [
     "abi", "DeltaError", "DeltaChunkFunction", "DeltaChunkGrads", "DeltaInput", "DeltaPath",
     "TriSolve", "beta_gates", "combined_backward", "delta_chunk_recalculated", "delta_step",
+    "unit_lower_inverse",
     "ConvActivation", "OutNorm", "QkActivation", "QkNorm", "Qkv", "QkvProjection", "QkvStep",
     "ShortConv", "WriteGate",
 ]

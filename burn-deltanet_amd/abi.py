@@ -25,6 +25,8 @@ DN_QKNORM_NONE, DN_QKNORM_L2, DN_QKNORM_SUM = 0, 1, 2
 DN_WRITE_FIXED, DN_WRITE_SCALAR, DN_WRITE_CHANNEL = 0, 1, 2
 FRONTEND_MAX_HEAD_DIM, FRONTEND_MAX_KERNEL = 256, 8
 OUT_NORM_MAX_HEAD_DIM = 1024
+DN_TRI_BLOCKED, DN_TRI_NEUMANN = 0, 1
+TRI_NEUMANN_MAX_SIZE = 140  # DN_TRI_NEUMANN_MAX_SIZE (deltanet_core.h)
 
 STATUS = {
     0: "DN_OK",
@@ -45,7 +47,7 @@ EXPORTS = [
     "dn_chunk_fwd_workspace_bytes",
     "dn_chunk_bwd_workspace_bytes", "dn_chunk_fwd_algo", "dn_chunk_bwd_algo",
     "dn_last_error", "dn_version", "dn_profile_enable", "dn_profile_read",
-    "dn_chunk_fwd_noalloc",
+    "dn_chunk_fwd_noalloc", "dn_unit_lower_inverse",
 ]
 NOALLOC_SCRATCH_BYTES = 64 << 20  # DN_NOALLOC_SCRATCH_BYTES (deltanet_core.h)
 
@@ -121,6 +123,13 @@ class OutNormArgs(ctypes.Structure):
     ]
 
 
+class TriArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i64), ("size", _i64), ("solve", _i32), ("check_finite", _i32),
+        ("n_strict", _vp), ("t", _vp),
+    ]
+
+
 _LIB = None
 
 
@@ -147,6 +156,8 @@ def lib() -> ctypes.CDLL:
         L.dn_frontend.restype = ctypes.c_int
         L.dn_out_norm.argtypes = [ctypes.POINTER(OutNormArgs), _vp]
         L.dn_out_norm.restype = ctypes.c_int
+        L.dn_unit_lower_inverse.argtypes = [ctypes.POINTER(TriArgs), _vp]
+        L.dn_unit_lower_inverse.restype = ctypes.c_int
         L.dn_chunk_fwd_workspace_bytes.argtypes = [ctypes.POINTER(ChunkFwdArgs)]
         L.dn_chunk_fwd_workspace_bytes.restype = _sz
         L.dn_chunk_bwd_workspace_bytes.argtypes = [ctypes.POINTER(ChunkBwdArgs)]
@@ -341,6 +352,22 @@ def out_norm_args(x, gate, weight, out, eps):
 
 def run_out_norm(args: OutNormArgs) -> None:
     check(lib().dn_out_norm(ctypes.byref(args), stream_handle()))
+
+
+def tri_args(n_strict, t, solve=DN_TRI_BLOCKED, check_finite=False) -> TriArgs:
+    """dn_tri_args over [..., size, size] float32 tensors (any leading axes)."""
+    size = n_strict.shape[-1]
+    a = TriArgs()
+    a.batch = n_strict.numel() // (size * size) if size else 0
+    a.size = size
+    a.solve = int(solve)
+    a.check_finite = 1 if check_finite else 0
+    a.n_strict, a.t = _ptr(n_strict), _ptr(t)
+    return a
+
+
+def run_unit_lower_inverse(args: TriArgs) -> None:
+    check(lib().dn_unit_lower_inverse(ctypes.byref(args), stream_handle()))
 
 
 def chunk_bwd_args(dy, dstate, q, k, v, erase, write, g, state, grads, chunk_len, scale,

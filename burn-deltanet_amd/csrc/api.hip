@@ -568,6 +568,33 @@ int dn_out_norm(const dn_out_norm_args* a, hipStream_t stream) {
   return DN_OK;
 }
 
+int dn_unit_lower_inverse(const dn_tri_args* a, hipStream_t stream) {
+  g_last_error.clear();
+  if (!a) return fail(DN_ERR_NULL, "args is NULL");
+  if (a->batch < 0 || a->size < 0) return fail(DN_ERR_SHAPE, "batch and size must be at least 0");
+  if (a->size > (int64_t(1) << 20) || a->batch * a->size * a->size >= (int64_t(1) << 40) ||
+      a->batch * ((a->size + 63) / 64) >= (int64_t(1) << 31))
+    return fail(DN_ERR_SHAPE, "tensor too large");
+  if (a->solve != DN_TRI_BLOCKED && a->solve != DN_TRI_NEUMANN)
+    return fail(DN_ERR_UNSUPPORTED, "solve must be DN_TRI_BLOCKED or DN_TRI_NEUMANN");
+  if (a->solve == DN_TRI_NEUMANN && a->size > DN_TRI_NEUMANN_MAX_SIZE)
+    return fail(DN_ERR_UNSUPPORTED, "DN_TRI_NEUMANN supports size up to " +
+                                        std::to_string(DN_TRI_NEUMANN_MAX_SIZE) +
+                                        "; DN_TRI_BLOCKED covers any size");
+  const size_t nm = size_t(a->batch) * a->size * a->size;
+  if (nm == 0) return DN_OK;
+  if (!a->n_strict || !a->t) return fail(DN_ERR_NULL, "a required tensor pointer is NULL");
+  if (a->check_finite) {
+    if (int rc = nonfinite_check({{a->n_strict, nm, DN_F32}}, stream, "inputs")) return rc;
+  }
+  hipError_t e = launch_unit_lower_inverse(*a, stream);
+  if (e != hipSuccess) return hip_fail(e, "dn_unit_lower_inverse launch");
+  if (a->check_finite) {
+    if (int rc = nonfinite_check({{a->t, nm, DN_F32}}, stream, "outputs")) return rc;
+  }
+  return DN_OK;
+}
+
 int dn_recurrent(const dn_recurrent_args* a, hipStream_t stream) {
   g_last_error.clear();
   if (!a) return fail(DN_ERR_NULL, "args is NULL");

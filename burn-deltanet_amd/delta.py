@@ -23,9 +23,9 @@ Tensor = torch.Tensor
 
 
 class TriSolve(Enum):
-    """src/delta/tri.rs:53-64. Both variants evaluate the same exact inverse
-    here (forward substitution); the reference's Neumann series exists only as
-    its own test baseline."""
+    """src/delta/tri.rs:53-64. Inside the chunk paths both variants evaluate
+    the same exact inverse (the reference's Neumann series is a test baseline
+    there); unit_lower_inverse honours the variant."""
 
     BLOCKED = "blocked"
     NEUMANN = "neumann"
@@ -184,6 +184,23 @@ def _qkv_dtype(*ts):
     if any(t.dtype != dt for t in ts):
         raise DeltaError(-7, "q, k and v must share one dtype")
     return dt
+
+
+def unit_lower_inverse(n_strict: Tensor, solve: TriSolve = TriSolve.BLOCKED,
+                       check_finite: bool = False) -> Tensor:
+    """src/delta/tri.rs:66-114: T = (I − N)⁻¹ for a batched strictly lower
+    triangular N of shape [..., size, size], computed in float32 by
+    dn_unit_lower_inverse and returned in N's dtype. BLOCKED reads only N's
+    strict lower triangle; NEUMANN sums I + N + … + N^{size−1} term by term over
+    the whole matrix, up to size abi.TRI_NEUMANN_MAX_SIZE. As in the reference,
+    the caller owes the strict lower property."""
+    if n_strict.dim() < 2 or n_strict.shape[-2] != n_strict.shape[-1]:
+        raise DeltaError(-2, "unit_lower_inverse expects a square trailing block")
+    n = _dev(n_strict, torch.float32)
+    t = torch.empty_like(n)
+    code = abi.DN_TRI_NEUMANN if solve == TriSolve.NEUMANN else abi.DN_TRI_BLOCKED
+    abi.run_unit_lower_inverse(abi.tri_args(n, t, code, check_finite))
+    return t if n_strict.dtype == torch.float32 else t.to(n_strict.dtype)
 
 
 def delta_chunk_recalculated(q_bshk, k_bshk, v_bshv, erase_bshK, write_bshV, g_bshK,

@@ -340,6 +340,28 @@ dn_step_args step_args(const Tensor& q, const Tensor& k, const Tensor& v, const 
 
 }  // namespace
 
+Tensor unit_lower_inverse(const Tensor& n_strict, TriSolve solve, hipStream_t stream,
+                          bool check_finite) {
+  const int r = n_strict.rank();
+  if (r < 2 || n_strict.dim(r - 2) != n_strict.dim(r - 1))
+    throw Error(DN_ERR_SHAPE, "unit_lower_inverse expects a square trailing block");
+  if (n_strict.dtype() != DType::F32)
+    throw Error(DN_ERR_DTYPE, "unit_lower_inverse: n_strict must be float32");
+  const int64_t size = n_strict.dim(r - 1);
+  Tensor t = Tensor::empty(n_strict.dims(), DType::F32);
+  if (n_strict.numel() == 0) return t;
+  require_defined(n_strict, "n_strict");
+  dn_tri_args a{};
+  a.batch = int64_t(n_strict.numel()) / (size * size);
+  a.size = size;
+  a.solve = solve == TriSolve::Neumann ? DN_TRI_NEUMANN : DN_TRI_BLOCKED;
+  a.check_finite = check_finite ? 1 : 0;
+  a.n_strict = static_cast<const float*>(n_strict.data());
+  a.t = static_cast<float*>(t.data());
+  check(dn_unit_lower_inverse(&a, stream));
+  return t;
+}
+
 std::pair<Tensor, Tensor> delta_step(const Tensor& q_bhk, const Tensor& k_bhk, const Tensor& v_bhv,
                                      const Tensor& erase_bhK, const Tensor& write_bhV,
                                      const std::optional<Tensor>& g_bhK, const Tensor& state_bhkv,

@@ -8,6 +8,7 @@
 //   delta_step                            src/delta/recurrent.rs:41-99
 //   DeltaChunkGrads, combined_backward    src/delta/chunk_recalculated/
 //                                         combined_backward.rs:50-189
+//   TriSolve, unit_lower_inverse          src/delta/tri.rs:53-114
 // Every computation is a call through the C ABI of deltanet_core.h. Where
 // the reference panics on an assert!, these functions throw deltanet::Error
 // carrying the same message (and the dn_status the C ABI uses for it).
@@ -77,8 +78,18 @@ class Tensor {
 };
 
 // How the WY transform's (I − N)⁻¹ is evaluated (src/delta/tri.rs:53-64).
-// Both evaluate the same exact inverse here (blocked forward substitution).
+// Inside the chunk paths both evaluate the same exact inverse (the
+// reference's Neumann series is a test baseline there); unit_lower_inverse
+// honours the variant.
 enum class TriSolve { Blocked, Neumann };
+
+// tri.rs:66-114: T = (I − N)⁻¹ for a batched strictly lower triangular N of
+// shape [..., size, size], float32. Blocked reads only N's strict lower
+// triangle; Neumann sums I + N + … + N^{size−1} term by term over the whole
+// matrix, up to DN_TRI_NEUMANN_MAX_SIZE. The caller owes the strict lower
+// property, as in the reference.
+Tensor unit_lower_inverse(const Tensor& n_strict, TriSolve solve = TriSolve::Blocked,
+                          hipStream_t stream = nullptr, bool check_finite = false);
 
 // Which evaluation of the delta rule runs (src/delta/path.rs:21-99).
 struct DeltaPath {

@@ -12,6 +12,10 @@
  *                   (src/delta/chunk_recalculated/combined_backward.rs:72-189,
  *                    called from the autodiff node, backward.rs:82-170)
  *
+ * Around them: dn_recurrent (DeltaInput::delta_recurrent), dn_frontend and
+ * dn_out_norm (the families' projection front-end and output norm) and
+ * dn_unit_lower_inverse (the public unit_lower_inverse, src/delta/tri.rs).
+ *
  * Conventions (src/delta/path.rs:120-141). All tensors are dense row-major
  * device buffers in the reference's axis order:
  *   q, k      [batch, sequence, nheads, head_k_dim]      dtype qkv_dtype
@@ -271,6 +275,34 @@ typedef struct {
  * delta rule by every family (deltanet.rs:171, 219; gated_deltanet_1.rs:183, 234;
  * gated_deltanet_2.rs:282, 367; delta_product.rs:230, 306). */
 int dn_out_norm(const dn_out_norm_args *args, hipStream_t stream);
+
+/* How unit_lower_inverse inverts I − N (TriSolve, src/delta/tri.rs:53-64). */
+typedef enum {
+  DN_TRI_BLOCKED = 0, /* the exact inverse without powers of N (the default) */
+  DN_TRI_NEUMANN = 1, /* the series I + N + … + N^{size−1}, term by term in fp32 */
+} dn_tri_solve;
+
+/* Largest `size` DN_TRI_NEUMANN serves (N and the running term in LDS). The
+ * reference keeps the series as a test baseline, usable to L ≈ 16
+ * (tri.rs:59-63). */
+#define DN_TRI_NEUMANN_MAX_SIZE 140
+
+typedef struct {
+  int64_t batch;          /* matrices: the product of the leading axes (≥ 0) */
+  int64_t size;           /* the square trailing block (≥ 0) */
+  int32_t solve;          /* dn_tri_solve */
+  int32_t check_finite;   /* the reference's sanity check of input and output */
+  const float *n_strict;  /* [batch, size, size] float32, strictly lower triangular */
+  float *t;               /* [batch, size, size] float32; must not alias n_strict */
+} dn_tri_args;
+
+/* Replaces unit_lower_inverse (src/delta/tri.rs:66-114): T = (I − N)⁻¹ for a
+ * batched strictly lower triangular N. As in the reference the caller owes the
+ * strict lower property: DN_TRI_BLOCKED reads only N's strict lower triangle,
+ * DN_TRI_NEUMANN multiplies the whole matrix. The square-block assert
+ * ("unit_lower_inverse expects a square trailing block") belongs to the
+ * caller, which passes one `size`. */
+int dn_unit_lower_inverse(const dn_tri_args *args, hipStream_t stream);
 
 /* Bytes of device workspace dn_chunk_fwd / dn_chunk_bwd need for these
  * arguments (0 on invalid arguments). Has no counterpart in the reference,

@@ -10,6 +10,8 @@
 //   recurrent<R>       src/delta/recurrent.rs:107-142      (DeltaInput::delta_recurrent)
 //   ladder_inverse<R>  src/delta/tri/prim.rs:28-74         (Blocked unit_lower_inverse,
 //                                                           the 24·L³ ladder as the reference runs it)
+//   neumann_inverse<R> src/delta/tri.rs:99-107             (Neumann unit_lower_inverse: the
+//                                                           series term by term, whole matrix)
 //   ChunkState<R>      src/delta/chunk_recalculated/forward.rs:154-206 (Chunked::prepare)
 //   wy<R>              forward.rs:235-332                  (Chunked::wy / scores / head_decay_mask / solve)
 //   BlockDecay<R>      forward.rs:451-556, src/delta/decay.rs:39-60 (per-channel decay split)
@@ -21,7 +23,8 @@
 // backward is pinned by central finite differences of `recurrent<double>` and
 // by torch float64 autograd of an independent recurrence; the ladder by
 // (I−N)T = I, unit-lower structure and the constant-key bound of
-// src/delta/tri/tests.rs.
+// src/delta/tri/tests.rs; the series by the ladder on strictly lower inputs
+// and by numpy's matrix powers on a full matrix.
 //
 // Parity unpinned: the per-channel decay when its clamp binds (an exponent
 // reaching MAX_EXPONENT = 48 within half a 16-row block, decay.rs:41-49).
@@ -265,6 +268,20 @@ Mat<R> ladder_inverse(const Mat<R>& n_strict) {
     p = add(p, mm(mm(p, x), p));
     lower = coarser;
     block *= 2;
+  }
+  return p;
+}
+
+// P = I + N + N² + … + N^{size−1}: term ← term·N, P ← P + term (tri.rs:99-107),
+// over the whole matrix as given.
+template <class R>
+Mat<R> neumann_inverse(const Mat<R>& n) {
+  const long size = n.r;
+  Mat<R> p(size, size), term(size, size);
+  for (long i = 0; i < size; ++i) p(i, i) = term(i, i) = 1;
+  for (long step = 1; step < size; ++step) {
+    term = mm(term, n);
+    p = add(p, term);
   }
   return p;
 }
@@ -723,6 +740,16 @@ int check_shape(const Shape& sh, long L) {
       Mat<R> m(size, size);                                                                    \
       std::memcpy(m.d.data(), n + f * size * size, sizeof(R) * size_t(size * size));           \
       Mat<R> inv = ladder_inverse(m);                                                          \
+      std::memcpy(t + f * size * size, inv.d.data(), sizeof(R) * size_t(size * size));         \
+    }                                                                                          \
+    return 0;                                                                                  \
+  }                                                                                            \
+  extern "C" int or_neumann_inverse_##SUF(long flat, long size, const R* n, R* t) {           \
+    if (flat < 1 || size < 1) return -1;                                                       \
+    for (long f = 0; f < flat; ++f) {                                                          \
+      Mat<R> m(size, size);                                                                    \
+      std::memcpy(m.d.data(), n + f * size * size, sizeof(R) * size_t(size * size));           \
+      Mat<R> inv = neumann_inverse(m);                                                         \
       std::memcpy(t + f * size * size, inv.d.data(), sizeof(R) * size_t(size * size));         \
     }                                                                                          \
     return 0;                                                                                  \

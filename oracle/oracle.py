@@ -152,8 +152,7 @@ def chunk_bwd(dy, dstate, q, k, v, erase, write, g, state, chunk_len=64, scale=N
     return dq, dk, dv, de, dwr, dg, ds
 
 
-def unit_lower_inverse(n, dtype=np.float64):
-    """The Blocked ladder (src/delta/tri/prim.rs:28-51) on [flat, size, size]."""
+def _tri(fn, n, dtype):
     (n,) = _prep(dtype, n)
     squeeze = n.ndim == 2
     if squeeze:
@@ -161,10 +160,20 @@ def unit_lower_inverse(n, dtype=np.float64):
     flat, size, _ = n.shape
     t = np.zeros_like(n)
     suf, _ = _suffix(dtype)
-    rc = getattr(lib(), f"or_unit_lower_inverse_{suf}")(ctypes.c_long(flat), ctypes.c_long(size),
-                                                        _ptr(n), _ptr(t))
-    _check(rc, "unit_lower_inverse")
+    rc = getattr(lib(), f"{fn}_{suf}")(ctypes.c_long(flat), ctypes.c_long(size), _ptr(n), _ptr(t))
+    _check(rc, fn)
     return t[0] if squeeze else t
+
+
+def unit_lower_inverse(n, dtype=np.float64):
+    """The Blocked ladder (src/delta/tri/prim.rs:28-51) on [flat, size, size]."""
+    return _tri("or_unit_lower_inverse", n, dtype)
+
+
+def neumann_inverse(n, dtype=np.float64):
+    """TriSolve::Neumann (src/delta/tri.rs:99-107): I + N + … + N^{size−1},
+    term by term over the whole matrix, on [flat, size, size]."""
+    return _tri("or_neumann_inverse", n, dtype)
 
 
 def l2_normalize(x, eps=1e-6):

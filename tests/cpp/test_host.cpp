@@ -243,6 +243,11 @@ void host_cases() {
   });
   expect_error("chunk_len_zero", DN_ERR_CHUNK_LEN, "chunk_len must be at least 1",
                [&] { good().run(DeltaPath::with_chunk_len(0)); });
+  // tri.rs:74-79.
+  expect_error("tri_square_block", DN_ERR_SHAPE, "unit_lower_inverse expects a square trailing block",
+               [&] { unit_lower_inverse(v4({3, 4, 5})); });
+  expect_error("tri_dtype", DN_ERR_DTYPE, "unit_lower_inverse: n_strict must be float32",
+               [&] { unit_lower_inverse(v4({3, 4, 4}, DType::BF16)); });
   expect_error("qkv_dtypes", DN_ERR_DTYPE, "q, k and v must share one dtype", [&] {
     DeltaInput in = good();
     in.q_bshk = v4({B, S, H, K}, DType::BF16);
@@ -582,6 +587,32 @@ void gpu_cases() {
     if (err > 1e-5) fail("out_norm closed form: max error " + std::to_string(err));
     ok("out_norm_closed_form");
   }
+  // unit_lower_inverse of a constant-key chunk, N = −β on the strict lower
+  // triangle: T[i][j] = −β(1 − β)^{i−j−1} below the diagonal (tri/tests.rs:
+  // 100-128), for both solves (the series only where it is conditioned).
+  for (const auto& [size, solve] : std::vector<std::pair<int64_t, TriSolve>>{
+           {40, TriSolve::Blocked}, {100, TriSolve::Blocked}, {12, TriSolve::Neumann}}) {
+    const double beta = 0.7;
+    Vec n(size_t(2 * size * size), 0.0), want(n.size(), 0.0);
+    for (int64_t b = 0; b < 2; ++b)
+      for (int64_t i = 0; i < size; ++i)
+        for (int64_t j = 0; j < size; ++j) {
+          const size_t at = size_t((b * size + i) * size + j);
+          if (j < i) {
+            n[at] = -beta;
+            want[at] = -beta * std::pow(1.0 - beta, double(i - j - 1));
+          } else if (i == j) {
+            want[at] = 1.0;
+          }
+        }
+    const Vec t = download(unit_lower_inverse(upload(n, {2, size, size}, DType::F32), solve));
+    double err = 0.0;
+    for (size_t i = 0; i < t.size(); ++i) err = std::max(err, std::fabs(t[i] - want[i]));
+    if (err > 1e-5)
+      fail("unit_lower_inverse closed form, size " + std::to_string(size) + ": max error " +
+           std::to_string(err));
+  }
+  ok("unit_lower_inverse_closed_form");
 }
 
 }  // namespace

@@ -267,3 +267,36 @@ def test_out_norm_rejects_invalid_arguments(over, code, msg):
         setattr(a, k, v)
     assert lib.dn_out_norm(ctypes.byref(a), None) == code
     assert msg in lib.dn_last_error().decode()
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(size=-1), -2, "at least 0"),
+    (dict(batch=-2), -2, "at least 0"),
+    (dict(size=1 << 21), -2, "too large"),
+    (dict(solve=2), -9, "DN_TRI_BLOCKED or DN_TRI_NEUMANN"),
+    (dict(solve=abi.DN_TRI_NEUMANN, size=abi.TRI_NEUMANN_MAX_SIZE + 1), -9, "up to 140"),
+    (dict(), -6, "NULL"),
+])
+def test_unit_lower_inverse_rejects_invalid_arguments(over, code, msg):
+    """dn_unit_lower_inverse's checks fire before any pointer is used (the
+    pointers here are NULL); the square-block assert of tri.rs:74-79 is the
+    mirrors' (tests/test_gpu_tri.py, tests/cpp/test_host.cpp)."""
+    lib = abi.lib()
+    a = abi.TriArgs()
+    a.batch, a.size, a.solve = 3, 16, abi.DN_TRI_BLOCKED
+    for k, v in over.items():
+        setattr(a, k, v)
+    assert lib.dn_unit_lower_inverse(ctypes.byref(a), None) == code
+    assert msg in lib.dn_last_error().decode()
+
+
+@pytest.mark.parametrize("batch,size", [(0, 16), (3, 0)])
+def test_unit_lower_inverse_of_nothing_is_a_no_op(batch, size):
+    a = abi.TriArgs()
+    a.batch, a.size, a.solve = batch, size, abi.DN_TRI_BLOCKED
+    assert abi.lib().dn_unit_lower_inverse(ctypes.byref(a), None) == 0
+
+
+def test_unit_lower_inverse_mirror_checks_the_square_block():
+    with pytest.raises(pkg.DeltaError, match="square trailing block"):
+        pkg.unit_lower_inverse(torch.zeros(2, 3, 4))

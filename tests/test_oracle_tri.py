@@ -45,3 +45,38 @@ def test_constant_key_chunk_stays_bounded(size, beta):
     t = O.unit_lower_inverse(n)
     i, j = 5, 2
     assert abs(t[i, j] - (-beta * (1 - beta) ** (i - j - 1))) < 1e-12
+
+
+@pytest.mark.parametrize("size", [1, 2, 3, 4, 5, 7, 8, 16, 32])
+def test_neumann_equals_the_ladder_on_strict_lower_input(rng, size):
+    """tri/tests.rs:40-46 and :50-82: where the series is conditioned both
+    solves are the same function; in float64 they agree to rounding."""
+    n = strict_lower(rng, 3, size, 0.3)
+    t = O.neumann_inverse(n)
+    assert np.abs(t - O.unit_lower_inverse(n)).max() < 1e-12
+    t32 = O.neumann_inverse(n, dtype=np.float32)
+    eye = np.eye(size)
+    assert np.abs((eye - n) @ t32 - eye).max() < 1e-3
+
+
+def test_neumann_multiplies_the_whole_matrix(rng):
+    """tri.rs:99-107 multiplies N as given (tri/tests.rs:55-58: the two solves
+    disagree about entries on and above the diagonal). On a full matrix the
+    result is the truncated series Σ_{j<size} Nʲ, formed here from numpy's
+    matrix powers; the ladder ignores those entries."""
+    size = 6
+    n = rng.normal(0.0, 0.2, (size, size))
+    want = sum(np.linalg.matrix_power(n, j) for j in range(size))
+    assert np.abs(O.neumann_inverse(n) - want).max() < 1e-12
+    assert np.abs(O.unit_lower_inverse(n) - O.unit_lower_inverse(np.tril(n, -1))).max() == 0.0
+
+
+def test_neumann_closed_form_on_a_constant_key_chunk():
+    """N = −β on the strict lower triangle, at a size where the series is still
+    conditioned in float64: T[i][j] = −β(1 − β)^{i−j−1} below the diagonal."""
+    size, beta = 8, 0.5
+    n = np.tril(np.full((size, size), -beta), -1)
+    t = O.neumann_inverse(n)
+    i, j = np.tril_indices(size, -1)
+    assert np.abs(t[i, j] - (-beta * (1 - beta) ** (i - j - 1))).max() < 1e-12
+    assert np.abs(np.diagonal(t) - 1.0).max() == 0.0
