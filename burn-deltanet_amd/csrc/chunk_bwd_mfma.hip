@@ -56,21 +56,34 @@ struct CbParams {
   // columns voff … voff + V − 1 of rows vs wide (v, dO, the write gate, dv,
   // S₀ and dS). pass 0: the only pass; 1: the first of several, whose
   // value-summed outputs go to the fp32 partials; 2: a middle one, added to
-  // them; 3: the last, which adds them and stores.
+  // them by atomics (nothing waits on them); 3: the last, which adds them and
+  // stores.
   int vs, voff, pass;
   float *pq, *pk, *pe, *pg, *pw;  // partials of d_q, d_k, d_erase, d_g, width-1 d_write
 };
 
 // A value-summed output (d_q, d_k, d_erase, d_g, a width-1 d_write): a sum
-// over the value axis, so over the passes (CbParams::pass).
+// over the value axis, so over the passes (CbParams::pass). The last pass
+// reads the partial here, a round trip before the store, unless the caller
+// loaded it ahead (st_last).
 template <class T>
 __device__ inline void st_sum(int pass, T* out, float* part, size_t i, float v) {
   if (pass == 1)
     part[i] = v;
   else if (pass == 2)
-    part[i] += v;
+    atomicAdd(part + i, v);
   else
     st(out, i, pass == 3 ? v + part[i] : v);
+}
+// st_sum with the last pass's partial already in `pre` (0 when not the last).
+template <class T>
+__device__ inline void st_pre(int pass, T* out, float* part, size_t i, float v, float pre) {
+  if (pass == 1)
+    part[i] = v;
+  else if (pass == 2)
+    atomicAdd(part + i, v);
+  else
+    st(out, i, v + pre);
 }
 
 __device__ inline uint16_t bf_bits(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
@@ -144,8 +157,12 @@ __device__ inline void stage_perm(uint16_t* R, int dst, const uint16_t* src, int
 // The 16 lower-or-diagonal and upper 16×16 tiles of a 64×64 matrix, two per
 // wave: tile t = wave + 8u is (t/4, t%4).
 
-template <int K, int V, bool PC, class TG>
+// LASTP (per-head gates, the last of several value passes): the partials
+// of the value-summed outputs are loaded at the start of phase D, so their
+// round trip overlaps the score backward instead of preceding each store.
+template <int K, int V, bool PC, class TG, bool LASTP = false>
 __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
+  static_assert(!(LASTP && PC), "the per-channel last pass reads its partials at the stores");
   constexpr bool F32DY = std::is_same<TG, float>::value;
   constexpr int TT = kL * kL, TK = kL * K, TV = kL * V;
   constexpr int OFF_A1 = 4 * TV > 8 * TT ? 4 * TV : 8 * TT;
@@ -783,6 +800,27 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   __syncthreads();
 
   // ---- phase D: score backward, gates, stores -----------------------------
+  // The last pass's partials: d_q and d_k at this lane's 16 rows and channel;
+  // the row sums (d_write, d_erase, d_g) at row `lane` (stored by wave 0).
+  float pre_q[16], pre_k[16], pre_w = 0.f, pre_e = 0.f, pre_g = 0.f;
+  if constexpr (LASTP) {
+    if (kwave) {
+#pragma unroll
+      for (int ib = 0; ib < 4; ++ib)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const size_t at = rowc(rowi(ib, r)) * K + c;
+          pre_q[4 * ib + r] = p.pq[at];
+          pre_k[4 * ib + r] = p.pk[at];
+        }
+    }
+    if (wave == 0) {
+      const size_t at = rowc(lane);
+      if (p.ww == 1) pre_w = p.pw[at];
+      pre_e = p.pe[at];
+      if (gated) pre_g = p.pg[at];
+    }
+  }
   if (kwave) {
     TG* gq = static_cast<TG*>(p.dq);
     TG* gk = static_cast<TG*>(p.dk);
@@ -1044,8 +1082,15 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
           const int i = rowi(ib, r);
           const bool ok = i < valid;
           if (ok) {
-            st_sum(p.pass, gq, p.pq, row_of(i) * K + c, dqA[ib][r] * p.scale);
-            st_sum(p.pass, gk, p.pk, row_of(i) * K + c, dkA[ib][r] + dkeA[ib][r] * er_s[i]);
+            const size_t at = row_of(i) * K + c;
+            const float vq = dqA[ib][r] * p.scale, vk = dkA[ib][r] + dkeA[ib][r] * er_s[i];
+            if constexpr (LASTP) {
+              st_pre(p.pass, gq, p.pq, at, vq, pre_q[4 * ib + r]);
+              st_pre(p.pass, gk, p.pk, at, vk, pre_k[4 * ib + r]);
+            } else {
+              st_sum(p.pass, gq, p.pq, at, vq);
+              st_sum(p.pass, gk, p.pk, at, vk);
+            }
           }
           rde[4 * ib + r] = dkeA[ib][r] * kv[r];
           if (p.ew != 1 && ok) st_sum(p.pass, p.derase, p.pe, row_of(i) * K + c, rde[4 * ib + r]);
@@ -1096,12 +1141,22 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
         const float t = __shfl_down(v, off);
         if (lane + off < 64) v += t;
       }
-      if (lane < valid) st_sum(p.pass, p.dg, p.pg, row_of(lane), v);
+      if (lane < valid) {
+        if constexpr (LASTP)
+          st_pre(p.pass, p.dg, p.pg, row_of(lane), v, pre_g);
+        else
+          st_sum(p.pass, p.dg, p.pg, row_of(lane), v);
+      }
     }
   }
   if (tid < valid) {
-    if (p.ww == 1) st_sum(p.pass, p.dwrite, p.pw, row_of(tid), racc[0][tid]);
-    if (p.ew == 1) st_sum(p.pass, p.derase, p.pe, row_of(tid), racc[1][tid]);
+    if constexpr (LASTP) {
+      if (p.ww == 1) st_pre(p.pass, p.dwrite, p.pw, row_of(tid), racc[0][tid], pre_w);
+      if (p.ew == 1) st_pre(p.pass, p.derase, p.pe, row_of(tid), racc[1][tid], pre_e);
+    } else {
+      if (p.ww == 1) st_sum(p.pass, p.dwrite, p.pw, row_of(tid), racc[0][tid]);
+      if (p.ew == 1) st_sum(p.pass, p.derase, p.pe, row_of(tid), racc[1][tid]);
+    }
   }
 }
 
@@ -1174,6 +1229,9 @@ hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const v
 #define DN_CB(KD, VD, PCV, TG)                                                                  \
   hipLaunchKernelGGL((mfma_chunk_bwd_kernel<KD, VD, PCV, TG>), dim3(unsigned(G)), dim3(kNT), 0, \
                      stream, p)
+#define DN_CB_L(KD, TG)                                                                        \
+  hipLaunchKernelGGL((mfma_chunk_bwd_kernel<KD, 128, false, TG, true>), dim3(unsigned(G)),      \
+                     dim3(kNT), 0, stream, p)
 #define DN_CB_T(KD, VD, PCV)              \
   do {                                    \
     if (f32) DN_CB(KD, VD, PCV, float);   \
@@ -1187,7 +1245,14 @@ hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const v
   for (int i = 0; i < passes; ++i) {
     p.voff = vd * i;
     p.pass = passes == 1 ? 0 : i == 0 ? 1 : i + 1 == passes ? 3 : 2;
-    if (d.K == 128) {
+    if (p.pass == 3 && !pc) {
+      // Several passes imply vd = 128.
+      if (d.K == 128) {
+        if (f32) DN_CB_L(128, float); else DN_CB_L(128, bf16);
+      } else {
+        if (f32) DN_CB_L(64, float); else DN_CB_L(64, bf16);
+      }
+    } else if (d.K == 128) {
       if (vd == 128) DN_CB_P(128, 128); else DN_CB_P(128, 64);
     } else {
       if (vd == 128) DN_CB_P(64, 128); else DN_CB_P(64, 64);
@@ -1196,6 +1261,7 @@ hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const v
     if (e != hipSuccess) return e;
   }
 #undef DN_CB_P
+#undef DN_CB_L
 #undef DN_CB_T
 #undef DN_CB
   return hipGetLastError();
