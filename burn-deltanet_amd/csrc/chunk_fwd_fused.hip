@@ -84,18 +84,6 @@ __device__ inline int opaque(int x) {
   return x;
 }
 
-// A workgroup barrier that orders LDS only: this wave's LDS accesses have
-// completed (lgkmcnt 0) when it arrives, and the compiler moves no memory
-// access across it. Unlike __syncthreads() it does not wait for HBM → LDS
-// copies still in flight, which the scan never reads before they are waited
-// for explicitly.
-__device__ inline void lds_barrier() {
-  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
 // σ⁻¹ of perm_pos (mfma_util.hpp): the row of Kcᵀ that holds key channel d.
 __device__ inline int perm_inv(int d) {
   return (d & ~31) + 16 * ((d >> 2) & 1) + 4 * ((d >> 3) & 3) + (d & 3);

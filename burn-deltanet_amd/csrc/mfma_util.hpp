@@ -67,6 +67,20 @@ __device__ inline int perm_pos(int k) {
 // Element (row, pos) of a tile with COLS bf16 per row; 16-byte chunks are
 // XOR-swizzled by row so the 16 rows of a fragment read land in 16 distinct
 // bank slots.
+// A workgroup barrier that orders LDS only: this wave's LDS accesses have
+// completed (lgkmcnt 0) when it arrives, and the compiler moves no memory
+// access across it. __syncthreads() also waits for every global load and
+// store in flight (vmcnt 0), so loads issued ahead of a barrier for use after
+// it would be waited for at the barrier; here they are waited for at their
+// first use. For barriers between waves that communicate through LDS only,
+// and for HBM → LDS copies that are waited for explicitly.
+__device__ inline void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 template <int COLS>
 __device__ inline int tile_at(int row, int pos) {
   const int sw = COLS >= 128 ? (row & 15) : ((row >> 1) & 7);
