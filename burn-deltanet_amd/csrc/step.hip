@@ -268,8 +268,16 @@ __global__ __launch_bounds__(kRowThreads) void step_row_kernel(StepParams p) {
 // the state held in registers from the first token to the last, so one call
 // reads and writes S once. Same work split as step_row_kernel: a workgroup
 // of 8 waves owns 64·C columns of one (head, batch) and all K rows; a lane
-// owns C columns of RPT rows. Per token the two key-axis reductions cross
-// the waves through LDS: two barriers per token, no traffic to S.
+// owns C columns of RPT rows. The key-axis reductions cross the waves
+// through LDS, two barriers per step. Tokens go two to a step: with α the
+// decay, kE = k⊙erase and q' = scale·q of tokens 1 and 2, one pass over S
+// gives the columns a = Sᵀ(α₁⊙kE₁), b = Sᵀ(α₁⊙q'₁), c = Sᵀ(α₁α₂⊙kE₂) and
+// d = Sᵀ(α₁α₂⊙q'₂), and then, per column,
+//   u₁ = vw₁ − a,  y₁ = b + (k₁·q'₁)·u₁,
+//   u₂ = vw₂ − c − ((α₂⊙k₁)·kE₂)·u₁,  y₂ = d + ((α₂⊙k₁)·q'₂)·u₁ + (k₂·q'₂)·u₂,
+//   S ← α₁α₂⊙S + (α₂⊙k₁)u₁ᵀ + k₂u₂ᵀ,
+// the two tokens' delta steps in closed form (the chunkwise WY form at two
+// tokens). A DeltaProduct decode token (u = 2 micro-steps) is one step.
 //
 // Token vectors are staged into LDS TB tokens at a time, every load of a
 // block issued before the first LDS write, and the next block is staged
@@ -279,7 +287,7 @@ __global__ __launch_bounds__(kRowThreads) void step_row_kernel(StepParams p) {
 // 0 included), so rows past K hold zeros throughout and every LDS read of a
 // row is one base register plus an immediate offset.
 template <class TQ, class TY, int RPT, int C>
-__global__ __launch_bounds__(kRowThreads) void recurrent_row_kernel(StepParams p) {
+__global__ __launch_bounds__(kRowThreads, RPT <= 16 ? 4 : 2) void recurrent_row_kernel(StepParams p) {
   constexpr int W = 64 * C;
   constexpr int KP = kRowWaves * RPT;          // padded rows
   constexpr int TB = 4;                        // tokens per staged block
@@ -289,17 +297,18 @@ __global__ __launch_bounds__(kRowThreads) void recurrent_row_kernel(StepParams p
   const int nblk = (p.V + W - 1) / W;
   const int cb = blockIdx.x % nblk, bh_id = blockIdx.x / nblk;
   const int h = bh_id % p.H, b = bh_id / p.H;
-  const int tid = threadIdx.x, lane = tid & 63, rg = tid >> 6;
+  // The wave index is uniform: as a scalar, every row index rg + 8r and the
+  // row offsets built on it stay out of the vector registers.
+  const int tid = threadIdx.x, lane = tid & 63, rg = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int K = p.K, V = p.V, S = p.S;
   const int jb = cb * W, j0 = jb + C * lane;
   const size_t bh = size_t(b) * p.H + h;
 
   __shared__ float tok[2][TB][4][KP];  // k, k⊙erase, scale·q, α per token
   __shared__ float vw[2][TB][W];       // v⊙write on the block's columns
-  __shared__ float red_r[kRowWaves][W];
-  __shared__ float red_q[kRowWaves][W];
-  __shared__ float s_u[W];
-  __shared__ float s_kq;
+  __shared__ float red[4][kRowWaves][W];  // per-wave partial sums of a, b, c, d
+  __shared__ float s_u[2][W];
+  __shared__ float s_dot[4];               // k₁·q'₁, (α₂⊙k₁)·kE₂, (α₂⊙k₁)·q'₂, k₂·q'₂
 
   const TQ* qp = static_cast<const TQ*>(p.q);
   const TQ* kp = static_cast<const TQ*>(p.k);
@@ -361,46 +370,109 @@ __global__ __launch_bounds__(kRowThreads) void recurrent_row_kernel(StepParams p
   for (int blk = 0; blk < nblocks; ++blk) {
     const int buf = blk & 1, t0 = blk * TB, tn = min(TB, S - t0);
 #pragma unroll 1
-    for (int tt = 0; tt < tn; ++tt) {
-      const float(*d)[KP] = tok[buf][tt];
-      if (tid < 64) {
-        float acc = 0.f;
+    for (int tt = 0; tt < tn;) {
+      const bool next = tt == 0 && blk + 1 < nblocks;  // stage the next block in this step
+      const size_t yrow = ((size_t(b) * S + t0 + tt) * p.H + h) * V + jb + tid;
+      if (tt + 1 < tn) {
+        // Tokens tt and tt + 1 as one step.
+        const float(*d1)[KP] = tok[buf][tt];
+        const float(*d2)[KP] = tok[buf][tt + 1];
+        // Wave w < 4 forms dot product w over the key axis.
+        if (rg < 4) {
+          float acc = 0.f;
 #pragma unroll
-        for (int i = tid; i < KP; i += 64) acc += d[0][i] * d[2][i];
-        acc = wave_sum(acc);
-        if (tid == 0) s_kq = acc;
-      }
-      // S⁻ = α⊙S, and the lane's partial sums of S⁻ᵀ(k⊙erase) and S⁻ᵀq'.
-      vec pr = vec(0.f), pq = vec(0.f);
-#pragma unroll
-      for (int r = 0; r < RPT; ++r) {
-        const int i = rg + kRowWaves * r;
-        s[r] *= d[3][i];
-        pr += s[r] * d[1][i];
-        pq += s[r] * d[2][i];
-      }
-      *reinterpret_cast<vec*>(&red_r[rg][C * lane]) = pr;
-      *reinterpret_cast<vec*>(&red_q[rg][C * lane]) = pq;
-      __syncthreads();
-      // u = v⊙write − S⁻ᵀ(k⊙erase), y = S⁻ᵀq' + u·(kᵀq') per column.
-      if (tid < W) {
-        const int j = jb + tid;
-        float rr = 0.f, qs = 0.f;
-#pragma unroll
-        for (int x = 0; x < kRowWaves; ++x) {
-          rr += red_r[x][tid];
-          qs += red_q[x][tid];
+          for (int i = lane; i < KP; i += 64) {
+            const float x = rg == 0 ? d1[0][i] : rg == 3 ? d2[0][i] : d1[0][i] * d2[3][i];
+            const float z = rg == 0 ? d1[2][i] : rg == 1 ? d2[1][i] : d2[2][i];
+            acc += x * z;
+          }
+          acc = wave_sum(acc);
+          if (lane == 0) s_dot[rg] = acc;
         }
-        const float u = vw[buf][tt][tid] - rr;
-        if (j < V) st(y, ((size_t(b) * S + t0 + tt) * p.H + h) * V + j, qs + u * s_kq);
-        s_u[tid] = u;
-      }
-      if (tt == 0 && blk + 1 < nblocks) stage(t0 + TB, buf ^ 1);
-      __syncthreads();
-      // S = S⁻ + k uᵀ.
-      const vec uv = *reinterpret_cast<const vec*>(&s_u[C * lane]);
+        vec pa = vec(0.f), pb = vec(0.f), pc = vec(0.f), pd = vec(0.f);
 #pragma unroll
-      for (int r = 0; r < RPT; ++r) s[r] += d[0][rg + kRowWaves * r] * uv;
+        for (int r = 0; r < RPT; ++r) {
+          const int i = rg + kRowWaves * r;
+          const float a1 = d1[3][i], a12 = a1 * d2[3][i];
+          pa += s[r] * (a1 * d1[1][i]);
+          pb += s[r] * (a1 * d1[2][i]);
+          pc += s[r] * (a12 * d2[1][i]);
+          pd += s[r] * (a12 * d2[2][i]);
+          s[r] *= a12;
+        }
+        *reinterpret_cast<vec*>(&red[0][rg][C * lane]) = pa;
+        *reinterpret_cast<vec*>(&red[1][rg][C * lane]) = pb;
+        *reinterpret_cast<vec*>(&red[2][rg][C * lane]) = pc;
+        *reinterpret_cast<vec*>(&red[3][rg][C * lane]) = pd;
+        __syncthreads();
+        if (tid < W) {
+          float a = 0.f, bq = 0.f, c = 0.f, dq = 0.f;
+#pragma unroll
+          for (int x = 0; x < kRowWaves; ++x) {
+            a += red[0][x][tid];
+            bq += red[1][x][tid];
+            c += red[2][x][tid];
+            dq += red[3][x][tid];
+          }
+          const float u1 = vw[buf][tt][tid] - a;
+          const float u2 = vw[buf][tt + 1][tid] - (c + u1 * s_dot[1]);
+          if (jb + tid < V) {
+            st(y, yrow, bq + u1 * s_dot[0]);
+            st(y, yrow + size_t(p.H) * V, dq + u1 * s_dot[2] + u2 * s_dot[3]);
+          }
+          s_u[0][tid] = u1;
+          s_u[1][tid] = u2;
+        }
+        if (next) stage(t0 + TB, buf ^ 1);
+        __syncthreads();
+        const vec u1v = *reinterpret_cast<const vec*>(&s_u[0][C * lane]);
+        const vec u2v = *reinterpret_cast<const vec*>(&s_u[1][C * lane]);
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) {
+          const int i = rg + kRowWaves * r;
+          s[r] += (d1[0][i] * d2[3][i]) * u1v + d2[0][i] * u2v;
+        }
+        tt += 2;
+      } else {
+        // The block's last token alone: S⁻ = α⊙S, u = vw − S⁻ᵀkE,
+        // y = S⁻ᵀq' + (k·q')u, S = S⁻ + kuᵀ.
+        const float(*d)[KP] = tok[buf][tt];
+        if (rg == 0) {
+          float acc = 0.f;
+#pragma unroll
+          for (int i = lane; i < KP; i += 64) acc += d[0][i] * d[2][i];
+          acc = wave_sum(acc);
+          if (lane == 0) s_dot[0] = acc;
+        }
+        vec pr = vec(0.f), pq = vec(0.f);
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) {
+          const int i = rg + kRowWaves * r;
+          s[r] *= d[3][i];
+          pr += s[r] * d[1][i];
+          pq += s[r] * d[2][i];
+        }
+        *reinterpret_cast<vec*>(&red[0][rg][C * lane]) = pr;
+        *reinterpret_cast<vec*>(&red[1][rg][C * lane]) = pq;
+        __syncthreads();
+        if (tid < W) {
+          float rr = 0.f, qs = 0.f;
+#pragma unroll
+          for (int x = 0; x < kRowWaves; ++x) {
+            rr += red[0][x][tid];
+            qs += red[1][x][tid];
+          }
+          const float u = vw[buf][tt][tid] - rr;
+          if (jb + tid < V) st(y, yrow, qs + u * s_dot[0]);
+          s_u[0][tid] = u;
+        }
+        if (next) stage(t0 + TB, buf ^ 1);
+        __syncthreads();
+        const vec uv = *reinterpret_cast<const vec*>(&s_u[0][C * lane]);
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) s[r] += d[0][rg + kRowWaves * r] * uv;
+        tt += 1;
+      }
     }
   }
   float* sout = p.s_out + bh * size_t(K) * V + j0;
