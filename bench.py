@@ -30,6 +30,7 @@ dk128) at 1 GPU; % roofline"):
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -250,6 +251,59 @@ def bench_out_norm(torch, pkg, steps, warmup):
             "roofline": _hbm(nbytes, k_ms) | {"kernel": "dn_out_norm",
                                                "traffic": traffic_from_profiles("dn_out_norm")},
             "kernels": kern}
+
+
+def bench_block_decode(torch, pkg, steps, warmup):
+    """One decode token of a Gated DeltaNet block after in_proj at the
+    config-3 shape (B=256, H=16, dk=128, dv=256; short conv of 4 with SiLU,
+    L2 q/k norm, scalar β, gated output norm; bf16 projection, window and
+    out, fp32 state updated in place): dn_block_step against the three calls
+    it fuses, dn_frontend's step (bf16 q/k/v), dn_step and dn_out_norm."""
+    B, H, K, V = 256, 16, 128, 256
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20260839)
+    proj = pkg.QkvProjection(nheads=H, head_k_dim=K, head_v_dim=V, has_gate=True)
+    proj.conv = pkg.ShortConv(torch.randn((proj.conv_dim(), 4), generator=gen, device=dev) * 0.5)
+    norm = pkg.OutNorm(torch.ones(V, device=dev), gated=True)
+    W = proj.d_in_proj()
+    p = torch.randn((B, W), generator=gen, device=dev).to(torch.bfloat16)
+    win = torch.randn((B, proj.conv_dim(), 4), generator=gen, device=dev).to(torch.bfloat16)
+    g = -torch.nn.functional.softplus(torch.randn((B, H, 1), generator=gen, device=dev)) * 0.05
+    s = torch.randn((B, H, K, V), generator=gen, device=dev) * 0.02
+    abi = pkg.abi
+    a, out, _, _, _, kept = pkg.frontend.block_step_args(proj, norm, p, win, g, s,
+                                                          out_dtype=torch.bfloat16, in_place=True)
+    fused_ms, fused_k = _timed(torch, abi, lambda: abi.run_block_step(a), steps, warmup)
+    # The three calls, bf16 between them.
+    q = torch.empty((B, 1, H, K), dtype=torch.bfloat16, device=dev)
+    k, v = torch.empty_like(q), torch.empty((B, 1, H, V), dtype=torch.bfloat16, device=dev)
+    beta = torch.empty((B, 1, H, 1), device=dev)
+    weight = proj.conv.weight.float().contiguous()
+    fe = abi.frontend_args(p.view(B, 1, W), weight, None, win, win, q, k, v, beta, beta,
+                           nheads=H, head_k_dim=K, head_v_dim=V, n_householder=1,
+                           conv_activation=abi.DN_ACT_SILU, qk_activation=abi.DN_ACT_SILU,
+                           qk_norm=abi.DN_QKNORM_L2, write_gate=abi.DN_WRITE_SCALAR,
+                           allow_neg_eigval=False)
+    y = torch.empty((B, H, V), dtype=torch.bfloat16, device=dev)
+    st = abi.step_args(q.view(B, H, K), k.view(B, H, K), v.view(B, H, V), beta.view(B, H, 1),
+                       beta.view(B, H, 1), g, s, y, s, None)
+    c0 = proj.conv_dim() + H
+    zg = p[:, c0:c0 + H * V].unflatten(1, (H, V))
+    on = abi.out_norm_args(y, zg, norm.weight, torch.empty_like(y), norm.eps)
+
+    def three():
+        abi.run_frontend(fe)
+        abi.check(abi.lib().dn_step(ctypes.byref(st), abi.stream_handle()))
+        abi.run_out_norm(on)
+    sep_ms, sep_k = _timed(torch, abi, three, steps, warmup)
+    nbytes = 2 * B * H * K * V * 4 + B * W * 2 + 2 * B * proj.conv_dim() * 4 * 2 + B * H * V * 2
+    del kept
+    return {"workload": "Gated DeltaNet block decode token after in_proj, config-3 shape "
+                        "(B=256 H=16 dk=128 dv=256), bf16 projection/window/out, fp32 state",
+            "fused_us": round(fused_ms * 1e3, 2), "three_calls_us": round(sep_ms * 1e3, 2),
+            "roofline": _hbm(nbytes, fused_ms), "kernels_fused": fused_k,
+            "kernels_three_calls": sep_k}
 
 
 def bench_unit_lower_inverse(torch, pkg, steps, warmup):
@@ -775,6 +829,10 @@ def main():
         print("[bench] output norm (dn_out_norm)", file=sys.stderr, flush=True)
         extra["out_norm"] = bench_out_norm(torch, pkg, args.extra_steps, MIN_WARMUP)
         print(f"[bench] out_norm {extra['out_norm']}", file=sys.stderr, flush=True)
+        torch.cuda.empty_cache()
+        print("[bench] block decode (dn_block_step)", file=sys.stderr, flush=True)
+        extra["block_decode"] = bench_block_decode(torch, pkg, args.extra_steps, MIN_WARMUP)
+        print(f"[bench] block_decode {extra['block_decode']}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
         print("[bench] unit_lower_inverse", file=sys.stderr, flush=True)
         extra["unit_lower_inverse"] = bench_unit_lower_inverse(torch, pkg, MIN_STEPS, MIN_WARMUP)

@@ -26,6 +26,7 @@ DN_WRITE_FIXED, DN_WRITE_SCALAR, DN_WRITE_CHANNEL = 0, 1, 2
 FRONTEND_MAX_HEAD_DIM, FRONTEND_MAX_KERNEL = 256, 8
 OUT_NORM_MAX_HEAD_DIM = 1024
 DN_TRI_BLOCKED, DN_TRI_NEUMANN = 0, 1
+BLOCK_STEP_MAX_HEAD_DIM = 256  # DN_BLOCK_STEP_MAX_HEAD_DIM (deltanet_core.h)
 TRI_NEUMANN_MAX_SIZE = 140  # DN_TRI_NEUMANN_MAX_SIZE (deltanet_core.h)
 
 STATUS = {
@@ -47,7 +48,7 @@ EXPORTS = [
     "dn_chunk_fwd_workspace_bytes",
     "dn_chunk_bwd_workspace_bytes", "dn_chunk_fwd_algo", "dn_chunk_bwd_algo",
     "dn_last_error", "dn_version", "dn_profile_enable", "dn_profile_read",
-    "dn_chunk_fwd_noalloc", "dn_unit_lower_inverse",
+    "dn_chunk_fwd_noalloc", "dn_unit_lower_inverse", "dn_block_step",
 ]
 NOALLOC_SCRATCH_BYTES = 64 << 20  # DN_NOALLOC_SCRATCH_BYTES (deltanet_core.h)
 
@@ -123,6 +124,20 @@ class OutNormArgs(ctypes.Structure):
     ]
 
 
+class BlockStepArgs(ctypes.Structure):
+    _fields_ = [
+        ("batch", _i64), ("nheads", _i64), ("head_k_dim", _i64), ("head_v_dim", _i64),
+        ("conv_kernel", _i64), ("proj_stride", _i64),
+        ("conv_activation", _i32), ("qk_activation", _i32), ("qk_norm", _i32),
+        ("write_gate", _i32), ("allow_neg_eigval", _i32), ("in_dtype", _i32),
+        ("out_dtype", _i32), ("has_gate", _i32), ("decay_width", _i64), ("scale", _f64),
+        ("eps", _f64), ("norm_gated", _i32), ("check_finite", _i32),
+        ("projected", _vp), ("conv_weight", _vp), ("conv_bias", _vp), ("window_in", _vp),
+        ("window_out", _vp), ("g", _vp), ("state_in", _vp), ("state_out", _vp),
+        ("norm_weight", _vp), ("out", _vp), ("y", _vp),
+    ]
+
+
 class TriArgs(ctypes.Structure):
     _fields_ = [
         ("batch", _i64), ("size", _i64), ("solve", _i32), ("check_finite", _i32),
@@ -156,6 +171,8 @@ def lib() -> ctypes.CDLL:
         L.dn_frontend.restype = ctypes.c_int
         L.dn_out_norm.argtypes = [ctypes.POINTER(OutNormArgs), _vp]
         L.dn_out_norm.restype = ctypes.c_int
+        L.dn_block_step.argtypes = [ctypes.POINTER(BlockStepArgs), _vp]
+        L.dn_block_step.restype = ctypes.c_int
         L.dn_unit_lower_inverse.argtypes = [ctypes.POINTER(TriArgs), _vp]
         L.dn_unit_lower_inverse.restype = ctypes.c_int
         L.dn_chunk_fwd_workspace_bytes.argtypes = [ctypes.POINTER(ChunkFwdArgs)]
@@ -364,6 +381,10 @@ def tri_args(n_strict, t, solve=DN_TRI_BLOCKED, check_finite=False) -> TriArgs:
     a.check_finite = 1 if check_finite else 0
     a.n_strict, a.t = _ptr(n_strict), _ptr(t)
     return a
+
+
+def run_block_step(args: BlockStepArgs) -> None:
+    check(lib().dn_block_step(ctypes.byref(args), stream_handle()))
 
 
 def run_unit_lower_inverse(args: TriArgs) -> None:

@@ -568,6 +568,83 @@ int dn_out_norm(const dn_out_norm_args* a, hipStream_t stream) {
   return DN_OK;
 }
 
+int dn_block_step(const dn_block_step_args* a, hipStream_t stream) {
+  g_last_error.clear();
+  if (!a) return fail(DN_ERR_NULL, "args is NULL");
+  if (a->batch < 1 || a->nheads < 1 || a->head_k_dim < 1 || a->head_v_dim < 1 ||
+      a->conv_kernel < 0)
+    return fail(DN_ERR_SHAPE, "batch, nheads, head_k_dim and head_v_dim must be at least 1, "
+                              "conv_kernel at least 0");
+  if (a->head_k_dim > DN_BLOCK_STEP_MAX_HEAD_DIM || a->head_v_dim > DN_BLOCK_STEP_MAX_HEAD_DIM)
+    return fail(DN_ERR_UNSUPPORTED, "dn_block_step supports head dims up to " +
+                                        std::to_string(DN_BLOCK_STEP_MAX_HEAD_DIM));
+  if (a->head_v_dim % block_step_cols(a->head_v_dim))
+    return fail(DN_ERR_UNSUPPORTED, "dn_block_step needs head_v_dim even above 64 and a "
+                                    "multiple of 4 above 128");
+  if (a->conv_kernel > DN_FRONTEND_MAX_KERNEL)
+    return fail(DN_ERR_UNSUPPORTED, "dn_block_step supports conv_kernel up to " +
+                                        std::to_string(DN_FRONTEND_MAX_KERNEL));
+  if (!valid_dtype(a->in_dtype) || !valid_dtype(a->out_dtype))
+    return fail(DN_ERR_DTYPE, "dtype must be DN_F32 or DN_BF16");
+  if (a->qk_norm == DN_QKNORM_SUM)
+    return fail(DN_ERR_UNSUPPORTED, "QkNorm::Sum is not offered (its epsilon is burn_stack's)");
+  if (a->qk_norm != DN_QKNORM_L2 && a->qk_norm != DN_QKNORM_NONE)
+    return fail(DN_ERR_SHAPE, "unknown qk_norm");
+  if (a->qk_activation < DN_ACT_IDENTITY || a->qk_activation > DN_ACT_ELU_PLUS_ONE)
+    return fail(DN_ERR_SHAPE, "unknown qk_activation");
+  if (a->conv_activation != DN_ACT_IDENTITY && a->conv_activation != DN_ACT_SILU)
+    return fail(DN_ERR_SHAPE, "conv_activation must be DN_ACT_SILU or DN_ACT_IDENTITY");
+  if (a->write_gate < DN_WRITE_FIXED || a->write_gate > DN_WRITE_CHANNEL)
+    return fail(DN_ERR_SHAPE, "unknown write_gate");
+  if (a->has_gate && a->decay_width != 1 && a->decay_width != a->head_k_dim)
+    return fail(DN_ERR_GATE_WIDTH, "forget gate: last axis must be 1 or " +
+                                       std::to_string(a->head_k_dim) + ", got " +
+                                       std::to_string(a->decay_width));
+  if (!(a->eps >= 0.0)) return fail(DN_ERR_SHAPE, "eps must be a non-negative number");
+  const bool has_conv = a->conv_kernel > 0;
+  if (has_conv != (a->window_in != nullptr) || has_conv != (a->window_out != nullptr))
+    return fail(DN_ERR_SHAPE, "convolution window presence must match the block's convolution");
+  const int64_t H = a->nheads, key_dim = H * a->head_k_dim, value_dim = H * a->head_v_dim;
+  const int64_t conv_dim = 2 * key_dim + value_dim;
+  const int64_t gate_w = a->write_gate == DN_WRITE_FIXED    ? 0
+                         : a->write_gate == DN_WRITE_SCALAR ? H
+                                                            : key_dim + value_dim;
+  const int64_t width = conv_dim + gate_w + (a->norm_gated ? value_dim : 0);
+  if (a->proj_stride < width)
+    return fail(DN_ERR_SHAPE, "proj_stride " + std::to_string(a->proj_stride) +
+                                  " is narrower than the conv, write-gate and norm-gate columns (" +
+                                  std::to_string(width) + ")");
+  if (a->batch * H >= (int64_t(1) << 31) || a->batch * a->proj_stride >= (int64_t(1) << 40))
+    return fail(DN_ERR_SHAPE, "tensor too large");
+  if (!a->projected || !a->state_in || !a->state_out || !a->norm_weight || !a->out ||
+      (has_conv && !a->conv_weight) || (a->has_gate && !a->g))
+    return fail(DN_ERR_NULL, "a required tensor pointer is NULL");
+  const int C = block_step_cols(a->head_v_dim);
+  if ((reinterpret_cast<uintptr_t>(a->state_in) | reinterpret_cast<uintptr_t>(a->state_out)) %
+      (4 * C))
+    return fail(DN_ERR_UNSUPPORTED, "dn_block_step needs the state aligned to " +
+                                        std::to_string(4 * C) + " bytes");
+  const size_t ns = size_t(a->batch) * H * a->head_k_dim * a->head_v_dim;
+  const size_t nw = has_conv ? size_t(a->batch) * conv_dim * a->conv_kernel : 0;
+  if (a->check_finite) {
+    std::vector<Guarded> in = {{a->projected, size_t(a->batch) * a->proj_stride, a->in_dtype},
+                               {a->window_in, nw, a->in_dtype},
+                               {a->has_gate ? a->g : nullptr, size_t(a->batch) * H * a->decay_width,
+                                DN_F32},
+                               {a->state_in, ns, DN_F32}};
+    if (int rc = nonfinite_check(in, stream, "inputs")) return rc;
+  }
+  hipError_t e = launch_block_step(*a, resolve_scale(a->scale, a->head_k_dim), stream);
+  if (e != hipSuccess) return hip_fail(e, "dn_block_step launch");
+  if (a->check_finite) {
+    std::vector<Guarded> out = {{a->out, size_t(a->batch) * value_dim, a->out_dtype},
+                                {a->window_out, nw, a->in_dtype},
+                                {a->state_out, ns, DN_F32}};
+    if (int rc = nonfinite_check(out, stream, "outputs")) return rc;
+  }
+  return DN_OK;
+}
+
 int dn_unit_lower_inverse(const dn_tri_args* a, hipStream_t stream) {
   g_last_error.clear();
   if (!a) return fail(DN_ERR_NULL, "args is NULL");

@@ -82,6 +82,8 @@ hipError_t launch_frontend(const dn_frontend_args& a, hipStream_t stream);
 // dn_out_norm: the per-head (gated) RMSNorm (out_norm.hip).
 hipError_t launch_out_norm(const dn_out_norm_args& a, hipStream_t stream);
 hipError_t launch_unit_lower_inverse(const dn_tri_args& a, hipStream_t stream);
+hipError_t launch_block_step(const dn_block_step_args& a, float scale, hipStream_t stream);
+int block_step_cols(int64_t head_v_dim);
 
 struct GenericFwdPlan {
   size_t ws_bytes;

@@ -27,6 +27,7 @@
 #include <algorithm>
 #include <type_traits>
 
+#include "activations.hpp"
 #include "dn_common.hpp"
 #include "mfma_util.hpp"
 
@@ -56,19 +57,6 @@ struct FrontParams {
   int post_act[3];     // activation after the convolution's (q/k: qk_activation, v: SiLU)
   int norm[3];         // 1: L2 over the head
 };
-
-// σ(x) = 1 / (1 + e^−x) with the hardware reciprocal (1 ulp).
-__device__ inline float sigmoidf_(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
-
-// QkActivation / ConvActivation (norm.rs:38-51, conv.rs:39-44).
-__device__ inline float activate(float x, int kind) {
-  switch (kind) {
-    case DN_ACT_SILU: return x * sigmoidf_(x);
-    case DN_ACT_RELU: return fmaxf(x, 0.f);
-    case DN_ACT_ELU_PLUS_ONE: return x < 0.f ? __expf(x) : x + 1.0f;
-    default: return x;
-  }
-}
 
 // Sum over each group of LPT lanes (16, 32 or 64), the result in every lane
 // of the group: DPP steps inside rows of 16 lanes, then a swizzle across the

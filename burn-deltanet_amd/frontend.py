@@ -283,3 +283,81 @@ class OutNorm:
         w = self.weight.float().contiguous()
         abi.run_out_norm(abi.out_norm_args(x, gate, w, out, self.eps))
         return out
+
+
+def block_step_args(proj: QkvProjection, norm: OutNorm, projected_bw: Tensor,
+                    conv_window_bwc: Optional[Tensor], g_bhK: Optional[Tensor],
+                    state_bhkv: Tensor, scale: Optional[float] = None, out_dtype=None,
+                    in_place: bool = False, return_y: bool = False, check_finite: bool = False):
+    """dn_block_step's arguments for `block_step` and the tensors it writes:
+    (args, out_bhv, next_window, next_state, y_bhv or None, kept) — `kept`
+    holds the converted inputs the arguments point into."""
+    from .delta import _dev
+    B, W = projected_bw.shape
+    if W != proj.d_in_proj():
+        raise DeltaError(-2, f"projection width {W} != d_in_proj {proj.d_in_proj()}")
+    if proj.n_householder != 1:
+        raise DeltaError(-9, "dn_block_step serves n_householder = 1 (dn_recurrent covers more)")
+    if (proj.conv is None) != (conv_window_bwc is None):
+        raise DeltaError(-2, "convolution window presence must match the block's convolution")
+    if norm.gated and not proj.has_gate:
+        raise DeltaError(-6, "OutNorm::Gated needs the projection's output gate")
+    H, dk, dv = proj.nheads, proj.head_k_dim, proj.head_v_dim
+    p = _dev(projected_bw)
+    state = _dev(state_bhkv, torch.float32)
+    g = _dev(g_bhK, torch.float32)
+    a = abi.BlockStepArgs()
+    a.batch, a.nheads, a.head_k_dim, a.head_v_dim = B, H, dk, dv
+    a.conv_kernel = proj.conv_kernel()
+    a.proj_stride = W
+    a.conv_activation = int(proj.conv.activation) if proj.conv is not None else 0
+    a.qk_activation, a.qk_norm = int(proj.qk_activation), int(proj.qk_norm)
+    a.write_gate, a.allow_neg_eigval = int(proj.write_gate), int(proj.allow_neg_eigval)
+    a.in_dtype = abi.dtype_tag(p.dtype)
+    od = p.dtype if out_dtype is None else out_dtype
+    a.out_dtype = abi.dtype_tag(od)
+    a.has_gate = 0 if g is None else 1
+    a.decay_width = 0 if g is None else g.shape[-1]
+    a.scale = abi.nan_scale(scale)  # NaN: 1/sqrt(head_k_dim)
+    a.eps = float(norm.eps)
+    a.norm_gated = int(norm.gated)
+    a.check_finite = int(check_finite)
+    kept = [p, state, g]
+    win_out = None
+    if proj.conv is not None:
+        weight = proj.conv.weight.reshape(proj.conv_dim(), -1).float().contiguous()
+        bias = None if proj.conv.bias is None else proj.conv.bias.float().contiguous()
+        win_in = conv_window_bwc.to(p.dtype).contiguous()
+        win_out = win_in if (in_place and win_in is conv_window_bwc) else torch.empty_like(win_in)
+        a.conv_weight, a.conv_bias = weight.data_ptr(), None if bias is None else bias.data_ptr()
+        a.window_in, a.window_out = win_in.data_ptr(), win_out.data_ptr()
+        kept += [weight, bias, win_in]
+    s_out = state if (in_place and state is state_bhkv) else torch.empty_like(state)
+    gamma = norm.weight.float().contiguous()
+    out = torch.empty((B, H, dv), dtype=od, device=p.device)
+    y = torch.empty((B, H, dv), dtype=torch.float32, device=p.device) if return_y else None
+    a.projected, a.g = p.data_ptr(), None if g is None else g.data_ptr()
+    a.state_in, a.state_out = state.data_ptr(), s_out.data_ptr()
+    a.norm_weight, a.out = gamma.data_ptr(), out.data_ptr()
+    a.y = None if y is None else y.data_ptr()
+    kept.append(gamma)
+    return a, out, win_out, s_out, y, kept
+
+
+def block_step(proj: QkvProjection, norm: OutNorm, projected_bw: Tensor,
+               conv_window_bwc: Optional[Tensor], g_bhK: Optional[Tensor], state_bhkv: Tensor,
+               scale: Optional[float] = None, out_dtype=None, in_place: bool = False,
+               return_y: bool = False, check_finite: bool = False):
+    """One decode token of a delta-rule block between in_proj and out_proj in
+    one launch (dn_block_step): `proj.step_projected`, `delta_step` and
+    `norm.forward`, as gated_deltanet_1.rs:218-234 runs them, given the forget
+    gate g = log α ([batch, nheads, 1 | head_k_dim], or None). q, k, v and y
+    stay in fp32 between the stages. Returns (out_bhv, next_window,
+    next_state[, y_bhv]); with in_place the state and the window are updated
+    where they are."""
+    a, out, win_out, s_out, y, kept = block_step_args(
+        proj, norm, projected_bw, conv_window_bwc, g_bhK, state_bhkv, scale, out_dtype,
+        in_place, return_y, check_finite)
+    abi.run_block_step(a)
+    del kept
+    return (out, win_out, s_out, y) if return_y else (out, win_out, s_out)

@@ -613,4 +613,65 @@ Tensor OutNorm::forward(const Tensor& x, const std::optional<Tensor>& gate,
   return out;
 }
 
+Tensor block_step(const QkvProjection& proj, const OutNorm& norm, const Tensor& projected_bw,
+                  const std::optional<Tensor>& conv_window_bwc,
+                  const std::optional<Tensor>& g_bhK, Tensor& state_bhkv, double scale,
+                  hipStream_t stream, std::optional<DType> out_dtype, bool check_finite) {
+  require_defined(projected_bw, "projected");
+  if (projected_bw.rank() != 2 || projected_bw.dim(1) != proj.d_in_proj())
+    throw Error(DN_ERR_SHAPE, "projected: expected [batch, " + std::to_string(proj.d_in_proj()) +
+                                  "]");
+  if (proj.n_householder != 1)
+    throw Error(DN_ERR_UNSUPPORTED, "dn_block_step serves n_householder = 1");
+  if (proj.conv.has_value() != conv_window_bwc.has_value())
+    throw Error(DN_ERR_SHAPE, "convolution window presence must match the block's convolution");
+  if (norm.gated && !proj.has_gate)
+    throw Error(DN_ERR_NULL, "OutNorm::Gated needs the projection's output gate");
+  const int64_t B = projected_bw.dim(0), H = proj.nheads, dk = proj.head_k_dim,
+                dv = proj.head_v_dim;
+  require_f32(state_bhkv, "state");
+  if (state_bhkv.dims() != std::vector<int64_t>{B, H, dk, dv})
+    throw Error(DN_ERR_SHAPE, "state: expected [batch, nheads, head_k_dim, head_v_dim]");
+  if (g_bhK) require_f32(*g_bhK, "forget gate");
+  require_f32(norm.weight, "norm weight");
+  if (conv_window_bwc && conv_window_bwc->dtype() != projected_bw.dtype())
+    throw Error(DN_ERR_DTYPE, "conv window: expected the projection's dtype");
+  Tensor out = Tensor::empty({B, H, dv}, out_dtype.value_or(projected_bw.dtype()));
+  dn_block_step_args a{};
+  a.batch = B;
+  a.nheads = H;
+  a.head_k_dim = dk;
+  a.head_v_dim = dv;
+  a.conv_kernel = proj.conv_kernel();
+  a.proj_stride = proj.d_in_proj();
+  a.conv_activation = proj.conv ? int32_t(proj.conv->activation) : DN_ACT_IDENTITY;
+  a.qk_activation = int32_t(proj.qk_activation);
+  a.qk_norm = int32_t(proj.qk_norm);
+  a.write_gate = int32_t(proj.write_gate);
+  a.allow_neg_eigval = proj.allow_neg_eigval;
+  a.in_dtype = int32_t(projected_bw.dtype());
+  a.out_dtype = int32_t(out.dtype());
+  a.has_gate = g_bhK.has_value();
+  a.decay_width = g_bhK ? g_bhK->dim(g_bhK->rank() - 1) : 0;
+  a.scale = scale;
+  a.eps = norm.eps;
+  a.norm_gated = norm.gated;
+  a.check_finite = check_finite;
+  a.projected = projected_bw.data();
+  if (proj.conv) {
+    require_f32(proj.conv->weight, "conv weight");
+    a.conv_weight = static_cast<const float*>(proj.conv->weight.data());
+    a.conv_bias = proj.conv->bias ? static_cast<const float*>(proj.conv->bias->data()) : nullptr;
+    a.window_in = conv_window_bwc->data();
+    a.window_out = conv_window_bwc->data();
+  }
+  a.g = g_bhK ? static_cast<const float*>(g_bhK->data()) : nullptr;
+  a.state_in = static_cast<const float*>(state_bhkv.data());
+  a.state_out = static_cast<float*>(state_bhkv.data());
+  a.norm_weight = static_cast<const float*>(norm.weight.data());
+  a.out = out.data();
+  check(dn_block_step(&a, stream));
+  return out;
+}
+
 }  // namespace deltanet

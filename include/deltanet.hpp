@@ -9,6 +9,8 @@
 //   DeltaChunkGrads, combined_backward    src/delta/chunk_recalculated/
 //                                         combined_backward.rs:50-189
 //   TriSolve, unit_lower_inverse          src/delta/tri.rs:53-114
+//   QkvProjection, OutNorm, block_step    src/common/qkv.rs, norm.rs, and
+//                                         gated_deltanet_1.rs:218-234
 // Every computation is a call through the C ABI of deltanet_core.h. Where
 // the reference panics on an assert!, these functions throw deltanet::Error
 // carrying the same message (and the dn_status the C ABI uses for it).
@@ -279,6 +281,20 @@ struct OutNorm {
                  int64_t gate_token_stride = 0, hipStream_t stream = nullptr,
                  std::optional<DType> out_dtype = std::nullopt) const;
 };
+
+// One decode token of a delta-rule block between in_proj and out_proj in one
+// launch (dn_block_step): proj.step_projected, delta_step and norm.forward as
+// gated_deltanet_1.rs:218-234 runs them, given the forget gate g = log α
+// [batch, nheads, 1 | head_k_dim] (nullopt: no decay); q, k, v and y stay in
+// fp32 between the stages. The state [batch, nheads, head_k_dim, head_v_dim]
+// and the conv window are updated in place; returns out [batch, nheads,
+// head_v_dim] in `out_dtype` (default: the projection's dtype).
+// n_householder = 1, head dims up to DN_BLOCK_STEP_MAX_HEAD_DIM.
+Tensor block_step(const QkvProjection& proj, const OutNorm& norm, const Tensor& projected_bw,
+                  const std::optional<Tensor>& conv_window_bwc,
+                  const std::optional<Tensor>& g_bhK, Tensor& state_bhkv, double scale,
+                  hipStream_t stream = nullptr, std::optional<DType> out_dtype = std::nullopt,
+                  bool check_finite = false);
 
 }  // namespace deltanet
 

@@ -276,6 +276,52 @@ typedef struct {
  * gated_deltanet_2.rs:282, 367; delta_product.rs:230, 306). */
 int dn_out_norm(const dn_out_norm_args *args, hipStream_t stream);
 
+/* One decode token of a delta-rule block between its in_proj and out_proj
+ * GEMMs, in one launch: QkvProjection::step (src/common/qkv.rs:454-516: the
+ * short-convolution step with its rolling window, the activations, the q/k
+ * L2 norm, the write gates), delta_step (src/delta/recurrent.rs:41-99) on the
+ * state, and OutNorm::forward (src/common/norm.rs:127-134): what a Gated
+ * DeltaNet block's step (gated_deltanet_1.rs:218-234) runs there, given its
+ * forget gate. Same fields and meaning as dn_frontend (sequence 1), dn_step
+ * and dn_out_norm, whose composition it equals, with q, k, v and y kept in
+ * fp32 between the stages. The output norm's gate, when present, is the
+ * projection's segment after the write gates (qkv.rs:237-262), read in place.
+ * One workgroup owns a (batch, head): n_householder = 1, head_k_dim and
+ * head_v_dim up to DN_BLOCK_STEP_MAX_HEAD_DIM; other shapes return
+ * DN_ERR_UNSUPPORTED (the three separate calls cover them). */
+#define DN_BLOCK_STEP_MAX_HEAD_DIM 256
+typedef struct {
+  int64_t batch, nheads, head_k_dim, head_v_dim;
+  int64_t conv_kernel;          /* 0: no short convolution; else 1..DN_FRONTEND_MAX_KERNEL */
+  int64_t proj_stride;          /* elements from one batch row of the projection to the next */
+  int32_t conv_activation;      /* DN_ACT_SILU or DN_ACT_IDENTITY */
+  int32_t qk_activation;        /* dn_activation */
+  int32_t qk_norm;              /* DN_QKNORM_L2 or DN_QKNORM_NONE */
+  int32_t write_gate;           /* dn_write_gate */
+  int32_t allow_neg_eigval;
+  int32_t in_dtype;             /* projected and the windows: DN_F32 or DN_BF16 */
+  int32_t out_dtype;            /* out: DN_F32 or DN_BF16 */
+  int32_t has_gate;             /* forget gate present */
+  int64_t decay_width;          /* 1 or head_k_dim, read when has_gate */
+  double scale;                 /* NaN => 1/sqrt(head_k_dim) */
+  double eps;                   /* the output norm's epsilon */
+  int32_t norm_gated;           /* OutNorm::Gated (the gate segment follows the write gates) */
+  int32_t check_finite;
+  const void *projected;        /* [batch, proj_stride] */
+  const float *conv_weight;     /* [conv_dim, conv_kernel] */
+  const float *conv_bias;       /* [conv_dim] or NULL */
+  const void *window_in;        /* [batch, conv_dim, conv_kernel], newest column last */
+  void *window_out;             /* same shape; may alias window_in */
+  const float *g;               /* [batch, nheads, decay_width] log forget gate */
+  const float *state_in;        /* [batch, nheads, head_k_dim, head_v_dim] */
+  float *state_out;             /* may alias state_in */
+  const float *norm_weight;     /* gamma [head_v_dim] */
+  void *out;                    /* [batch, nheads, head_v_dim] */
+  float *y;                     /* optional [batch, nheads, head_v_dim]: the output before the norm */
+} dn_block_step_args;
+
+int dn_block_step(const dn_block_step_args *args, hipStream_t stream);
+
 /* How unit_lower_inverse inverts I − N (TriSolve, src/delta/tri.rs:53-64). */
 typedef enum {
   DN_TRI_BLOCKED = 0, /* the exact inverse without powers of N (the default) */

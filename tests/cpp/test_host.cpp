@@ -243,6 +243,20 @@ void host_cases() {
   });
   expect_error("chunk_len_zero", DN_ERR_CHUNK_LEN, "chunk_len must be at least 1",
                [&] { good().run(DeltaPath::with_chunk_len(0)); });
+  {
+    QkvProjection pr;
+    pr.nheads = 2;
+    pr.head_k_dim = 4;
+    pr.head_v_dim = 6;
+    pr.n_householder = 2;
+    Tensor st = Tensor::view(fake, {1, 2, 4, 6}, DType::F32);
+    expect_error("block_step_householder", DN_ERR_UNSUPPORTED,
+                 "dn_block_step serves n_householder = 1", [&] {
+                   block_step(pr, OutNorm{Tensor::view(fake, {6}, DType::F32), false},
+                              Tensor::view(fake, {1, pr.d_in_proj()}, DType::F32), std::nullopt,
+                              std::nullopt, st, 0.5);
+                 });
+  }
   // tri.rs:74-79.
   expect_error("tri_square_block", DN_ERR_SHAPE, "unit_lower_inverse expects a square trailing block",
                [&] { unit_lower_inverse(v4({3, 4, 5})); });
@@ -613,6 +627,41 @@ void gpu_cases() {
            std::to_string(err));
   }
   ok("unit_lower_inverse_closed_form");
+  // block_step (dn_block_step) equals step_projected + delta_step + OutNorm::forward
+  // on the same token, fp32 throughout; the state and window updated in place.
+  {
+    const int64_t B = 3, H = 2, dk = 32, dv = 64, KC = 4;
+    QkvProjection pr;
+    pr.nheads = H;
+    pr.head_k_dim = dk;
+    pr.head_v_dim = dv;
+    pr.has_gate = true;
+    const int64_t cd = pr.conv_dim(), W = pr.d_in_proj();
+    Rng r(11);
+    Vec wt = r.normals(size_t(cd * KC), 0.5), raw = r.normals(size_t(B * W));
+    Vec win = r.normals(size_t(B * cd * KC)), st0 = r.normals(size_t(B * H * dk * dv), 0.1);
+    Vec gv(size_t(B * H), 0.0), gam(size_t(dv), 0.0);
+    for (size_t i = 0; i < gv.size(); ++i) gv[i] = -0.05 * double(1 + i % 5);
+    for (int64_t i = 0; i < dv; ++i) gam[size_t(i)] = 1.0 + 0.01 * double(i);
+    pr.conv = ShortConv{upload(wt, {cd, KC}, DType::F32), std::nullopt, ConvActivation::Silu};
+    OutNorm norm{upload(gam, {dv}, DType::F32), true, 1e-5};
+    Tensor tp = upload(raw, {B, W}, DType::F32), tg = upload(gv, {B, H, 1}, DType::F32);
+    const double scale = 1.0 / std::sqrt(double(dk));
+    auto [st, wn] = pr.step_projected(tp, upload(win, {B, cd, KC}, DType::F32));
+    auto [y, s_ref] = delta_step(st.q_bhk, st.k_buhk.reshape({B, H, dk}),
+                                 st.v_buhv.reshape({B, H, dv}), st.erase_buhK.reshape({B, H, 1}),
+                                 st.write_buhV.reshape({B, H, 1}), tg,
+                                 upload(st0, {B, H, dk, dv}, DType::F32), scale);
+    const int64_t gc = cd + pr.write_gate_width();
+    Tensor zg = Tensor::view(static_cast<float*>(tp.data()) + gc, {B, H, dv}, DType::F32);
+    const Vec want = download(norm.forward(y, zg, W));
+    Tensor s = upload(st0, {B, H, dk, dv}, DType::F32), tw = upload(win, {B, cd, KC}, DType::F32);
+    const Vec got = download(block_step(pr, norm, tp, tw, tg, s, scale));
+    expect_close("block_step_out", got, want, 1e-5);
+    expect_close("block_step_state", download(s), download(s_ref), 1e-5);
+    if (rel_err(download(tw), download(*wn)) != 0.0) fail("block_step: window");
+    ok("block_step_equals_three_calls");
+  }
 }
 
 }  // namespace

@@ -300,3 +300,39 @@ def test_unit_lower_inverse_of_nothing_is_a_no_op(batch, size):
 def test_unit_lower_inverse_mirror_checks_the_square_block():
     with pytest.raises(pkg.DeltaError, match="square trailing block"):
         pkg.unit_lower_inverse(torch.zeros(2, 3, 4))
+
+
+def block_step_args(**over):
+    a = abi.BlockStepArgs()
+    a.batch, a.nheads, a.head_k_dim, a.head_v_dim = 2, 2, 16, 64
+    a.conv_kernel, a.proj_stride = 0, 2 * 2 * 16 + 2 * 64 + 2 + 2 * 64
+    a.conv_activation, a.qk_activation = abi.DN_ACT_SILU, abi.DN_ACT_SILU
+    a.qk_norm, a.write_gate = abi.DN_QKNORM_L2, abi.DN_WRITE_SCALAR
+    a.in_dtype = a.out_dtype = abi.DN_F32
+    a.has_gate, a.decay_width, a.scale, a.eps, a.norm_gated = 1, 1, float("nan"), 1e-5, 1
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(batch=0), -2, "at least 1"),
+    (dict(head_v_dim=300), -9, "up to 256"),
+    (dict(head_v_dim=130), -9, "multiple of 4 above 128"),
+    (dict(conv_kernel=9), -9, "conv_kernel up to 8"),
+    (dict(in_dtype=3), -7, "dtype"),
+    (dict(qk_norm=abi.DN_QKNORM_SUM), -9, "QkNorm::Sum"),
+    (dict(write_gate=5), -2, "unknown write_gate"),
+    (dict(decay_width=3), -3, "forget gate: last axis must be 1 or 16, got 3"),
+    (dict(eps=-1.0), -2, "eps"),
+    (dict(conv_kernel=4), -2, "window presence"),
+    (dict(proj_stride=100), -2, "narrower than the conv, write-gate and norm-gate columns"),
+    (dict(), -6, "NULL"),
+])
+def test_block_step_rejects_invalid_arguments(over, code, msg):
+    """dn_block_step's checks fire before any pointer is used (all NULL here):
+    dn_frontend's, dn_step's and dn_out_norm's, and its own limits."""
+    lib = abi.lib()
+    a = block_step_args(**over)
+    assert lib.dn_block_step(ctypes.byref(a), None) == code
+    assert msg in lib.dn_last_error().decode()
