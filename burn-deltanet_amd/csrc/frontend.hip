@@ -35,6 +35,7 @@ namespace dn {
 namespace {
 
 constexpr int kFrontThreads = 256;  // 4 waves
+constexpr int kRowsMaxSeq = 16;     // sequences up to this take frontend_rows_kernel
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
 struct FrontParams {
@@ -47,6 +48,9 @@ struct FrontParams {
   int conv_dim;        // channels of the convolution (window rows)
   int D;               // head width of this launch's units
   int conv_act;        // applied to the convolution's output
+  int win_vec;         // conv length 4 with 16-byte weight rows and aligned windows
+  int rows_win;        // the rows kernel writes the next window (one token, win_vec)
+  void* wout;          // window_out
   // Up to three unit groups (q, k, v) of head width D in one launch: group g
   // has n[g] units starting at input channel ch0[g], writes nu[g] units per
   // token to out[g], then its activation and norm.
@@ -369,6 +373,162 @@ __global__ __launch_bounds__(kFrontThreads) void frontend_window_kernel(FrontPar
     if (j < p.K) st(wout, j, v[j]);
 }
 
+// Short sequences (a decode step is one token): a lane row per (batch, token)
+// row of one unit instead of per TL tokens of one sequence, so a one-token
+// call fills the lanes (the sequence layout leaves 15 of 16 lane rows idle).
+// A token's earlier conv inputs come from the projection or, before the
+// sequence, from the window, per lane row. Same arithmetic in the same order
+// as frontend_heads_kernel. KT = 4: a channel's 4 weights and its window row
+// are one vector load each; KT < 0: any conv length up to
+// DN_FRONTEND_MAX_KERNEL, element loads; KT = 0: no conv. Vector-aligned rows
+// only. WIN (one token per sequence): the lane row also writes the next
+// window of its channels, [window[1:], x], from the values it read (no other
+// lane reads that row, so window_out may alias window_in).
+template <class TI, class TO, int LPT, int CPL, int KT, bool FSILU, bool WIN>
+__global__ __launch_bounds__(kFrontThreads) void frontend_rows_kernel(FrontParams p) {
+  constexpr int R = 64 / LPT;
+  constexpr int RB = 4 * R;  // (batch, token) rows per workgroup
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int row = lane / LPT, l = lane % LPT;
+  const int units = p.n[0] + p.n[1] + p.n[2];
+  const int unit = blockIdx.x % units;
+  const int64_t nrow = int64_t(p.B) * p.S;
+  const int64_t rid = int64_t(blockIdx.x / units) * RB + wave * R + row;
+  // Rows past the end run on the last row (their lanes take part in no
+  // other row's reduction) and store nothing.
+  const int64_t rc = rid < nrow ? rid : nrow - 1;
+  const int b = int(rc / p.S), t = int(rc - int64_t(b) * p.S);
+  const int g = unit < p.n[0] ? 0 : unit < p.n[0] + p.n[1] ? 1 : 2;
+  const int r = unit - (g == 0 ? 0 : g == 1 ? p.n[0] : p.n[0] + p.n[1]);
+  const int D = p.D, c0 = l * CPL;
+  const int K = KT >= 0 ? KT : p.K;
+  const int ch = p.ch0[g] + r * D + c0;
+  const TI* proj = static_cast<const TI*>(p.proj) + size_t(b) * p.S * p.stride + ch;
+  float x[CPL];
+  load_n<TI, CPL, true>(proj + size_t(t) * p.stride, x, CPL);
+  if (K > 0) {
+    float y[CPL];
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) y[i] = p.bias ? p.bias[ch + i] : 0.f;
+    const size_t wrow = size_t(b) * p.conv_dim + ch;  // window row of channel ch
+    if constexpr (KT == 4) {
+      // Taps 0..3 weigh x[t−3], x[t−2], x[t−1], x[t].
+      float w[CPL][4], xv[CPL][4];
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        const float4 w4 = *reinterpret_cast<const float4*>(p.w + size_t(ch + i) * 4);
+        w[i][0] = w4.x;
+        w[i][1] = w4.y;
+        w[i][2] = w4.z;
+        w[i][3] = w4.w;
+      }
+      if (t < 3) {  // the window supplies x[t−3 .. −1]: window[tp + 4] holds x[tp]
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+          const TI* wr = static_cast<const TI*>(p.win) + (wrow + i) * 4;
+          if constexpr (sizeof(TI) == 2) {
+            const uint2 u = *reinterpret_cast<const uint2*>(wr);
+            xv[i][0] = __uint_as_float(u.x << 16);
+            xv[i][1] = __uint_as_float(u.x & 0xffff0000u);
+            xv[i][2] = __uint_as_float(u.y << 16);
+            xv[i][3] = __uint_as_float(u.y & 0xffff0000u);
+          } else {
+            const float4 u = *reinterpret_cast<const float4*>(wr);
+            xv[i][0] = u.x;
+            xv[i][1] = u.y;
+            xv[i][2] = u.z;
+            xv[i][3] = u.w;
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const int tp = t - 3 + j;
+        if (tp >= 0) {
+          float pv[CPL];
+          load_n<TI, CPL, true>(proj + size_t(tp) * p.stride, pv, CPL);
+#pragma unroll
+          for (int i = 0; i < CPL; ++i) xv[i][j] = pv[i];
+        } else {
+#pragma unroll
+          for (int i = 0; i < CPL; ++i) xv[i][j] = xv[i][tp + 4];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < CPL; ++i) {
+        xv[i][3] = x[i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) y[i] = fmaf(w[i][j], xv[i][j], y[i]);
+      }
+      if constexpr (WIN) {
+        // The next window (one token): the padded input [window[1:], x],
+        // which is this token's four taps (bf16 values round-trip exactly).
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) {
+          TI* wo = static_cast<TI*>(p.wout) + (wrow + i) * 4;
+          if constexpr (sizeof(TI) == 2)
+            *reinterpret_cast<uint2*>(wo) = make_uint2(pk_bf16(xv[i][0], xv[i][1]),
+                                                       pk_bf16(xv[i][2], xv[i][3]));
+          else
+            *reinterpret_cast<float4*>(wo) = make_float4(xv[i][0], xv[i][1], xv[i][2], xv[i][3]);
+        }
+      }
+    } else {
+      // Tap j weighs x[t − (K−1−j)].
+      for (int j = 0; j < K; ++j) {
+        const int tp = t - (K - 1 - j);
+        float xv[CPL];
+        if (tp == t) {
+#pragma unroll
+          for (int i = 0; i < CPL; ++i) xv[i] = x[i];
+        } else if (tp >= 0) {
+          load_n<TI, CPL, true>(proj + size_t(tp) * p.stride, xv, CPL);
+        } else {  // window[tp + K] holds x[tp] for −(K−1) ≤ tp < 0
+#pragma unroll
+          for (int i = 0; i < CPL; ++i)
+            xv[i] = ld(static_cast<const TI*>(p.win), (wrow + i) * K + tp + K);
+        }
+#pragma unroll
+        for (int i = 0; i < CPL; ++i) y[i] = fmaf(p.w[size_t(ch + i) * K + j], xv[i], y[i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) x[i] = FSILU ? y[i] * sigmoidf_(y[i]) : activate(y[i], p.conv_act);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    if constexpr (!FSILU) x[i] = activate(x[i], p.post_act[g]);
+    ss = fmaf(x[i], x[i], ss);
+  }
+  if (p.norm[g]) {
+    const float inv = rsqrtf(group_sum<LPT>(ss) + 1e-6f);  // norm.rs:83-90
+#pragma unroll
+    for (int i = 0; i < CPL; ++i) x[i] *= inv;
+  }
+  if (rid < nrow)
+    store_n<TO, CPL, true>(static_cast<TO*>(p.out[g]) + (size_t(rc) * p.nu[g] + r) * D + c0, x,
+                           CPL);
+}
+
+template <class TI, class TO, int LPT, int CPL, int KT, bool FSILU, bool WIN>
+void launch_rows(const FrontParams& p, hipStream_t stream) {
+  constexpr int RB = 4 * (64 / LPT);
+  const int64_t nblk = (int64_t(p.B) * p.S + RB - 1) / RB;
+  const unsigned grid = unsigned(nblk * (p.n[0] + p.n[1] + p.n[2]));
+  hipLaunchKernelGGL((frontend_rows_kernel<TI, TO, LPT, CPL, KT, FSILU, WIN>), dim3(grid),
+                     dim3(kFrontThreads), 0, stream, p);
+}
+
+template <class TI, class TO, int KT, bool FSILU, bool WIN>
+void launch_rows_vec(const FrontParams& p, int lpt, int cpl, hipStream_t stream) {
+  if (lpt == 32) return launch_rows<TI, TO, 32, 8, KT, FSILU, WIN>(p, stream);  // D = 256
+  if (cpl == 8) return launch_rows<TI, TO, 16, 8, KT, FSILU, WIN>(p, stream);
+  if (cpl == 4) return launch_rows<TI, TO, 16, 4, KT, FSILU, WIN>(p, stream);
+  if (cpl == 2) return launch_rows<TI, TO, 16, 2, KT, FSILU, WIN>(p, stream);
+  return launch_rows<TI, TO, 16, 1, KT, FSILU, WIN>(p, stream);
+}
+
 template <class TI, class TO, int LPT, int CPL, int TL, int KT, bool GENERIC, bool FSILU = false>
 void launch_heads(const FrontParams& p, hipStream_t stream) {
   constexpr int TB = 4 * (64 / LPT) * TL;
@@ -396,12 +556,34 @@ void launch_vec(const FrontParams& p, int lpt, int cpl, hipStream_t stream) {
   return launch_heads<TI, TO, 16, 1, 8, KT, false, FSILU>(p, stream);
 }
 
-// vec_ok: the host checked that rows, bases and outputs are aligned for the
-// vector path's CPL.
+// vec_ok: rows, bases and outputs are aligned for the vector path's CPL.
+// rows: short sequences take frontend_rows_kernel (needs vec_ok).
 template <class TI, class TO>
-hipError_t dispatch_heads(const FrontParams& p, bool vec_ok, hipStream_t stream) {
+hipError_t dispatch_heads(const FrontParams& p, bool vec_ok, bool rows, hipStream_t stream) {
   int lpt = 16;
   const int cpl = vec_cpl(p.D, &lpt);
+  // The default activations at any conv length (with no conv, none is fused).
+  const bool fsilu = p.K > 0 && p.conv_act == DN_ACT_SILU &&
+                     (p.n[0] == 0 || p.post_act[0] == DN_ACT_IDENTITY) &&
+                     (p.n[1] == 0 || p.post_act[1] == DN_ACT_IDENTITY) &&
+                     (p.n[2] == 0 || p.post_act[2] == DN_ACT_IDENTITY);
+  if (rows) {
+    if (p.K == 0) {
+      launch_rows_vec<TI, TO, 0, false, false>(p, lpt, cpl, stream);
+    } else if (p.K == 4 && p.win_vec) {
+      if (p.rows_win) {
+        if (fsilu) launch_rows_vec<TI, TO, 4, true, true>(p, lpt, cpl, stream);
+        else launch_rows_vec<TI, TO, 4, false, true>(p, lpt, cpl, stream);
+      } else {
+        if (fsilu) launch_rows_vec<TI, TO, 4, true, false>(p, lpt, cpl, stream);
+        else launch_rows_vec<TI, TO, 4, false, false>(p, lpt, cpl, stream);
+      }
+    } else {
+      if (fsilu) launch_rows_vec<TI, TO, -1, true, false>(p, lpt, cpl, stream);
+      else launch_rows_vec<TI, TO, -1, false, false>(p, lpt, cpl, stream);
+    }
+    return hipGetLastError();
+  }
   if (!vec_ok || cpl == 0 || (lpt == 32 && cpl != 8) || (p.K != 0 && p.K != 4)) {
     launch_heads<TI, TO, 64, 4, 4, 8, true>(p, stream);  // any head width ≤ 256, K ≤ 8
   } else if (p.K == 0) {
@@ -479,17 +661,35 @@ hipError_t frontend_typed(const dn_frontend_args& a, hipStream_t stream) {
   // multiple of head_k_dim, a v head is dv/dk units of width dk ([.., H, dv]
   // and [.., H·dv/dk, dk] are the same bytes), and q, k and v share a launch.
   const int vch = key_dim * (1 + u);
+  const bool one_launch = qk_vec && dv % dk == 0 && vec_ok(dk, vch, a.v);
+  const bool v_vec = one_launch || vec_ok(dv, vch, a.v);
+  // Short sequences take the row-per-token kernel wherever the vector path
+  // exists; a one-token call with a conv of 4 also writes the next window
+  // there, when every unit goes through it.
+  auto has_vec = [](int D, bool aligned) {
+    int lpt = 16;
+    const int cpl = vec_cpl(D, &lpt);
+    return aligned && cpl != 0 && !(lpt == 32 && cpl != 8);
+  };
+  const bool short_seq = p.S <= kRowsMaxSeq;
+  const bool rows_qk = short_seq && has_vec(dk, qk_vec);
+  const bool rows_v = short_seq && (one_launch ? rows_qk : has_vec(dv, v_vec));
+  // Conv length 4 reads a channel's weights and window row as one vector.
+  p.win_vec = K == 4 && aligned(a.conv_weight, 16) && aligned(a.window_in, 4 * sizeof(TI)) &&
+              aligned(a.window_out, 4 * sizeof(TI));
+  p.rows_win = p.S == 1 && p.win_vec && rows_qk && rows_v;
+  p.wout = a.window_out;
   hipError_t e;
-  if (qk_vec && dv % dk == 0 && vec_ok(dk, vch, a.v)) {
+  if (one_launch) {
     p.n[2] = u * H * (dv / dk);
     p.ch0[2] = vch;
     p.nu[2] = u * H * (dv / dk);
     p.out[2] = a.v;
     p.post_act[2] = v_post;
     p.norm[2] = 0;
-    e = dispatch_heads<TI, TO>(p, true, stream);
+    e = dispatch_heads<TI, TO>(p, true, rows_qk, stream);
   } else {
-    e = dispatch_heads<TI, TO>(p, qk_vec, stream);
+    e = dispatch_heads<TI, TO>(p, qk_vec, rows_qk, stream);
     if (e != hipSuccess) return e;
     p.D = dv;
     p.n[0] = u * H;
@@ -500,7 +700,7 @@ hipError_t frontend_typed(const dn_frontend_args& a, hipStream_t stream) {
     p.out[1] = p.out[2] = nullptr;
     p.post_act[0] = v_post;
     p.norm[0] = 0;
-    e = dispatch_heads<TI, TO>(p, vec_ok(dv, vch, a.v), stream);
+    e = dispatch_heads<TI, TO>(p, v_vec, rows_v, stream);
   }
   if (e != hipSuccess) return e;
   // Write gates.
@@ -538,8 +738,9 @@ hipError_t frontend_typed(const dn_frontend_args& a, hipStream_t stream) {
     e = launch_gate<TI>(g, stream);
   }
   if (e != hipSuccess) return e;
-  // The next window, after every read of the old one above.
-  if (K > 0) {
+  // The next window, after every read of the old one above (unless the
+  // rows kernel wrote it).
+  if (K > 0 && !p.rows_win) {
     p.out[0] = a.window_out;
     const unsigned grid = unsigned((int64_t(p.B) * conv_dim + kFrontThreads - 1) / kFrontThreads);
     hipLaunchKernelGGL(frontend_window_kernel<TI>, dim3(grid), dim3(kFrontThreads), 0, stream, p);

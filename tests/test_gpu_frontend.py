@@ -44,6 +44,13 @@ CASES = [
      False, torch.bfloat16, torch.float32, 0),
     (2, 2, 2, 64, 64, 1, 4, F.ACT_SILU, F.ACT_SILU, F.QKNORM_L2, F.WRITE_SCALAR, False,
      False, torch.float32, torch.float32, 0),
+    # short sequences (decode steps) take the row-per-token kernel
+    (3, 1, 4, 128, 256, 1, 4, F.ACT_SILU, F.ACT_SILU, F.QKNORM_L2, F.WRITE_SCALAR, False,
+     False, torch.bfloat16, torch.bfloat16, 0),
+    (2, 3, 2, 64, 128, 2, 4, F.ACT_IDENTITY, F.ACT_RELU, F.QKNORM_L2, F.WRITE_CHANNEL, True,
+     True, torch.float32, torch.float32, 0),
+    (4, 16, 2, 32, 32, 1, 6, F.ACT_SILU, F.ACT_SILU, F.QKNORM_L2, F.WRITE_SCALAR, False,
+     True, torch.float32, torch.bfloat16, 2),
 ]
 
 
@@ -116,10 +123,13 @@ def test_frontend_matches_oracle(rng, case):
     check(run_abi(p, conv, case), oracle_of(p, conv, case), case[14])
 
 
-def test_frontend_window_in_place(rng):
-    """window_out aliasing window_in (the decode cache updated in place)."""
-    case = CASES[1]
-    announce("dn_frontend in-place window")
+@pytest.mark.parametrize("ci", [1, 11, 12])
+def test_frontend_window_in_place(rng, ci):
+    """window_out aliasing window_in (the decode cache updated in place): a
+    sequence, a one-token step (whose kernel writes the next window itself)
+    and a 3-token call."""
+    case = CASES[ci]
+    announce(f"dn_frontend in-place window, case {ci}")
     p, conv = make_case(rng, case)
     want = oracle_of(p, conv, case)
     check(run_abi(p, conv, case, alias_window=True), want, case[14])
