@@ -402,6 +402,7 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
       const uint4 xl = frag_lo(X[2 * kk], X[2 * kk + 1], xh);
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib) {
+        if (kk > (ib >> 1)) continue;  // T is lower triangular
         const int at = tile_at<kL>(16 * ib + r16, 32 * kk + k8);
         const uint4 th = ld8u(&R[oTh + at]), tl = ld8u(&R[oTl + at]);
         Vn[ib] = mfma16(th, xh, Vn[ib]);
@@ -419,6 +420,7 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
       dV[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
+        if (kk < (ib >> 1)) continue;  // attnᵀ is upper triangular
         const uint4 a = ld8u(&R[oAt + tile_at<kL>(16 * ib + r16, 32 * kk + k8)]);
         dV[ib] = mfma16(a, yh[kk], dV[ib]);
         if constexpr (F32DY) dV[ib] = mfma16(a, yl[kk], dV[ib]);
@@ -453,6 +455,7 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
       const uint4 vl = frag_lo(dV[2 * kk], dV[2 * kk + 1], vh);
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib) {
+        if (kk < (ib >> 1)) continue;  // Tᵀ is upper triangular
         const int at = tile_at<kL>(16 * ib + r16, 32 * kk + k8);
         const uint4 th = ld8u(&R[oTth + at]), tl = ld8u(&R[oTtl + at]);
         dW[ib] = mfma16(th, vh, dW[ib]);
@@ -720,6 +723,9 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
+      // dTᵀ and Tᵀ are upper triangular: k-step 0 (j < 32) vanishes for
+      // row blocks 2 and 3 of either.
+      if (kk < (max(bt, it) >> 1)) continue;
       const int aa = tile_at<kL>(16 * bt + r16, 32 * kk + k8);
       const int ab = tile_at<kL>(16 * it + r16, 32 * kk + k8);
       const uint4 ah = ld8u(&R[oDTh + aa]), al = ld8u(&R[oDTl + aa]);

@@ -539,24 +539,23 @@ __global__ __launch_bounds__(kT) void fused_fwd_kernel(FusedParams p) {
         xh[kk] = frag_hi(X[2 * kk], X[2 * kk + 1]);
         xl[kk] = frag_lo(X[2 * kk], X[2 * kk + 1], xh[kk]);
       }
+      // T is lower triangular: its six nonzero (row block, k-step) pairs.
+      auto at = [&](int st) { return tile_at<kL>(16 * tril_tb(st) + r16, 32 * tril_kk(st) + k8); };
       bf16x8 th[2], tlo[2];
-      th[0] = ld8(&T.Th[tile_at<kL>(r16, k8)]);
-      tlo[0] = ld8(&T.Tl[tile_at<kL>(r16, k8)]);
+      th[0] = ld8(&T.Th[at(0)]);
+      tlo[0] = ld8(&T.Tl[at(0)]);
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb) {
-        Vp[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int tb = 0; tb < 4; ++tb) Vp[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const int st = 2 * tb + kk, nx = st + 1;
-          if (nx < 8) {
-            const int at = tile_at<kL>(16 * (nx >> 1) + r16, 32 * (nx & 1) + k8);
-            th[nx & 1] = ld8(&T.Th[at]);
-            tlo[nx & 1] = ld8(&T.Tl[at]);
-          }
-          Vp[tb] = mfma16(th[st & 1], as8(xh[kk]), Vp[tb]);
-          Vp[tb] = mfma16(tlo[st & 1], as8(xh[kk]), Vp[tb]);
-          Vp[tb] = mfma16(th[st & 1], as8(xl[kk]), Vp[tb]);
+      for (int st = 0; st < kTriSteps; ++st) {
+        if (st + 1 < kTriSteps) {
+          th[(st + 1) & 1] = ld8(&T.Th[at(st + 1)]);
+          tlo[(st + 1) & 1] = ld8(&T.Tl[at(st + 1)]);
         }
+        const int tb = tril_tb(st), kk = tril_kk(st);
+        Vp[tb] = mfma16(th[st & 1], as8(xh[kk]), Vp[tb]);
+        Vp[tb] = mfma16(tlo[st & 1], as8(xh[kk]), Vp[tb]);
+        Vp[tb] = mfma16(th[st & 1], as8(xl[kk]), Vp[tb]);
       }
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) vf[kk] = frag_hi(Vp[2 * kk], Vp[2 * kk + 1]);
@@ -572,14 +571,14 @@ __global__ __launch_bounds__(kT) void fused_fwd_kernel(FusedParams p) {
       for (int rb = 0; rb < RBK; ++rb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) S[rb][r] *= egl;
+      // attn is lower triangular too.
+      auto at = [&](int st) { return tile_at<kL>(16 * tril_tb(st) + r16, 32 * tril_kk(st) + k8); };
       bf16x8 fr[2];
-      fr[0] = ld8(&T.At[tile_at<kL>(r16, k8)]);
+      fr[0] = ld8(&T.At[at(0)]);
 #pragma unroll
-      for (int st = 0; st < 8; ++st) {
-        if (st + 1 < 8)
-          fr[(st + 1) & 1] =
-              ld8(&T.At[tile_at<kL>(16 * ((st + 1) >> 1) + r16, 32 * ((st + 1) & 1) + k8)]);
-        yt[st >> 1] = mfma16(as8(vf[st & 1]), fr[st & 1], yt[st >> 1]);
+      for (int st = 0; st < kTriSteps; ++st) {
+        if (st + 1 < kTriSteps) fr[(st + 1) & 1] = ld8(&T.At[at(st + 1)]);
+        yt[tril_tb(st)] = mfma16(as8(vf[tril_kk(st)]), fr[st & 1], yt[tril_tb(st)]);
       }
     }
     // S += Kcᵀ·V' for state row blocks rb0 … rb0+3

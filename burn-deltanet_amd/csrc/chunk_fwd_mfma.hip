@@ -1031,25 +1031,24 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
       xl[kk] = frag_lo(X[2 * kk], X[2 * kk + 1], xh[kk]);
     }
     f32x4 Vp[4];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) Vp[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
     {
+      // T is lower triangular: its six nonzero (row block, k-step) pairs.
+      auto at = [&](int st) { return tile_at<kL>(16 * tril_tb(st) + r16, 32 * tril_kk(st) + k8); };
       bf16x8 th[2], tlo[2];
-      th[0] = ld8(&tl[oT + tile_at<kL>(r16, k8)]);
-      tlo[0] = ld8(&tl[oTl + tile_at<kL>(r16, k8)]);
+      th[0] = ld8(&tl[oT + at(0)]);
+      tlo[0] = ld8(&tl[oTl + at(0)]);
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb) {
-        Vp[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const int step = 2 * tb + kk, nx = step + 1;
-          if (nx < 8) {
-            const int at = tile_at<kL>(16 * (nx >> 1) + r16, 32 * (nx & 1) + k8);
-            th[nx & 1] = ld8(&tl[oT + at]);
-            tlo[nx & 1] = ld8(&tl[oTl + at]);
-          }
-          Vp[tb] = mfma16(th[step & 1], as8(xh[kk]), Vp[tb]);
-          Vp[tb] = mfma16(tlo[step & 1], as8(xh[kk]), Vp[tb]);
-          Vp[tb] = mfma16(th[step & 1], as8(xl[kk]), Vp[tb]);
+      for (int st = 0; st < kTriSteps; ++st) {
+        if (st + 1 < kTriSteps) {
+          th[(st + 1) & 1] = ld8(&tl[oT + at(st + 1)]);
+          tlo[(st + 1) & 1] = ld8(&tl[oTl + at(st + 1)]);
         }
+        const int tb = tril_tb(st), kk = tril_kk(st);
+        Vp[tb] = mfma16(th[st & 1], as8(xh[kk]), Vp[tb]);
+        Vp[tb] = mfma16(tlo[st & 1], as8(xh[kk]), Vp[tb]);
+        Vp[tb] = mfma16(th[st & 1], as8(xl[kk]), Vp[tb]);
       }
     }
 
@@ -1060,11 +1059,12 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) vf[kk] = frag_hi(Vp[2 * kk], Vp[2 * kk + 1]);
     {
-      // 8 attn steps, then 2·RBK Kcᵀ steps, reads one step ahead.
-      constexpr int NS = 8 + 2 * RBK;
+      // The six nonzero steps of the lower-triangular attn, then 2·RBK Kcᵀ
+      // steps, reads one step ahead.
+      constexpr int NA = kTriSteps, NS = NA + 2 * RBK;
       auto addr = [&](int st) {
-        return st < 8 ? oAt + tile_at<kL>(16 * (st >> 1) + r16, 32 * (st & 1) + k8)
-                      : oKc + tile_at<kL>(16 * ((st - 8) >> 1) + r16, 32 * ((st - 8) & 1) + k8);
+        return st < NA ? oAt + tile_at<kL>(16 * tril_tb(st) + r16, 32 * tril_kk(st) + k8)
+                       : oKc + tile_at<kL>(16 * ((st - NA) >> 1) + r16, 32 * ((st - NA) & 1) + k8);
       };
       bf16x8 fr[2];
       fr[0] = ld8(&tl[addr(0)]);
@@ -1075,11 +1075,10 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
         if (st + 1 < NS) fr[(st + 1) & 1] = ld8(&tl[addr(st + 1)]);
-        const int kk = st & 1;
-        if (st < 8)
-          yt[st >> 1] = mfma16(as8(vf[kk]), fr[st & 1], yt[st >> 1]);
+        if (st < NA)
+          yt[tril_tb(st)] = mfma16(as8(vf[tril_kk(st)]), fr[st & 1], yt[tril_tb(st)]);
         else
-          S[(st - 8) >> 1] = mfma16(fr[st & 1], as8(vf[kk]), S[(st - 8) >> 1]);
+          S[(st - NA) >> 1] = mfma16(fr[st & 1], as8(vf[(st - NA) & 1]), S[(st - NA) >> 1]);
       }
     }
     // y: lane (r16, q4) holds columns jw + 4q4 … +3 of token 16tb + r16;
@@ -1419,6 +1418,9 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_rev_scan_kernel(RevParams p) 
     load_dy(nn);
 
     // Phase 2: Z = Tᵀ·dV' with hi + lo parts of both factors.
+    // (Tᵀ and attnᵀ are upper triangular, but skipping their zero blocks
+    // here measured slower: 1010 → 1265 µs for the two-wave reverse scan of
+    // BASELINE config 5, with the same register use.)
     uint4 vh[2], vl[2];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {

@@ -64,9 +64,6 @@ __device__ inline int perm_pos(int k) {
   const int m = k & 31;
   return (k & ~31) + 8 * ((m & 15) >> 2) + 4 * (m >> 4) + (m & 3);
 }
-// Element (row, pos) of a tile with COLS bf16 per row; 16-byte chunks are
-// XOR-swizzled by row so the 16 rows of a fragment read land in 16 distinct
-// bank slots.
 // A workgroup barrier that orders LDS only: this wave's LDS accesses have
 // completed (lgkmcnt 0) when it arrives, and the compiler moves no memory
 // access across it. __syncthreads() also waits for every global load and
@@ -81,6 +78,9 @@ __device__ inline void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// Element (row, pos) of a tile with COLS bf16 per row; 16-byte chunks are
+// XOR-swizzled by row so the 16 rows of a fragment read land in 16 distinct
+// bank slots.
 template <int COLS>
 __device__ inline int tile_at(int row, int pos) {
   const int sw = COLS >= 128 ? (row & 15) : ((row >> 1) & 7);
@@ -99,5 +99,13 @@ __device__ inline uint4 frag_lo(const f32x4& a, const f32x4& b, const uint4& h) 
                     pk_bf16(b[0] - lo_f(h.z), b[1] - hi_f(h.z)),
                     pk_bf16(b[2] - lo_f(h.w), b[3] - hi_f(h.w)));
 }
+
+// A 64×64 triangular tile times a 64-row operand, as MFMA steps over 4 row
+// blocks of 16 and 2 k-steps of 32: six of the eight (row block, k-step)
+// pairs are nonzero. Lower triangular (T, attn): row blocks 0 and 1 have no
+// k-step 1. Step s of the six, in row-block order.
+constexpr int kTriSteps = 6;
+__host__ __device__ constexpr int tril_tb(int s) { return s < 2 ? s : 2 + ((s - 2) >> 1); }
+__host__ __device__ constexpr int tril_kk(int s) { return s < 2 ? 0 : (s - 2) & 1; }
 
 }  // namespace dn
