@@ -26,11 +26,13 @@
 // src/delta/tri/tests.rs; the series by the ladder on strictly lower inputs
 // and by numpy's matrix powers on a full matrix.
 //
-// Parity unpinned: the per-channel decay when its clamp binds (an exponent
-// reaching MAX_EXPONENT = 48 within half a 16-row block, decay.rs:41-49).
-// block_decay/channel_scores_backward follow the reference's formula there,
-// but no reference-held vector or closed form fixes those "wrong-but-finite"
-// values; gates in the documented range [-5, 0) never reach the clamp.
+// The per-channel decay where its clamp binds (an exponent reaching
+// MAX_EXPONENT = 48 within half a 16-row block, decay.rs:41-49), which no
+// reference-held vector covers, is pinned by a closed form: a chunk with
+// g = −10 and two orthogonal key → query pairs, one with its row exponent
+// clamped and one with its column exponent clamped, whose outputs and
+// gradients (a clamped exponent passes none, combined_backward.rs:480-496)
+// follow by hand (tests/conftest.py, clamp_regime_case).
 //
 // Layouts are the reference's (src/delta/path.rs:120-141): row-major
 //   q,k [B,S,H,K]  v [B,S,H,V]  erase [B,S,H,ew]  write [B,S,H,ww]

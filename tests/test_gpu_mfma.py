@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import l2, rel_err
+from conftest import clamp_regime_case, closed_form_err, l2, rel_err
 from gpu_util import DEV, announce, as_oracle_inputs, np_of, pkg, to_gpu
 from oracle import oracle as O
 
@@ -209,6 +209,42 @@ BWD_CASES = [
     (1, 128, 2, 128, 256, None),
     (1, 256, 2, 128, 256, "head", {"const_keys": True}),
 ]
+
+
+@pytest.mark.parametrize("algo", [MFMA, pkg.abi.DN_ALGO_GENERIC])
+def test_channel_decay_clamp_closed_form(algo):
+    """The per-channel decay where its clamp binds (decay.rs:41-49,
+    combined_backward.rs:480-496), forward and backward on the MFMA and
+    generic kernels, against the closed forms of conftest.clamp_regime_case
+    (also the oracle's, tests/test_oracle_invariants.py). Relative 2e-2 on
+    the MFMA path (bf16 operands), 1e-5 on the fp32 generic path; every
+    other entry below 1e-3 of the smallest expected one."""
+    announce(f"channel decay clamp closed form, algo {algo}")
+    args, dy, want = clamp_regime_case()
+    q, k, v, e, w, g, s = to_gpu(args, torch.bfloat16)
+    V = v.shape[3]
+    y = torch.empty(v.shape, dtype=torch.float32, device=DEV)
+    s_out = torch.empty_like(s)
+    a = pkg.abi.chunk_fwd_args(q, k, v, e, w, g, s, y, s_out, 64, None, algo=algo)
+    assert pkg.abi.lib().dn_chunk_fwd_algo(a) == algo
+    pkg.abi.run_chunk_fwd(a)
+    torch.cuda.synchronize()
+    tol = TOL if algo == MFMA else 1e-5
+    rel, rest = closed_form_err(np_of(y), want["y"])
+    print(f"  y rel {rel:.2e} rest {rest:.2e}", flush=True)
+    assert rel < tol and rest < 1e-3
+    assert np_of(s_out).max() == 0.0 and np_of(s_out).min() == 0.0
+    tdy = torch.tensor(dy, dtype=torch.float32, device=DEV)
+    grads = pkg.combined_backward(tdy, torch.zeros_like(s), q, k, v, e, w, g, s, 64,
+                                  1.0 / np.sqrt(q.shape[3]), algo=algo)
+    torch.cuda.synchronize()
+    got = dict(zip(["d_q", "d_k", "d_v", "d_erase", "d_write", "d_g"],
+                   [grads.d_q_bshk, grads.d_k_bshk, grads.d_v_bshv, grads.d_erase_bshK,
+                    grads.d_write_bshV, grads.d_g_bshK]))
+    for name, t in got.items():
+        rel, rest = closed_form_err(np_of(t), want[name])
+        print(f"  {name} rel {rel:.2e} rest {rest:.2e}", flush=True)
+        assert rel < tol and rest < 1e-3, name
 
 
 def bwd_inputs(rng, B, S, H, K, V, gates, opts=None):

@@ -9,7 +9,7 @@ gated_deltanet_2/tests.rs:461-526.
 import numpy as np
 import pytest
 
-from conftest import l2, random_raw
+from conftest import clamp_regime_case, closed_form_err, l2, random_raw
 from oracle import oracle as O
 
 
@@ -127,3 +127,18 @@ def test_deltaproduct_fold_with_one_householder_is_gdn1(rng):
                         fold(g, np.zeros_like(g)), s, chunk_len=4)
     assert np.abs(y[:, 1::2] - y0).max() < 1e-10
     assert np.abs(s1 - s0).max() < 1e-10
+
+
+@pytest.mark.parametrize("chunk_len", [16, 64])
+def test_block_decay_clamp_closed_form(chunk_len):
+    """The per-channel decay where its clamp binds (decay.rs:41-49), forward
+    and backward, against the closed forms of conftest.clamp_regime_case."""
+    args, dy, want = clamp_regime_case()
+    y, s = O.chunk_fwd(*args, chunk_len=chunk_len)
+    rel, rest = closed_form_err(y, want["y"])
+    assert rel < 1e-12 and rest < 1e-12
+    assert np.abs(s).max() < 1e-200
+    grads = O.chunk_bwd(dy, np.zeros_like(args[6]), *args, chunk_len=chunk_len)
+    for name, got in zip(["d_q", "d_k", "d_v", "d_erase", "d_write", "d_g"], grads):
+        rel, rest = closed_form_err(got, want[name])
+        assert rel < 1e-12 and rest < 1e-12, (name, rel, rest)
