@@ -14,7 +14,8 @@ kernels at small sizes in the other GPU tests):
   f(S1 + S2) = f(S1) + f(S2) − f(0), for the next state and for y.
 - config 4 (DeltaProduct u = 2 fold) and config 5 (GDN-2 per-channel gates):
   the MFMA forward, and for config 5 the MFMA backward, agree with the
-  generic fp32 kernels, which share no code with them.
+  generic fp32 kernels, which share no code with them; the MFMA forward
+  also agrees with `dn_recurrent`, the token-by-token recurrence.
 - the projection front-end at the config-2 shape: a sequence split in two,
   with the conv window carried across (conv.rs:14-20), gives the same bits
   as one call. The output norm at config 2's output shape agrees with its
@@ -176,6 +177,13 @@ def test_config4_mfma_forward_agrees_with_generic():
     ey, es = rel_err(y_m, y_g), rel_err(s_m, s_g)
     print(f"  rel err y {ey:.2e} state {es:.2e}", flush=True)
     assert ey < TOL_BF16 and es < TOL_BF16
+    del y_g, s_g
+    # An independent algorithm: the token-by-token recurrence (dn_recurrent).
+    y_r, s_r = pkg.DeltaInput(q, k, v, beta, beta, g, s0).delta_recurrent()
+    torch.cuda.synchronize()
+    ey, es = rel_err(y_m, y_r), rel_err(s_m, s_r)
+    print(f"  vs dn_recurrent: rel err y {ey:.2e} state {es:.2e}", flush=True)
+    assert ey < TOL_BF16 and es < TOL_BF16
 
 
 def test_config5_mfma_forward_and_backward_agree_with_generic():
@@ -195,7 +203,14 @@ def test_config5_mfma_forward_and_backward_agree_with_generic():
     ey, es = rel_err(y_m, y_g), rel_err(s_m, s_g)
     print(f"  forward rel err y {ey:.2e} state {es:.2e}", flush=True)
     assert ey < TOL_BF16 and es < TOL_BF16
-    del y_m, s_m, y_g, s_g
+    del y_g, s_g
+    # An independent algorithm: the token-by-token recurrence (dn_recurrent).
+    y_r, s_r = pkg.DeltaInput(q, k, v, e, w, g, s0).delta_recurrent()
+    torch.cuda.synchronize()
+    ey, es = rel_err(y_m, y_r), rel_err(s_m, s_r)
+    print(f"  forward vs dn_recurrent: rel err y {ey:.2e} state {es:.2e}", flush=True)
+    assert ey < TOL_BF16 and es < TOL_BF16
+    del y_m, s_m, y_r, s_r
     dy = torch.randn((B, T, H, V), generator=gr, device=DEV)
     ds = torch.randn((B, H, K, V), generator=gr, device=DEV) * 0.5
     scale = 1.0 / np.sqrt(K)
