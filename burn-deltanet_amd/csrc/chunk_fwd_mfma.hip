@@ -795,12 +795,15 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   auto ld16 = [](const uint16_t* base, uint32_t elems) {
     return *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(base) + 2u * elems);
   };
-  auto fetch = [&](int n) {
+  // fetch / stage cover rounds m0 … m1−1 of the staging, the gates with
+  // round 0 (every call passes constants).
+  auto fetch = [&](int n, int m0, int m1) {
     const size_t cid = chunk_of(n);
     const int rl = min(kL, p.S - n * kL);  // valid rows of this chunk (≥ 1)
     const size_t row0 = bh_row0 + size_t(n) * kL * tokstride;
 #pragma unroll
     for (int m = 0; m < NPF; ++m) {
+      if (m < m0 || m >= m1) continue;
       // The tile boundaries are multiples of NT, so the kind of chunk
       // tid + NT·m depends on m only (a constant once the loop is unrolled).
       const int i0 = NT * m;
@@ -827,6 +830,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
         pf[m] = ld16(p.KcT + cid * K * kL + 8 * e0, 8u * tid);
       }
     }
+    if (m0 > 0) return;
     if constexpr (PC) {
       pch = p.egl[cid * K + (tid % K)];
     } else {
@@ -854,10 +858,11 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   const int aK0x = K >= 128 ? addr_k(8, 0) : aK0;
   const int aK1x = K >= 128 ? addr_k(8, 1) : aK1;
   const int a60 = tile_at<kL>(r6, perm_pos(8 * c6)), a61 = tile_at<kL>(r6, perm_pos(8 * c6 + 4));
-  auto stage = [&](int buf) {
+  auto stage = [&](int buf, int m0, int m1) {
     uint16_t* tl = tiles[buf];
 #pragma unroll
     for (int m = 0; m < NPF; ++m) {
+      if (m < m0 || m >= m1) continue;
       const int i0 = NT * m;
       int b0, b1;
       if (i0 < NKQ * kL * K / 8) {
@@ -881,6 +886,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
       *reinterpret_cast<uint2*>(&tl[b0]) = make_uint2(pf[m].x, pf[m].y);
       *reinterpret_cast<uint2*>(&tl[b1]) = make_uint2(pf[m].z, pf[m].w);
     }
+    if (m0 > 0) return;
     if constexpr (PC) {
       if (tid < K) gch[tid] = pch;
     } else if (wave == 0) {
@@ -941,10 +947,10 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   };
   auto as8 = [](const uint4& x) { return __builtin_bit_cast(bf16x8, x); };
 
-  fetch(0);
+  fetch(0, 0, NPF);
   load_v(0);
   load_w(0);
-  stage(0);
+  stage(0, 0, NPF);
   __syncthreads();
   for (int n = 0; n < p.N; ++n) {
     const int cur = PC ? 0 : (n & 1);
@@ -957,7 +963,14 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
     // per-channel states mode (the backward's recompute) measured slower so
     // (1055 → 1105 µs): its fetch stays after phase 1.
     constexpr bool kFetchTop = !(PC && ST);
-    if constexpr (kFetchTop) fetch(nn);
+    // Eight-wave double-buffered scans: the next chunk's tiles in two
+    // halves, the first staged after phase 1 (the other buffer is free all
+    // chunk), which halves the registers holding them (config 2 scan 339 →
+    // 312 µs). The two-wave scan (36 rounds per lane) and the states mode
+    // measured slower so (config 4 1.09 → 1.24 ms).
+    constexpr bool kHalf = NBUF == 2 && WAVES == 8 && !ST;
+    constexpr int NH = kHalf ? (NPF + 1) / 2 : NPF;
+    if constexpr (kFetchTop) fetch(nn, 0, NH);
     if constexpr (ST) {
       float* sdst = p.states + chunk_of(n) * K * p.V + jl;
 #pragma unroll
@@ -977,32 +990,35 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
       yt[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
     {
-      bf16x8 kf[2], qf[2], kl[2];
-      kf[0] = ld8(&tl[oK + tile_at<K>(r16, k8)]);
-      qf[0] = ld8(&tl[oQ + tile_at<K>(r16, k8)]);
-      if constexpr (PC) kl[0] = ld8(&tl[oKl + tile_at<K>(r16, k8)]);
+      // Fragment reads run PD steps ahead of the MFMAs (a ring of PD + 1).
+      constexpr int PD = 2, NR = PD + 1, NSTEP = 4 * KK;
+      bf16x8 kf[NR], qf[NR], kl[NR];
+      auto rd = [&](int st) {
+        const int at = tile_at<K>(16 * (st & 3) + r16, 32 * (st >> 2) + k8);
+        kf[st % NR] = ld8(&tl[oK + at]);
+        qf[st % NR] = ld8(&tl[oQ + at]);
+        if constexpr (PC) kl[st % NR] = ld8(&tl[oKl + at]);
+      };
+#pragma unroll
+      for (int st = 0; st < PD; ++st) rd(st);
 #pragma unroll
       for (int kk = 0; kk < KK; ++kk) {
         const uint4 sh = frag_hi(S[2 * kk], S[2 * kk + 1]);
         const uint4 sl = frag_lo(S[2 * kk], S[2 * kk + 1], sh);
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
-          const int step = 4 * kk + tb, nx = step + 1;
-          if (nx < 4 * KK) {
-            const int at = tile_at<K>(16 * (nx & 3) + r16, 32 * (nx >> 2) + k8);
-            kf[nx & 1] = ld8(&tl[oK + at]);
-            qf[nx & 1] = ld8(&tl[oQ + at]);
-            if constexpr (PC) kl[nx & 1] = ld8(&tl[oKl + at]);
-          }
-          X[tb] = mfma16(kf[step & 1], as8(sh), X[tb]);
-          X[tb] = mfma16(kf[step & 1], as8(sl), X[tb]);
+          const int step = 4 * kk + tb;
+          if (step + PD < NSTEP) rd(step + PD);
+          const int c = step % NR;
+          X[tb] = mfma16(kf[c], as8(sh), X[tb]);
+          X[tb] = mfma16(kf[c], as8(sl), X[tb]);
           // kg carries the fp32 gate factors, so it has a lo part too.
-          if constexpr (PC) X[tb] = mfma16(kl[step & 1], as8(sh), X[tb]);
-          yt[tb] = mfma16(as8(sh), qf[step & 1], yt[tb]);
+          if constexpr (PC) X[tb] = mfma16(kl[c], as8(sh), X[tb]);
+          yt[tb] = mfma16(as8(sh), qf[c], yt[tb]);
         }
       }
     }
-    if constexpr (!kFetchTop) fetch(nn);
+    if constexpr (!kFetchTop) fetch(nn, 0, NPF);
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
 #pragma unroll
@@ -1021,6 +1037,10 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
     }
     load_v(nn);
     load_w(nn);
+    if constexpr (kHalf) {
+      stage(cur ^ 1, 0, NH);
+      fetch(nn, NH, NPF);
+    }
 
     // Phase 2: V' = T·X with hi + lo parts of both factors (for a chunk of
     // near-identical keys T differences near-equal rows of X).
@@ -1100,11 +1120,11 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
               make_float4(yt[tb][0], yt[tb][1], yt[tb][2], yt[tb][3]);
       }
     }
-    if constexpr (PC) {
+    if constexpr (NBUF == 1) {
       __syncthreads();  // every wave is done with this chunk's tiles
-      stage(0);
+      stage(0, 0, NPF);
     } else {
-      stage(cur ^ 1);
+      stage(cur ^ 1, kHalf ? NH : 0, NPF);
     }
     __syncthreads();
   }
