@@ -713,6 +713,10 @@ def main():
         bench_frontend(torch, pkg, 2, 0)
         bench_out_norm(torch, pkg, 2, 0)
         bench_config5(torch, pkg, 1, 0)
+        bench_config4(torch, pkg, 1, 0)
+        bench_config2_bwd(torch, pkg, 1, 0)
+        bench_block_decode(torch, pkg, 2, 0)
+        bench_unit_lower_inverse(torch, pkg, 2, 0)
         torch.cuda.synchronize()
         print("[bench] profile pass done", file=sys.stderr, flush=True)
         return
