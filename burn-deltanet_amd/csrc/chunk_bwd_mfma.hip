@@ -60,6 +60,10 @@ struct CbParams {
   // stores.
   int vs, voff, pass;
   float *pq, *pk, *pe, *pg, *pw;  // partials of d_q, d_k, d_erase, d_g, width-1 d_write
+  // Per-head gates over several passes: each thread's partial sums of dattn
+  // and dT (16 fp32 per thread per chunk-head), which the passes before the
+  // last hand on so that the last runs the score backward once.
+  float* pda;
 };
 
 // A value-summed output (d_q, d_k, d_erase, d_g, a width-1 d_write): a sum
@@ -160,9 +164,16 @@ __device__ inline void stage_perm(uint16_t* R, int dst, const uint16_t* src, int
 // LASTP (per-head gates, the last of several value passes): the partials
 // of the value-summed outputs are loaded at the start of phase D, so their
 // round trip overlaps the score backward instead of preceding each store.
-template <int K, int V, bool PC, class TG, bool LASTP = false>
+// EARLY (per-head gates, the passes before the last): dattn and dT are sums
+// over the value axis, and everything after them is linear in them, so these
+// passes add their partial sums to p.pda and stop after phase C's first
+// product; the score backward (the rest of phase C and phase D's scores) runs
+// once, in the last pass, on the summed dattn and dT. They still store their
+// share of the value-summed gradients (phase B's terms).
+template <int K, int V, bool PC, class TG, bool LASTP = false, bool EARLY = false>
 __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   static_assert(!(LASTP && PC), "the per-channel last pass reads its partials at the stores");
+  static_assert(!(EARLY && (PC || LASTP)), "partial score sums: per-head gates, not the last pass");
   constexpr bool F32DY = std::is_same<TG, float>::value;
   constexpr int TT = kL * kL, TK = kL * K, TV = kL * V;
   constexpr int OFF_A1 = 4 * TV > 8 * TT ? 4 * TV : 8 * TT;
@@ -615,6 +626,14 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
       }
     }
   }
+  // The earlier passes' dattn and dT partial sums (this thread's 16 slots).
+  float* const da = PC || !p.pda ? nullptr : p.pda + (size_t(cid) * kNT + tid) * 16;
+  f32x4 pda_r[4];
+  if constexpr (!PC) {
+    if (LASTP || (EARLY && p.pass == 2))
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pda_r[j] = reinterpret_cast<const f32x4*>(da)[j];
+  }
   __syncthreads();
   // Per-channel erase gate at the lane's rows, for phase D: loaded here so
   // that phase B does not hold it, its latency covered by phase C. One load
@@ -644,33 +663,44 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
         R[oDl + at] = bf_bits(dV[ib][r] - bf16_to_f32(dh));
       }
   }
+  if constexpr (!PC) {
+    if (LASTP || (EARLY && p.pass == 2))
+#pragma unroll
+      for (int u = 0; u < 2; ++u) dat[u] += pda_r[u];
+  }
+  if constexpr (EARLY) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) reinterpret_cast<f32x4*>(da)[u] = dat[u];
+  }
   // dAqk = tril(dattn) (per-head decay: ⊙ e^{Gᵢ−Gⱼ}, the head mask) as
   // [i][j] and as [j][i] (per-head: times the readout scale).
+  if constexpr (!EARLY) {
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int t = wave + 8 * u, ti = t >> 2, tj = t & 3;
-    const int j = 16 * tj + r16;
-    float f[4], ft[4];
+    for (int u = 0; u < 2; ++u) {
+      const int t = wave + 8 * u, ti = t >> 2, tj = t & 3;
+      const int j = 16 * tj + r16;
+      float f[4], ft[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 16 * ti + 4 * g4 + r;
-      float val = 0.f;
-      if (j <= i) {
-        val = dat[u][r];
-        if (!PC && gated) val *= __expf(Gc[i] - Gc[j]);
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * ti + 4 * g4 + r;
+        float val = 0.f;
+        if (j <= i) {
+          val = dat[u][r];
+          if (!PC && gated) val *= __expf(Gc[i] - Gc[j]);
+        }
+        f[r] = val;
+        ft[r] = PC ? val : val * p.scale;
+        const int at = tile_at<kL>(i, j);
+        const uint16_t vh = bf_bits(val);
+        R[oA1h + at] = vh;
+        R[oA1l + at] = bf_bits(val - bf16_to_f32(vh));
       }
-      f[r] = val;
-      ft[r] = PC ? val : val * p.scale;
-      const int at = tile_at<kL>(i, j);
-      const uint16_t vh = bf_bits(val);
-      R[oA1h + at] = vh;
-      R[oA1l + at] = bf_bits(val - bf16_to_f32(vh));
+      uint2 hh, ll;
+      split4(ft, hh, ll);
+      const int at = tile_at<kL>(j, 16 * ti + 4 * g4);
+      *reinterpret_cast<uint2*>(&R[oA1th + at]) = hh;
+      *reinterpret_cast<uint2*>(&R[oA1tl + at]) = ll;
     }
-    uint2 hh, ll;
-    split4(ft, hh, ll);
-    const int at = tile_at<kL>(j, 16 * ti + 4 * g4);
-    *reinterpret_cast<uint2*>(&R[oA1th + at]) = hh;
-    *reinterpret_cast<uint2*>(&R[oA1tl + at]) = ll;
   }
   __syncthreads();
 
@@ -694,101 +724,111 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
     }
   }
   __syncthreads();
-  // dTᵀ with dT's row index permuted (it is the contraction index of dTᵀ·T);
-  // T and Tᵀ staged again.
+  if constexpr (!PC) {
+    if (LASTP || (EARLY && p.pass == 2))
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int t = wave + 8 * u, ti = t >> 2, tj = t & 3;
-    float f[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int a = 16 * ti + 4 * g4 + r, bcol = 16 * tj + r16;
-      f[r] = bcol < a ? dTt[u][r] : 0.f;
-    }
-    uint2 hh, ll;
-    split4(f, hh, ll);
-    const int at = tile_at<kL>(16 * tj + r16, 32 * (ti >> 1) + 8 * g4 + 4 * (ti & 1));
-    *reinterpret_cast<uint2*>(&R[oDTh + at]) = hh;
-    *reinterpret_cast<uint2*>(&R[oDTl + at]) = ll;
+      for (int u = 0; u < 2; ++u) dTt[u] += pda_r[2 + u];
   }
-  stage_perm(R, oTh, p.T + o64, tid);
-  stage_perm(R, oTl, p.Tlo + o64, tid);
-  stage_perm(R, oTth, p.Tt + o64, tid);
-  stage_perm(R, oTtl, p.Ttl + o64, tid);
-  __syncthreads();
-  // M₁ᵀ = dTᵀ·T (all 16 tiles), stored as M₁ with its column index permuted.
+  if constexpr (EARLY) {
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int t = wave + 8 * u, bt = t >> 2, it = t & 3;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < 2; ++u) reinterpret_cast<f32x4*>(da)[2 + u] = dTt[u];
+  } else {
+    // dTᵀ with dT's row index permuted (it is the contraction index of dTᵀ·T);
+    // T and Tᵀ staged again.
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      // dTᵀ and Tᵀ are upper triangular: k-step 0 (j < 32) vanishes for
-      // row blocks 2 and 3 of either.
-      if (kk < (max(bt, it) >> 1)) continue;
-      const int aa = tile_at<kL>(16 * bt + r16, 32 * kk + k8);
-      const int ab = tile_at<kL>(16 * it + r16, 32 * kk + k8);
-      const uint4 ah = ld8u(&R[oDTh + aa]), al = ld8u(&R[oDTl + aa]);
-      const uint4 bh = ld8u(&R[oTth + ab]), bl = ld8u(&R[oTtl + ab]);
-      acc = mfma16(ah, bh, acc);
-      acc = mfma16(al, bh, acc);
-      acc = mfma16(ah, bl, acc);
+    for (int u = 0; u < 2; ++u) {
+      const int t = wave + 8 * u, ti = t >> 2, tj = t & 3;
+      float f[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int a = 16 * ti + 4 * g4 + r, bcol = 16 * tj + r16;
+        f[r] = bcol < a ? dTt[u][r] : 0.f;
+      }
+      uint2 hh, ll;
+      split4(f, hh, ll);
+      const int at = tile_at<kL>(16 * tj + r16, 32 * (ti >> 1) + 8 * g4 + 4 * (ti & 1));
+      *reinterpret_cast<uint2*>(&R[oDTh + at]) = hh;
+      *reinterpret_cast<uint2*>(&R[oDTl + at]) = ll;
     }
-    float f[4] = {acc[0], acc[1], acc[2], acc[3]};
-    uint2 hh, ll;
-    split4(f, hh, ll);
-    const int at = tile_at<kL>(16 * it + r16, 32 * (bt >> 1) + 8 * g4 + 4 * (bt & 1));
-    *reinterpret_cast<uint2*>(&R[oM1h + at]) = hh;
-    *reinterpret_cast<uint2*>(&R[oM1l + at]) = ll;
-  }
-  __syncthreads();
-  // dAkk = −tril(M₁·Tᵀ, −1); T[j][b] vanishes for b > j.
-  f32x4 dak[2];
+    stage_perm(R, oTh, p.T + o64, tid);
+    stage_perm(R, oTl, p.Tlo + o64, tid);
+    stage_perm(R, oTth, p.Tt + o64, tid);
+    stage_perm(R, oTtl, p.Ttl + o64, tid);
+    __syncthreads();
+    // M₁ᵀ = dTᵀ·T (all 16 tiles), stored as M₁ with its column index permuted.
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int t = wave + 8 * u, ti = t >> 2, tj = t & 3;
-    dak[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (tj <= ti) {
+    for (int u = 0; u < 2; ++u) {
+      const int t = wave + 8 * u, bt = t >> 2, it = t & 3;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        if (kk > (tj >> 1)) continue;
-        const int aa = tile_at<kL>(16 * ti + r16, 32 * kk + k8);
-        const int ab = tile_at<kL>(16 * tj + r16, 32 * kk + k8);
-        const uint4 ah = ld8u(&R[oM1h + aa]), al = ld8u(&R[oM1l + aa]);
-        const uint4 bh = ld8u(&R[oTh + ab]), bl = ld8u(&R[oTl + ab]);
-        dak[u] = mfma16(ah, bh, dak[u]);
-        dak[u] = mfma16(al, bh, dak[u]);
-        dak[u] = mfma16(ah, bl, dak[u]);
+        // dTᵀ and Tᵀ are upper triangular: k-step 0 (j < 32) vanishes for
+        // row blocks 2 and 3 of either.
+        if (kk < (max(bt, it) >> 1)) continue;
+        const int aa = tile_at<kL>(16 * bt + r16, 32 * kk + k8);
+        const int ab = tile_at<kL>(16 * it + r16, 32 * kk + k8);
+        const uint4 ah = ld8u(&R[oDTh + aa]), al = ld8u(&R[oDTl + aa]);
+        const uint4 bh = ld8u(&R[oTth + ab]), bl = ld8u(&R[oTtl + ab]);
+        acc = mfma16(ah, bh, acc);
+        acc = mfma16(al, bh, acc);
+        acc = mfma16(ah, bl, acc);
+      }
+      float f[4] = {acc[0], acc[1], acc[2], acc[3]};
+      uint2 hh, ll;
+      split4(f, hh, ll);
+      const int at = tile_at<kL>(16 * it + r16, 32 * (bt >> 1) + 8 * g4 + 4 * (bt & 1));
+      *reinterpret_cast<uint2*>(&R[oM1h + at]) = hh;
+      *reinterpret_cast<uint2*>(&R[oM1l + at]) = ll;
+    }
+    __syncthreads();
+    // dAkk = −tril(M₁·Tᵀ, −1); T[j][b] vanishes for b > j.
+    f32x4 dak[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int t = wave + 8 * u, ti = t >> 2, tj = t & 3;
+      dak[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (tj <= ti) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          if (kk > (tj >> 1)) continue;
+          const int aa = tile_at<kL>(16 * ti + r16, 32 * kk + k8);
+          const int ab = tile_at<kL>(16 * tj + r16, 32 * kk + k8);
+          const uint4 ah = ld8u(&R[oM1h + aa]), al = ld8u(&R[oM1l + aa]);
+          const uint4 bh = ld8u(&R[oTh + ab]), bl = ld8u(&R[oTl + ab]);
+          dak[u] = mfma16(ah, bh, dak[u]);
+          dak[u] = mfma16(al, bh, dak[u]);
+          dak[u] = mfma16(ah, bl, dak[u]);
+        }
       }
     }
-  }
-  __syncthreads();
-  // dAkk (per-head decay: ⊙ the head mask) as [i][j] and as [j][i]
-  // (per-head: times the erase gate of row i); Kᵀ and Qᵀ.
+    __syncthreads();
+    // dAkk (per-head decay: ⊙ the head mask) as [i][j] and as [j][i]
+    // (per-head: times the erase gate of row i); Kᵀ and Qᵀ.
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int t = wave + 8 * u, ti = t >> 2, tj = t & 3;
-    const int j = 16 * tj + r16;
-    float ft[4];
+    for (int u = 0; u < 2; ++u) {
+      const int t = wave + 8 * u, ti = t >> 2, tj = t & 3;
+      const int j = 16 * tj + r16;
+      float ft[4];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = 16 * ti + 4 * g4 + r;
-      float val = 0.f;
-      if (j < i) {
-        val = -dak[u][r];
-        if (!PC && gated) val *= __expf(Gc[i] - Gc[j]);
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * ti + 4 * g4 + r;
+        float val = 0.f;
+        if (j < i) {
+          val = -dak[u][r];
+          if (!PC && gated) val *= __expf(Gc[i] - Gc[j]);
+        }
+        ft[r] = PC ? val : val * er_s[i];
+        const int at = tile_at<kL>(i, j);
+        const uint16_t vh = bf_bits(val);
+        R[oA0h + at] = vh;
+        R[oA0l + at] = bf_bits(val - bf16_to_f32(vh));
       }
-      ft[r] = PC ? val : val * er_s[i];
-      const int at = tile_at<kL>(i, j);
-      const uint16_t vh = bf_bits(val);
-      R[oA0h + at] = vh;
-      R[oA0l + at] = bf_bits(val - bf16_to_f32(vh));
+      uint2 hh, ll;
+      split4(ft, hh, ll);
+      const int at = tile_at<kL>(j, 16 * ti + 4 * g4);
+      *reinterpret_cast<uint2*>(&R[oA0th + at]) = hh;
+      *reinterpret_cast<uint2*>(&R[oA0tl + at]) = ll;
     }
-    uint2 hh, ll;
-    split4(ft, hh, ll);
-    const int at = tile_at<kL>(j, 16 * ti + 4 * g4);
-    *reinterpret_cast<uint2*>(&R[oA0th + at]) = hh;
-    *reinterpret_cast<uint2*>(&R[oA0tl + at]) = ll;
   }
   for (int idx = tid; idx < kL * K / 8; idx += kNT) {
     const int i = idx / (K / 8), c8 = idx % (K / 8);
@@ -864,7 +904,9 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
         if (lane == 0) atomicAdd(&racc[2][kL - 1], tot);
       }
     }
-    if constexpr (!PC) {
+    if constexpr (EARLY) {
+      // the score backward runs in the last pass
+    } else if constexpr (!PC) {
       // head_scores_backward (combined_backward.rs:376-416) with drkk = dAkk⊙M,
       // drqk = dAqk⊙M: d_ke += drkk·K, d_qs += drqk·K, d_k += drkkᵀ·ke +
       // drqkᵀ·qs. The d_G term Σⱼ d_diff[i][j] − d_diff[j][i] of
@@ -1179,7 +1221,10 @@ bool mfma_chunk_bwd_supported(const Dims& d, int qkv_dtype) {
 size_t mfma_chunk_bwd_partials(const Dims& d) {
   if (d.V <= 128) return 0;
   const size_t rows = size_t(d.B) * d.S * d.H;
-  return align_up(rows * (2 * d.K + d.ew + d.dw + (d.ww == 1 ? 1 : 0)) * sizeof(float), 256);
+  const bool pc = d.dw == d.K && d.K > 1;
+  const size_t G = size_t(d.B) * d.N * d.H;
+  return align_up(rows * (2 * d.K + d.ew + d.dw + (d.ww == 1 ? 1 : 0)) * sizeof(float), 256) +
+         (pc ? 0 : G * kNT * 16 * sizeof(float));  // dattn and dT partial sums
 }
 
 hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const void* q,
@@ -1231,12 +1276,21 @@ hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const v
   p.pe = p.pk ? p.pk + rows * d.K : nullptr;
   p.pg = p.pe ? p.pe + rows * d.ew : nullptr;
   p.pw = p.pg ? p.pg + rows * d.dw : nullptr;
+  p.pda = nullptr;
+  if (partials && !pc) {
+    const size_t head = align_up(rows * (2 * d.K + d.ew + d.dw + (d.ww == 1 ? 1 : 0)) *
+                                     sizeof(float), 256);
+    p.pda = reinterpret_cast<float*>(reinterpret_cast<char*>(partials) + head);
+  }
   ProfScope ps("dn_mfma_chunk_bwd", stream);
 #define DN_CB(KD, VD, PCV, TG)                                                                  \
   hipLaunchKernelGGL((mfma_chunk_bwd_kernel<KD, VD, PCV, TG>), dim3(unsigned(G)), dim3(kNT), 0, \
                      stream, p)
 #define DN_CB_L(KD, TG)                                                                        \
   hipLaunchKernelGGL((mfma_chunk_bwd_kernel<KD, 128, false, TG, true>), dim3(unsigned(G)),      \
+                     dim3(kNT), 0, stream, p)
+#define DN_CB_E(KD, TG)                                                                          \
+  hipLaunchKernelGGL((mfma_chunk_bwd_kernel<KD, 128, false, TG, false, true>), dim3(unsigned(G)), \
                      dim3(kNT), 0, stream, p)
 #define DN_CB_T(KD, VD, PCV)              \
   do {                                    \
@@ -1258,6 +1312,12 @@ hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const v
       } else {
         if (f32) DN_CB_L(64, float); else DN_CB_L(64, bf16);
       }
+    } else if ((p.pass == 1 || p.pass == 2) && !pc) {
+      if (d.K == 128) {
+        if (f32) DN_CB_E(128, float); else DN_CB_E(128, bf16);
+      } else {
+        if (f32) DN_CB_E(64, float); else DN_CB_E(64, bf16);
+      }
     } else if (d.K == 128) {
       if (vd == 128) DN_CB_P(128, 128); else DN_CB_P(128, 64);
     } else {
@@ -1267,6 +1327,7 @@ hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const v
     if (e != hipSuccess) return e;
   }
 #undef DN_CB_P
+#undef DN_CB_E
 #undef DN_CB_L
 #undef DN_CB_T
 #undef DN_CB
