@@ -201,8 +201,12 @@ BWD_CASES = [
     (1, 256, 2, 128, 128, (128, 128), {"const_keys": True}),
     (1, 192, 2, 128, 128, "head", {"beta_scale": 2.0}),
     # head_v_dim a multiple of 128 above 128: the chunk-local kernel in passes
-    # of 128 value columns, the value-summed gradients added across them
+    # of 128 value columns, the value-summed gradients added across them, and
+    # (per-head gates) dattn and dT handed to the last pass, which runs the
+    # score backward once
     (1, 128, 2, 128, 256, "head"),
+    (1, 150, 2, 64, 256, "head"),
+    (1, 128, 2, 64, 384, None),
     (1, 200, 2, 128, 256, (128, 256)),
     (1, 130, 2, 128, 256, (1, 1)),
     (1, 192, 2, 128, 384, "head"),
