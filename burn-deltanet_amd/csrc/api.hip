@@ -217,12 +217,20 @@ int check_bwd(const dn_chunk_bwd_args* a) {
 
 bool mfma_requested(int algo) { return algo == DN_ALGO_MFMA || algo == DN_ALGO_MFMA_FUSED; }
 
+// The MFMA kernels read q and k in 16-byte words and v in 4-byte words; a
+// tensor view that starts off those boundaries takes the generic kernels.
+bool mfma_aligned(const void* q, const void* k, const void* v) {
+  return reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(v) % 4 == 0;
+}
+
 // The forward's kernels: DN_ALGO_GENERIC, DN_ALGO_MFMA (intra + scan) or,
 // on request only, DN_ALGO_MFMA_FUSED (one kernel; at BASELINE config 2 on
 // a warm MI355X 0.48 ms against the two kernels' 0.45 ms).
 int fwd_algo(const dn_chunk_fwd_args* a, const Dims& d) {
   if (a->algo == DN_ALGO_GENERIC) return DN_ALGO_GENERIC;
-  const bool fits = mfma_fwd_supported(d, a->qkv_dtype, a->y_dtype);
+  const bool fits =
+      mfma_fwd_supported(d, a->qkv_dtype, a->y_dtype) && mfma_aligned(a->q, a->k, a->v);
   if (a->algo == DN_ALGO_MFMA_FUSED)
     return fits && fused_fwd_supported(d, a->qkv_dtype) ? DN_ALGO_MFMA_FUSED
                                                          : DN_ERR_UNSUPPORTED;
@@ -246,7 +254,8 @@ Dims bwd_dims(const dn_chunk_bwd_args* a) {
 // gradients too; otherwise those stay on the generic fp32 kernel.
 int bwd_algo(const dn_chunk_bwd_args* a, const Dims& d) {
   if (a->algo == DN_ALGO_GENERIC) return DN_ALGO_GENERIC;
-  const bool fits = mfma_fwd_supported(d, a->qkv_dtype, DN_BF16);
+  const bool fits =
+      mfma_fwd_supported(d, a->qkv_dtype, DN_BF16) && mfma_aligned(a->q, a->k, a->v);
   if (mfma_requested(a->algo)) return fits ? DN_ALGO_MFMA : DN_ERR_UNSUPPORTED;
   return fits ? DN_ALGO_MFMA : DN_ALGO_GENERIC;
 }

@@ -150,6 +150,24 @@ def test_forward_algorithm_choice():
 
 
 @fake_pointers
+def test_mfma_paths_need_word_aligned_qkv():
+    """The MFMA kernels read q and k in 16-byte words and v in 4-byte words:
+    a view that starts off those boundaries runs the generic kernels under
+    AUTO, and an explicit MFMA request is refused (no pointer is read)."""
+    lib = abi.lib()
+    base = dict(batch=8, sequence=4096, nheads=16, head_k_dim=128, head_v_dim=256,
+                qkv_dtype=abi.DN_BF16, y_dtype=abi.DN_BF16)
+    for over, auto in ((dict(), abi.DN_ALGO_MFMA), (dict(q=0x1008), abi.DN_ALGO_GENERIC),
+                       (dict(k=0x1002), abi.DN_ALGO_GENERIC), (dict(v=0x1002), abi.DN_ALGO_GENERIC),
+                       (dict(v=0x1004), abi.DN_ALGO_MFMA)):
+        a = fwd_args(**base, **over, algo=abi.DN_ALGO_AUTO)
+        assert lib.dn_chunk_fwd_algo(ctypes.byref(a)) == auto, over
+        a = fwd_args(**base, **over, algo=abi.DN_ALGO_MFMA)
+        want = abi.DN_ALGO_MFMA if auto == abi.DN_ALGO_MFMA else -9
+        assert lib.dn_chunk_fwd_algo(ctypes.byref(a)) == want, over
+
+
+@fake_pointers
 def test_bwd_rejects_missing_d_g():
     lib = abi.lib()
     a = abi.ChunkBwdArgs()
