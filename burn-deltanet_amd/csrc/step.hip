@@ -360,7 +360,9 @@ __global__ __launch_bounds__(kRowThreads, RPT <= 16 ? 4 : 2) void recurrent_row_
 #pragma unroll
   for (int r = 0; r < RPT; ++r) {
     const int i = rg + kRowWaves * r;
-    s[r] = (i < K && colok) ? *reinterpret_cast<const vec*>(sin + size_t(i) * V) : vec(0.f);
+    s[r] = (i < K && colok)
+               ? __builtin_nontemporal_load(reinterpret_cast<const vec*>(sin + size_t(i) * V))
+               : vec(0.f);
   }
   stage(0, 0);
   __syncthreads();
@@ -479,7 +481,7 @@ __global__ __launch_bounds__(kRowThreads, RPT <= 16 ? 4 : 2) void recurrent_row_
 #pragma unroll
   for (int r = 0; r < RPT; ++r) {
     const int i = rg + kRowWaves * r;
-    if (i < K && colok) *reinterpret_cast<vec*>(sout + size_t(i) * V) = s[r];
+    if (i < K && colok) __builtin_nontemporal_store(s[r], reinterpret_cast<vec*>(sout + size_t(i) * V));
   }
 }
 
