@@ -2,8 +2,10 @@
 // reference's assertions, workspace management and kernel dispatch.
 
 #include <cmath>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <initializer_list>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -100,13 +102,30 @@ hipError_t scratch_ptr(void** out) {
 
 bool valid_dtype(int t) { return t == DN_F32 || t == DN_BF16; }
 
+// The product of the extents, or -1 when one of them exceeds INT32_MAX (the
+// kernels' index width) or the product overflows.
+int64_t extent(std::initializer_list<int64_t> xs) {
+  int64_t n = 1;
+  for (const int64_t x : xs)
+    if (x > INT32_MAX || __builtin_mul_overflow(n, x, &n)) return -1;
+  return n;
+}
+// An extent that is unrepresentable or reaches `limit`.
+bool too_large(std::initializer_list<int64_t> xs, int64_t limit) {
+  const int64_t n = extent(xs);
+  return n < 0 || n >= limit;
+}
+
 // The reference's shape/gate checks (path.rs:177-208, recurrent.rs:51-54).
 int check_common(int64_t batch, int64_t sequence, int64_t nheads, int64_t K, int64_t V,
                  int64_t ew, int64_t ww, int64_t dw, int32_t has_gate) {
   if (sequence < 1) return fail(DN_ERR_SEQUENCE, "sequence length must be at least 1");
   if (batch < 1 || nheads < 1 || K < 1 || V < 1)
     return fail(DN_ERR_SHAPE, "batch, nheads, head_k_dim and head_v_dim must be at least 1");
-  if (batch * sequence * nheads * (K > V ? K : V) >= (int64_t(1) << 40))
+  // Every extent fits the kernels' 32-bit index arithmetic, and the largest
+  // tensor stays below 2^40 elements (checked factor by factor, so the
+  // product cannot overflow on the way).
+  if (too_large({batch, sequence, nheads, K > V ? K : V}, int64_t(1) << 40))
     return fail(DN_ERR_SHAPE, "tensor too large");
   if (!(ew == 1 || ew == K))
     return fail(DN_ERR_GATE_WIDTH, "erase gate: last axis must be 1 or " + std::to_string(K) +
@@ -186,12 +205,22 @@ int nonfinite_check(const std::vector<Guarded>& list, hipStream_t stream, const 
   return DN_OK;
 }
 
+// The generic kernels index a chunk's L×L and L×head-dim tiles with 32-bit
+// integers (a chunk longer than the sequence is padded to its full length).
+int check_chunk_len(int64_t L, int64_t K, int64_t V) {
+  if (L < 1) return fail(DN_ERR_CHUNK_LEN, "chunk_len must be at least 1");
+  if (L * L > INT32_MAX || L * (K > V ? K : V) > INT32_MAX)
+    return fail(DN_ERR_CHUNK_LEN, "chunk_len too large: chunk_len² and chunk_len·head dim must "
+                                  "stay below 2^31");
+  return DN_OK;
+}
+
 int check_fwd(const dn_chunk_fwd_args* a) {
   if (!a) return fail(DN_ERR_NULL, "args is NULL");
   if (int rc = check_common(a->batch, a->sequence, a->nheads, a->head_k_dim, a->head_v_dim,
                             a->erase_width, a->write_width, a->decay_width, a->has_gate))
     return rc;
-  if (a->chunk_len < 1) return fail(DN_ERR_CHUNK_LEN, "chunk_len must be at least 1");
+  if (int rc = check_chunk_len(a->chunk_len, a->head_k_dim, a->head_v_dim)) return rc;
   if (!valid_dtype(a->qkv_dtype) || !valid_dtype(a->y_dtype))
     return fail(DN_ERR_DTYPE, "dtype must be DN_F32 or DN_BF16");
   if (!a->q || !a->k || !a->v || !a->erase || !a->write || !a->state_in || !a->y ||
@@ -205,7 +234,7 @@ int check_bwd(const dn_chunk_bwd_args* a) {
   if (int rc = check_common(a->batch, a->sequence, a->nheads, a->head_k_dim, a->head_v_dim,
                             a->erase_width, a->write_width, a->decay_width, a->has_gate))
     return rc;
-  if (a->chunk_len < 1) return fail(DN_ERR_CHUNK_LEN, "chunk_len must be at least 1");
+  if (int rc = check_chunk_len(a->chunk_len, a->head_k_dim, a->head_v_dim)) return rc;
   if (!valid_dtype(a->qkv_dtype) || !valid_dtype(a->grad_dtype))
     return fail(DN_ERR_DTYPE, "dtype must be DN_F32 or DN_BF16");
   if (!a->d_y || !a->q || !a->k || !a->v || !a->erase || !a->write || !a->state_in ||
@@ -532,6 +561,9 @@ int dn_frontend(const dn_frontend_args* a, hipStream_t stream) {
   const bool has_conv = a->conv_kernel > 0;
   if (has_conv != (a->window_in != nullptr) || has_conv != (a->window_out != nullptr))
     return fail(DN_ERR_SHAPE, "convolution window presence must match the block's convolution");
+  // Bounds the column arithmetic below (head dims are at most 4096).
+  if (too_large({a->nheads, a->n_householder}, int64_t(1) << 31))
+    return fail(DN_ERR_SHAPE, "tensor too large");
   const int64_t H = a->nheads, u = a->n_householder;
   const int64_t key_dim = H * a->head_k_dim, value_dim = H * a->head_v_dim;
   const int64_t conv_dim = key_dim + u * (key_dim + value_dim);
@@ -542,9 +574,9 @@ int dn_frontend(const dn_frontend_args* a, hipStream_t stream) {
     return fail(DN_ERR_SHAPE, "proj_stride " + std::to_string(a->proj_stride) +
                                   " is narrower than the conv and write-gate columns (" +
                                   std::to_string(conv_dim + gate_w) + ")");
-  if (a->batch * a->sequence >= (int64_t(1) << 31) || conv_dim >= (int64_t(1) << 31) ||
-      a->batch * a->sequence * a->proj_stride >= (int64_t(1) << 40) ||
-      a->batch * a->sequence * (gate_w > u * H ? gate_w : u * H) >= (int64_t(1) << 32))
+  if (too_large({a->batch, a->sequence}, int64_t(1) << 31) || conv_dim >= (int64_t(1) << 31) ||
+      too_large({a->batch, a->sequence, a->proj_stride}, int64_t(1) << 40) ||
+      too_large({a->batch, a->sequence, gate_w > u * H ? gate_w : u * H}, int64_t(1) << 32))
     return fail(DN_ERR_SHAPE, "tensor too large");
   if (!a->projected || !a->q || !a->k || !a->v || !a->erase || !a->write ||
       (has_conv && !a->conv_weight))
@@ -571,7 +603,8 @@ int dn_out_norm(const dn_out_norm_args* a, hipStream_t stream) {
   if (a->gate && a->gate_stride < a->nheads * a->head_v_dim)
     return fail(DN_ERR_SHAPE, "gate_stride is narrower than one token's gates");
   if (!(a->eps >= 0.0)) return fail(DN_ERR_SHAPE, "eps must be a non-negative number");
-  if (a->tokens * a->nheads >= (int64_t(1) << 40)) return fail(DN_ERR_SHAPE, "tensor too large");
+  if (too_large({a->tokens, a->nheads}, int64_t(1) << 40))
+    return fail(DN_ERR_SHAPE, "tensor too large");
   hipError_t e = launch_out_norm(*a, stream);
   if (e != hipSuccess) return hip_fail(e, "dn_out_norm launch");
   return DN_OK;
@@ -613,6 +646,7 @@ int dn_block_step(const dn_block_step_args* a, hipStream_t stream) {
   const bool has_conv = a->conv_kernel > 0;
   if (has_conv != (a->window_in != nullptr) || has_conv != (a->window_out != nullptr))
     return fail(DN_ERR_SHAPE, "convolution window presence must match the block's convolution");
+  if (a->nheads > INT32_MAX) return fail(DN_ERR_SHAPE, "tensor too large");
   const int64_t H = a->nheads, key_dim = H * a->head_k_dim, value_dim = H * a->head_v_dim;
   const int64_t conv_dim = 2 * key_dim + value_dim;
   const int64_t gate_w = a->write_gate == DN_WRITE_FIXED    ? 0
@@ -623,7 +657,8 @@ int dn_block_step(const dn_block_step_args* a, hipStream_t stream) {
     return fail(DN_ERR_SHAPE, "proj_stride " + std::to_string(a->proj_stride) +
                                   " is narrower than the conv, write-gate and norm-gate columns (" +
                                   std::to_string(width) + ")");
-  if (a->batch * H >= (int64_t(1) << 31) || a->batch * a->proj_stride >= (int64_t(1) << 40))
+  if (too_large({a->batch, H}, int64_t(1) << 31) ||
+      too_large({a->batch, a->proj_stride}, int64_t(1) << 40))
     return fail(DN_ERR_SHAPE, "tensor too large");
   if (!a->projected || !a->state_in || !a->state_out || !a->norm_weight || !a->out ||
       (has_conv && !a->conv_weight) || (a->has_gate && !a->g))
@@ -658,8 +693,8 @@ int dn_unit_lower_inverse(const dn_tri_args* a, hipStream_t stream) {
   g_last_error.clear();
   if (!a) return fail(DN_ERR_NULL, "args is NULL");
   if (a->batch < 0 || a->size < 0) return fail(DN_ERR_SHAPE, "batch and size must be at least 0");
-  if (a->size > (int64_t(1) << 20) || a->batch * a->size * a->size >= (int64_t(1) << 40) ||
-      a->batch * ((a->size + 63) / 64) >= (int64_t(1) << 31))
+  if (a->size > (int64_t(1) << 20) || too_large({a->batch, a->size, a->size}, int64_t(1) << 40) ||
+      too_large({a->batch, (a->size + 63) / 64}, int64_t(1) << 31))
     return fail(DN_ERR_SHAPE, "tensor too large");
   if (a->solve != DN_TRI_BLOCKED && a->solve != DN_TRI_NEUMANN)
     return fail(DN_ERR_UNSUPPORTED, "solve must be DN_TRI_BLOCKED or DN_TRI_NEUMANN");

@@ -80,7 +80,8 @@ typedef enum {
   DN_ERR_SHAPE = -2,       /* a dimension < 1, or shapes that disagree (path.rs:180-185,
                               recurrent.rs:51-54) */
   DN_ERR_GATE_WIDTH = -3,  /* "{gate}: last axis must be 1 or {full}" (path.rs:187-197) */
-  DN_ERR_CHUNK_LEN = -4,   /* "chunk_len must be at least 1" (path.rs:219) */
+  DN_ERR_CHUNK_LEN = -4,   /* "chunk_len must be at least 1" (path.rs:219); also chunk_len²
+                              or chunk_len·max(head_k_dim, head_v_dim) at or above 2^31 */
   DN_ERR_NONFINITE = -5,   /* NaN/Inf guard on inputs or outputs (sanity, path.rs:198-207) */
   DN_ERR_NULL = -6,        /* a required pointer is NULL */
   DN_ERR_DTYPE = -7,       /* unknown dtype tag */

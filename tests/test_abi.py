@@ -63,6 +63,14 @@ def fwd_args(**over):
     (dict(write_width=5), -3, "write gate: last axis must be 1 or 6, got 5"),
     (dict(decay_width=2), -3, "forget gate: last axis must be 1 or 4, got 2"),
     (dict(chunk_len=0), -4, "chunk_len must be at least 1"),
+    # The generic kernels' 32-bit tile indexing: chunk_len² and chunk_len·dv.
+    (dict(chunk_len=46341), -4, "chunk_len too large"),
+    (dict(chunk_len=1 << 15, head_v_dim=1 << 16, write_width=1), -4, "chunk_len too large"),
+    (dict(chunk_len=46340, q=None), -6, "NULL"),  # the largest accepted, then the next check
+    # Extents past 32 bits, or a product that would overflow on the way,
+    # are refused rather than narrowed.
+    (dict(sequence=(1 << 31) + 1), -2, "tensor too large"),
+    (dict(batch=1 << 30, sequence=1 << 30, nheads=1 << 30), -2, "tensor too large"),
     (dict(qkv_dtype=7), -7, "dtype"),
     (dict(q=None), -6, "NULL"),
 ])
@@ -254,6 +262,9 @@ def frontend_args(**over):
     (dict(out_dtype=5), -7, "dtype"),
     (dict(q=None), -6, "NULL"),
     (dict(write_gate=abi.DN_WRITE_CHANNEL, proj_stride=100), -2, "separate buffers"),
+    # Extents past 32 bits, or products that would overflow int64, are refused.
+    (dict(nheads=1 << 31, proj_stride=10 ** 5), -2, "tensor too large"),
+    (dict(batch=1 << 40, sequence=1 << 40), -2, "tensor too large"),
 ])
 @fake_pointers
 def test_frontend_rejects_invalid_arguments(over, code, msg):
@@ -272,6 +283,7 @@ def test_frontend_rejects_invalid_arguments(over, code, msg):
     (dict(eps=-1.0), -2, "eps"),
     (dict(out_dtype=4), -7, "dtype"),
     (dict(weight=None), -6, "NULL"),
+    (dict(nheads=1 << 31, gate_stride=1 << 40), -2, "tensor too large"),
 ])
 @fake_pointers
 def test_out_norm_rejects_invalid_arguments(over, code, msg):
@@ -291,6 +303,7 @@ def test_out_norm_rejects_invalid_arguments(over, code, msg):
     (dict(size=-1), -2, "at least 0"),
     (dict(batch=-2), -2, "at least 0"),
     (dict(size=1 << 21), -2, "too large"),
+    (dict(batch=1 << 62, size=64), -2, "too large"),  # the product would overflow int64
     (dict(solve=2), -9, "DN_TRI_BLOCKED or DN_TRI_NEUMANN"),
     (dict(solve=abi.DN_TRI_NEUMANN, size=abi.TRI_NEUMANN_MAX_SIZE + 1), -9, "up to 140"),
     (dict(), -6, "NULL"),
@@ -345,6 +358,7 @@ def block_step_args(**over):
     (dict(eps=-1.0), -2, "eps"),
     (dict(conv_kernel=4), -2, "window presence"),
     (dict(proj_stride=100), -2, "narrower than the conv, write-gate and norm-gate columns"),
+    (dict(nheads=1 << 31), -2, "tensor too large"),
     (dict(), -6, "NULL"),
 ])
 def test_block_step_rejects_invalid_arguments(over, code, msg):
