@@ -310,7 +310,13 @@ def run_recurrent(args: RecurrentArgs) -> None:
 
 
 def _ptr(t):
-    return None if t is None else t.data_ptr()
+    """A tensor's address for the C ABI, whose kernels read it on the GPU: a
+    host tensor is refused here rather than handed over as a host pointer."""
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise DeltaError(-6, "tensors must live on the GPU (no CPU fallback)")
+    return t.data_ptr()
 
 
 def frontend_args(projected, conv_weight, conv_bias, window_in, window_out, q, k, v, erase,

@@ -98,16 +98,8 @@ class DeltaInput:
 
     def sanity(self) -> None:
         """path.rs:177-208 (shape and gate-width checks)."""
-        batch, sequence, nheads, head_k_dim, head_v_dim = self.dims()
-        if sequence <= 0:
-            raise DeltaError(-1, "sequence length must be at least 1")
-        _expect(self.k_bshk, (batch, sequence, nheads, head_k_dim), "k")
-        _expect(self.v_bshv, (batch, sequence, nheads, head_v_dim), "v")
-        _expect(self.state_bhkv, (batch, nheads, head_k_dim, head_v_dim), "state")
-        _gate_axis(self.erase_bshK, (batch, sequence, nheads), head_k_dim, "erase gate")
-        _gate_axis(self.write_bshV, (batch, sequence, nheads), head_v_dim, "write gate")
-        if self.g_bshK is not None:
-            _gate_axis(self.g_bshK, (batch, sequence, nheads), head_k_dim, "forget gate")
+        _check_shapes(self.q_bshk, self.k_bshk, self.v_bshv, self.erase_bshK, self.write_bshV,
+                      self.g_bshK, self.state_bhkv)
 
     def run(self, path: DeltaPath = DeltaPath.default(), check_finite: bool = False):
         """path.rs:215-231. Returns (y_bshv, final_state_bhkv)."""
@@ -123,6 +115,7 @@ class DeltaInput:
         """recurrent.rs:107-142: delta_step unrolled over the sequence — one
         dn_recurrent call (the state stays on chip across the tokens), or
         dn_step per token for head_k_dim above dn_recurrent's limit."""
+        self.sanity()
         batch, sequence, nheads, head_k_dim, head_v_dim = self.dims()
         scale = self.resolved_scale()
         if head_k_dim <= abi.RECURRENT_MAX_K:
@@ -163,10 +156,34 @@ def _expect(t: Tensor, shape, what):
 
 
 def _gate_axis(t: Tensor, lead, full, what):
-    if t.dim() != 4 or tuple(t.shape[:3]) != tuple(lead):
+    n = len(lead)
+    if t.dim() != n + 1 or tuple(t.shape[:n]) != tuple(lead):
         raise DeltaError(-2, f"{what}: expected leading dims {list(lead)}, got {list(t.shape)}")
-    if t.shape[3] not in (1, full):
-        raise DeltaError(-3, f"{what}: last axis must be 1 or {full}, got {t.shape[3]}")
+    if t.shape[n] not in (1, full):
+        raise DeltaError(-3, f"{what}: last axis must be 1 or {full}, got {t.shape[n]}")
+
+
+def _check_shapes(q, k, v, erase, write, g, state, sequence_axis: bool = True):
+    """path.rs:177-208's shape and gate-width checks (recurrent.rs:51-54 for a
+    step, sequence_axis=False), run by every entry that hands buffers to the C
+    ABI: the library sees plain pointers and sizes taken from q and v, so a
+    tensor that disagrees with them would be read out of bounds."""
+    nd = 4 if sequence_axis else 3
+    what = "[batch, sequence, nheads, ·]" if sequence_axis else "[batch, nheads, ·]"
+    for t, name in ((q, "q"), (v, "v")):
+        if t.dim() != nd:
+            raise DeltaError(-2, f"{name}: expected {what}, got {list(t.shape)}")
+    lead, head_k_dim, head_v_dim = tuple(q.shape[:-1]), q.shape[-1], v.shape[-1]
+    if sequence_axis and lead[1] <= 0:
+        raise DeltaError(-1, "sequence length must be at least 1")
+    batch, nheads = lead[0], lead[-1]
+    _expect(k, lead + (head_k_dim,), "k")
+    _expect(v, lead + (head_v_dim,), "v")
+    _expect(state, (batch, nheads, head_k_dim, head_v_dim), "state")
+    _gate_axis(erase, lead, head_k_dim, "erase gate")
+    _gate_axis(write, lead, head_v_dim, "write gate")
+    if g is not None:
+        _gate_axis(g, lead, head_k_dim, "forget gate")
 
 
 def _dev(t: Optional[Tensor], dtype=None) -> Optional[Tensor]:
@@ -209,6 +226,8 @@ def delta_chunk_recalculated(q_bshk, k_bshk, v_bshv, erase_bshK, write_bshV, g_b
                              y_dtype=None):
     """DeltaChunkBackendExt::delta_chunk_recalculated (chunk_recalculated.rs:110-151):
     `g_bshK` is read only when `has_gate`."""
+    _check_shapes(q_bshk, k_bshk, v_bshv, erase_bshK, write_bshV,
+                  g_bshK if has_gate else None, state_bhkv)
     dt = _qkv_dtype(q_bshk, k_bshk, v_bshv)
     q, k, v = _dev(q_bshk), _dev(k_bshk), _dev(v_bshv)
     e, w = _dev(erase_bshK, torch.float32), _dev(write_bshV, torch.float32)
@@ -241,10 +260,10 @@ def delta_step(q_bhk, k_bhk, v_bhv, erase_bhK, write_bhV, g_bhK, state_bhkv, sca
                check_finite: bool = False, in_place: bool = False, y_dtype=None):
     """recurrent.rs:41-99. Returns (y_bhv, next_state_bhkv). With
     `in_place=True` the state buffer itself is updated and returned."""
+    _check_shapes(q_bhk, k_bhk, v_bhv, erase_bhK, write_bhV, g_bhK, state_bhkv,
+                  sequence_axis=False)
     batch, nheads, head_k_dim = q_bhk.shape
     head_v_dim = v_bhv.shape[2]
-    _expect(k_bhk, (batch, nheads, head_k_dim), "k")
-    _expect(state_bhkv, (batch, nheads, head_k_dim, head_v_dim), "state")
     dt = _qkv_dtype(q_bhk, k_bhk, v_bhv)
     q, k, v = _dev(q_bhk), _dev(k_bhk), _dev(v_bhv)
     e, w = _dev(erase_bhK, torch.float32), _dev(write_bhV, torch.float32)
@@ -274,6 +293,10 @@ def combined_backward(d_y_bshv, d_final_state_bhkv, q_bshk, k_bshk, v_bshv, eras
                       algo: int = abi.DN_ALGO_AUTO, check_finite: bool = False):
     """combined_backward.rs:72-189: recompute the chunk forward, then its
     closed-form gradient. Returns DeltaChunkGrads."""
+    _check_shapes(q_bshk, k_bshk, v_bshv, erase_bshK, write_bshV, g_bshK, state_bhkv)
+    _expect(d_y_bshv, tuple(q_bshk.shape[:3]) + (v_bshv.shape[3],), "d_y")
+    if d_final_state_bhkv is not None:
+        _expect(d_final_state_bhkv, tuple(state_bhkv.shape), "d_final_state")
     _qkv_dtype(q_bshk, k_bshk, v_bshv)
     q, k, v = _dev(q_bshk), _dev(k_bshk), _dev(v_bshv)
     e, w = _dev(erase_bshK, torch.float32), _dev(write_bshV, torch.float32)

@@ -220,10 +220,13 @@ class QkvProjection:
         if (self.conv is None) != (window is None):
             raise DeltaError(-2, "convolution window presence must match the block's "
                                  "convolution")  # qkv.rs:397-401
+        B, S, _ = p.shape
+        if window is not None and tuple(window.shape) != (B, self.conv_dim(), self.conv_kernel()):
+            raise DeltaError(-2, f"conv window: expected {[B, self.conv_dim(), self.conv_kernel()]}"
+                                 f", got {list(window.shape)}")
         if not p.is_cuda:
             raise DeltaError(-6, "tensors must live on the GPU (no CPU fallback)")
         p = p.contiguous()
-        B, S, _ = p.shape
         H, dk, dv, u = self.nheads, self.head_k_dim, self.head_v_dim, self.n_householder
         od = p.dtype if out_dtype is None else out_dtype
         dev = p.device
@@ -275,6 +278,8 @@ class OutNorm:
             raise DeltaError(-6, "OutNorm::Gated needs an output gate")
         if not self.gated and gate is not None:
             raise DeltaError(-2, "OutNorm::Plain takes no output gate")
+        if self.weight.numel() != x.shape[-1]:
+            raise DeltaError(-2, f"weight: expected {x.shape[-1]} values, got {self.weight.numel()}")
         if not x.is_cuda:
             raise DeltaError(-6, "tensors must live on the GPU (no CPU fallback)")
         x = x.contiguous()
@@ -292,7 +297,7 @@ def block_step_args(proj: QkvProjection, norm: OutNorm, projected_bw: Tensor,
     """dn_block_step's arguments for `block_step` and the tensors it writes:
     (args, out_bhv, next_window, next_state, y_bhv or None, kept) — `kept`
     holds the converted inputs the arguments point into."""
-    from .delta import _dev
+    from .delta import _dev, _expect, _gate_axis
     B, W = projected_bw.shape
     if W != proj.d_in_proj():
         raise DeltaError(-2, f"projection width {W} != d_in_proj {proj.d_in_proj()}")
@@ -303,6 +308,15 @@ def block_step_args(proj: QkvProjection, norm: OutNorm, projected_bw: Tensor,
     if norm.gated and not proj.has_gate:
         raise DeltaError(-6, "OutNorm::Gated needs the projection's output gate")
     H, dk, dv = proj.nheads, proj.head_k_dim, proj.head_v_dim
+    # The library sizes every buffer from these dims: a tensor that disagrees
+    # would be read out of bounds.
+    _expect(state_bhkv, (B, H, dk, dv), "state")
+    if g_bhK is not None:
+        _gate_axis(g_bhK, (B, H), dk, "forget gate")
+    if conv_window_bwc is not None:
+        _expect(conv_window_bwc, (B, proj.conv_dim(), proj.conv_kernel()), "conv window")
+    if norm.weight.numel() != dv:
+        raise DeltaError(-2, f"norm weight: expected {dv} values, got {norm.weight.numel()}")
     p = _dev(projected_bw)
     state = _dev(state_bhkv, torch.float32)
     g = _dev(g_bhK, torch.float32)
@@ -329,8 +343,8 @@ def block_step_args(proj: QkvProjection, norm: OutNorm, projected_bw: Tensor,
         bias = None if proj.conv.bias is None else proj.conv.bias.float().contiguous()
         win_in = conv_window_bwc.to(p.dtype).contiguous()
         win_out = win_in if (in_place and win_in is conv_window_bwc) else torch.empty_like(win_in)
-        a.conv_weight, a.conv_bias = weight.data_ptr(), None if bias is None else bias.data_ptr()
-        a.window_in, a.window_out = win_in.data_ptr(), win_out.data_ptr()
+        a.conv_weight, a.conv_bias = abi._ptr(weight), abi._ptr(bias)
+        a.window_in, a.window_out = abi._ptr(win_in), abi._ptr(win_out)
         kept += [weight, bias, win_in]
     s_out = state if (in_place and state is state_bhkv) else torch.empty_like(state)
     gamma = norm.weight.float().contiguous()
@@ -338,7 +352,7 @@ def block_step_args(proj: QkvProjection, norm: OutNorm, projected_bw: Tensor,
     y = torch.empty((B, H, dv), dtype=torch.float32, device=p.device) if return_y else None
     a.projected, a.g = p.data_ptr(), None if g is None else g.data_ptr()
     a.state_in, a.state_out = state.data_ptr(), s_out.data_ptr()
-    a.norm_weight, a.out = gamma.data_ptr(), out.data_ptr()
+    a.norm_weight, a.out = abi._ptr(gamma), out.data_ptr()
     a.y = None if y is None else y.data_ptr()
     kept.append(gamma)
     return a, out, win_out, s_out, y, kept
