@@ -1001,20 +1001,58 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
       };
 #pragma unroll
       for (int st = 0; st < PD; ++st) rd(st);
+      // Two-wave per-head scans (one wave per SIMD) split the next k-step's
+      // S fragments while this one's MFMAs run, interleaved one MFMA to two
+      // VALU instructions (config 4 1.09 → 1.05 ms). With two waves per
+      // SIMD the other wave covers the split, and so interleaved the
+      // eight-wave scan measured slower (315 → 345 µs), as did the
+      // per-channel states mode.
+      constexpr bool kPipe = WAVES == 2 && !PC && !ST;
+      if constexpr (kPipe) {
+        uint4 sh = frag_hi(S[0], S[1]);
+        uint4 sl = frag_lo(S[0], S[1], sh);
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        const uint4 sh = frag_hi(S[2 * kk], S[2 * kk + 1]);
-        const uint4 sl = frag_lo(S[2 * kk], S[2 * kk + 1], sh);
+        for (int kk = 0; kk < KK; ++kk) {
+          uint4 shn = sh, sln = sl;
+          if (kk + 1 < KK) {
+            shn = frag_hi(S[2 * kk + 2], S[2 * kk + 3]);
+            sln = frag_lo(S[2 * kk + 2], S[2 * kk + 3], shn);
+          }
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
-          const int step = 4 * kk + tb;
-          if (step + PD < NSTEP) rd(step + PD);
-          const int c = step % NR;
-          X[tb] = mfma16(kf[c], as8(sh), X[tb]);
-          X[tb] = mfma16(kf[c], as8(sl), X[tb]);
-          // kg carries the fp32 gate factors, so it has a lo part too.
-          if constexpr (PC) X[tb] = mfma16(kl[c], as8(sh), X[tb]);
-          yt[tb] = mfma16(as8(sh), qf[c], yt[tb]);
+          for (int tb = 0; tb < 4; ++tb) {
+            const int step = 4 * kk + tb;
+            if (step + PD < NSTEP) rd(step + PD);
+            const int c = step % NR;
+            X[tb] = mfma16(kf[c], as8(sh), X[tb]);
+            X[tb] = mfma16(kf[c], as8(sl), X[tb]);
+            yt[tb] = mfma16(as8(sh), qf[c], yt[tb]);
+          }
+          if (kk + 1 < KK) {
+#pragma unroll
+            for (int i = 0; i < 12; ++i) {
+              __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+              __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // two VALU
+            }
+          }
+          sh = shn;
+          sl = sln;
+        }
+      } else {
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+          const uint4 sh = frag_hi(S[2 * kk], S[2 * kk + 1]);
+          const uint4 sl = frag_lo(S[2 * kk], S[2 * kk + 1], sh);
+#pragma unroll
+          for (int tb = 0; tb < 4; ++tb) {
+            const int step = 4 * kk + tb;
+            if (step + PD < NSTEP) rd(step + PD);
+            const int c = step % NR;
+            X[tb] = mfma16(kf[c], as8(sh), X[tb]);
+            X[tb] = mfma16(kf[c], as8(sl), X[tb]);
+            // kg carries the fp32 gate factors, so it has a lo part too.
+            if constexpr (PC) X[tb] = mfma16(kl[c], as8(sh), X[tb]);
+            yt[tb] = mfma16(as8(sh), qf[c], yt[tb]);
+          }
         }
       }
     }
