@@ -983,6 +983,15 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
     // yᵀ = Sᵀ·Qᵀ in [column][token] orientation. The S fragments (hi, lo) of
     // k-step kk are the B operand of K·S and the A operand of Sᵀ·Qᵀ (same
     // lane layout). Fragment reads run one (kk, tb) step ahead of the MFMAs.
+    // Two-wave per-head scans (one wave per SIMD) interleave VALU work with
+    // independent MFMAs by hand: in phase 1 the next k-step's S fragments
+    // are split while this one's MFMAs run, one MFMA to two VALU
+    // instructions (config 4 1.09 → 1.05 ms). With two waves per SIMD the
+    // other wave covers the split, and so interleaved the eight-wave scan
+    // measured slower (315 → 345 µs), as did the per-channel states mode;
+    // S's gate products placed under phase 3's attn MFMAs likewise (config 4
+    // 1.05 → 1.20 ms).
+    constexpr bool kPipe = WAVES == 2 && !PC && !ST;
     f32x4 X[4], yt[4];
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
@@ -1001,13 +1010,6 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
       };
 #pragma unroll
       for (int st = 0; st < PD; ++st) rd(st);
-      // Two-wave per-head scans (one wave per SIMD) split the next k-step's
-      // S fragments while this one's MFMAs run, interleaved one MFMA to two
-      // VALU instructions (config 4 1.09 → 1.05 ms). With two waves per
-      // SIMD the other wave covers the split, and so interleaved the
-      // eight-wave scan measured slower (315 → 345 µs), as did the
-      // per-channel states mode.
-      constexpr bool kPipe = WAVES == 2 && !PC && !ST;
       if constexpr (kPipe) {
         uint4 sh = frag_hi(S[0], S[1]);
         uint4 sl = frag_lo(S[0], S[1], sh);
