@@ -1455,24 +1455,69 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_rev_scan_kernel(RevParams p) 
                            pk_bf16(dyR[kk][4], dyR[kk][5]), pk_bf16(dyR[kk][6], dyR[kk][7]));
 
     // Phase 1: dV' = attnᵀ·dY + Kc·dS in [token][column] orientation.
+    // Two-wave workgroups (one wave per SIMD) split each k-step's dS
+    // fragments under the previous step's MFMAs (the first under attnᵀ·dY),
+    // one MFMA to three VALU instructions: config 5's reverse scan 1010 →
+    // 893 µs. With two waves per SIMD the other wave covers the split, and
+    // so interleaved the eight-wave scan measured slower (875 → 904 µs).
+    constexpr bool kPipe = WAVES == 2;
     f32x4 dV[4];
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-      dV[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int tb = 0; tb < 4; ++tb) dV[tb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (kPipe) {
+      uint4 sh = frag_hi(dS[0], dS[1]);
+      uint4 sl = frag_lo(dS[0], dS[1], sh);
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-        dV[tb] = mfma16(ld8(&tl[oAt + tile_at<kL>(16 * tb + r16, 32 * kk + k8)]), as8(dyf[kk]),
-                        dV[tb]);
-    }
+      for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      const uint4 sh = frag_hi(dS[2 * kk], dS[2 * kk + 1]);
-      const uint4 sl = frag_lo(dS[2 * kk], dS[2 * kk + 1], sh);
+        for (int kk = 0; kk < 2; ++kk)
+          dV[tb] = mfma16(ld8(&tl[oAt + tile_at<kL>(16 * tb + r16, 32 * kk + k8)]),
+                          as8(dyf[kk]), dV[tb]);
 #pragma unroll
-      for (int tb = 0; tb < 4; ++tb) {
-        const bf16x8 kf = ld8(&tl[oKc + tile_at<K>(16 * tb + r16, 32 * kk + k8)]);
-        dV[tb] = mfma16(kf, as8(sh), dV[tb]);
-        dV[tb] = mfma16(kf, as8(sl), dV[tb]);
+      for (int i = 0; i < 8; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+      }
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        uint4 shn = sh, sln = sl;
+        if (kk + 1 < KK) {
+          shn = frag_hi(dS[2 * kk + 2], dS[2 * kk + 3]);
+          sln = frag_lo(dS[2 * kk + 2], dS[2 * kk + 3], shn);
+        }
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+          const bf16x8 kf = ld8(&tl[oKc + tile_at<K>(16 * tb + r16, 32 * kk + k8)]);
+          dV[tb] = mfma16(kf, as8(sh), dV[tb]);
+          dV[tb] = mfma16(kf, as8(sl), dV[tb]);
+        }
+        if (kk + 1 < KK) {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // three VALU
+          }
+        }
+        sh = shn;
+        sl = sln;
+      }
+    } else {
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+          dV[tb] = mfma16(ld8(&tl[oAt + tile_at<kL>(16 * tb + r16, 32 * kk + k8)]),
+                          as8(dyf[kk]), dV[tb]);
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        const uint4 sh = frag_hi(dS[2 * kk], dS[2 * kk + 1]);
+        const uint4 sl = frag_lo(dS[2 * kk], dS[2 * kk + 1], sh);
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+          const bf16x8 kf = ld8(&tl[oKc + tile_at<K>(16 * tb + r16, 32 * kk + k8)]);
+          dV[tb] = mfma16(kf, as8(sh), dV[tb]);
+          dV[tb] = mfma16(kf, as8(sl), dV[tb]);
+        }
       }
     }
     load_dy(nn);
