@@ -990,7 +990,8 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
     // other wave covers the split, and so interleaved the eight-wave scan
     // measured slower (315 → 345 µs), as did the per-channel states mode;
     // S's gate products placed under phase 3's attn MFMAs likewise (config 4
-    // 1.05 → 1.20 ms).
+    // 1.05 → 1.20 ms), and X's second k-step split under phase 2's first
+    // nine MFMAs (1.05 → 1.14 ms).
     constexpr bool kPipe = WAVES == 2 && !PC && !ST;
     f32x4 X[4], yt[4];
 #pragma unroll
