@@ -210,6 +210,7 @@ BWD_CASES = [
     (1, 200, 2, 128, 256, (128, 256)),
     (1, 130, 2, 128, 256, (1, 1)),
     (1, 192, 2, 128, 384, "head"),
+    (1, 96, 2, 64, 512, "head"),  # two middle passes, each adding to the handed-on sums
     (1, 128, 2, 128, 256, None),
     (1, 256, 2, 128, 256, "head", {"const_keys": True}),
 ]
