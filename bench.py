@@ -327,17 +327,28 @@ def bench_unit_lower_inverse(torch, pkg, steps, warmup):
 
 
 MIN_STEPS, MIN_WARMUP = 20, 2  # timed calls and warm-ups of every line
+# Untimed run-in before every timed region's warm-up steps: the GPU's clocks
+# ramp over its first ~0.1 s of work after idling (config 2 at 5 warm-ups
+# measured 0.49-0.53 ms per step, at 100 warm-ups 0.43-0.45 ms). The W
+# warm-up steps the caller asks for still run right before the K timed ones.
+SETTLE_S = 0.3
 _EXACT = {"on": False}  # --profile-pass: run exactly the calls asked for, no profiler pass
 
 
 def _timed_raw(torch, abi, fn, steps, warmup):
-    """Mean ms per call of fn() over max(steps, 20) calls after max(warmup, 2),
+    """Mean ms per call of fn() over max(steps, 20) calls after a SETTLE_S
+    run-in and then max(warmup, 2) warm-up calls,
     timed with HIP events on torch's current stream (the stream the library
     launches on) and nothing else recorded inside the timed region; then a
     separate pass with the library's per-kernel HIP-event profiler on, which
     gives {kernel: (total_ms, launches)}."""
     if not _EXACT["on"]:
         steps, warmup = max(steps, MIN_STEPS), max(warmup, MIN_WARMUP)
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < SETTLE_S:
+            for _ in range(4):
+                fn()
+            torch.cuda.synchronize()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -674,7 +685,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=100,
-                    help="untimed steps first (about 50 ms of work: the clocks ramp up)")
+                    help="untimed steps right before the timed ones (after a "
+                         f"{SETTLE_S} s run-in that lets the clocks ramp up)")
     ap.add_argument("--decode-steps", type=int, default=1000)
     ap.add_argument("--algo", choices=["auto", "generic", "mfma", "fused"], default="auto")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -858,6 +870,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle_s": SETTLE_S,
         "ms_per_step": round(fw["ms"], 4),
         "higher_is_better": True,
         "scaling": "weak",

@@ -255,7 +255,7 @@ bool mfma_aligned(const void* q, const void* k, const void* v) {
 
 // The forward's kernels: DN_ALGO_GENERIC, DN_ALGO_MFMA (intra + scan) or,
 // on request only, DN_ALGO_MFMA_FUSED (one kernel; at BASELINE config 2 on
-// a warm MI355X 0.48 ms against the two kernels' 0.45 ms).
+// a warm MI355X 0.47-0.49 ms against the two kernels' 0.43-0.45 ms).
 int fwd_algo(const dn_chunk_fwd_args* a, const Dims& d) {
   if (a->algo == DN_ALGO_GENERIC) return DN_ALGO_GENERIC;
   const bool fits =
@@ -281,10 +281,12 @@ Dims bwd_dims(const dn_chunk_bwd_args* a) {
 // MFMA: the two scans of the backward on bf16 MFMA (the forward MFMA path's
 // shapes, bf16 q/k/v), and for head_v_dim 64 or 128 the chunk-local
 // gradients too; otherwise those stay on the generic fp32 kernel.
+// The backward's MFMA kernels also read d_y in 16-byte words.
 int bwd_algo(const dn_chunk_bwd_args* a, const Dims& d) {
   if (a->algo == DN_ALGO_GENERIC) return DN_ALGO_GENERIC;
-  const bool fits =
-      mfma_fwd_supported(d, a->qkv_dtype, DN_BF16) && mfma_aligned(a->q, a->k, a->v);
+  const bool fits = mfma_fwd_supported(d, a->qkv_dtype, DN_BF16) &&
+                    mfma_aligned(a->q, a->k, a->v) &&
+                    reinterpret_cast<uintptr_t>(a->d_y) % 16 == 0;
   if (mfma_requested(a->algo)) return fits ? DN_ALGO_MFMA : DN_ERR_UNSUPPORTED;
   return fits ? DN_ALGO_MFMA : DN_ALGO_GENERIC;
 }

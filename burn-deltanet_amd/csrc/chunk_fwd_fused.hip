@@ -651,7 +651,7 @@ size_t region(size_t bytes) { return align_up(bytes, 256); }
 // bf16 q/k/v.
 bool fused_fwd_supported(const Dims& d, int qkv_dtype) {
   return qkv_dtype == DN_BF16 && d.K == 128 && d.V % kBW == 0 && d.L == kL && d.ew == 1 &&
-         d.ww == 1 && d.dw <= 1;
+         d.ww == 1 && d.dw <= 1 && token_rows_fit_32bit(d);
 }
 
 // The sink row: the target of y rows past the sequence end.

@@ -1833,6 +1833,7 @@ bool mfma_fwd_supported(const Dims& d, int qkv_dtype, int y_dtype) {
   (void)y_dtype;
   if (!(qkv_dtype == DN_BF16 && (d.K == 64 || d.K == 128) && d.V % kBV == 0 && d.L == kL))
     return false;
+  if (!token_rows_fit_32bit(d)) return false;
   if (per_channel(d)) return (d.ew == 1 || d.ew == d.K) && (d.ww == 1 || d.ww == d.V);
   return d.ew == 1 && d.ww == 1 && d.dw <= 1;
 }

@@ -70,6 +70,15 @@ struct Dims {
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+// The MFMA kernels address a chunk's token rows from a per-chunk base with
+// 32-bit byte offsets: up to 63 token strides of H·max(K, V) elements, 4
+// bytes each for an fp32 y. Shapes whose offsets would wrap take the
+// generic kernels (or are refused when MFMA is requested).
+inline bool token_rows_fit_32bit(const Dims& d) {
+  const int64_t row = int64_t(d.H) * (d.K > d.V ? d.K : d.V);
+  return int64_t(4) * 64 * row < (int64_t(1) << 31);
+}
+
 // Launch helpers (defined in the per-path translation units).
 hipError_t launch_step(const dn_step_args& a, float scale, hipStream_t stream);
 // dn_recurrent: the whole sequence in one pass over the state (head_k_dim up

@@ -463,8 +463,11 @@ __global__ __launch_bounds__(kFrontThreads) void frontend_rows_kernel(FrontParam
       if constexpr (WIN) {
         // The next window (one token): the padded input [window[1:], x],
         // which is this token's four taps (bf16 values round-trip exactly).
+        // Only real rows write it: a padded row runs on the last real row's
+        // channels, and with window_out aliasing window_in it could read that
+        // row's window after the real row has replaced it.
 #pragma unroll
-        for (int i = 0; i < CPL; ++i) {
+        for (int i = 0; i < CPL && rid < nrow; ++i) {
           TI* wo = static_cast<TI*>(p.wout) + (wrow + i) * 4;
           if constexpr (sizeof(TI) == 2)
             *reinterpret_cast<uint2*>(wo) = make_uint2(pk_bf16(xv[i][0], xv[i][1]),

@@ -2,7 +2,9 @@
 // src/delta/path.rs:198-207, compiled in by its check-nan/check-inf features).
 
 #include <atomic>
+#include <map>
 #include <mutex>
+#include <utility>
 
 #include "dn_common.hpp"
 
@@ -22,24 +24,26 @@ __global__ __launch_bounds__(256) void nonfinite_kernel(const T* p, size_t n, in
 }  // namespace
 
 namespace {
-// One second stream per device (default priority, non-blocking) and its
-// fork / join events, created on first use and kept until the process ends.
+// A second stream (default priority, non-blocking) and its fork / join
+// events per (device, calling stream), created on first use and kept until
+// the process ends. Keying by the calling stream keeps callers on different
+// streams apart: their backward calls neither serialise on one side stream
+// nor pull one another's work into a HIP graph that one of them captures
+// (a side stream joins its calling stream's capture through the fork event).
 struct Side {
   hipStream_t s = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
 };
-constexpr int kMaxSides = 64;
 std::mutex side_mu;
-Side sides[kMaxSides];
+std::map<std::pair<int, hipStream_t>, Side> sides;
 }  // namespace
 
 hipError_t side_fork(hipStream_t main, hipStream_t* side) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
-  if (dev < 0 || dev >= kMaxSides) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(side_mu);
-  Side& sd = sides[dev];
+  Side& sd = sides[{dev, main}];
   if (!sd.s) {
     if ((e = hipStreamCreateWithFlags(&sd.s, hipStreamNonBlocking)) != hipSuccess) return e;
     if ((e = hipEventCreateWithFlags(&sd.fork, hipEventDisableTiming)) != hipSuccess) return e;
@@ -55,10 +59,10 @@ hipError_t side_join(hipStream_t main) {
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
-  if (dev < 0 || dev >= kMaxSides) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lock(side_mu);
-  Side& sd = sides[dev];
-  if (!sd.s) return hipErrorInvalidHandle;
+  const auto it = sides.find({dev, main});
+  if (it == sides.end() || !it->second.s) return hipErrorInvalidHandle;
+  Side& sd = it->second;
   if ((e = hipEventRecord(sd.join, sd.s)) != hipSuccess) return e;
   return hipStreamWaitEvent(main, sd.join, 0);
 }

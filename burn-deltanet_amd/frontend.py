@@ -307,6 +307,9 @@ def block_step_args(proj: QkvProjection, norm: OutNorm, projected_bw: Tensor,
         raise DeltaError(-2, "convolution window presence must match the block's convolution")
     if norm.gated and not proj.has_gate:
         raise DeltaError(-6, "OutNorm::Gated needs the projection's output gate")
+    if proj.has_gate and not norm.gated:
+        # norm.rs OutNorm::forward panics on a gate given to the plain norm
+        raise DeltaError(-2, "OutNorm::Plain takes no output gate")
     H, dk, dv = proj.nheads, proj.head_k_dim, proj.head_v_dim
     # The library sizes every buffer from these dims: a tensor that disagrees
     # would be read out of bounds.

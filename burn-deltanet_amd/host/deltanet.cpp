@@ -13,6 +13,8 @@
 #include <algorithm>
 #include <cmath>
 #include <limits>
+#include <memory>
+#include <vector>
 #include <sstream>
 
 namespace deltanet {
@@ -72,7 +74,32 @@ double nan_scale(const std::optional<double>& s) {
   return s ? *s : std::numeric_limits<double>::quiet_NaN();
 }
 
+// The calling thread's Workspace on the current device (the default of the
+// functions that take a Workspace*).
+Workspace& thread_workspace() {
+  thread_local std::vector<std::unique_ptr<Workspace>> per_device;
+  int dev = 0;
+  check_hip(hipGetDevice(&dev), "hipGetDevice");
+  if (size_t(dev) >= per_device.size()) per_device.resize(size_t(dev) + 1);
+  if (!per_device[size_t(dev)]) per_device[size_t(dev)] = std::make_unique<Workspace>();
+  return *per_device[size_t(dev)];
+}
+
 }  // namespace
+
+Workspace::~Workspace() {
+  if (ptr_) (void)hipFree(ptr_);
+}
+
+void* Workspace::reserve(size_t bytes, hipStream_t stream) {
+  if (bytes <= bytes_) return ptr_;
+  if (ptr_) check_hip(hipFreeAsync(ptr_, stream), "hipFreeAsync");
+  ptr_ = nullptr;
+  bytes_ = 0;
+  check_hip(hipMallocAsync(&ptr_, bytes, stream), "hipMallocAsync");
+  bytes_ = bytes;
+  return ptr_;
+}
 
 Error::Error(int status, const std::string& what) : std::runtime_error(what), status_(status) {}
 
@@ -161,19 +188,20 @@ void DeltaInput::sanity() const {
 }
 
 std::pair<Tensor, Tensor> DeltaInput::run(const DeltaPath& path, hipStream_t stream,
-                                          bool check_finite) const {
+                                          bool check_finite, Workspace* ws) const {
   sanity();
   if (path.kind == DeltaPath::Kind::Recurrent) return delta_recurrent(stream, check_finite);
   const int64_t chunk_len = path.chunk_len.value_or(DeltaPath::DEFAULT_CHUNK_LEN);
   if (chunk_len <= 0) throw Error(DN_ERR_CHUNK_LEN, "chunk_len must be at least 1");
   // Chunk and ChunkRecalculated compute identical values; they differ only in
   // what a tape keeps, and this forward keeps nothing.
-  return delta_chunk_recalculated(chunk_len, stream, check_finite);
+  return delta_chunk_recalculated(chunk_len, stream, check_finite, ws);
 }
 
 std::pair<Tensor, Tensor> DeltaInput::delta_chunk_recalculated(int64_t chunk_len,
                                                                hipStream_t stream,
-                                                               bool check_finite) const {
+                                                               bool check_finite,
+                                                               Workspace* ws) const {
   sanity();
   if (chunk_len <= 0) throw Error(DN_ERR_CHUNK_LEN, "chunk_len must be at least 1");
   if (chunk_len > std::numeric_limits<int32_t>::max())
@@ -207,6 +235,13 @@ std::pair<Tensor, Tensor> DeltaInput::delta_chunk_recalculated(int64_t chunk_len
   a.state_in = static_cast<const float*>(state_bhkv.data());
   a.y = y.data();
   a.state_out = static_cast<float*>(s.data());
+  // The workspace is this mirror's (the caller's, or the thread's own), never
+  // the library's shared pool.
+  const size_t need = dn_chunk_fwd_workspace_bytes(&a);
+  if (need) {
+    a.workspace = (ws ? *ws : thread_workspace()).reserve(need, stream);
+    a.workspace_bytes = need;
+  }
   check(dn_chunk_fwd(&a, stream));
   return {y, s};
 }
@@ -399,7 +434,7 @@ DeltaChunkGrads combined_backward(const Tensor& d_y_bshv,
                                   const Tensor& erase_bshK, const Tensor& write_bshV,
                                   const std::optional<Tensor>& g_bshK, const Tensor& state_bhkv,
                                   int64_t chunk_len, double scale, hipStream_t stream,
-                                  bool check_finite) {
+                                  bool check_finite, Workspace* ws) {
   DeltaInput in{q_bshk, k_bshk, v_bshv, erase_bshK, write_bshV, g_bshK, state_bhkv, scale};
   in.sanity();
   if (chunk_len <= 0) throw Error(DN_ERR_CHUNK_LEN, "chunk_len must be at least 1");
@@ -454,6 +489,11 @@ DeltaChunkGrads combined_backward(const Tensor& d_y_bshv,
   a.d_write = static_cast<float*>(g.d_write_bshV.data());
   a.d_g = g.d_g_bshK ? static_cast<float*>(g.d_g_bshK->data()) : nullptr;
   a.d_state = static_cast<float*>(g.d_state_bhkv.data());
+  const size_t need = dn_chunk_bwd_workspace_bytes(&a);
+  if (need) {
+    a.workspace = (ws ? *ws : thread_workspace()).reserve(need, stream);
+    a.workspace_bytes = need;
+  }
   check(dn_chunk_bwd(&a, stream));
   return g;
 }
@@ -627,6 +667,8 @@ Tensor block_step(const QkvProjection& proj, const OutNorm& norm, const Tensor& 
     throw Error(DN_ERR_SHAPE, "convolution window presence must match the block's convolution");
   if (norm.gated && !proj.has_gate)
     throw Error(DN_ERR_NULL, "OutNorm::Gated needs the projection's output gate");
+  if (proj.has_gate && !norm.gated)
+    throw Error(DN_ERR_SHAPE, "OutNorm::Plain takes no output gate");  // norm.rs OutNorm::forward
   const int64_t B = projected_bw.dim(0), H = proj.nheads, dk = proj.head_k_dim,
                 dv = proj.head_v_dim;
   require_f32(state_bhkv, "state");

@@ -79,6 +79,30 @@ class Tensor {
   DType dtype_ = DType::F32;
 };
 
+// Device scratch for the chunk calls (dn_chunk_fwd / dn_chunk_bwd), owned by
+// the caller of this mirror, so no call falls back on the library's shared
+// pool. reserve() grows it on the stream it is used on: the old buffer is
+// released and the new one taken stream-ordered (hipFreeAsync /
+// hipMallocAsync), so growth neither drains the device nor frees memory a
+// queued call still reads. A Workspace serves one stream at a time; calls
+// on two streams at once need one each. The functions below that take a
+// `Workspace*` use the calling thread's own per-device Workspace when it is
+// null.
+class Workspace {
+ public:
+  Workspace() = default;
+  ~Workspace();
+  Workspace(const Workspace&) = delete;
+  Workspace& operator=(const Workspace&) = delete;
+  // At least `bytes` of device memory for work queued on `stream`.
+  void* reserve(size_t bytes, hipStream_t stream);
+  size_t capacity() const { return bytes_; }
+
+ private:
+  void* ptr_ = nullptr;
+  size_t bytes_ = 0;
+};
+
 // How the WY transform's (I − N)⁻¹ is evaluated (src/delta/tri.rs:53-64).
 // Inside the chunk paths both evaluate the same exact inverse (the
 // reference's Neumann series is a test baseline there); unit_lower_inverse
@@ -146,14 +170,15 @@ struct DeltaInput {
   void sanity() const;
   // path.rs:215-231. Returns (y_bshv, final_state_bhkv).
   std::pair<Tensor, Tensor> run(const DeltaPath& path = DeltaPath{}, hipStream_t stream = nullptr,
-                                bool check_finite = false) const;
+                                bool check_finite = false, Workspace* ws = nullptr) const;
   // recurrent.rs:107-142: delta_step unrolled over the sequence.
   std::pair<Tensor, Tensor> delta_recurrent(hipStream_t stream = nullptr,
                                             bool check_finite = false) const;
   // chunk_recalculated.rs:36-83 → DeltaChunkBackendExt::delta_chunk_recalculated.
   std::pair<Tensor, Tensor> delta_chunk_recalculated(int64_t chunk_len,
                                                      hipStream_t stream = nullptr,
-                                                     bool check_finite = false) const;
+                                                     bool check_finite = false,
+                                                     Workspace* ws = nullptr) const;
 };
 
 // recurrent.rs:41-99. Returns (y_bhv, next_state_bhkv).
@@ -184,7 +209,7 @@ DeltaChunkGrads combined_backward(const Tensor& d_y_bshv,
                                   const Tensor& erase_bshK, const Tensor& write_bshV,
                                   const std::optional<Tensor>& g_bshK, const Tensor& state_bhkv,
                                   int64_t chunk_len, double scale, hipStream_t stream = nullptr,
-                                  bool check_finite = false);
+                                  bool check_finite = false, Workspace* ws = nullptr);
 
 // ---------------------------------------------------------------------------
 // The projection front-end (src/common/qkv.rs, conv.rs, norm.rs) over

@@ -58,7 +58,11 @@ typedef enum {
 } dn_dtype;
 
 /* Which kernels run dn_chunk_fwd / dn_chunk_bwd. AUTO picks the MFMA path
- * (DN_ALGO_MFMA) whenever the shape and dtypes allow it. */
+ * (DN_ALGO_MFMA) whenever the shape, dtypes and pointers allow it: q and k
+ * (and, for the backward, d_y) at 16-byte boundaries, v at a 4-byte one, and
+ * nheads·max(head_k_dim, head_v_dim) below 2^23 (the kernels address a
+ * chunk's token rows with 32-bit byte offsets). Otherwise AUTO runs the
+ * generic kernels and an explicit MFMA request is refused. */
 typedef enum {
   DN_ALGO_AUTO = 0,
   DN_ALGO_GENERIC = 1, /* fp32 arithmetic, any shape */
@@ -113,7 +117,12 @@ typedef struct {
 /* combined_backward (combined_backward.rs:72-189). Same leaves as the forward,
  * plus the two incoming cotangents; writes the seven gradients. d_erase,
  * d_write and d_g are reduced to their gate's own width (forward.rs:106-112);
- * d_g is the gradient with respect to g = log α. */
+ * d_g is the gradient with respect to g = log α.
+ * On the MFMA path the call forks its reverse scan onto a second stream that
+ * the library keeps per (device, calling stream), and joins it back into the
+ * calling stream before its last kernel: everything the call does is ordered
+ * on `stream`. Callers on different streams get different second streams;
+ * under HIP graph capture of `stream` the second stream joins the capture. */
 typedef struct {
   int64_t batch, sequence, nheads, head_k_dim, head_v_dim;
   int64_t erase_width, write_width, decay_width;

@@ -484,6 +484,43 @@ void gpu_cases() {
     expect_close("bf16_state", download(s), s0, 2e-2);
     ok("bf16_mfma_path");
   }
+  // A caller-owned Workspace: the chunk calls take their scratch from it
+  // (never the library's shared pool); a larger call grows it on the stream,
+  // and a later smaller one reuses it. Values as without it.
+  {
+    Workspace ws;
+    Case c1 = make_case(19, 1, 64, 2, 128, 128, 1, 1, 1, 0.05, 0.02);
+    Case c2 = make_case(23, 2, 200, 2, 128, 128, 1, 1, 1, 0.05, 0.02);
+    DeltaInput in1 = to_device(c1, DType::BF16), in2 = to_device(c2, DType::BF16);
+    auto [y1, s1] = in1.run(DeltaPath::chunk(), nullptr, false, &ws);
+    const size_t cap1 = ws.capacity();
+    if (cap1 == 0) fail("workspace: the first call reserved nothing");
+    auto [y2, s2] = in2.run(DeltaPath::chunk(), nullptr, false, &ws);
+    if (ws.capacity() <= cap1) fail("workspace: the larger call did not grow it");
+    auto [y3, s3] = in1.run(DeltaPath::chunk(), nullptr, false, &ws);
+    const auto [y10, s10] = oracle_fwd(c1, 64, 1.0 / std::sqrt(128.0));
+    const auto [y20, s20] = oracle_fwd(c2, 64, 1.0 / std::sqrt(128.0));
+    expect_close("workspace_y1", download(y1), y10, 2e-2);
+    expect_close("workspace_y2", download(y2), y20, 2e-2);
+    expect_close("workspace_s2", download(s2), s20, 2e-2);
+    expect_close("workspace_y1_again", download(y3), download(y1), 0.0);
+    Rng r(5);
+    Vec dy = r.normals(size_t(2 * 200 * 2 * 128));
+    Tensor tdy = upload(dy, {2, 200, 2, 128}, DType::BF16);
+    const size_t before = ws.capacity();
+    DeltaChunkGrads gr = combined_backward(tdy, std::nullopt, in2.q_bshk, in2.k_bshk,
+                                           in2.v_bshv, in2.erase_bshK, in2.write_bshV,
+                                           in2.g_bshK, in2.state_bhkv, 64,
+                                           1.0 / std::sqrt(128.0), nullptr, false, &ws);
+    if (ws.capacity() < before) fail("workspace: shrank");
+    DeltaChunkGrads gd = combined_backward(tdy, std::nullopt, in2.q_bshk, in2.k_bshk,
+                                           in2.v_bshv, in2.erase_bshK, in2.write_bshV,
+                                           in2.g_bshK, in2.state_bhkv, 64,
+                                           1.0 / std::sqrt(128.0));
+    expect_close("workspace_bwd_dq", download(gr.d_q_bshk), download(gd.d_q_bshk), 0.0);
+    expect_close("workspace_bwd_dg", download(*gr.d_g_bshK), download(*gd.d_g_bshK), 0.0);
+    ok("caller_workspace");
+  }
   // The projection front-end. With the newest conv tap 1 and the others 0,
   // identity activations and no norm, q and k are the raw columns, v their
   // SiLU (qkv.rs:413-421), erase 2σ and write σ of theirs (qkv.rs:356-366),

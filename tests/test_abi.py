@@ -175,6 +175,54 @@ def test_mfma_paths_need_word_aligned_qkv():
         assert lib.dn_chunk_fwd_algo(ctypes.byref(a)) == want, over
 
 
+def test_mfma_paths_refuse_rows_past_32_bit_offsets():
+    """The MFMA kernels address a chunk's 64 token rows with 32-bit byte
+    offsets (4-byte y included): nheads·max(dk, dv) must stay below 2^23.
+    Above it AUTO runs the generic kernels and an MFMA request is refused,
+    rather than the offsets wrapping (no pointer is read)."""
+    lib = abi.lib()
+    base = dict(batch=1, sequence=64, head_k_dim=128, qkv_dtype=abi.DN_BF16,
+                y_dtype=abi.DN_F32)
+    for nheads, dv, auto in ((1 << 14, 256, abi.DN_ALGO_MFMA),
+                             ((1 << 15) - 1, 256, abi.DN_ALGO_MFMA),
+                             (1 << 15, 256, abi.DN_ALGO_GENERIC),
+                             (1, 1 << 23, abi.DN_ALGO_GENERIC)):
+        over = dict(nheads=nheads, head_v_dim=dv)
+        for algo, want in ((abi.DN_ALGO_AUTO, auto),
+                           (abi.DN_ALGO_MFMA, auto if auto == abi.DN_ALGO_MFMA else -9),
+                           (abi.DN_ALGO_MFMA_FUSED,
+                            abi.DN_ALGO_MFMA_FUSED if auto == abi.DN_ALGO_MFMA else -9)):
+            a = fwd_args(**base, **over, algo=algo)
+            assert lib.dn_chunk_fwd_algo(ctypes.byref(a)) == want, (over, algo)
+
+
+def bwd_args(**over):
+    a = abi.ChunkBwdArgs()
+    a.batch, a.sequence, a.nheads, a.head_k_dim, a.head_v_dim = 8, 4096, 16, 128, 256
+    a.erase_width = a.write_width = a.decay_width = 1
+    a.has_gate, a.chunk_len, a.scale = 1, 64, float("nan")
+    a.qkv_dtype = a.grad_dtype = abi.DN_BF16
+    for f in ["d_y", "q", "k", "v", "erase", "write", "g", "state_in", "d_q", "d_k", "d_v",
+              "d_erase", "d_write", "d_g", "d_state"]:
+        setattr(a, f, 0x1000)
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_mfma_backward_needs_a_16_byte_aligned_d_y():
+    """The backward's MFMA kernels read d_y in 16-byte words: an offset d_y
+    view runs the generic kernels under AUTO, and an MFMA request is refused
+    (no pointer is read)."""
+    lib = abi.lib()
+    for over, auto in ((dict(), abi.DN_ALGO_MFMA), (dict(d_y=0x1008), abi.DN_ALGO_GENERIC),
+                       (dict(d_y=0x1002), abi.DN_ALGO_GENERIC), (dict(q=0x1008), abi.DN_ALGO_GENERIC)):
+        assert lib.dn_chunk_bwd_algo(ctypes.byref(bwd_args(**over))) == auto, over
+        a = bwd_args(**over, algo=abi.DN_ALGO_MFMA)
+        want = abi.DN_ALGO_MFMA if auto == abi.DN_ALGO_MFMA else -9
+        assert lib.dn_chunk_bwd_algo(ctypes.byref(a)) == want, over
+
+
 @fake_pointers
 def test_bwd_rejects_missing_d_g():
     lib = abi.lib()

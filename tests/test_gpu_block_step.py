@@ -5,7 +5,10 @@ delta_step (dn_step, recurrent.rs:41-99) and the output norm (dn_out_norm,
 norm.rs:127-134), each pinned against the oracle by its own tests. The fused
 path keeps q, k, v and y in fp32 between the stages, so the bar is the
 composition with fp32 intermediates at 1e-5 normwise; the next conv window
-must match bit for bit (it is the projection's values, moved). A chain of
+must match bit for bit (it is the projection's values, moved). The fused
+step also meets the oracle's own composition (oracle/frontend.py's
+front-end, the C++ oracle's delta_step, oracle/frontend.py's out_norm) in
+float64 at 1e-4. A chain of
 decode tokens must match the block's forward over the sequence (the forward
 ≡ step contract of gated_deltanet_1/tests.rs:61-155) at 1e-4 absolute."""
 
@@ -14,6 +17,8 @@ import pytest
 import torch
 
 from gpu_util import DEV, announce, pkg
+from oracle import frontend as F
+from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
 
@@ -98,6 +103,55 @@ def test_block_step_equals_the_three_calls(rng, case):
     assert max(e) < 1e-5
     if win is not None:
         assert torch.equal(win2, want_win.to(win2.dtype))
+
+
+def oracle_block_step(proj, norm, p, win, g, s, scale):
+    """The same token through the oracle's composition, in float64: the
+    front-end's forward over a one-token sequence (oracle/frontend.py,
+    QkvProjection::step ≡ forward on one token, qkv.rs:454-516), delta_step
+    (oracle.cpp, recurrent.rs:41-99), then OutNorm::forward (norm.rs:106-144)
+    with the output gate read from the projection row after the write
+    gates (qkv.rs:237-262)."""
+    npf = lambda t: None if t is None else t.double().cpu().numpy()
+    H, dk, dv = proj.nheads, proj.head_k_dim, proj.head_v_dim
+    pn = npf(p)
+    conv = None
+    if proj.conv is not None:
+        conv = dict(weight=npf(proj.conv.weight), bias=npf(proj.conv.bias), window=npf(win),
+                    activation=int(proj.conv.activation))
+    fr = F.frontend(pn[:, None], nheads=H, head_k_dim=dk, head_v_dim=dv, conv=conv,
+                    qk_activation=int(proj.qk_activation), qk_norm_kind=int(proj.qk_norm),
+                    write_gate=int(proj.write_gate), allow_neg_eigval=proj.allow_neg_eigval)
+    y, s2 = O.delta_step(fr["q"][:, 0], fr["k"][:, 0], fr["v"][:, 0], fr["erase"][:, 0],
+                         fr["write"][:, 0], npf(g), npf(s), scale=scale)
+    gate = None
+    if norm.gated:
+        g0 = F.conv_dim(H, dk, dv, 1) + F.gate_width(H, dk, dv, 1, int(proj.write_gate))
+        gate = pn[:, g0:g0 + H * dv].reshape(-1, H, dv)
+    out = F.out_norm(y, gate, npf(norm.weight), norm.eps)
+    return out, fr["window"], s2, y
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_block_step_matches_the_oracle_composition(rng, case):
+    """dn_block_step straight against the oracle's front-end step, delta_step
+    and output norm (float64), at 1e-4 normwise: its stages keep fp32
+    intermediates, so the difference is fp32 rounding."""
+    name, B, H, dk, dv, opts, in_dtype, dw = case
+    announce(f"block step vs oracle composition: {name}")
+    proj, norm, p, win, g, s = case_inputs(rng, B, H, dk, dv, opts, in_dtype, dw)
+    scale = 1.0 / np.sqrt(dk)
+    out, win2, s2, y = pkg.block_step(proj, norm, p, win, g, s, scale, out_dtype=torch.float32,
+                                      return_y=True)
+    torch.cuda.synchronize()
+    w_out, w_win, w_s, w_y = oracle_block_step(proj, norm, p, win, g, s, scale)
+    npd = lambda t: t.double().cpu().numpy()
+    re = lambda a, b: float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+    e = (re(npd(out), w_out), re(npd(s2), w_s), re(npd(y), w_y))
+    print(f"  out {e[0]:.2e} state {e[1]:.2e} y {e[2]:.2e}", flush=True)
+    assert max(e) < 1e-4
+    if win is not None:
+        assert np.array_equal(npd(win2), w_win)
 
 
 def test_block_step_bf16_out_and_in_place(rng):

@@ -127,7 +127,11 @@ def test_frontend_matches_oracle(rng, case):
 def test_frontend_window_in_place(rng, ci):
     """window_out aliasing window_in (the decode cache updated in place): a
     sequence, a one-token step (whose kernel writes the next window itself)
-    and a 3-token call."""
+    and a 3-token call. Case 11 (B = 3, one token) is the regression case
+    for the row kernel's padded rows: its workgroup holds 16 (batch, token)
+    rows over four waves, 13 of them padded onto the last real row, and only
+    real rows may write the window (a padded row in another wave could read
+    the window after the real row replaced it and write it shifted twice)."""
     case = CASES[ci]
     announce(f"dn_frontend in-place window, case {ci}")
     p, conv = make_case(rng, case)

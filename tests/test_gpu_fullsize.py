@@ -14,7 +14,8 @@ kernels at small sizes in the other GPU tests):
   f(S1 + S2) = f(S1) + f(S2) − f(0), for the next state and for y.
 - config 4 (DeltaProduct u = 2 fold) and config 5 (GDN-2 per-channel gates):
   the MFMA forward, and for config 5 the MFMA backward, agree with the
-  generic fp32 kernels, which share no code with them; the MFMA forward
+  generic fp32 kernels, which share no code with them (so does the backward
+  at the config-2 shape, head_v_dim 256 in two value passes); the MFMA forward
   also agrees with `dn_recurrent`, the token-by-token recurrence.
 - the projection front-end at the config-2 shape: a sequence split in two,
   with the conv window carried across (conv.rs:14-20), gives the same bits
@@ -217,6 +218,33 @@ def test_config5_mfma_forward_and_backward_agree_with_generic():
     got = {}
     for algo in (MFMA, GENERIC):
         r = pkg.combined_backward(dy, ds, q, k, v, e, w, g, s0, 64, scale, algo=algo)
+        torch.cuda.synchronize()
+        got[algo] = [x.clone() for x in (r.d_q_bshk, r.d_k_bshk, r.d_v_bshv, r.d_erase_bshK,
+                                        r.d_write_bshV, r.d_g_bshK, r.d_state_bhkv)]
+        del r
+    for name, m, gn in zip(["dq", "dk", "dv", "d_erase", "d_write", "dg", "d_state"],
+                           got[MFMA], got[GENERIC]):
+        err = rel_err(m, gn)
+        print(f"  backward {name} rel err {err:.2e}", flush=True)
+        assert err < TOL_BF16, name
+
+
+def test_config2_shape_mfma_backward_agrees_with_generic():
+    """The backward at the config-2 shape (per-head gates, head_v_dim 256: the
+    chunk-local kernel runs two value passes, the first handing its partial
+    dattn and dT to the second) against the generic fp32 kernels, all seven
+    gradients, with a nonzero initial state and final-state cotangent."""
+    announce("config 2 shape: backward, MFMA (two value passes) vs generic")
+    B, T, H, K, V = 8, 4096, 16, 128, 256
+    gr = gen(10)
+    q, k, v, beta, g = gdn_inputs(gr, B, T, H, K, V, torch.bfloat16)
+    s0 = torch.randn((B, H, K, V), generator=gr, device=DEV) * 0.02
+    dy = torch.randn((B, T, H, V), generator=gr, device=DEV).to(torch.bfloat16)
+    ds = torch.randn((B, H, K, V), generator=gr, device=DEV) * 0.5
+    scale = 1.0 / np.sqrt(K)
+    got = {}
+    for algo in (MFMA, GENERIC):
+        r = pkg.combined_backward(dy, ds, q, k, v, beta, beta, g, s0, 64, scale, algo=algo)
         torch.cuda.synchronize()
         got[algo] = [x.clone() for x in (r.d_q_bshk, r.d_k_bshk, r.d_v_bshv, r.d_erase_bshK,
                                         r.d_write_bshV, r.d_g_bshK, r.d_state_bhkv)]

@@ -145,3 +145,16 @@ def test_frontend_checks_the_window_shape():
     with pytest.raises(DeltaError) as ex:
         proj.forward_projected(p, torch.zeros(2, proj.conv_dim(), 2))
     assert code_of(ex) == -2 and "conv window" in str(ex.value)
+
+
+def test_block_step_refuses_a_gate_for_the_plain_norm():
+    """A projection with an output gate and OutNorm::Plain: the reference's
+    OutNorm::forward panics on the gate (norm.rs), and so does the mirror,
+    before any library call."""
+    proj, _ = _block()
+    B = 2
+    with pytest.raises(DeltaError) as ex:
+        pkg.block_step(proj, pkg.OutNorm(torch.ones(6), gated=False),
+                       torch.zeros(B, proj.d_in_proj()), torch.zeros(B, proj.conv_dim(), 3),
+                       torch.zeros(B, 2, 1), torch.zeros(B, 2, 4, 6))
+    assert code_of(ex) == -2 and "OutNorm::Plain takes no output gate" in str(ex.value)
