@@ -521,10 +521,11 @@ def bench_config2_bwd(torch, pkg, steps, warmup):
             "kernels": kern}
 
 
-def bench_generic_fallback(torch, pkg, steps, warmup):
-    """The fp32 kernels every shape the MFMA path does not cover falls back
-    to, at the config-2 workload: forced (DN_ALGO_GENERIC), and as AUTO picks
-    them for chunk_len 32."""
+def bench_chunk_lengths(torch, pkg, steps, warmup):
+    """Config 2 at other chunk lengths as AUTO serves them (the MFMA kernels'
+    64-token chunks: with a per-head forget gate the chunk length orders the
+    roundings only), and the fp32 kernels that shapes outside the MFMA path
+    fall back to, forced (DN_ALGO_GENERIC) at chunk 64."""
     B, T, H, K, V = 8, 4096, 16, 128, 256
     dev = torch.device("cuda:0")
     q, k, v, beta, g = gdn_inputs(torch, B, T, H, K, V, 0.05, 20260837, torch.bfloat16, dev)
@@ -532,9 +533,10 @@ def bench_generic_fallback(torch, pkg, steps, warmup):
     y = torch.empty((B, T, H, V), dtype=torch.bfloat16, device=dev)
     s1 = torch.empty_like(s0)
     abi = pkg.abi
-    out = {"workload": "config 2 (B=8 T=4096 H=16 dk=128 dv=256, bf16 q/k/v) on the generic "
-                       "fp32 kernels"}
-    for name, L, algo in (("forced_chunk64", 64, 1), ("auto_chunk32", 32, 0)):
+    out = {"workload": "config 2 (B=8 T=4096 H=16 dk=128 dv=256, bf16 q/k/v) at chunk_len 32 "
+                       "and 128 under AUTO, and on the generic fp32 kernels at 64"}
+    for name, L, algo in (("auto_chunk32", 32, 0), ("auto_chunk128", 128, 0),
+                          ("forced_generic_chunk64", 64, 1)):
         a = abi.chunk_fwd_args(q, k, v, beta, beta, g, s0, y, s1, L, None, algo=algo)
         ws = torch.empty(max(abi.lib().dn_chunk_fwd_workspace_bytes(a), 1), dtype=torch.uint8,
                          device=dev)
@@ -833,9 +835,9 @@ def main():
         extra["block_forward"] = bench_block_forward(torch, pkg, args.extra_steps, MIN_WARMUP)
         print(f"[bench] block_forward {extra['block_forward']}", file=sys.stderr, flush=True)
         torch.cuda.empty_cache()
-        print("[bench] generic fallback", file=sys.stderr, flush=True)
-        extra["generic_fallback"] = bench_generic_fallback(torch, pkg, MIN_STEPS, MIN_WARMUP)
-        print(f"[bench] generic_fallback {extra['generic_fallback']}", file=sys.stderr,
+        print("[bench] chunk lengths", file=sys.stderr, flush=True)
+        extra["chunk_lengths"] = bench_chunk_lengths(torch, pkg, MIN_STEPS, MIN_WARMUP)
+        print(f"[bench] chunk_lengths {extra['chunk_lengths']}", file=sys.stderr,
               flush=True)
         torch.cuda.empty_cache()
         print("[bench] projection front-end (dn_frontend)", file=sys.stderr, flush=True)

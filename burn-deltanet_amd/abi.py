@@ -49,6 +49,7 @@ EXPORTS = [
     "dn_chunk_bwd_workspace_bytes", "dn_chunk_fwd_algo", "dn_chunk_bwd_algo",
     "dn_last_error", "dn_version", "dn_profile_enable", "dn_profile_read",
     "dn_chunk_fwd_noalloc", "dn_unit_lower_inverse", "dn_block_step",
+    "dn_chunk_fwd_out_norm", "dn_chunk_fwd_out_norm_workspace_bytes", "dn_wait_give_ups",
 ]
 NOALLOC_SCRATCH_BYTES = 64 << 20  # DN_NOALLOC_SCRATCH_BYTES (deltanet_core.h)
 
@@ -124,6 +125,13 @@ class OutNormArgs(ctypes.Structure):
     ]
 
 
+class ChunkFwdOutNormArgs(ctypes.Structure):
+    _fields_ = [
+        ("fwd", ChunkFwdArgs), ("gate", _vp), ("gate_stride", _i64), ("gate_dtype", _i32),
+        ("weight", _vp), ("eps", _f64),
+    ]
+
+
 class BlockStepArgs(ctypes.Structure):
     _fields_ = [
         ("batch", _i64), ("nheads", _i64), ("head_k_dim", _i64), ("head_v_dim", _i64),
@@ -171,6 +179,12 @@ def lib() -> ctypes.CDLL:
         L.dn_frontend.restype = ctypes.c_int
         L.dn_out_norm.argtypes = [ctypes.POINTER(OutNormArgs), _vp]
         L.dn_out_norm.restype = ctypes.c_int
+        L.dn_chunk_fwd_out_norm.argtypes = [ctypes.POINTER(ChunkFwdOutNormArgs), _vp]
+        L.dn_chunk_fwd_out_norm.restype = ctypes.c_int
+        L.dn_chunk_fwd_out_norm_workspace_bytes.argtypes = [ctypes.POINTER(ChunkFwdOutNormArgs)]
+        L.dn_chunk_fwd_out_norm_workspace_bytes.restype = _sz
+        L.dn_wait_give_ups.argtypes = []
+        L.dn_wait_give_ups.restype = ctypes.c_int64
         L.dn_block_step.argtypes = [ctypes.POINTER(BlockStepArgs), _vp]
         L.dn_block_step.restype = ctypes.c_int
         L.dn_unit_lower_inverse.argtypes = [ctypes.POINTER(TriArgs), _vp]
@@ -375,6 +389,37 @@ def out_norm_args(x, gate, weight, out, eps):
 
 def run_out_norm(args: OutNormArgs) -> None:
     check(lib().dn_out_norm(ctypes.byref(args), stream_handle()))
+
+
+def chunk_fwd_out_norm_args(fwd: ChunkFwdArgs, gate, weight, eps) -> ChunkFwdOutNormArgs:
+    """dn_chunk_fwd_out_norm's arguments: `fwd` (whose y receives the norm's
+    output) with the output norm's gate ([batch, sequence, nheads, head_v_dim]
+    or a column view of the projection with evenly strided tokens; None for
+    the plain norm), weight γ [head_v_dim] and eps."""
+    a = ChunkFwdOutNormArgs()
+    a.fwd = fwd
+    H, D = fwd.nheads, fwd.head_v_dim
+    if gate is not None:
+        want = (fwd.batch, fwd.sequence, H, D)
+        if tuple(gate.shape) != want:
+            raise DeltaError(-2, f"gate: expected shape {list(want)}, got {list(gate.shape)}")
+        if gate.stride(3) != 1 or gate.stride(2) != D or (
+                fwd.sequence > 1 and fwd.batch > 1 and gate.stride(0) != gate.stride(1) * fwd.sequence):
+            raise DeltaError(-2, "gate: heads contiguous within a token, tokens evenly strided")
+        a.gate_stride = gate.stride(1) if fwd.sequence > 1 else gate.stride(0)
+        a.gate_dtype = dtype_tag(gate.dtype)
+    a.gate, a.weight, a.eps = _ptr(gate), _ptr(weight), float(eps)
+    return a
+
+
+def run_chunk_fwd_out_norm(args: ChunkFwdOutNormArgs) -> None:
+    check(lib().dn_chunk_fwd_out_norm(ctypes.byref(args), stream_handle()))
+
+
+def wait_give_ups() -> int:
+    """dn_wait_give_ups: bounded cross-workgroup waits that gave up on this
+    device so far (synchronises)."""
+    return int(lib().dn_wait_give_ups())
 
 
 def tri_args(n_strict, t, solve=DN_TRI_BLOCKED, check_finite=False) -> TriArgs:

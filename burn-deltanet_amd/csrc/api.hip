@@ -185,6 +185,30 @@ hipError_t guard_flag(int** out) {
   return hipSuccess;
 }
 
+// The give-up counter of the bounded cross-workgroup waits (the fused output
+// norm's exchange), one device int per device, zeroed when allocated.
+hipError_t give_up_counter(int** out) {
+  static std::mutex mu;
+  static std::vector<int*> counters;
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  std::lock_guard<std::mutex> lock(mu);
+  if (size_t(dev) >= counters.size()) counters.resize(size_t(dev) + 1, nullptr);
+  if (!counters[size_t(dev)]) {
+    void* p = nullptr;
+    if ((e = hipMalloc(&p, sizeof(int))) != hipSuccess) return e;
+    if ((e = hipMemset(p, 0, sizeof(int))) != hipSuccess) return e;
+    counters[size_t(dev)] = static_cast<int*>(p);
+  }
+  *out = counters[size_t(dev)];
+  return hipSuccess;
+}
+
+// Polls before an exchange wait gives up: about 0.2 s of 128-cycle sleeps,
+// far beyond the microseconds a resident partner takes.
+constexpr int kNormSpin = 1 << 22;
+
 int nonfinite_check(const std::vector<Guarded>& list, hipStream_t stream, const char* when) {
   int* flag = nullptr;
   hipError_t e = guard_flag(&flag);
@@ -246,6 +270,25 @@ int check_bwd(const dn_chunk_bwd_args* a) {
 
 bool mfma_requested(int algo) { return algo == DN_ALGO_MFMA || algo == DN_ALGO_MFMA_FUSED; }
 
+// The MFMA kernels walk 64-token chunks. Without a per-key-channel forget
+// gate the chunk length orders the roundings and nothing else: the chunk
+// form and the token recurrence are one function (path.rs:15-19, 46-49), so
+// a request for another chunk length runs those kernels at 64. With a
+// per-channel forget gate the reference's block decay clamps exponents
+// inside a chunk (decay.rs:39-60), which makes its values in that regime
+// depend on where chunks start: such requests keep their own chunk length
+// (and, at lengths other than 64, the generic kernels).
+constexpr int kMfmaChunk = 64;
+Dims mfma_dims(const Dims& d) {
+  if (d.L == kMfmaChunk || (d.dw == d.K && d.K > 1)) return d;
+  Dims m = d;
+  m.L = kMfmaChunk;
+  m.N = (d.S + kMfmaChunk - 1) / kMfmaChunk;
+  return m;
+}
+// The dims a call runs with: its own for the generic kernels.
+Dims run_dims(const Dims& d, int algo) { return algo == DN_ALGO_GENERIC ? d : mfma_dims(d); }
+
 // The MFMA kernels read q and k in 16-byte words and v in 4-byte words; a
 // tensor view that starts off those boundaries takes the generic kernels.
 bool mfma_aligned(const void* q, const void* k, const void* v) {
@@ -256,8 +299,9 @@ bool mfma_aligned(const void* q, const void* k, const void* v) {
 // The forward's kernels: DN_ALGO_GENERIC, DN_ALGO_MFMA (intra + scan) or,
 // on request only, DN_ALGO_MFMA_FUSED (one kernel; at BASELINE config 2 on
 // a warm MI355X 0.47-0.49 ms against the two kernels' 0.43-0.45 ms).
-int fwd_algo(const dn_chunk_fwd_args* a, const Dims& d) {
+int fwd_algo(const dn_chunk_fwd_args* a, const Dims& d0) {
   if (a->algo == DN_ALGO_GENERIC) return DN_ALGO_GENERIC;
+  const Dims d = mfma_dims(d0);
   const bool fits =
       mfma_fwd_supported(d, a->qkv_dtype, a->y_dtype) && mfma_aligned(a->q, a->k, a->v);
   if (a->algo == DN_ALGO_MFMA_FUSED)
@@ -282,8 +326,9 @@ Dims bwd_dims(const dn_chunk_bwd_args* a) {
 // shapes, bf16 q/k/v), and for head_v_dim 64 or 128 the chunk-local
 // gradients too; otherwise those stay on the generic fp32 kernel.
 // The backward's MFMA kernels also read d_y in 16-byte words.
-int bwd_algo(const dn_chunk_bwd_args* a, const Dims& d) {
+int bwd_algo(const dn_chunk_bwd_args* a, const Dims& d0) {
   if (a->algo == DN_ALGO_GENERIC) return DN_ALGO_GENERIC;
+  const Dims d = mfma_dims(d0);
   const bool fits = mfma_fwd_supported(d, a->qkv_dtype, DN_BF16) &&
                     mfma_aligned(a->q, a->k, a->v) &&
                     reinterpret_cast<uintptr_t>(a->d_y) % 16 == 0;
@@ -332,7 +377,7 @@ size_t dn_chunk_fwd_workspace_bytes(const dn_chunk_fwd_args* a) {
                      a->erase_width, a->write_width, a->decay_width, a->has_gate, a->chunk_len,
                      a->scale);
   const int algo = fwd_algo(a, d);
-  return algo < 0 ? 0 : fwd_workspace(d, algo);
+  return algo < 0 ? 0 : fwd_workspace(run_dims(d, algo), algo);
 }
 
 int dn_chunk_fwd(const dn_chunk_fwd_args* a, hipStream_t stream) {
@@ -344,6 +389,7 @@ int dn_chunk_fwd(const dn_chunk_fwd_args* a, hipStream_t stream) {
   const int algo = fwd_algo(a, d);
   if (algo < 0)
     return fail(DN_ERR_UNSUPPORTED, "the requested MFMA path does not cover this shape/dtype");
+  d = run_dims(d, algo);
   const size_t need = fwd_workspace(d, algo);
   void* ws = a->workspace;
   if (ws) {
@@ -394,6 +440,7 @@ int dn_chunk_fwd_noalloc(const dn_chunk_fwd_args* a, hipStream_t stream) {
   const int algo = fwd_algo(a, d);
   if (algo < 0)
     return fail(DN_ERR_UNSUPPORTED, "the requested MFMA path does not cover this shape/dtype");
+  d = run_dims(d, algo);
   const size_t need = fwd_workspace(d, algo);
   if (need > size_t(DN_NOALLOC_SCRATCH_BYTES))
     return fail(DN_ERR_WORKSPACE,
@@ -417,6 +464,134 @@ int dn_chunk_fwd_noalloc(const dn_chunk_fwd_args* a, hipStream_t stream) {
   return DN_OK;
 }
 
+namespace {
+
+int check_fwd_norm(const dn_chunk_fwd_out_norm_args* a) {
+  if (!a) return fail(DN_ERR_NULL, "args is NULL");
+  if (int rc = check_fwd(&a->fwd)) return rc;
+  if (!a->weight) return fail(DN_ERR_NULL, "norm weight is NULL");
+  if (!(a->eps >= 0.0) || !std::isfinite(a->eps))
+    return fail(DN_ERR_SHAPE, "eps must be finite and non-negative");
+  if (a->fwd.head_v_dim > DN_OUT_NORM_MAX_HEAD_DIM)
+    return fail(DN_ERR_UNSUPPORTED,
+                "the output norm supports head_v_dim up to " +
+                    std::to_string(DN_OUT_NORM_MAX_HEAD_DIM));
+  if (a->gate) {
+    if (!valid_dtype(a->gate_dtype)) return fail(DN_ERR_DTYPE, "dtype must be DN_F32 or DN_BF16");
+    if (a->gate_stride < a->fwd.nheads * a->fwd.head_v_dim)
+      return fail(DN_ERR_SHAPE, "gate_stride must cover nheads * head_v_dim");
+  }
+  return DN_OK;
+}
+
+// The fused norm reads the gate and γ in 8- or 16-byte words per 4 columns.
+bool norm_fusable(const dn_chunk_fwd_out_norm_args* a) {
+  const size_t gbytes = a->gate_dtype == DN_BF16 ? 2 : 4;
+  const bool gate_ok = !a->gate || (reinterpret_cast<uintptr_t>(a->gate) % (4 * gbytes) == 0 &&
+                                    (size_t(a->gate_stride) * gbytes) % (4 * gbytes) == 0);
+  return gate_ok && reinterpret_cast<uintptr_t>(a->weight) % 16 == 0 &&
+         reinterpret_cast<uintptr_t>(a->fwd.y) % (a->fwd.y_dtype == DN_BF16 ? 8 : 16) == 0;
+}
+
+}  // namespace
+
+size_t dn_chunk_fwd_out_norm_workspace_bytes(const dn_chunk_fwd_out_norm_args* a) {
+  if (check_fwd_norm(a)) return 0;
+  const dn_chunk_fwd_args* f = &a->fwd;
+  Dims d = make_dims(f->batch, f->sequence, f->nheads, f->head_k_dim, f->head_v_dim,
+                     f->erase_width, f->write_width, f->decay_width, f->has_gate, f->chunk_len,
+                     f->scale);
+  const int algo = fwd_algo(f, d);
+  if (algo < 0) return 0;
+  d = run_dims(d, algo);
+  return algo == DN_ALGO_MFMA ? mfma_fwd_norm_workspace(d) : fwd_workspace(d, algo);
+}
+
+int dn_chunk_fwd_out_norm(const dn_chunk_fwd_out_norm_args* a, hipStream_t stream) {
+  g_last_error.clear();
+  if (int rc = check_fwd_norm(a)) return rc;
+  const dn_chunk_fwd_args* f = &a->fwd;
+  Dims d = make_dims(f->batch, f->sequence, f->nheads, f->head_k_dim, f->head_v_dim,
+                     f->erase_width, f->write_width, f->decay_width, f->has_gate, f->chunk_len,
+                     f->scale);
+  const int algo = fwd_algo(f, d);
+  if (algo < 0)
+    return fail(DN_ERR_UNSUPPORTED, "the requested MFMA path does not cover this shape/dtype");
+  d = run_dims(d, algo);
+  const size_t need = algo == DN_ALGO_MFMA ? mfma_fwd_norm_workspace(d) : fwd_workspace(d, algo);
+  void* ws = f->workspace;
+  if (ws) {
+    if (f->workspace_bytes < need)
+      return fail(DN_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) +
+                                        " bytes");
+  } else if (need) {
+    hipError_t e = pool_get(need, &ws, stream);
+    if (e != hipSuccess) return hip_fail(e, "workspace allocation");
+  }
+  const size_t nq = size_t(d.B) * d.S * d.H, ns = size_t(d.B) * d.H * d.K * d.V;
+  if (f->check_finite) {
+    std::vector<Guarded> in = {{f->q, nq * d.K, f->qkv_dtype},
+                               {f->k, nq * d.K, f->qkv_dtype},
+                               {f->v, nq * d.V, f->qkv_dtype},
+                               {f->erase, nq * d.ew, DN_F32},
+                               {f->write, nq * d.ww, DN_F32},
+                               {f->has_gate ? f->g : nullptr, nq * d.dw, DN_F32},
+                               {f->state_in, ns, DN_F32},
+                               {a->weight, size_t(d.V), DN_F32}};
+    if (int rc = nonfinite_check(in, stream, "inputs")) return rc;
+  }
+  const float* g = f->has_gate ? f->g : nullptr;
+  hipError_t e = hipErrorCooperativeLaunchTooLarge;
+  if (algo == DN_ALGO_MFMA && norm_fusable(a)) {
+    int* fault = nullptr;
+    if ((e = give_up_counter(&fault)) != hipSuccess) return hip_fail(e, "wait counter");
+    FwdNorm nm{a->gate, (long long)a->gate_stride, a->gate_dtype == DN_BF16 ? 1 : 0, a->weight,
+               float(a->eps), fault, kNormSpin};
+    e = mfma_fwd_norm(d, f->y_dtype, f->q, f->k, f->v, f->erase, f->write, g, f->state_in, f->y,
+                      f->state_out, ws, nm, stream);
+  }
+  if (e == hipErrorCooperativeLaunchTooLarge) {
+    // The forward, then the norm in place on y.
+    if (algo != DN_ALGO_GENERIC)
+      e = mfma_fwd(d, f->y_dtype, f->q, f->k, f->v, f->erase, f->write, g, f->state_in, f->y,
+                   f->state_out, ws, stream, algo == DN_ALGO_MFMA_FUSED);
+    else
+      e = generic_fwd(d, f->qkv_dtype, f->y_dtype, f->q, f->k, f->v, f->erase, f->write, g,
+                      f->state_in, f->y, f->state_out, ws, stream);
+    if (e == hipSuccess) {
+      dn_out_norm_args n{};
+      n.tokens = int64_t(d.B) * d.S;
+      n.nheads = d.H;
+      n.head_v_dim = d.V;
+      n.gate_stride = a->gate_stride;
+      n.eps = a->eps;
+      n.x_dtype = n.out_dtype = f->y_dtype;
+      n.gate_dtype = a->gate_dtype;
+      n.x = f->y;
+      n.gate = a->gate;
+      n.weight = a->weight;
+      n.out = f->y;
+      e = launch_out_norm(n, stream);
+    }
+  }
+  if (e != hipSuccess) return hip_fail(e, "dn_chunk_fwd_out_norm launch");
+  if (f->check_finite) {
+    std::vector<Guarded> out = {{f->y, nq * d.V, f->y_dtype}, {f->state_out, ns, DN_F32}};
+    if (int rc = nonfinite_check(out, stream, "outputs")) return rc;
+  }
+  return DN_OK;
+}
+
+int64_t dn_wait_give_ups(void) {
+  g_last_error.clear();
+  int* c = nullptr;
+  if (give_up_counter(&c) != hipSuccess) return -1;
+  if (hipDeviceSynchronize() != hipSuccess) return -1;
+  int host = 0;
+  if (hipMemcpy(&host, c, sizeof(int), hipMemcpyDeviceToHost) != hipSuccess) return -1;
+  return host;
+}
+
 int dn_chunk_bwd_algo(const dn_chunk_bwd_args* a) {
   if (int rc = check_bwd(a)) return rc;
   return bwd_algo(a, bwd_dims(a));
@@ -426,17 +601,18 @@ size_t dn_chunk_bwd_workspace_bytes(const dn_chunk_bwd_args* a) {
   if (check_bwd(a)) return 0;
   const Dims d = bwd_dims(a);
   const int algo = bwd_algo(a, d);
-  return algo < 0 ? 0 : bwd_workspace(d, algo, a->qkv_dtype);
+  return algo < 0 ? 0 : bwd_workspace(run_dims(d, algo), algo, a->qkv_dtype);
 }
 
 int dn_chunk_bwd(const dn_chunk_bwd_args* a, hipStream_t stream) {
   g_last_error.clear();
   if (int rc = check_bwd(a)) return rc;
-  const Dims d = bwd_dims(a);
-  const int algo = bwd_algo(a, d);
+  const int algo = bwd_algo(a, bwd_dims(a));
   if (algo < 0)
     return fail(DN_ERR_UNSUPPORTED, "DN_ALGO_MFMA needs bf16 q/k/v, head_k_dim 64 or 128, "
-                                    "head_v_dim a multiple of 64 and chunk_len 64");
+                                    "head_v_dim a multiple of 64, and chunk_len 64 with a "
+                                    "per-channel forget gate");
+  const Dims d = run_dims(bwd_dims(a), algo);
   const size_t need = bwd_workspace(d, algo, a->qkv_dtype);
   void* ws = a->workspace;
   if (ws) {

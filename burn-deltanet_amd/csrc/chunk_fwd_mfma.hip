@@ -36,6 +36,7 @@
 #include <algorithm>
 
 #include "dn_common.hpp"
+#include "activations.hpp"
 #include "mfma_util.hpp"
 #include "wy_inverse.hpp"
 
@@ -80,6 +81,24 @@ struct MfmaParams {
   float* seg_h;     // [B·seg_p·H][K][V] H of each segment (seg = 1)
   float* seg_start; // [B·seg_p·H][K][V] each segment's start state (the carry's output)
   float* seg_final; // [B·H][K][V] the last segments' end states (seg = 2)
+  // The output norm fused into the y write (NORM scans): OutNorm::forward
+  // (norm.rs:106-144), y / √(mean_v(y²) + ε) · γ [· silu(gate)], per token
+  // and head over the head's V columns.
+  const void* ng;           // gate rows (NULL: OutNorm::Plain); token row r, head h at
+                            // ng + r·ng_stride + h·V
+  long long ng_stride;
+  int ng_bf16;              // gate dtype: bf16 (else fp32)
+  const float* nw;          // γ [V]
+  float neps;
+  // A head's V columns span `ntile` workgroups; each publishes its per-token
+  // partial sums of y² for chunk n as 64-bit words (n + 1) << 32 | bits,
+  // [launch B·H][ntile][4 slots by chunk][64 tokens], cleared before the
+  // launch, and reads its partners' (a cooperative launch keeps the whole
+  // grid resident). A wait that reaches nspin polls gives up, counts itself
+  // in *nfault and uses 0 for the missing sum.
+  unsigned long long* nx;
+  int* nfault;
+  int nspin;
 };
 
 // The backward's transposed tiles. The reverse scan contracts over a chunk's
@@ -725,8 +744,17 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p, B
 // ST (states mode, for the backward's recompute): the fp32 state entering
 // each chunk is written to p.states and y is not written. SEG: the
 // segmented scan's mode (MfmaParams::seg), 0 for an unsegmented scan.
-template <int K, class TY, int WAVES, bool PC, bool ST = false, int SEG = 0>
+// NORM (SEG ≠ 1, not ST): y leaves through OutNorm. Chunk n's y is written
+// unnormalised, its per-token partial Σy² over the workgroup's columns goes
+// to LDS; at the top of chunk n+1 wave 0 sums the waves' partials and
+// publishes them to the head's other column workgroups; after phase 2 of
+// chunk n+2 every lane reads its tokens' partner sums (published a chunk and
+// a half earlier, so in the steady state nothing waits), re-reads its own y
+// values of chunk n and the gate, and after phase 3 writes the normalised
+// output over them. The last two chunks finish after the loop.
+template <int K, class TY, int WAVES, bool PC, bool ST = false, int SEG = 0, bool NORM = false>
 __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
+  static_assert(!NORM || (!ST && SEG != 1), "the output norm applies to y");
   constexpr int KK = K / 32;      // 32-deep k-steps over the key axis
   constexpr int RBK = K / 16;     // 16-row blocks of the state
   constexpr int NT = 64 * WAVES;
@@ -746,6 +774,10 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t tiles[NBUF][BUF];
   __shared__ float gxe[NBUF][kL], gwr[NBUF][kL], gys[NBUF][kL], gegl[NBUF];
   __shared__ float gch[PC ? K : 1];  // e^{G_last} per key channel (per-channel gates)
+  // NORM: per-wave partial Σy² of chunk n [n & 1][token][wave] (pitch
+  // WAVES + 1), and the workgroup's sum per token [n & 1][token].
+  __shared__ float nsq[NORM ? 2 : 1][NORM ? kL : 1][NORM ? WAVES + 1 : 1];
+  __shared__ float nown[NORM ? 2 : 1][NORM ? kL : 1];
 
   const int ntile = (SEG == 1 ? p.vx : p.V) / BW;
   const int BH = p.B * p.H;
@@ -947,6 +979,154 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   };
   auto as8 = [](const uint4& x) { return __builtin_bit_cast(bf16x8, x); };
 
+  // --- NORM: the output norm over the head's V columns ---------------------
+  // Lane (r16, q4) holds value columns jw + 4q4 … +3 of token 16tb + r16 in
+  // yt[tb]. Partial Σy² of chunk n over this wave's 16 columns, per token,
+  // into nsq[n & 1][token][wave].
+  auto norm_partial = [&](int n, const f32x4* yv) {
+    if constexpr (NORM) {
+      float ps[4];
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        float x = yv[tb][0] * yv[tb][0];
+#pragma unroll
+        for (int r = 1; r < 4; ++r) x = fmaf(yv[tb][r], yv[tb][r], x);
+        x += __shfl_xor(x, 16, 64);
+        x += __shfl_xor(x, 32, 64);
+        ps[tb] = x;
+      }
+      // lane 16·q4 + r16 keeps token 16·q4 + r16, i.e. token = lane
+      const float mine = q4 == 0 ? ps[0] : q4 == 1 ? ps[1] : q4 == 2 ? ps[2] : ps[3];
+      nsq[n & 1][lane][wave] = mine;
+    }
+  };
+  // Wave 0, after the barrier that ends chunk n: the workgroup's sums of
+  // chunk n, kept in nown and published to the head's other workgroups.
+  auto norm_publish = [&](int n) {
+    if constexpr (NORM) {
+      if (wave == 0) {
+        float sum = 0.f;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) sum += nsq[n & 1][lane][w];
+        nown[n & 1][lane] = sum;
+        if (ntile > 1) {
+          const unsigned long long word =
+              (static_cast<unsigned long long>(n + 1) << 32) | __float_as_uint(sum);
+          __hip_atomic_store(p.nx + ((size_t(bh) * ntile + tile) * 4 + (n & 3)) * kL + lane, word,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+  };
+  // 1/√(mean + ε) of chunk n's tokens 16·tb + r16 (published by every
+  // workgroup of the head at least a barrier earlier), and this lane's y and
+  // gate values of chunk n loaded for norm_finish.
+  float nrs[4];
+  uint4 nyv[4], ngv[4];
+  auto norm_start = [&](int n) {
+    if constexpr (NORM) {
+      const int rl = min(kL, p.S - n * kL);
+      const unsigned long long want = static_cast<unsigned long long>(n + 1);
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) nrs[tb] = nown[n & 1][16 * tb + r16];
+      for (int j = 0; j < ntile; ++j) {
+        if (j == tile) continue;
+        const unsigned long long* src = p.nx + ((size_t(bh) * ntile + j) * 4 + (n & 3)) * kL;
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+          unsigned long long w =
+              __hip_atomic_load(src + 16 * tb + r16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          for (int it = 0; (w >> 32) != want; ++it) {
+            if (it >= p.nspin) {
+              atomicAdd(p.nfault, 1);
+              w = want << 32;
+              break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+            w = __hip_atomic_load(src + 16 * tb + r16, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          nrs[tb] += __uint_as_float(uint32_t(w));
+        }
+      }
+      const float invv = 1.0f / float(p.V);
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) nrs[tb] = rsqrtf(nrs[tb] * invv + p.neps);
+      // Own y values (written unnormalised by this lane) and the gate, rows
+      // past the sequence end clamped to its last row (nothing is stored there).
+      const size_t row0 = size_t(b) * p.S + size_t(n) * kL;  // token row of the chunk's first token
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const int t = min(16 * tb + r16, rl - 1);
+        const size_t yo = ((row0 + t) * p.H + h) * size_t(p.V) + jw + 4 * q4;
+        if constexpr (sizeof(TY) == 2) {
+          const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const TY*>(p.y) + yo);
+          nyv[tb] = make_uint4(u.x, u.y, 0u, 0u);
+        } else {
+          nyv[tb] = *reinterpret_cast<const uint4*>(static_cast<const TY*>(p.y) + yo);
+        }
+        if (p.ng) {
+          const size_t go = (row0 + t) * size_t(p.ng_stride) + size_t(h) * p.V + jw + 4 * q4;
+          if (p.ng_bf16) {
+            const uint2 u = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.ng) + go);
+            ngv[tb] = make_uint4(u.x, u.y, 0u, 0u);
+          } else {
+            ngv[tb] = *reinterpret_cast<const uint4*>(static_cast<const float*>(p.ng) + go);
+          }
+        }
+      }
+    }
+  };
+  // The normalised output of chunk n over its unnormalised y.
+  auto norm_finish = [&](int n) {
+    if constexpr (NORM) {
+      const int rl = min(kL, p.S - n * kL);
+      const float4 gw = *reinterpret_cast<const float4*>(p.nw + jw + 4 * q4);
+      const float gam[4] = {gw.x, gw.y, gw.z, gw.w};
+      const size_t row0 = size_t(b) * p.S + size_t(n) * kL;
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const int t = 16 * tb + r16;
+        float yv[4], gv[4];
+        if constexpr (sizeof(TY) == 2) {
+          yv[0] = lo_f(nyv[tb].x);
+          yv[1] = hi_f(nyv[tb].x);
+          yv[2] = lo_f(nyv[tb].y);
+          yv[3] = hi_f(nyv[tb].y);
+        } else {
+          yv[0] = __uint_as_float(nyv[tb].x);
+          yv[1] = __uint_as_float(nyv[tb].y);
+          yv[2] = __uint_as_float(nyv[tb].z);
+          yv[3] = __uint_as_float(nyv[tb].w);
+        }
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = yv[r] * nrs[tb] * gam[r];
+        if (p.ng) {
+          if (p.ng_bf16) {
+            gv[0] = lo_f(ngv[tb].x);
+            gv[1] = hi_f(ngv[tb].x);
+            gv[2] = lo_f(ngv[tb].y);
+            gv[3] = hi_f(ngv[tb].y);
+          } else {
+            gv[0] = __uint_as_float(ngv[tb].x);
+            gv[1] = __uint_as_float(ngv[tb].y);
+            gv[2] = __uint_as_float(ngv[tb].z);
+            gv[3] = __uint_as_float(ngv[tb].w);
+          }
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[r] *= gv[r] * sigmoidf_(gv[r]);
+        }
+        if (t < rl) {
+          TY* dst = static_cast<TY*>(p.y) + ((row0 + t) * p.H + h) * size_t(p.V) + jw + 4 * q4;
+          if constexpr (sizeof(TY) == 2)
+            *reinterpret_cast<uint2*>(dst) = make_uint2(pk_bf16(o[0], o[1]), pk_bf16(o[2], o[3]));
+          else
+            *reinterpret_cast<float4*>(dst) = make_float4(o[0], o[1], o[2], o[3]);
+        }
+      }
+    }
+  };
+
   fetch(0, 0, NPF);
   load_v(0);
   load_w(0);
@@ -971,6 +1151,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
     constexpr bool kHalf = NBUF == 2 && WAVES == 8 && !ST;
     constexpr int NH = kHalf ? (NPF + 1) / 2 : NPF;
     if constexpr (kFetchTop) fetch(nn, 0, NH);
+    if (n >= 1) norm_publish(n - 1);
     if constexpr (ST) {
       float* sdst = p.states + chunk_of(n) * K * p.V + jl;
 #pragma unroll
@@ -1113,6 +1294,8 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
       }
     }
 
+    if (n >= 2) norm_start(n - 2);
+
     // Phase 3: yᵀ += V'ᵀ·attnᵀ and S ← e^{G_last}⊙S + (e^{G_last−G}⊙K)ᵀ·V';
     // the bf16 V' fragment is the A operand of the first and the B operand
     // of the second.
@@ -1160,6 +1343,8 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
           *reinterpret_cast<float4*>(dst) =
               make_float4(yt[tb][0], yt[tb][1], yt[tb][2], yt[tb][3]);
       }
+      norm_partial(n, yt);
+      if (n >= 2) norm_finish(n - 2);
     }
     if constexpr (NBUF == 1) {
       __syncthreads();  // every wave is done with this chunk's tiles
@@ -1168,6 +1353,18 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
       stage(cur ^ 1, kHalf ? NH : 0, NPF);
     }
     __syncthreads();
+  }
+
+  if constexpr (NORM) {
+    // Chunks N−2 (its sums published at the top of chunk N−1) and N−1.
+    if (p.N >= 2) {
+      norm_start(p.N - 2);
+      norm_finish(p.N - 2);
+    }
+    norm_publish(p.N - 1);
+    __syncthreads();
+    norm_start(p.N - 1);
+    norm_finish(p.N - 1);
   }
 
   float* sout = p.s_out + size_t(bh) * K * p.V + jl;
@@ -1826,6 +2023,101 @@ hipError_t launch_scan(const MfmaParams& p, const Dims& d, bool yb, hipStream_t 
   return hipGetLastError();
 }
 
+// Clears the output norm's exchange words (a fill kernel: the launch may be
+// captured into a HIP graph, where memset nodes are avoided).
+__global__ __launch_bounds__(256) void zero_words_kernel(unsigned long long* w, size_t n) {
+  for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += size_t(gridDim.x) * 256)
+    w[i] = 0ull;
+}
+
+// The exchange words of the output norm: [B·P·H][V/32][4][64] (room for the
+// narrowest scan workgroups), and the words a launch of `waves`-wave
+// workgroups uses.
+size_t norm_words(const Dims& d, int P, int waves) {
+  return size_t(d.B) * P * d.H * (d.V / (16 * waves)) * 4 * kL;
+}
+size_t norm_exchange_bytes(const Dims& d) { return region(norm_words(d, seg_parts(d), 2) * 8); }
+
+// The output-norm scan kernel (NORM) for a launch of `waves`-wave workgroups;
+// seg: the segmented scan's output pass.
+const void* norm_scan_fn(const Dims& d, bool seg, bool yb, int waves) {
+  const bool pc = per_channel(d);
+#define DN_NK(KD, TY, W, PCV, SG) \
+  return reinterpret_cast<const void*>(&mfma_scan_kernel<KD, TY, W, PCV, false, SG, true>)
+#define DN_NK_W(KD, TY, PCV, SG)                 \
+  do {                                           \
+    if (waves == 8) DN_NK(KD, TY, 8, PCV, SG);   \
+    if (waves == 4) DN_NK(KD, TY, 4, PCV, SG);   \
+    DN_NK(KD, TY, 2, PCV, SG);                   \
+  } while (0)
+#define DN_NK_PC(KD, TY, SG)              \
+  do {                                    \
+    if (pc) DN_NK_W(KD, TY, true, SG);    \
+    DN_NK_W(KD, TY, false, SG);           \
+  } while (0)
+  if (seg) {
+    if (yb) {
+      if (pc) DN_NK(128, bf16, 8, true, 2);
+      DN_NK(128, bf16, 8, false, 2);
+    }
+    if (pc) DN_NK(128, float, 8, true, 2);
+    DN_NK(128, float, 8, false, 2);
+  }
+  if (d.K == 128) {
+    if (yb) DN_NK_PC(128, bf16, 0);
+    DN_NK_PC(128, float, 0);
+  }
+  if (yb) DN_NK_PC(64, bf16, 0);
+  DN_NK_PC(64, float, 0);
+#undef DN_NK_PC
+#undef DN_NK_W
+#undef DN_NK
+}
+
+// The output-norm scan's launch geometry for dims `d` (the segmented output
+// pass's dims when seg): workgroup waves and column workgroups per head.
+struct NormLaunch {
+  const void* fn;
+  int waves, ntile;
+  unsigned blocks;
+};
+NormLaunch norm_launch(const Dims& d, bool seg, bool yb) {
+  NormLaunch l;
+  l.waves = seg ? 8 : scan_waves(d);
+  l.ntile = d.V / (16 * l.waves);
+  l.blocks = unsigned(((d.B * d.H + 7) / 8) * 8 * l.ntile);
+  l.fn = norm_scan_fn(d, seg, yb, l.waves);
+  return l;
+}
+
+// When a head's columns span several workgroups, they exchange per-token
+// sums mid-kernel, so the whole grid must be resident: a cooperative launch.
+// hipErrorCooperativeLaunchTooLarge when the device cannot hold it (the
+// caller then runs the plain forward and a separate norm pass).
+hipError_t norm_launch_fits(const NormLaunch& l) {
+  if (l.ntile == 1) return hipSuccess;
+  int per_cu = 0;
+  hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, l.fn, 64 * l.waves, 0);
+  if (e != hipSuccess) return e;
+  return size_t(per_cu) * device_cu_count() >= l.blocks ? hipSuccess
+                                                         : hipErrorCooperativeLaunchTooLarge;
+}
+
+hipError_t launch_scan_norm(const MfmaParams& p, const Dims& d, bool yb, hipStream_t stream) {
+  const NormLaunch l = norm_launch(d, p.seg != 0, yb);
+  MfmaParams q = p;
+  {
+    const size_t nw = norm_words(d, 1, l.waves);
+    hipLaunchKernelGGL(zero_words_kernel, dim3(unsigned(std::min<size_t>((nw + 255) / 256, 1024))),
+                       dim3(256), 0, stream, q.nx, nw);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  ProfScope ps(per_channel(d) ? "dn_mfma_scan_pc_norm" : "dn_mfma_scan_norm", stream);
+  void* args[] = {&q};
+  if (l.ntile == 1) return hipLaunchKernel(l.fn, dim3(l.blocks), dim3(64 * l.waves), args, 0, stream);
+  return hipLaunchCooperativeKernel(l.fn, dim3(l.blocks), dim3(64 * l.waves), args, 0, stream);
+}
 
 }  // namespace
 
@@ -1880,6 +2172,63 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
   pc.y = y;
   pc.seg_final = state_out;
   return launch_scan<false>(pc, ds, y_dtype == DN_BF16, stream);
+}
+
+size_t mfma_fwd_norm_workspace(const Dims& d) {
+  return tiles_workspace(d) + seg_workspace(d) + norm_exchange_bytes(d);
+}
+
+hipError_t mfma_fwd_norm(const Dims& d, int y_dtype, const void* q, const void* k, const void* v,
+                         const float* erase, const float* write, const float* g,
+                         const float* state_in, void* y, float* state_out, void* ws,
+                         const FwdNorm& nm, hipStream_t stream) {
+  MfmaParams p = make_params(d, q, k, v, erase, write, g, state_in, y, state_out, ws);
+  p.ng = nm.gate;
+  p.ng_stride = nm.gate_stride;
+  p.ng_bf16 = nm.gate_bf16;
+  p.nw = nm.weight;
+  p.neps = nm.eps;
+  p.nx = reinterpret_cast<unsigned long long*>(static_cast<char*>(ws) + tiles_workspace(d) +
+                                               seg_workspace(d));
+  p.nfault = nm.fault;
+  p.nspin = nm.spin;
+  const int P = seg_parts(d);
+  // Whether the scan can run as launched, decided before any launch so that
+  // the caller's fallback starts from a clean slate.
+  {
+    hipError_t e = norm_launch_fits(norm_launch(P > 1 ? seg_dims(d, P) : d, P > 1,
+                                                y_dtype == DN_BF16));
+    if (e != hipSuccess) return e;
+  }
+  hipError_t e = launch_intra(p, d, stream);
+  if (e != hipSuccess) return e;
+  if (P == 1) return launch_scan_norm(p, d, y_dtype == DN_BF16, stream);
+  carve_seg(p, d, static_cast<char*>(ws) + tiles_workspace(d));
+  const Dims ds = seg_dims(d, P);
+  MfmaParams pa = p;
+  pa.B = ds.B;
+  pa.S = ds.S;
+  pa.N = ds.N;
+  pa.seg = 1;
+  pa.seg_p = P;
+  pa.vx = d.V + d.K;
+  pa.y = nullptr;
+  if ((e = launch_scan<false>(pa, ds, y_dtype == DN_BF16, stream)) != hipSuccess) return e;
+  {
+    ProfScope ps("dn_mfma_seg_carry", stream);
+    MfmaParams pb = p;
+    pb.seg_p = P;
+    hipLaunchKernelGGL(seg_carry_kernel<128>, dim3(unsigned(d.B * d.H * (d.V / 16))), dim3(256),
+                       0, stream, pb);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  MfmaParams pc = pa;
+  pc.seg = 2;
+  pc.vx = d.V;
+  pc.s_in = p.seg_start;
+  pc.y = y;
+  pc.seg_final = state_out;
+  return launch_scan_norm(pc, ds, y_dtype == DN_BF16, stream);
 }
 
 MfmaTiles mfma_bwd_tiles(const Dims& d, void* ws) {

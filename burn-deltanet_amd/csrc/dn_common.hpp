@@ -119,6 +119,24 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
                     const float* erase, const float* write, const float* g,
                     const float* state_in, void* y, float* state_out, void* ws,
                     hipStream_t stream, bool fused = false);
+// The MFMA forward with the output norm applied in the scan's y write
+// (OutNorm::forward, norm.rs:106-144): y receives the normalised output.
+// hipErrorCooperativeLaunchTooLarge, before any launch, when the scan's grid
+// cannot be resident at once (its column workgroups exchange sums).
+struct FwdNorm {
+  const void* gate;       // NULL: OutNorm::Plain
+  long long gate_stride;  // elements between consecutive tokens' gate rows
+  int gate_bf16;
+  const float* weight;    // γ [V]
+  float eps;
+  int* fault;             // counts cross-workgroup waits that gave up
+  int spin;               // polls before a wait gives up
+};
+size_t mfma_fwd_norm_workspace(const Dims& d);
+hipError_t mfma_fwd_norm(const Dims& d, int y_dtype, const void* q, const void* k, const void* v,
+                         const float* erase, const float* write, const float* g,
+                         const float* state_in, void* y, float* state_out, void* ws,
+                         const FwdNorm& nm, hipStream_t stream);
 // The fused forward: per-head gates at head_k_dim 128, head_v_dim a multiple
 // of 128, bf16 q/k/v.
 bool fused_fwd_supported(const Dims& d, int qkv_dtype);

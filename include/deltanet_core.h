@@ -286,6 +286,41 @@ typedef struct {
  * gated_deltanet_2.rs:282, 367; delta_product.rs:230, 306). */
 int dn_out_norm(const dn_out_norm_args *args, hipStream_t stream);
 
+/* The chunk forward followed by the output norm, as every family runs them
+ * over a sequence: DeltaChunkBackendExt::delta_chunk_recalculated
+ * (chunk_recalculated.rs:115-151), then OutNorm::forward
+ * (src/common/norm.rs:106-144) on its y (gated_deltanet_1.rs:183-186 and the
+ * others listed at dn_out_norm). `fwd` as for dn_chunk_fwd, except that
+ * fwd.y receives OutNorm's output (dtype fwd.y_dtype) in place of the delta
+ * rule's y; the gate, weight and eps as for dn_out_norm, the gate rows
+ * [batch, sequence] gate_stride elements apart (a column view of the
+ * projection), head h's gates at h*head_v_dim. On the MFMA path (AUTO or
+ * DN_ALGO_MFMA) the norm runs in the scan's output write: y never makes a
+ * round trip through HBM. A head's columns may span several scan workgroups,
+ * which then exchange per-token sums of squares during the kernel; that
+ * launch is cooperative (the grid must be resident at once), and where the
+ * device cannot hold it, or on the other paths, the call runs dn_chunk_fwd
+ * and then dn_out_norm in place on fwd.y. Each exchange wait is bounded: one
+ * that gives up (which a cooperative launch rules out) is counted, and
+ * dn_wait_give_ups() reports the count. fwd.workspace, if given, holds
+ * dn_chunk_fwd_out_norm_workspace_bytes(). */
+typedef struct {
+  dn_chunk_fwd_args fwd;
+  const void *gate;       /* NULL for OutNorm::Plain */
+  int64_t gate_stride;    /* elements between consecutive tokens' gate rows */
+  int32_t gate_dtype;     /* DN_F32 or DN_BF16 */
+  const float *weight;    /* gamma [head_v_dim] */
+  double eps;
+} dn_chunk_fwd_out_norm_args;
+
+int dn_chunk_fwd_out_norm(const dn_chunk_fwd_out_norm_args *args, hipStream_t stream);
+size_t dn_chunk_fwd_out_norm_workspace_bytes(const dn_chunk_fwd_out_norm_args *args);
+
+/* Bounded cross-workgroup waits that gave up on the current device since the
+ * library was loaded (synchronises the device). No counterpart in the
+ * reference; nonzero means an output of dn_chunk_fwd_out_norm was wrong. */
+int64_t dn_wait_give_ups(void);
+
 /* One decode token of a delta-rule block between its in_proj and out_proj
  * GEMMs, in one launch: QkvProjection::step (src/common/qkv.rs:454-516: the
  * short-convolution step with its rolling window, the activations, the q/k

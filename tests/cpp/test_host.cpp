@@ -517,8 +517,9 @@ void gpu_cases() {
                                            in2.v_bshv, in2.erase_bshK, in2.write_bshV,
                                            in2.g_bshK, in2.state_bhkv, 64,
                                            1.0 / std::sqrt(128.0));
-    expect_close("workspace_bwd_dq", download(gr.d_q_bshk), download(gd.d_q_bshk), 0.0);
-    expect_close("workspace_bwd_dg", download(*gr.d_g_bshK), download(*gd.d_g_bshK), 0.0);
+    // The backward sums some gradients with atomics: equal up to their order.
+    expect_close("workspace_bwd_dq", download(gr.d_q_bshk), download(gd.d_q_bshk), 1e-5);
+    expect_close("workspace_bwd_dg", download(*gr.d_g_bshK), download(*gd.d_g_bshK), 1e-5);
     ok("caller_workspace");
   }
   // The projection front-end. With the newest conv tap 1 and the others 0,

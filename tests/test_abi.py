@@ -24,7 +24,7 @@ fake_pointers = pytest.mark.skipif(
 
 def header_symbols():
     text = (ROOT / "include" / "deltanet_core.h").read_text()
-    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char \*)\s*(dn_\w+)\s*\(", text,
+    return sorted(set(re.findall(r"^\s*(?:int64_t|int|size_t|const char \*)\s*(dn_\w+)\s*\(", text,
                                  re.M)))
 
 
@@ -173,6 +173,78 @@ def test_mfma_paths_need_word_aligned_qkv():
         a = fwd_args(**base, **over, algo=abi.DN_ALGO_MFMA)
         want = abi.DN_ALGO_MFMA if auto == abi.DN_ALGO_MFMA else -9
         assert lib.dn_chunk_fwd_algo(ctypes.byref(a)) == want, over
+
+
+def test_mfma_serves_any_chunk_len_for_per_head_gates():
+    """The MFMA kernels' 64-token chunks serve every chunk_len when the
+    forget gate is per head or absent (the chunk length changes only the
+    order of roundings), with chunk 64's workspace; with a per-channel forget
+    gate, whose block-decay clamp depends on where chunks start, only 64 is
+    served there. No pointer is read."""
+    lib = abi.lib()
+    base = dict(batch=2, sequence=1000, nheads=4, head_k_dim=128, head_v_dim=128,
+                qkv_dtype=abi.DN_BF16, y_dtype=abi.DN_BF16)
+    ref = fwd_args(**base, chunk_len=64)
+    ws64 = lib.dn_chunk_fwd_workspace_bytes(ctypes.byref(ref))
+    for L in (1, 16, 32, 100, 128, 4096):
+        for algo, want in ((abi.DN_ALGO_AUTO, abi.DN_ALGO_MFMA),
+                           (abi.DN_ALGO_MFMA, abi.DN_ALGO_MFMA),
+                           (abi.DN_ALGO_MFMA_FUSED, abi.DN_ALGO_MFMA_FUSED)):
+            a = fwd_args(**base, chunk_len=L, algo=algo)
+            assert lib.dn_chunk_fwd_algo(ctypes.byref(a)) == want, (L, algo)
+        a = fwd_args(**base, chunk_len=L)
+        assert lib.dn_chunk_fwd_workspace_bytes(ctypes.byref(a)) == ws64, L
+        a = fwd_args(**base, chunk_len=L, has_gate=0)
+        assert lib.dn_chunk_fwd_algo(ctypes.byref(a)) == abi.DN_ALGO_MFMA, L
+        b = bwd_args(chunk_len=L)
+        assert lib.dn_chunk_bwd_algo(ctypes.byref(b)) == abi.DN_ALGO_MFMA, L
+        assert (lib.dn_chunk_bwd_workspace_bytes(ctypes.byref(b)) ==
+                lib.dn_chunk_bwd_workspace_bytes(ctypes.byref(bwd_args(chunk_len=64)))), L
+    pc = dict(base, erase_width=128, write_width=128, decay_width=128)
+    assert lib.dn_chunk_fwd_algo(ctypes.byref(fwd_args(**pc, chunk_len=64))) == abi.DN_ALGO_MFMA
+    for L in (32, 128):
+        assert lib.dn_chunk_fwd_algo(ctypes.byref(fwd_args(**pc, chunk_len=L))) == \
+            abi.DN_ALGO_GENERIC
+        a = fwd_args(**pc, chunk_len=L, algo=abi.DN_ALGO_MFMA)
+        assert lib.dn_chunk_fwd_algo(ctypes.byref(a)) == -9
+        b = bwd_args(chunk_len=L, head_v_dim=128, erase_width=128, write_width=128,
+                     decay_width=128)
+        assert lib.dn_chunk_bwd_algo(ctypes.byref(b)) == abi.DN_ALGO_GENERIC
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(weight=None), -6, "norm weight is NULL"),
+    (dict(eps=-1.0), -2, "eps must be finite and non-negative"),
+    (dict(eps=float("inf")), -2, "eps must be finite and non-negative"),
+    (dict(gate_stride=5), -2, "gate_stride must cover nheads * head_v_dim"),
+    (dict(gate_dtype=9), -7, "dtype"),
+    (dict(fwd_over=dict(sequence=0)), -1, "sequence length must be at least 1"),
+    (dict(fwd_over=dict(head_v_dim=2048, write_width=1)), -9, "head_v_dim up to 1024"),
+])
+@fake_pointers
+def test_chunk_fwd_out_norm_rejects_invalid_arguments(over, code, msg):
+    lib = abi.lib()
+    a = abi.ChunkFwdOutNormArgs()
+    a.fwd = fwd_args(**over.pop("fwd_over", {}))
+    a.gate, a.gate_stride, a.gate_dtype = 0x1000, a.fwd.nheads * a.fwd.head_v_dim, abi.DN_F32
+    a.weight, a.eps = 0x1000, 1e-5
+    for k, v in over.items():
+        setattr(a, k, v)
+    assert lib.dn_chunk_fwd_out_norm(ctypes.byref(a), None) == code
+    assert msg in lib.dn_last_error().decode()
+    assert lib.dn_chunk_fwd_out_norm_workspace_bytes(ctypes.byref(a)) == 0
+
+
+def test_chunk_fwd_out_norm_workspace_covers_the_forward():
+    """The fused norm's workspace holds the forward's and the exchange words."""
+    lib = abi.lib()
+    f = fwd_args(batch=8, sequence=4096, nheads=16, head_k_dim=128, head_v_dim=256,
+                 qkv_dtype=abi.DN_BF16, y_dtype=abi.DN_BF16)
+    a = abi.ChunkFwdOutNormArgs()
+    a.fwd, a.weight, a.eps = f, 0x1000, 1e-5
+    fwd_ws = lib.dn_chunk_fwd_workspace_bytes(ctypes.byref(f))
+    ws = lib.dn_chunk_fwd_out_norm_workspace_bytes(ctypes.byref(a))
+    assert ws >= fwd_ws + 8 * 16 * (256 // 32) * 4 * 64 * 8
 
 
 def test_mfma_paths_refuse_rows_past_32_bit_offsets():

@@ -113,14 +113,76 @@ def test_mfma_constant_keys_stay_bounded(rng):
 
 
 def test_other_shapes_take_the_generic_path(rng):
-    """dk outside {64, 128} or chunk ≠ 64 are served by the generic kernels under AUTO."""
+    """dk outside {64, 128}, or a per-channel forget gate at a chunk length
+    other than 64, is served by the generic kernels under AUTO."""
     announce("mfma coverage")
-    for K, L in [(96, 64), (128, 32)]:
-        g_args = to_gpu(gdn_inputs(rng, 1, 100, 2, K, 64, True), torch.bfloat16)
+    for K, L, gates in [(96, 64, "head"), (128, 32, "channel")]:
+        if gates == "head":
+            g_args = to_gpu(gdn_inputs(rng, 1, 100, 2, K, 64, True), torch.bfloat16)
+        else:
+            g_args = to_gpu(gdn2_inputs(rng, 1, 100, 2, K, 64, K, 64), torch.bfloat16)
         q, k, v, e, w, g, s = g_args
         y = torch.empty((1, 100, 2, 64), dtype=torch.bfloat16, device=DEV)
         a = pkg.abi.chunk_fwd_args(q, k, v, e, w, g, s, y, torch.empty_like(s), L, None)
         assert pkg.abi.lib().dn_chunk_fwd_algo(a) == pkg.abi.DN_ALGO_GENERIC
+
+
+CHUNK_LEN_CASES = [
+    # chunk_len, B, S, H, K, V, gated: any chunk length runs the MFMA kernels'
+    # 64-token chunks when the forget gate is per head (or absent)
+    (32, 2, 256, 2, 128, 256, True),
+    (128, 1, 300, 2, 128, 128, True),
+    (16, 1, 200, 2, 64, 64, False),
+    (100, 2, 250, 2, 128, 128, True),
+    (1, 1, 70, 2, 128, 64, True),
+]
+
+
+@pytest.mark.parametrize("case", CHUNK_LEN_CASES)
+def test_mfma_serves_other_chunk_lengths(rng, case):
+    """path.rs:15-19: the chunk length trades intra-chunk work against serial
+    steps; the chunk form computes the token recurrence at any length. The
+    MFMA path serves a request for chunk_len L (per-head gates) with its own
+    64-token chunks: against the oracle's chunk forward at L itself, forward
+    and all seven gradients, at the bf16 bar."""
+    L, B, S, H, K, V, gated = case
+    announce(f"mfma at chunk_len {L}: {case[1:]}")
+    args = gdn_inputs(rng, B, S, H, K, V, gated, state_std=0.02)
+    g_args = to_gpu(args, torch.bfloat16)
+    q, k, v, e, w, g, s = g_args
+    y = torch.empty((B, S, H, V), dtype=torch.float32, device=DEV)
+    s_out = torch.empty_like(s)
+    a = pkg.abi.chunk_fwd_args(q, k, v, e, w, g, s, y, s_out, L, None)
+    assert pkg.abi.lib().dn_chunk_fwd_algo(a) == MFMA
+    pkg.abi.run_chunk_fwd(a)
+    torch.cuda.synchronize()
+    ref = as_oracle_inputs(g_args)
+    y0, s0 = O.chunk_fwd(*ref, chunk_len=L, dtype=np.float64)
+    ey, es = rel_err(np_of(y), y0), rel_err(np_of(s_out), s0)
+    print(f"  forward rel err y {ey:.2e} state {es:.2e}", flush=True)
+    assert ey < TOL and es < TOL
+    dy = rng.standard_normal((B, S, H, V))
+    ds = rng.standard_normal((B, H, K, V)) * 0.5
+    tdy = torch.tensor(dy, dtype=torch.float32, device=DEV)
+    tds = torch.tensor(ds, dtype=torch.float32, device=DEV)
+    grads = (torch.empty(q.shape, device=DEV), torch.empty(k.shape, device=DEV),
+             torch.empty(v.shape, device=DEV), torch.empty_like(e), torch.empty_like(w),
+             None if g is None else torch.empty_like(g), torch.empty_like(s))
+    assert pkg.abi.lib().dn_chunk_bwd_algo(
+        pkg.abi.chunk_bwd_args(tdy, tds, q, k, v, e, w, g, s, grads, L, None)) == MFMA
+    got = pkg.combined_backward(tdy, tds, q, k, v, e, w, g, s, L, 1.0 / np.sqrt(K))
+    torch.cuda.synchronize()
+    want = O.chunk_bwd(dy, ds, *ref, chunk_len=L)
+    names = ["d_q", "d_k", "d_v", "d_erase", "d_write", "d_g", "d_state"]
+    vals = [got.d_q_bshk, got.d_k_bshk, got.d_v_bshv, got.d_erase_bshK, got.d_write_bshV,
+            got.d_g_bshK, got.d_state_bhkv]
+    for name, a_, b in zip(names, vals, want):
+        if b is None:
+            assert a_ is None
+            continue
+        err = rel_err(np_of(a_), b)
+        print(f"  {name} rel err {err:.2e}", flush=True)
+        assert err < TOL, name
 
 
 def gdn2_inputs(rng, B, S, H, K, V, ew, ww, state_std=0.0, g_scale=0.05, beta_scale=1.0):
