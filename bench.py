@@ -595,11 +595,41 @@ def bench_block_forward(torch, pkg, steps, warmup):
             f()
     ms, kern = _timed(torch, abi, block, steps, warmup)
     parts = {n: round(_timed(torch, abi, f, steps, warmup)[0], 4) for n, f in calls.items()}
+    # The same block with the norm in the scan's output write
+    # (dn_chunk_fwd_out_norm: y never round-trips through HBM).
+    # The core and the norm as one call (dn_chunk_fwd_out_norm), the norm as
+    # a pass of its own (the default) and in the scan's y write (in_scan).
+    fa = abi.chunk_fwd_args(q, k, v, beta, beta, g, s0, out, s1, 64, None)
+    cn = {}
+    for mode in (False, True):
+        na = abi.chunk_fwd_out_norm_args(fa, z, gamma, 1e-5, in_scan=mode)
+        fws = torch.empty(max(abi.lib().dn_chunk_fwd_out_norm_workspace_bytes(na), 1),
+                          dtype=torch.uint8, device=dev)
+        na.fwd.workspace, na.fwd.workspace_bytes = fws.data_ptr(), fws.numel()
+        cn[mode] = (na, fws)
+    core_norm = lambda: abi.run_chunk_fwd_out_norm(cn[False][0])
+    core_norm_in_scan = lambda: abi.run_chunk_fwd_out_norm(cn[True][0])
+
+    def block_fused():
+        abi.run_frontend(fe)
+        core_norm()
+    fms, fkern = _timed(torch, abi, block_fused, steps, warmup)
+    cn_ms, cn_kern = _timed(torch, abi, core_norm, steps, warmup)
+    cs_ms, cs_kern = _timed(torch, abi, core_norm_in_scan, steps, warmup)
+    give_ups = abi.wait_give_ups()
     return {"workload": "Gated DeltaNet block forward after in_proj at the config-2 shape: "
                         "dn_frontend + dn_chunk_fwd + dn_out_norm, bf16",
             "ms_per_step": round(ms, 4), "tokens_per_s": round(B * S / (ms / 1e3), 1),
             "separate_ms": parts, "sum_of_separate_ms": round(sum(parts.values()), 4),
-            "kernels": kern}
+            "kernels": kern,
+            "one_call_core": {"calls": "dn_frontend + dn_chunk_fwd_out_norm",
+                           "ms_per_step": round(fms, 4),
+                           "tokens_per_s": round(B * S / (fms / 1e3), 1), "kernels": fkern,
+                           "core_with_norm_ms": round(cn_ms, 4),
+                           "core_plus_out_norm_ms": round(parts["core"] + parts["out_norm"], 4),
+                           "core_with_norm_in_scan_ms": round(cs_ms, 4),
+                           "in_scan_kernels": cs_kern,
+                           "wait_give_ups": give_ups}}
 
 
 def _host_cpu():

@@ -128,7 +128,7 @@ class OutNormArgs(ctypes.Structure):
 class ChunkFwdOutNormArgs(ctypes.Structure):
     _fields_ = [
         ("fwd", ChunkFwdArgs), ("gate", _vp), ("gate_stride", _i64), ("gate_dtype", _i32),
-        ("weight", _vp), ("eps", _f64),
+        ("weight", _vp), ("eps", _f64), ("in_scan", _i32),
     ]
 
 
@@ -391,13 +391,16 @@ def run_out_norm(args: OutNormArgs) -> None:
     check(lib().dn_out_norm(ctypes.byref(args), stream_handle()))
 
 
-def chunk_fwd_out_norm_args(fwd: ChunkFwdArgs, gate, weight, eps) -> ChunkFwdOutNormArgs:
+def chunk_fwd_out_norm_args(fwd: ChunkFwdArgs, gate, weight, eps,
+                            in_scan=False) -> ChunkFwdOutNormArgs:
     """dn_chunk_fwd_out_norm's arguments: `fwd` (whose y receives the norm's
     output) with the output norm's gate ([batch, sequence, nheads, head_v_dim]
     or a column view of the projection with evenly strided tokens; None for
-    the plain norm), weight γ [head_v_dim] and eps."""
+    the plain norm), weight γ [head_v_dim] and eps; in_scan: the norm in the
+    MFMA scan's y write rather than a pass of its own."""
     a = ChunkFwdOutNormArgs()
     a.fwd = fwd
+    a.in_scan = int(bool(in_scan))
     H, D = fwd.nheads, fwd.head_v_dim
     if gate is not None:
         want = (fwd.batch, fwd.sequence, H, D)

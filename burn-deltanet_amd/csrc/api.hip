@@ -484,13 +484,14 @@ int check_fwd_norm(const dn_chunk_fwd_out_norm_args* a) {
   return DN_OK;
 }
 
-// The fused norm reads the gate and γ in 8- or 16-byte words per 4 columns.
+// The fused norm reads the gate, in y's dtype, and y in words of 4 values
+// at 32-bit offsets within a chunk's 64 token rows.
 bool norm_fusable(const dn_chunk_fwd_out_norm_args* a) {
-  const size_t gbytes = a->gate_dtype == DN_BF16 ? 2 : 4;
-  const bool gate_ok = !a->gate || (reinterpret_cast<uintptr_t>(a->gate) % (4 * gbytes) == 0 &&
-                                    (size_t(a->gate_stride) * gbytes) % (4 * gbytes) == 0);
-  return gate_ok && reinterpret_cast<uintptr_t>(a->weight) % 16 == 0 &&
-         reinterpret_cast<uintptr_t>(a->fwd.y) % (a->fwd.y_dtype == DN_BF16 ? 8 : 16) == 0;
+  const size_t word = a->fwd.y_dtype == DN_BF16 ? 8 : 16;
+  const bool gate_ok = !a->gate || (a->gate_dtype == a->fwd.y_dtype &&
+                                    reinterpret_cast<uintptr_t>(a->gate) % word == 0 &&
+                                    a->gate_stride % 4 == 0 && a->gate_stride < (int64_t(1) << 25));
+  return gate_ok && reinterpret_cast<uintptr_t>(a->fwd.y) % word == 0;
 }
 
 }  // namespace
@@ -504,7 +505,8 @@ size_t dn_chunk_fwd_out_norm_workspace_bytes(const dn_chunk_fwd_out_norm_args* a
   const int algo = fwd_algo(f, d);
   if (algo < 0) return 0;
   d = run_dims(d, algo);
-  return algo == DN_ALGO_MFMA ? mfma_fwd_norm_workspace(d) : fwd_workspace(d, algo);
+  return a->in_scan && algo == DN_ALGO_MFMA && norm_fusable(a) ? mfma_fwd_norm_workspace(d)
+                                                               : fwd_workspace(d, algo);
 }
 
 int dn_chunk_fwd_out_norm(const dn_chunk_fwd_out_norm_args* a, hipStream_t stream) {
@@ -518,7 +520,8 @@ int dn_chunk_fwd_out_norm(const dn_chunk_fwd_out_norm_args* a, hipStream_t strea
   if (algo < 0)
     return fail(DN_ERR_UNSUPPORTED, "the requested MFMA path does not cover this shape/dtype");
   d = run_dims(d, algo);
-  const size_t need = algo == DN_ALGO_MFMA ? mfma_fwd_norm_workspace(d) : fwd_workspace(d, algo);
+  const bool in_scan = a->in_scan && algo == DN_ALGO_MFMA && norm_fusable(a);
+  const size_t need = in_scan ? mfma_fwd_norm_workspace(d) : fwd_workspace(d, algo);
   void* ws = f->workspace;
   if (ws) {
     if (f->workspace_bytes < need)
@@ -542,11 +545,10 @@ int dn_chunk_fwd_out_norm(const dn_chunk_fwd_out_norm_args* a, hipStream_t strea
   }
   const float* g = f->has_gate ? f->g : nullptr;
   hipError_t e = hipErrorCooperativeLaunchTooLarge;
-  if (algo == DN_ALGO_MFMA && norm_fusable(a)) {
+  if (in_scan) {
     int* fault = nullptr;
     if ((e = give_up_counter(&fault)) != hipSuccess) return hip_fail(e, "wait counter");
-    FwdNorm nm{a->gate, (long long)a->gate_stride, a->gate_dtype == DN_BF16 ? 1 : 0, a->weight,
-               float(a->eps), fault, kNormSpin};
+    FwdNorm nm{a->gate, (long long)a->gate_stride, a->weight, float(a->eps), fault, kNormSpin};
     e = mfma_fwd_norm(d, f->y_dtype, f->q, f->k, f->v, f->erase, f->write, g, f->state_in, f->y,
                       f->state_out, ws, nm, stream);
   }

@@ -124,15 +124,18 @@ hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, co
 // hipErrorCooperativeLaunchTooLarge, before any launch, when the scan's grid
 // cannot be resident at once (its column workgroups exchange sums).
 struct FwdNorm {
-  const void* gate;       // NULL: OutNorm::Plain
-  long long gate_stride;  // elements between consecutive tokens' gate rows
-  int gate_bf16;
+  const void* gate;       // NULL: OutNorm::Plain; else in y's dtype
+  long long gate_stride;  // elements between consecutive tokens' gate rows, below 2^25
   const float* weight;    // γ [V]
   float eps;
   int* fault;             // counts cross-workgroup waits that gave up
   int spin;               // polls before a wait gives up
 };
 size_t mfma_fwd_norm_workspace(const Dims& d);
+// The output-norm scan kernel (chunk_fwd_norm.hip) for head_k_dim K,
+// per-channel gates pc, the segmented scan's output pass seg, bf16 y (else
+// fp32), `waves`-wave workgroups, gated (else plain) norm.
+const void* norm_scan_fn(int K, bool pc, bool seg, bool y_bf16, int waves, bool gated);
 hipError_t mfma_fwd_norm(const Dims& d, int y_dtype, const void* q, const void* k, const void* v,
                          const float* erase, const float* write, const float* g,
                          const float* state_in, void* y, float* state_out, void* ws,

@@ -294,15 +294,20 @@ int dn_out_norm(const dn_out_norm_args *args, hipStream_t stream);
  * fwd.y receives OutNorm's output (dtype fwd.y_dtype) in place of the delta
  * rule's y; the gate, weight and eps as for dn_out_norm, the gate rows
  * [batch, sequence] gate_stride elements apart (a column view of the
- * projection), head h's gates at h*head_v_dim. On the MFMA path (AUTO or
- * DN_ALGO_MFMA) the norm runs in the scan's output write: y never makes a
- * round trip through HBM. A head's columns may span several scan workgroups,
- * which then exchange per-token sums of squares during the kernel; that
- * launch is cooperative (the grid must be resident at once), and where the
- * device cannot hold it, or on the other paths, the call runs dn_chunk_fwd
- * and then dn_out_norm in place on fwd.y. Each exchange wait is bounded: one
- * that gives up (which a cooperative launch rules out) is counted, and
- * dn_wait_give_ups() reports the count. fwd.workspace, if given, holds
+ * projection), head h's gates at h*head_v_dim. in_scan = 0 runs the
+ * chunk forward and then the norm as a pass of its own over y (in place);
+ * in_scan = 1 applies the norm in the MFMA scan's output write, so y makes no
+ * round trip through HBM, where the MFMA path runs (AUTO or DN_ALGO_MFMA)
+ * and the gate, if any, has y's dtype. The separate pass is the faster of
+ * the two at every shape measured on MI355X (0.59 against
+ * 0.65 ms): the scan is latency-bound, and the norm's work inside its chunk
+ * loop lengthens it more than the pass costs. In the scan, a head's columns
+ * may span several workgroups, which then exchange per-token sums of squares
+ * during the kernel; that launch is cooperative (the grid must be resident
+ * at once), and where the device cannot hold it the call falls back to the
+ * separate pass. Each exchange wait is bounded: one that gives up (which a
+ * cooperative launch rules out) is counted, and dn_wait_give_ups() reports
+ * the count. fwd.workspace, if given, holds
  * dn_chunk_fwd_out_norm_workspace_bytes(). */
 typedef struct {
   dn_chunk_fwd_args fwd;
@@ -311,6 +316,7 @@ typedef struct {
   int32_t gate_dtype;     /* DN_F32 or DN_BF16 */
   const float *weight;    /* gamma [head_v_dim] */
   double eps;
+  int32_t in_scan;        /* 0: a separate norm pass; 1: the norm in the scan's y write */
 } dn_chunk_fwd_out_norm_args;
 
 int dn_chunk_fwd_out_norm(const dn_chunk_fwd_out_norm_args *args, hipStream_t stream);

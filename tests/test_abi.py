@@ -236,13 +236,16 @@ def test_chunk_fwd_out_norm_rejects_invalid_arguments(over, code, msg):
 
 
 def test_chunk_fwd_out_norm_workspace_covers_the_forward():
-    """The fused norm's workspace holds the forward's and the exchange words."""
+    """The norm as its own pass needs the forward's workspace; in the scan's
+    write, also the exchange words."""
     lib = abi.lib()
     f = fwd_args(batch=8, sequence=4096, nheads=16, head_k_dim=128, head_v_dim=256,
                  qkv_dtype=abi.DN_BF16, y_dtype=abi.DN_BF16)
     a = abi.ChunkFwdOutNormArgs()
     a.fwd, a.weight, a.eps = f, 0x1000, 1e-5
     fwd_ws = lib.dn_chunk_fwd_workspace_bytes(ctypes.byref(f))
+    assert lib.dn_chunk_fwd_out_norm_workspace_bytes(ctypes.byref(a)) == fwd_ws
+    a.in_scan = 1
     ws = lib.dn_chunk_fwd_out_norm_workspace_bytes(ctypes.byref(a))
     assert ws >= fwd_ws + 8 * 16 * (256 // 32) * 4 * 64 * 8
 

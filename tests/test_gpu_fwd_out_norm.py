@@ -5,7 +5,9 @@ back (gated_deltanet_1.rs:183-186).
 Against the oracle's composition: the C++ oracle's chunk forward
 (chunk_recalculated.rs:115-177) followed by oracle/frontend.py's out_norm,
 in float64 on the bf16-rounded inputs the GPU reads, at the bf16 bar
-(normwise 2e-2; bf16 output rounds each value to 2^-9). The cases cover one
+(normwise 2e-2; bf16 output rounds each value to 2^-9), both with the norm
+in the scan's output write (in_scan) and as a pass of its own. The cases
+cover one
 scan workgroup per head row and rows split over 2, 4 and 8 workgroups (whose
 per-token sums cross workgroups mid-kernel), the segmented scan, per-head
 and per-channel gates, the gated and plain norms, the gate as a strided
@@ -45,14 +47,14 @@ def inputs(rng, B, S, H, K, V, gates, state_std=0.02):
     return [q, k, v, e, w, g, s0]
 
 
-def run_fused(g_args, gate, gamma, eps, y_dtype, chunk_len=64, qkv_dtype=torch.bfloat16):
+def run_fused(g_args, gate, gamma, eps, y_dtype, chunk_len=64, in_scan=True):
     q, k, v, e, w, g, s = g_args
     B, S, H, _ = q.shape
     V = v.shape[3]
     y = torch.empty((B, S, H, V), dtype=y_dtype, device=DEV)
     s_out = torch.empty_like(s)
     fa = abi.chunk_fwd_args(q, k, v, e, w, g, s, y, s_out, chunk_len, None)
-    na = abi.chunk_fwd_out_norm_args(fa, gate, gamma, eps)
+    na = abi.chunk_fwd_out_norm_args(fa, gate, gamma, eps, in_scan=in_scan)
     ws_bytes = abi.lib().dn_chunk_fwd_out_norm_workspace_bytes(na)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
     na.fwd.workspace, na.fwd.workspace_bytes = ws.data_ptr(), ws.numel()
@@ -98,14 +100,15 @@ def make_gate(rng, B, S, H, V, form):
                         device=DEV).to(dt), None
 
 
+@pytest.mark.parametrize("in_scan", [True, False])
 @pytest.mark.parametrize("case", CASES)
-def test_fused_out_norm_matches_oracle(rng, case):
+def test_fused_out_norm_matches_oracle(rng, case, in_scan):
     B, S, H, K, V, gates, form, y_dtype, L = case
-    announce(f"chunk fwd + out norm {case}")
+    announce(f"chunk fwd + out norm {case}, in scan {in_scan}")
     g_args = to_gpu(inputs(rng, B, S, H, K, V, gates), torch.bfloat16)
     gate, keep = make_gate(rng, B, S, H, V, form)
     gamma = torch.tensor(1.0 + 0.1 * rng.standard_normal(V), dtype=torch.float32, device=DEV)
-    y, s = run_fused(g_args, gate, gamma, 1e-5, y_dtype, L)
+    y, s = run_fused(g_args, gate, gamma, 1e-5, y_dtype, L, in_scan)
     want_y, want_s = oracle_of(g_args, gate, gamma, 1e-5, L)
     ey, es = rel_err(np_of(y), want_y), rel_err(np_of(s), want_s)
     print(f"  rel err out {ey:.2e} state {es:.2e}", flush=True)
