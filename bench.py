@@ -534,7 +534,8 @@ def bench_chunk_lengths(torch, pkg, steps, warmup):
     s1 = torch.empty_like(s0)
     abi = pkg.abi
     out = {"workload": "config 2 (B=8 T=4096 H=16 dk=128 dv=256, bf16 q/k/v) at chunk_len 32 "
-                       "and 128 under AUTO, and on the generic fp32 kernels at 64"}
+                       "and 128 under AUTO, on the generic fp32 kernels at 64, and with "
+                       "per-channel erase/write gates under AUTO"}
     for name, L, algo in (("auto_chunk32", 32, 0), ("auto_chunk128", 128, 0),
                           ("forced_generic_chunk64", 64, 1)):
         a = abi.chunk_fwd_args(q, k, v, beta, beta, g, s0, y, s1, L, None, algo=algo)
@@ -547,6 +548,22 @@ def bench_chunk_lengths(torch, pkg, steps, warmup):
                      "ms_per_step": round(ms, 3), "tokens_per_s": round(B * T / (ms / 1e3), 1),
                      "kernels": kern}
         del ws
+    # WriteGate::Channel (erase [.., dk], write [.., dv]) beside config 2's
+    # per-head forget gate: the per-channel MFMA kernels with the head mask.
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(20260838)
+    e = torch.sigmoid(torch.randn((B, T, H, K), generator=gen, device=dev))
+    w = torch.sigmoid(torch.randn((B, T, H, V), generator=gen, device=dev))
+    a = abi.chunk_fwd_args(q, k, v, e, w, g, s0, y, s1, 64, None)
+    ws = torch.empty(max(abi.lib().dn_chunk_fwd_workspace_bytes(a), 1), dtype=torch.uint8,
+                     device=dev)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+    chosen = abi.lib().dn_chunk_fwd_algo(a)
+    ms, kern = _timed(torch, abi, lambda: abi.run_chunk_fwd(a), steps, warmup)
+    out["auto_channel_write_gates"] = {
+        "gates": "erase [.., dk], write [.., dv], per-head forget gate",
+        "algo": ALGO_NAMES.get(chosen, chosen), "ms_per_step": round(ms, 3),
+        "tokens_per_s": round(B * T / (ms / 1e3), 1), "kernels": kern}
     return out
 
 

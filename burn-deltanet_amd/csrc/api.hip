@@ -329,8 +329,7 @@ Dims bwd_dims(const dn_chunk_bwd_args* a) {
 int bwd_algo(const dn_chunk_bwd_args* a, const Dims& d0) {
   if (a->algo == DN_ALGO_GENERIC) return DN_ALGO_GENERIC;
   const Dims d = mfma_dims(d0);
-  const bool fits = mfma_fwd_supported(d, a->qkv_dtype, DN_BF16) &&
-                    mfma_aligned(a->q, a->k, a->v) &&
+  const bool fits = mfma_bwd_supported(d, a->qkv_dtype) && mfma_aligned(a->q, a->k, a->v) &&
                     reinterpret_cast<uintptr_t>(a->d_y) % 16 == 0;
   if (mfma_requested(a->algo)) return fits ? DN_ALGO_MFMA : DN_ERR_UNSUPPORTED;
   return fits ? DN_ALGO_MFMA : DN_ALGO_GENERIC;

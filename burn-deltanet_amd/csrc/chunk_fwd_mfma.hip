@@ -325,8 +325,13 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
 // BT (the backward's recompute): the kernel also writes the reverse scan's
 // transposed tiles (Tᵀ hi/lo, attnᵀ, Kc, Qgᵀ, Kgᵀ, e^{G_last}), the same
 // values the transposing pass of the per-head backward produces. EW1: the
-// erase gate has width 1 (else K).
-template <int K, bool BT, bool EW1>
+// erase gate has width 1 (else K). HD: the forget gate is per head (width 1,
+// or none) while the erase or write gate is per channel (WriteGate::Channel
+// blocks of Gated DeltaNet / DeltaNet): G is the same in every channel, and
+// the scores take the reference's head mask e^{Gᵢ−Gⱼ} (head_decay_mask,
+// forward.rs:290-312) on the fp32 accumulators in place of the block factors,
+// so the block decay's clamp (a per-channel device) never applies.
+template <int K, bool BT, bool EW1, bool HD = false>
 __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p, BwdTiles bt) {
   constexpr int GP = K + 4;  // fp32 row pitch of G
   constexpr int KS8 = K / 8;
@@ -416,7 +421,15 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p, B
 #pragma unroll
     for (int t = 0; t < RUN; ++t) {
       const int tt = part * RUN + t;
-      const float x = p.g[rowc(tt) * K + d];
+      float x;
+      if constexpr (HD) {
+        // Width 1 (or no forget gate: a valid row read and dropped, with no
+        // branch around the load).
+        x = (p.gated ? p.g : p.erase)[rowc(tt)];
+        if (!p.gated) x = 0.f;
+      } else {
+        x = p.g[rowc(tt) * K + d];
+      }
       vals[t] = tt < valid ? x : 0.f;
     }
   }
@@ -462,7 +475,7 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p, B
       float ak[8], aq[8], kg[8], qg[8];
 #pragma unroll
       for (int x = 0; x < 8; ++x) {
-        const float rf = __expf(fminf(gi[x] - gr[x], kMaxExp));
+        const float rf = HD ? 1.f : __expf(fminf(gi[x] - gr[x], kMaxExp));
         const float eg = __expf(gi[x]);
         const float ke = kf[x] * ef[rb][x], qs = qf[x] * p.scale;
         ak[x] = ke * rf;
@@ -549,7 +562,8 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p, B
           *reinterpret_cast<float4*>(gr + 4) = *reinterpret_cast<const float4*>(&Gc[r * GP + d0 + 4]);
           float c[8];
 #pragma unroll
-          for (int x = 0; x < 8; ++x) c[x] = kf[x] * __expf(fminf(gr[x] - gj[x], kMaxExp));
+          for (int x = 0; x < 8; ++x)
+            c[x] = HD ? kf[x] : kf[x] * __expf(fminf(gr[x] - gj[x], kMaxExp));
           uint4 bh, bl;
           bh.x = pk_bf16(c[0], c[1]);
           bh.y = pk_bf16(c[2], c[3]);
@@ -564,8 +578,19 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p, B
           const bf16x8 a_h = ld8(&RT[0][at]);
           acck = mfma16(a_h, b_h, acck);
           acck = mfma16(ld8(&RT[1][at]), b_h, acck);
-          acck = mfma16(a_h, b_l, acck);
+          if constexpr (!HD) acck = mfma16(a_h, b_l, acck);  // HD: K is exact in bf16
           accq = mfma16(ld8(&RT[2][at]), b_h, accq);
+        }
+        if constexpr (HD) {
+          // The head mask e^{Gᵢ−Gⱼ} (≤ 1 where kept; clamped at 0 above the
+          // diagonal, which the masks below drop).
+          const float gjv = Gc[j * GP];
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const float dm = __expf(fminf(Gc[(16 * rb + 4 * q4 + rr) * GP] - gjv, 0.f));
+            acck[rr] *= dm;
+            accq[rr] *= dm;
+          }
         }
         uint32_t av[4];
 #pragma unroll
@@ -1078,6 +1103,10 @@ size_t region(size_t bytes) { return align_up(bytes, 256); }
 
 // Per-key-channel decay (GDN-2): the block-decay scores and the kg/qg tiles.
 bool per_channel(const Dims& d) { return d.dw == d.K && d.K > 1; }
+// The per-channel kernels: a per-key-channel forget gate, or a per-channel
+// erase or write gate beside a per-head (or no) forget gate, which they serve
+// with the head mask (mfma_intra_pc_kernel's HD).
+bool pc_path(const Dims& d) { return per_channel(d) || d.ew > 1 || d.ww > 1; }
 
 MfmaParams make_params(const Dims& d, const void* q, const void* k, const void* v,
                        const float* erase, const float* write, const float* g,
@@ -1122,7 +1151,7 @@ MfmaParams make_params(const Dims& d, const void* q, const void* k, const void* 
   base += region(size_t(d.V) * 4);
   p.Kg = p.Kglo = p.Qg = nullptr;
   p.egl = nullptr;
-  if (per_channel(d)) {
+  if (pc_path(d)) {
     p.Kg = reinterpret_cast<uint16_t*>(base);
     base += region(G * kL * size_t(d.K) * 2);
     p.Kglo = reinterpret_cast<uint16_t*>(base);
@@ -1139,7 +1168,7 @@ size_t tiles_workspace(const Dims& d) {
   const size_t G = size_t(d.B) * d.N * d.H;
   size_t bytes = 3 * region(G * kL * kL * 2) + region(G * kL * 4) +
                  region(G * size_t(d.K) * kL * 2) + region(size_t(d.V) * 4);
-  if (per_channel(d)) bytes += 3 * region(G * kL * size_t(d.K) * 2) + region(G * size_t(d.K) * 4);
+  if (pc_path(d)) bytes += 3 * region(G * kL * size_t(d.K) * 2) + region(G * size_t(d.K) * 4);
   return bytes;
 }
 
@@ -1168,11 +1197,18 @@ BwdTiles carve_bwd_tiles(const Dims& d, void* ws) {
 hipError_t launch_intra(const MfmaParams& p, const Dims& d, hipStream_t stream,
                         const BwdTiles* bt = nullptr) {
   const size_t G = size_t(d.B) * d.N * d.H;
-  if (per_channel(d)) {
+  if (pc_path(d)) {
     ProfScope ps(bt ? "dn_mfma_intra_pc_bwd" : "dn_mfma_intra_pc", stream);
-#define DN_IPC(KD, BTV, EW)                                                                     \
-  hipLaunchKernelGGL((mfma_intra_pc_kernel<KD, BTV, EW>), dim3(unsigned(G)), dim3(kThreads), 0, \
-                     stream, p, bt ? *bt : BwdTiles{})
+    const bool hd = !per_channel(d);
+#define DN_IPC(KD, BTV, EW)                                                                        \
+  do {                                                                                           \
+    if (hd)                                                                                      \
+      hipLaunchKernelGGL((mfma_intra_pc_kernel<KD, BTV, EW, true>), dim3(unsigned(G)),           \
+                         dim3(kThreads), 0, stream, p, bt ? *bt : BwdTiles{});                   \
+    else                                                                                         \
+      hipLaunchKernelGGL((mfma_intra_pc_kernel<KD, BTV, EW>), dim3(unsigned(G)), dim3(kThreads), \
+                         0, stream, p, bt ? *bt : BwdTiles{});                                   \
+  } while (0)
 #define DN_IPC_E(KD, BTV)                         \
   do {                                            \
     if (d.ew == 1) DN_IPC(KD, BTV, true);         \
@@ -1267,7 +1303,7 @@ Dims seg_dims(const Dims& d, int P) {
 
 template <bool ST>
 hipError_t launch_scan(const MfmaParams& p, const Dims& d, bool yb, hipStream_t stream) {
-  const bool pc = per_channel(d);
+  const bool pc = pc_path(d);
   if constexpr (!ST) {
     if (p.seg) {
       // The segmented scans: 8-wave workgroups, head_k_dim 128.
@@ -1347,7 +1383,7 @@ NormLaunch norm_launch(const Dims& d, bool seg, bool yb, bool gated) {
   l.waves = seg ? 8 : scan_waves(d);
   l.ntile = d.V / (16 * l.waves);
   l.blocks = unsigned(((d.B * d.H + 7) / 8) * 8 * l.ntile);
-  l.fn = norm_scan_fn(d.K, per_channel(d), seg, yb, l.waves, gated);
+  l.fn = norm_scan_fn(d.K, pc_path(d), seg, yb, l.waves, gated);
   return l;
 }
 
@@ -1374,7 +1410,7 @@ hipError_t launch_scan_norm(const MfmaParams& p, const Dims& d, bool yb, hipStre
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  ProfScope ps(per_channel(d) ? "dn_mfma_scan_pc_norm" : "dn_mfma_scan_norm", stream);
+  ProfScope ps(pc_path(d) ? "dn_mfma_scan_pc_norm" : "dn_mfma_scan_norm", stream);
   void* args[] = {&q};
   if (l.ntile == 1) return hipLaunchKernel(l.fn, dim3(l.blocks), dim3(64 * l.waves), args, 0, stream);
   return hipLaunchCooperativeKernel(l.fn, dim3(l.blocks), dim3(64 * l.waves), args, 0, stream);
@@ -1387,8 +1423,16 @@ bool mfma_fwd_supported(const Dims& d, int qkv_dtype, int y_dtype) {
   if (!(qkv_dtype == DN_BF16 && (d.K == 64 || d.K == 128) && d.V % kBV == 0 && d.L == kL))
     return false;
   if (!token_rows_fit_32bit(d)) return false;
-  if (per_channel(d)) return (d.ew == 1 || d.ew == d.K) && (d.ww == 1 || d.ww == d.V);
+  if (pc_path(d)) return (d.ew == 1 || d.ew == d.K) && (d.ww == 1 || d.ww == d.V);
   return d.ew == 1 && d.ww == 1 && d.dw <= 1;
+}
+
+// The MFMA backward: its chunk-local kernel and scans know the per-head
+// gates and the all-per-channel ones (GDN-2); per-channel erase or write
+// gates beside a per-head forget gate take the generic kernels.
+bool mfma_bwd_supported(const Dims& d, int qkv_dtype) {
+  return mfma_fwd_supported(d, qkv_dtype, DN_BF16) &&
+         (per_channel(d) || (d.ew == 1 && d.ww == 1));
 }
 
 size_t mfma_fwd_workspace(const Dims& d, bool fused) {

@@ -111,6 +111,7 @@ hipError_t generic_bwd(const Dims& d, int qkv_dtype, int grad_dtype, const void*
                        void* mfma_ws = nullptr);
 
 bool mfma_fwd_supported(const Dims& d, int qkv_dtype, int y_dtype);
+bool mfma_bwd_supported(const Dims& d, int qkv_dtype);
 // The MFMA forward: the intra kernel and the scan as two launches with their
 // tiles in the workspace, or with `fused` (where fused_fwd_supported holds)
 // the one kernel of chunk_fwd_fused.hip.

@@ -250,6 +250,24 @@ def test_chunk_fwd_out_norm_workspace_covers_the_forward():
     assert ws >= fwd_ws + 8 * 16 * (256 // 32) * 4 * 64 * 8
 
 
+def test_channel_write_gates_with_a_head_decay_take_mfma_forward_generic_backward():
+    """erase [.., dk] and/or write [.., dv] beside a per-head (or no) forget
+    gate: the MFMA forward (per-channel kernels, head mask), the generic
+    backward. No pointer is read."""
+    lib = abi.lib()
+    base = dict(batch=2, sequence=1000, nheads=4, head_k_dim=128, head_v_dim=128,
+                qkv_dtype=abi.DN_BF16, y_dtype=abi.DN_BF16)
+    for ew, ww, dw, gated in ((128, 128, 1, 1), (128, 1, 1, 1), (1, 128, 1, 1),
+                              (128, 128, 0, 0)):
+        over = dict(erase_width=ew, write_width=ww, decay_width=dw, has_gate=gated)
+        a = fwd_args(**base, **over)
+        assert lib.dn_chunk_fwd_algo(ctypes.byref(a)) == abi.DN_ALGO_MFMA, over
+        b = bwd_args(head_v_dim=128, **over)
+        assert lib.dn_chunk_bwd_algo(ctypes.byref(b)) == abi.DN_ALGO_GENERIC, over
+        b.algo = abi.DN_ALGO_MFMA
+        assert lib.dn_chunk_bwd_algo(ctypes.byref(b)) == -9, over
+
+
 def test_mfma_paths_refuse_rows_past_32_bit_offsets():
     """The MFMA kernels address a chunk's 64 token rows with 32-bit byte
     offsets (4-byte y included): nheads·max(dk, dv) must stay below 2^23.

@@ -224,6 +224,51 @@ def test_mfma_fwd_channel_gates_match_oracle(rng, case):
     assert ey < TOL and es < TOL
 
 
+HD_CASES = [
+    # B, S, H, K, V, ew, ww, forget gate ("head" | None), g scale: per-channel
+    # erase or write gates beside a per-head (or no) forget gate, on the
+    # per-channel kernels with the head mask
+    (1, 256, 2, 128, 128, 128, 128, "head", 0.05),
+    (2, 200, 2, 128, 256, 128, 1, "head", 0.05),
+    (1, 130, 2, 64, 64, 1, 64, "head", 0.05),
+    (1, 192, 2, 128, 128, 128, 128, None, 0.0),
+    # decay of ~8 nats per token: the block decay's clamp would bind here, the
+    # head mask is exact (the reference runs head_decay_mask for these widths)
+    (1, 128, 2, 128, 64, 128, 64, "head", 8.0),
+]
+
+
+@pytest.mark.parametrize("case", HD_CASES)
+def test_mfma_fwd_channel_write_gates_head_decay(rng, case):
+    """WriteGate::Channel blocks (erase [.., dk], write [.., dv]) with a
+    per-head forget gate: AUTO runs MFMA, against the oracle."""
+    B, S, H, K, V, ew, ww, decay, gs = case
+    announce(f"mfma fwd channel gates, head decay {case}")
+    q = l2(rng.standard_normal((B, S, H, K)))
+    k = l2(rng.standard_normal((B, S, H, K)))
+    v = rng.standard_normal((B, S, H, V))
+    e = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, S, H, ew))))
+    w = 1.0 / (1.0 + np.exp(-rng.standard_normal((B, S, H, ww))))
+    g = None
+    if decay == "head":
+        g = (-np.log1p(np.exp(rng.standard_normal((B, S, H, 1)))) * gs if gs < 1
+             else np.full((B, S, H, 1), -gs))
+    s0 = rng.normal(0.0, 0.02, (B, H, K, V))
+    g_args = to_gpu([q, k, v, e, w, g, s0], torch.bfloat16)
+    y, s = run_mfma(g_args)
+    y0, s0r = O.chunk_fwd(*as_oracle_inputs(g_args), chunk_len=64, dtype=np.float64)
+    ey, es = rel_err(y, y0), rel_err(s, s0r)
+    print(f"  rel err y {ey:.2e} state {es:.2e}", flush=True)
+    assert ey < TOL and es < TOL
+    # The backward for these widths runs the generic kernels under AUTO.
+    qq, kk, vv, ee, ww_, gg, ss = g_args
+    grads = tuple(torch.empty_like(x) if x is not None else None
+                  for x in (qq, kk, vv, ee, ww_, gg, ss))
+    a = pkg.abi.chunk_bwd_args(torch.zeros((B, S, H, V), device=DEV), None, qq, kk, vv, ee, ww_,
+                               gg, ss, grads, 64, None)
+    assert pkg.abi.lib().dn_chunk_bwd_algo(a) == pkg.abi.DN_ALGO_GENERIC
+
+
 def test_mfma_channel_gates_constant_keys(rng):
     """Constant keys with β up to 1.8 per channel: the cancelling retrieval
     and the WY inverse stay within the bar (kg and S carry lo parts)."""
