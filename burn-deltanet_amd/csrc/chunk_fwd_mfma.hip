@@ -7,8 +7,8 @@
 //
 // Two kernels on v_mfma_f32_16x16x32_bf16 (64-lane waves):
 //
-// intra  chunk-heads (b, n, h) are fully parallel; two resident workgroups
-//        per CU walk them, prefetching the next chunk's K/Q/gates into
+// intra  chunk-heads (b, n, h) are fully parallel; the resident workgroups
+//        (two per CU) walk them, prefetching the next chunk's K/Q/gates into
 //        registers. K·Kᵀ and Q·Kᵀ (the ten lower 16×16 block pairs) run on
 //        MFMA with the per-head decay e^{Gᵢ−Gⱼ}, the erase gate and the
 //        readout scale applied to the fp32 accumulators; T = (I + tril(Akk,
@@ -16,24 +16,27 @@
 //        diagonal blocks by column elimination, then two doubling merges
 //        T₂₁ = −T₂₂ A₂₁ T₁₁ on fp32 MFMA) — the reference's ladder
 //        (tri/prim.rs:28-51) at L³/3 instead of 24·L³ flops. Writes T as bf16
-//        hi + lo parts, attn = tril(Aqk) and Kcᵀ = (e^{G_last−G}⊙K)ᵀ as bf16,
-//        and the in-chunk cumulative gate G as fp32.
+//        hi + lo parts, attn = tril(Aqk) as bf16 and the in-chunk cumulative
+//        gate G as fp32.
 //
 // scan   one workgroup per (b, h, block of 16·W value columns), serial over
 //        chunks; each of its W waves owns 16 value columns and all K state
 //        rows, in fp32 MFMA accumulators for the whole sequence. A chunk's
-//        operand tiles (K, Q, T hi/lo, attn, Kcᵀ) are staged once in LDS
+//        operand tiles (K, Q, T hi/lo, attn) are staged once in LDS
 //        (double-buffered: one barrier per chunk); everything that depends on
 //        the state stays in the wave. Per chunk, with U − W S = T (w⊙V −
 //        e⊙e^G⊙(K S)) so that neither U nor W is ever formed:
 //          X  = w⊙V − (e⊙e^G)⊙(K·S)                 S as bf16 hi + lo parts
 //          yᵀ = (scale·e^G)⊙(Sᵀ·Qᵀ)                 same S fragments
 //          V' = T·X                                 hi + lo parts of T and X
-//          yᵀ += V'ᵀ·attnᵀ;  S ← e^{G_last}⊙S + Kcᵀ·V'   one V' fragment
+//          yᵀ += V'ᵀ·attnᵀ;  S ← e^{G_last}⊙S + Kᵀ·(e^{G_last−G}⊙V')
+//        (Kᵀ's fragments through the LDS transpose read of the K tile).
 //        The contraction index of the staged tiles is permuted inside each
 //        32-deep k-step so accumulator tiles serve as MFMA operands in place.
 
 #include <algorithm>
+#include <map>
+#include <mutex>
 
 #include "dn_common.hpp"
 #include "mfma_scan.hpp"
@@ -232,14 +235,12 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
 
     diag_inverse(A, Tm, wave, lane);
     {
-      // Kcᵀ = (e^{G_last−G} ⊙ K)ᵀ for the scan's state update, while the K
-      // tile is in LDS.
-      const float glast = gcs[kL - 1];
-      auto kcs = [&](int t) { return GATED ? __expf(glast - gcs[t]) : 1.f; };
-      scaled_t(Ks, p.KcT + size_t(cid) * K * kL, kcs);
+      // The backward's Kgᵀ = (e⊙e^G⊙K)ᵀ, Kc = e^{G_last−G}⊙K row-major and
+      // e^{G_last} per key channel, while the K tile is in LDS. (The scan
+      // reads Kᵀ from its own K tile.)
       if constexpr (BT) {
-        // Kgᵀ = (e⊙e^G⊙K)ᵀ, Kc = e^{G_last−G}⊙K row-major (the same products
-        // as Kcᵀ) and e^{G_last} per key channel.
+        const float glast = gcs[kL - 1];
+        auto kcs = [&](int t) { return GATED ? __expf(glast - gcs[t]) : 1.f; };
         scaled_t(Ks, bt.KgT + size_t(cid) * K * kL,
                  [&](int t) { return ers[t] * (GATED ? __expf(gcs[t]) : 1.f); });
         for (int idx = tid; idx < kL * KS8; idx += kThreads) {
@@ -1145,8 +1146,13 @@ MfmaParams make_params(const Dims& d, const void* q, const void* k, const void* 
   base += region(G * kL * kL * 2);
   p.gc = reinterpret_cast<float*>(base);
   base += region(G * kL * 4);
-  p.KcT = reinterpret_cast<uint16_t*>(base);
-  base += region(G * size_t(d.K) * kL * 2);
+  // Kcᵀ: per-channel gates only (with per-head gates the scan forms it from
+  // the K tile).
+  p.KcT = nullptr;
+  if (pc_path(d)) {
+    p.KcT = reinterpret_cast<uint16_t*>(base);
+    base += region(G * size_t(d.K) * kL * 2);
+  }
   p.sink = reinterpret_cast<uint16_t*>(base);
   base += region(size_t(d.V) * 4);
   p.Kg = p.Kglo = p.Qg = nullptr;
@@ -1166,9 +1172,10 @@ MfmaParams make_params(const Dims& d, const void* q, const void* k, const void* 
 // The two-kernel forward's tiles (make_params' layout).
 size_t tiles_workspace(const Dims& d) {
   const size_t G = size_t(d.B) * d.N * d.H;
-  size_t bytes = 3 * region(G * kL * kL * 2) + region(G * kL * 4) +
-                 region(G * size_t(d.K) * kL * 2) + region(size_t(d.V) * 4);
-  if (pc_path(d)) bytes += 3 * region(G * kL * size_t(d.K) * 2) + region(G * size_t(d.K) * 4);
+  size_t bytes = 3 * region(G * kL * kL * 2) + region(G * kL * 4) + region(size_t(d.V) * 4);
+  if (pc_path(d))
+    bytes += region(G * size_t(d.K) * kL * 2) + 3 * region(G * kL * size_t(d.K) * 2) +
+             region(G * size_t(d.K) * 4);
   return bytes;
 }
 
@@ -1194,6 +1201,23 @@ BwdTiles carve_bwd_tiles(const Dims& d, void* ws) {
 }
 
 // bt (per-channel gates only): also write the backward's transposed tiles.
+// Workgroups of `threads` threads of kernel `fn` resident on one CU at once
+// (at least 1), cached per device and kernel.
+int resident_per_cu(const void* fn, int threads) {
+  static std::mutex mu;
+  static std::map<std::pair<int, const void*>, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 1;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = cache.find({dev, fn});
+  if (it != cache.end()) return it->second;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, threads, 0) != hipSuccess || n < 1)
+    n = 1;
+  cache[{dev, fn}] = n;
+  return n;
+}
+
 hipError_t launch_intra(const MfmaParams& p, const Dims& d, hipStream_t stream,
                         const BwdTiles* bt = nullptr) {
   const size_t G = size_t(d.B) * d.N * d.H;
@@ -1222,12 +1246,17 @@ hipError_t launch_intra(const MfmaParams& p, const Dims& d, hipStream_t stream,
 #undef DN_IPC_E
 #undef DN_IPC
   } else {
-    // Two resident workgroups per CU (LDS-bound) walk all chunk-heads.
-    const int grid = int(std::min<size_t>(G, size_t(2) * device_cu_count()));
+    // As many workgroups as are resident at once walk all chunk-heads: a
+    // workgroup that had to wait for a slot would double the tail.
     ProfScope ps(bt ? "dn_mfma_intra_bwd" : "dn_mfma_intra", stream);
 #define DN_INTRA(KD, GT, BTV)                                                                    \
-  hipLaunchKernelGGL((mfma_intra_kernel<KD, GT, BTV>), dim3(unsigned(grid)), dim3(kThreads), 0, \
-                     stream, p, int(G), bt ? *bt : BwdTiles{})
+  do {                                                                                           \
+    const void* fn = reinterpret_cast<const void*>(&mfma_intra_kernel<KD, GT, BTV>);             \
+    const int grid = int(std::min<size_t>(G, size_t(resident_per_cu(fn, kThreads)) *             \
+                                                 device_cu_count()));                            \
+    hipLaunchKernelGGL((mfma_intra_kernel<KD, GT, BTV>), dim3(unsigned(grid)), dim3(kThreads),   \
+                       0, stream, p, int(G), bt ? *bt : BwdTiles{});                             \
+  } while (0)
 #define DN_INTRA_G(KD, BTV)                              \
   do {                                                   \
     if (p.gated) DN_INTRA(KD, true, BTV);                \

@@ -103,19 +103,26 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   constexpr int NT = 64 * WAVES;
   constexpr int BW = 16 * WAVES;  // value columns per workgroup
   // One chunk's operand tiles (bf16 elements): K, Q [64][K] (per-channel
-  // gates: kg hi, qg and kg lo instead); T, Tlo, attn [64][64]; Kcᵀ [K][64].
+  // gates: kg hi, qg and kg lo instead); T, Tlo, attn [64][64]; per-channel
+  // gates only: Kcᵀ [K][64]. With per-head gates the state update reads Kᵀ
+  // from the K tile through the LDS transpose read and puts the factor
+  // e^{G_last−G} on V' (Kcᵀ·V' = Kᵀ·(e^{G_last−G}⊙V')), which saves Kcᵀ's
+  // round trip through HBM.
   // Double-buffered for per-head gates: the next chunk is staged while this
   // one is consumed, so one barrier per chunk suffices. The per-channel
   // tiles do not fit twice in LDS: they are staged between two barriers.
   constexpr int NKQ = PC ? 3 : 2;  // K-wide tiles
   constexpr int oK = 0, oQ = oK + kL * K, oKl = oQ + kL * K, oT = NKQ * kL * K,
-                oTl = oT + kL * kL, oAt = oTl + kL * kL, oKc = oAt + kL * kL, BUF = oKc + K * kL;
+                oTl = oT + kL * kL, oAt = oTl + kL * kL, oKc = oAt + kL * kL,
+                BUF = oKc + (PC ? K * kL : 0);
   constexpr int C16 = BUF / 8;    // 16-byte chunks per chunk's tiles
   static_assert(C16 % NT == 0, "staging assumes whole rounds");
   constexpr int NPF = C16 / NT;   // chunks staged per lane
   constexpr int NBUF = PC ? 1 : 2;
   __shared__ __attribute__((aligned(16))) uint16_t tiles[NBUF][BUF];
   __shared__ float gxe[NBUF][kL], gwr[NBUF][kL], gys[NBUF][kL], gegl[NBUF];
+  // e^{G_last−G} per token (per-head gates), rows of V' for the state update.
+  __shared__ __attribute__((aligned(16))) float gkc[PC ? 1 : NBUF][kL];
   __shared__ float gch[PC ? K : 1];  // e^{G_last} per key channel (per-channel gates)
   // NORM: per-wave partial Σy² of chunk n [n & 1][token][wave] (pitch
   // WAVES + 1), and the workgroup's sum per token [n & 1][token].
@@ -272,6 +279,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
       gxe[buf][lane] = per * eg;
       gwr[buf][lane] = pwr;
       gys[buf][lane] = p.scale * eg;
+      gkc[buf][lane] = __expf(pgl - pgc);
       if (lane == 0) gegl[buf] = __expf(pgl);
     }
   };
@@ -683,30 +691,70 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
     // Phase 3: yᵀ += V'ᵀ·attnᵀ and S ← e^{G_last}⊙S + (e^{G_last−G}⊙K)ᵀ·V';
     // the bf16 V' fragment is the A operand of the first and the B operand
     // of the second.
-    uint4 vf[2];
+    uint4 vf[2], vc[2];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) vf[kk] = frag_hi(Vp[2 * kk], Vp[2 * kk + 1]);
+    if constexpr (!PC) {
+      // e^{G_last−G}⊙V': lane (r16, q4) holds rows 16tb + 4q4 … +3 of Vp[tb].
+#pragma unroll
+      for (int tb = 0; tb < 4; ++tb) {
+        const float4 c = *reinterpret_cast<const float4*>(&gkc[cur][16 * tb + 4 * q4]);
+        Vp[tb][0] *= c.x;
+        Vp[tb][1] *= c.y;
+        Vp[tb][2] *= c.z;
+        Vp[tb][3] *= c.w;
+      }
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) vc[kk] = frag_hi(Vp[2 * kk], Vp[2 * kk + 1]);
+    }
     {
-      // The six nonzero steps of the lower-triangular attn, then 2·RBK Kcᵀ
-      // steps, reads one step ahead.
+      // The six nonzero steps of the lower-triangular attn, then 2·RBK state
+      // update steps, reads one step ahead.
       constexpr int NA = kTriSteps, NS = NA + 2 * RBK;
       auto addr = [&](int st) {
         return st < NA ? oAt + tile_at<kL>(16 * tril_tb(st) + r16, 32 * tril_kk(st) + k8)
                        : oKc + tile_at<kL>(16 * ((st - NA) >> 1) + r16, 32 * ((st - NA) & 1) + k8);
       };
+      // Kᵀ's fragment of state rows 16rb … +15 and k-step kk (tokens 32kk …
+      // +31 in the permuted order) from the K tile: ds_read_b64_tr_b16 gives
+      // lane i of each 16-lane group element i of the 4×4 block that lanes
+      // 4j … 4j+3 of the group supply (lane 4j + m: 4 consecutive
+      // elements), as its element j. Lane (r16, q4) supplies channels
+      // 16rb + 4(r16 & 3) … +3 of token 32kk + 4q4 + (r16 >> 2), and of the
+      // token 16 further for the second half, so lane (r16, q4) receives
+      // channel 16rb + r16 of tokens 32kk + 4q4 … +3 and 32kk + 16 + 4q4 … +3:
+      // operand positions 8q4 … 8q4+7 of the permuted order.
+      auto kt_frag = [&](int rb, int kk) {
+        const int t = 32 * kk + 4 * q4 + (r16 >> 2);
+        const int pos = 32 * (rb >> 1) + 8 * (r16 & 3) + 4 * (rb & 1);
+        typedef short v4s __attribute__((ext_vector_type(4)));
+        typedef __attribute__((address_space(3))) v4s lds_v4s;
+        const v4s a = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4s*)(&tl[oK + tile_at<K>(t, pos)]));
+        const v4s b = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4s*)(&tl[oK + tile_at<K>(t + 16, pos)]));
+        const uint2 ua = __builtin_bit_cast(uint2, a), ub = __builtin_bit_cast(uint2, b);
+        return __builtin_bit_cast(bf16x8, make_uint4(ua.x, ua.y, ub.x, ub.y));
+      };
+      auto frag = [&](int st) {
+        if constexpr (!PC)
+          if (st >= NA) return kt_frag((st - NA) >> 1, (st - NA) & 1);
+        return ld8(&tl[addr(st)]);
+      };
       bf16x8 fr[2];
-      fr[0] = ld8(&tl[addr(0)]);
+      fr[0] = frag(0);
 #pragma unroll
       for (int rb = 0; rb < RBK; ++rb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) S[rb][r] *= PC ? gch[16 * rb + 4 * q4 + r] : egl;
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
-        if (st + 1 < NS) fr[(st + 1) & 1] = ld8(&tl[addr(st + 1)]);
+        if (st + 1 < NS) fr[(st + 1) & 1] = frag(st + 1);
         if (st < NA)
           yt[tril_tb(st)] = mfma16(as8(vf[tril_kk(st)]), fr[st & 1], yt[tril_tb(st)]);
         else
-          S[(st - NA) >> 1] = mfma16(fr[st & 1], as8(vf[(st - NA) & 1]), S[(st - NA) >> 1]);
+          S[(st - NA) >> 1] =
+              mfma16(fr[st & 1], as8(PC ? vf[(st - NA) & 1] : vc[(st - NA) & 1]), S[(st - NA) >> 1]);
       }
     }
     // The norm's loads before this chunk's y stores: the wait for them at
