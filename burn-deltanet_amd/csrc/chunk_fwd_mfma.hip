@@ -88,6 +88,9 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
   __shared__ float gcs[kL], ers[kL];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // attn goes out where p.attn is set (the forward; the backward's recompute
+  // forms it for attnᵀ only).
+  const bool attn_out = p.attn != nullptr;
   // attn's blocks above the diagonal are zero for every chunk.
   for (int idx = tid; idx < kL * kL; idx += kThreads) {
     const int i = idx / kL, j = idx % kL;
@@ -131,13 +134,15 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
     const size_t off = size_t(pend_cid) * kL * kL + row * kL + c0;
     uint4* tdst = reinterpret_cast<uint4*>(p.T + off);
     uint4* ldst = reinterpret_cast<uint4*>(p.Tlo + off);
-    uint4* adst = reinterpret_cast<uint4*>(p.attn + off);
     tdst[0] = pend[0];
     tdst[1] = pend[1];
     ldst[0] = pend[2];
     ldst[1] = pend[3];
-    adst[0] = pend[4];
-    adst[1] = pend[5];
+    if (attn_out) {
+      uint4* adst = reinterpret_cast<uint4*>(p.attn + off);
+      adst[0] = pend[4];
+      adst[1] = pend[5];
+    }
   };
 
   // dstᵀ[d][t] = bf16(X[t][d]·rowsc(t)) for a [64][K] tile X in LDS: an item
@@ -1593,6 +1598,8 @@ hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
   float* s_scratch = reinterpret_cast<float*>(reinterpret_cast<char*>(bt.egl) + region(G * K * 4));
   MfmaParams p = make_params(d, q, k, v, erase, write, g, state_in, nullptr, s_scratch, ws);
   p.states = states;
+  // The states mode reads no attn (the intra kernel still forms it for attnᵀ).
+  if (!pc_path(d)) p.attn = nullptr;
   // The intra kernel writes the reverse scan's transposed tiles too.
   hipError_t e = launch_intra(p, d, stream, &bt);
   if (e != hipSuccess) return e;

@@ -111,10 +111,14 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   // Double-buffered for per-head gates: the next chunk is staged while this
   // one is consumed, so one barrier per chunk suffices. The per-channel
   // tiles do not fit twice in LDS: they are staged between two barriers.
+  // The states mode and the transition pass write no y: they fetch no attn
+  // (per-head gates).
   constexpr int NKQ = PC ? 3 : 2;  // K-wide tiles
+  constexpr bool kYOut = !ST && SEG != 1;              // y is written
+  constexpr int NLL = PC || kYOut ? 3 : 2;             // [64][64] tiles: T, Tlo (, attn)
   constexpr int oK = 0, oQ = oK + kL * K, oKl = oQ + kL * K, oT = NKQ * kL * K,
                 oTl = oT + kL * kL, oAt = oTl + kL * kL, oKc = oAt + kL * kL,
-                BUF = oKc + (PC ? K * kL : 0);
+                BUF = NKQ * kL * K + NLL * kL * kL + (PC ? K * kL : 0);
   constexpr int C16 = BUF / 8;    // 16-byte chunks per chunk's tiles
   static_assert(C16 % NT == 0, "staging assumes whole rounds");
   constexpr int NPF = C16 / NT;   // chunks staged per lane
@@ -205,13 +209,13 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
           const uint32_t klast = uint32_t((rl - 1) * HK) + kcol;
           pf[m] = ld16((which ? p.q : p.k) + row0 * K, min(koff + rowc * uint32_t(HK), klast));
         }
-      } else if (i0 < (NKQ * kL * K + 3 * kL * kL) / 8) {
+      } else if (i0 < (NKQ * kL * K + NLL * kL * kL) / 8) {
         const int ii0 = i0 - NKQ * kL * K / 8;
         const int which = ii0 / (kL * kL / 8);
         const uint16_t* base = which == 0 ? p.T : which == 1 ? p.Tlo : p.attn;
         pf[m] = ld16(base + cid * kL * kL + 8 * (ii0 - which * (kL * kL / 8)), 8u * tid);
       } else {
-        const int e0 = i0 - (NKQ * kL * K + 3 * kL * kL) / 8;
+        const int e0 = i0 - (NKQ * kL * K + NLL * kL * kL) / 8;
         pf[m] = ld16(p.KcT + cid * K * kL + 8 * e0, 8u * tid);
       }
     }
@@ -257,14 +261,14 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
         const bool flip = K >= 128 && (dr & 8);
         b0 = base + (flip ? aK0x : aK0);
         b1 = base + (flip ? aK1x : aK1);
-      } else if (i0 < (NKQ * kL * K + 3 * kL * kL) / 8) {
+      } else if (i0 < (NKQ * kL * K + NLL * kL * kL) / 8) {
         const int ii0 = i0 - NKQ * kL * K / 8;
         const int which = ii0 / (kL * kL / 8), dr = (ii0 - which * (kL * kL / 8)) / LC8;
         const int base = (which == 0 ? oT : which == 1 ? oTl : oAt) + dr * kL;
         b0 = base + a60;
         b1 = base + a61;
       } else {
-        const int dr = (i0 - (NKQ * kL * K + 3 * kL * kL) / 8) / LC8;
+        const int dr = (i0 - (NKQ * kL * K + NLL * kL * kL) / 8) / LC8;
         b0 = oKc + dr * kL + a60;
         b1 = oKc + dr * kL + a61;
       }
@@ -708,9 +712,9 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
       for (int kk = 0; kk < 2; ++kk) vc[kk] = frag_hi(Vp[2 * kk], Vp[2 * kk + 1]);
     }
     {
-      // The six nonzero steps of the lower-triangular attn, then 2·RBK state
-      // update steps, reads one step ahead.
-      constexpr int NA = kTriSteps, NS = NA + 2 * RBK;
+      // The six nonzero steps of the lower-triangular attn (when y is
+      // written), then 2·RBK state update steps, reads one step ahead.
+      constexpr int NA = kYOut ? kTriSteps : 0, NS = NA + 2 * RBK;
       auto addr = [&](int st) {
         return st < NA ? oAt + tile_at<kL>(16 * tril_tb(st) + r16, 32 * tril_kk(st) + k8)
                        : oKc + tile_at<kL>(16 * ((st - NA) >> 1) + r16, 32 * ((st - NA) & 1) + k8);
