@@ -93,12 +93,12 @@ def bench_chunk_fwd(torch, pkg, steps, warmup, algo):
     st = B * H * K * V * 4              # one fp32 state
     tri = 3 * G * L * L * 2             # T (hi, lo) and attn, bf16
     gcb = G * L * 4                     # in-chunk cumulative gate, fp32
-    kct = G * K * L * 2                 # (e^{G_last-G} k)^T, bf16
     # The bytes each kernel moves by its own design (intermediates included),
-    # beside the path's algorithmic bytes.
+    # beside the path's algorithmic bytes. (The scan forms (e^{G_last-G} k)^T
+    # from its own K tile, so it does not go through HBM.)
     kernel_bytes = {
-        "dn_mfma_intra": qk + gates + tri + gcb + kct,
-        "dn_mfma_scan": qk + vb + yb + gates + tri + gcb + kct + 2 * st,
+        "dn_mfma_intra": qk + gates + tri + gcb,
+        "dn_mfma_scan": qk + vb + yb + gates + tri + gcb + 2 * st,
         "dn_mfma_fused": qk + vb + yb + gates + 2 * st,
     }
     flops_unit = 6 * L * L * K + 4 * L * L * V + 6 * L * K * V + L ** 3 / 3
