@@ -298,7 +298,7 @@ bool mfma_aligned(const void* q, const void* k, const void* v) {
 
 // The forward's kernels: DN_ALGO_GENERIC, DN_ALGO_MFMA (intra + scan) or,
 // on request only, DN_ALGO_MFMA_FUSED (one kernel; at BASELINE config 2 on
-// a warm MI355X 0.47-0.49 ms against the two kernels' 0.43-0.45 ms).
+// a warm MI355X 0.47 ms against the two kernels' 0.38-0.39 ms).
 int fwd_algo(const dn_chunk_fwd_args* a, const Dims& d0) {
   if (a->algo == DN_ALGO_GENERIC) return DN_ALGO_GENERIC;
   const Dims d = mfma_dims(d0);

@@ -72,7 +72,7 @@ typedef enum {
   DN_ALGO_MFMA_FUSED = 3, /* the MFMA forward as one kernel that builds each chunk's WY
                              tiles in LDS beside the scan: q/k/v read once, no tile
                              traffic, a 1 KB workspace instead of the two-kernel path's
-                             tiles (338 MB at BASELINE config 2), about 7% slower there.
+                             tiles (203 MB at BASELINE config 2), about 20% slower there.
                              Per-head gates, head_k_dim 128, head_v_dim a multiple of 128,
                              bf16 q/k/v; DN_ERR_UNSUPPORTED otherwise. Never chosen by AUTO;
                              the backward treats it as DN_ALGO_MFMA. */
@@ -299,8 +299,8 @@ int dn_out_norm(const dn_out_norm_args *args, hipStream_t stream);
  * in_scan = 1 applies the norm in the MFMA scan's output write, so y makes no
  * round trip through HBM, where the MFMA path runs (AUTO or DN_ALGO_MFMA)
  * and the gate, if any, has y's dtype. The separate pass is the faster of
- * the two at every shape measured on MI355X (0.59 against
- * 0.65 ms): the scan is latency-bound, and the norm's work inside its chunk
+ * the two at every shape measured on MI355X (0.53 against
+ * 0.60 ms): the scan is latency-bound, and the norm's work inside its chunk
  * loop lengthens it more than the pass costs. In the scan, a head's columns
  * may span several workgroups, which then exchange per-token sums of squares
  * during the kernel; that launch is cooperative (the grid must be resident
@@ -426,8 +426,9 @@ size_t dn_chunk_bwd_workspace_bytes(const dn_chunk_bwd_args *args);
  * hipFree or other allocating routine. Limits:
  *   - arguments whose dn_chunk_fwd_workspace_bytes() exceeds
  *     DN_NOALLOC_SCRATCH_BYTES return DN_ERR_WORKSPACE (the MFMA path needs
- *     40.25 KiB per (batch, head, chunk of 64 tokens) at head_k_dim 128, so
- *     64 MiB covers 1628 of them, e.g. batch 1 x 16 heads x 6500 tokens);
+ *     24.25 KiB per (batch, head, chunk of 64 tokens) with per-head gates,
+ *     so 64 MiB covers 2700 of them, e.g. batch 1 x 16 heads x 10,700
+ *     tokens);
  *   - check_finite is refused (DN_ERR_UNSUPPORTED): the guard allocates its
  *     flag and synchronises;
  *   - every call on one device shares that device's array, so calls that
