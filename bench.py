@@ -569,10 +569,13 @@ def bench_chunk_lengths(torch, pkg, steps, warmup):
 
 def bench_block_forward(torch, pkg, steps, warmup):
     """A Gated DeltaNet block's forward after in_proj at the config-2 shape
-    (B=8, T=4096, H=16, dk=128, dv=256): dn_frontend (short conv of 4 with
-    SiLU, L2 q/k norm, scalar β), dn_chunk_fwd (with a synthetic decay of
-    config 2's distribution) and dn_out_norm (gated, bf16), as one step of
-    three calls, against the sum of the three timed one by one."""
+    (B=8, T=4096, H=16, dk=128, dv=256): the front-end (short conv of 4 with
+    SiLU, L2 q/k norm, scalar β), the chunk forward (with a synthetic decay
+    of config 2's distribution) and the gated output norm (bf16). The step is
+    dn_frontend_chunk_fwd (the front-end's q/k formed in the chunk forward's
+    load stage) then dn_out_norm; beside it the same block as three calls
+    (dn_frontend, dn_chunk_fwd, dn_out_norm), each of them timed alone, and
+    the core and the norm as one call (dn_chunk_fwd_out_norm)."""
     B, S, H, K, V, KC = 8, 4096, 16, 128, 256, 4
     dev = torch.device("cuda:0")
     gen = torch.Generator(device=dev)
@@ -610,8 +613,20 @@ def bench_block_forward(torch, pkg, steps, warmup):
     def block():
         for f in calls.values():
             f()
-    ms, kern = _timed(torch, abi, block, steps, warmup)
+    ms3, kern3 = _timed(torch, abi, block, steps, warmup)
     parts = {n: round(_timed(torch, abi, f, steps, warmup)[0], 4) for n, f in calls.items()}
+    # The front-end's q/k in the chunk forward's load stage, then the norm.
+    fca = abi.frontend_chunk_fwd_args(fe, ca)
+    fcws = torch.empty(max(abi.lib().dn_frontend_chunk_fwd_workspace_bytes(fca), 1),
+                       dtype=torch.uint8, device=dev)
+    fca.fwd.workspace, fca.fwd.workspace_bytes = fcws.data_ptr(), fcws.numel()
+    ona = abi.out_norm_args(y, z, gamma, out, 1e-5)
+
+    def block_fe():
+        abi.run_frontend_chunk_fwd(fca)
+        abi.run_out_norm(ona)
+    ms, kern = _timed(torch, abi, block_fe, steps, warmup)
+    fe_core_ms = _timed(torch, abi, lambda: abi.run_frontend_chunk_fwd(fca), steps, warmup)[0]
     # The same block with the norm in the scan's output write
     # (dn_chunk_fwd_out_norm: y never round-trips through HBM).
     # The core and the norm as one call (dn_chunk_fwd_out_norm), the norm as
@@ -635,10 +650,15 @@ def bench_block_forward(torch, pkg, steps, warmup):
     cs_ms, cs_kern = _timed(torch, abi, core_norm_in_scan, steps, warmup)
     give_ups = abi.wait_give_ups()
     return {"workload": "Gated DeltaNet block forward after in_proj at the config-2 shape: "
-                        "dn_frontend + dn_chunk_fwd + dn_out_norm, bf16",
+                        "dn_frontend_chunk_fwd (front-end q/k in the load stage) + "
+                        "dn_out_norm, bf16",
             "ms_per_step": round(ms, 4), "tokens_per_s": round(B * S / (ms / 1e3), 1),
-            "separate_ms": parts, "sum_of_separate_ms": round(sum(parts.values()), 4),
             "kernels": kern,
+            "frontend_chunk_fwd_ms": round(fe_core_ms, 4),
+            "frontend_plus_core_ms": round(parts["frontend"] + parts["core"], 4),
+            "three_calls": {"calls": "dn_frontend + dn_chunk_fwd + dn_out_norm",
+                            "ms_per_step": round(ms3, 4), "kernels": kern3},
+            "separate_ms": parts, "sum_of_separate_ms": round(sum(parts.values()), 4),
             "one_call_core": {"calls": "dn_frontend + dn_chunk_fwd_out_norm",
                            "ms_per_step": round(fms, 4),
                            "tokens_per_s": round(B * S / (fms / 1e3), 1), "kernels": fkern,

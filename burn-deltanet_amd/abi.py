@@ -50,6 +50,7 @@ EXPORTS = [
     "dn_last_error", "dn_version", "dn_profile_enable", "dn_profile_read",
     "dn_chunk_fwd_noalloc", "dn_unit_lower_inverse", "dn_block_step",
     "dn_chunk_fwd_out_norm", "dn_chunk_fwd_out_norm_workspace_bytes", "dn_wait_give_ups",
+    "dn_frontend_chunk_fwd", "dn_frontend_chunk_fwd_workspace_bytes",
 ]
 NOALLOC_SCRATCH_BYTES = 64 << 20  # DN_NOALLOC_SCRATCH_BYTES (deltanet_core.h)
 
@@ -125,6 +126,10 @@ class OutNormArgs(ctypes.Structure):
     ]
 
 
+class FrontendChunkFwdArgs(ctypes.Structure):
+    _fields_ = [("fe", FrontendArgs), ("fwd", ChunkFwdArgs)]
+
+
 class ChunkFwdOutNormArgs(ctypes.Structure):
     _fields_ = [
         ("fwd", ChunkFwdArgs), ("gate", _vp), ("gate_stride", _i64), ("gate_dtype", _i32),
@@ -183,6 +188,10 @@ def lib() -> ctypes.CDLL:
         L.dn_chunk_fwd_out_norm.restype = ctypes.c_int
         L.dn_chunk_fwd_out_norm_workspace_bytes.argtypes = [ctypes.POINTER(ChunkFwdOutNormArgs)]
         L.dn_chunk_fwd_out_norm_workspace_bytes.restype = _sz
+        L.dn_frontend_chunk_fwd.argtypes = [ctypes.POINTER(FrontendChunkFwdArgs), _vp]
+        L.dn_frontend_chunk_fwd.restype = ctypes.c_int
+        L.dn_frontend_chunk_fwd_workspace_bytes.argtypes = [ctypes.POINTER(FrontendChunkFwdArgs)]
+        L.dn_frontend_chunk_fwd_workspace_bytes.restype = _sz
         L.dn_wait_give_ups.argtypes = []
         L.dn_wait_give_ups.restype = ctypes.c_int64
         L.dn_block_step.argtypes = [ctypes.POINTER(BlockStepArgs), _vp]
@@ -417,6 +426,18 @@ def chunk_fwd_out_norm_args(fwd: ChunkFwdArgs, gate, weight, eps,
 
 def run_chunk_fwd_out_norm(args: ChunkFwdOutNormArgs) -> None:
     check(lib().dn_chunk_fwd_out_norm(ctypes.byref(args), stream_handle()))
+
+
+def frontend_chunk_fwd_args(fe: FrontendArgs, fwd: ChunkFwdArgs) -> FrontendChunkFwdArgs:
+    """dn_frontend_chunk_fwd's arguments: dn_frontend's `fe`, then the chunk
+    forward `fwd` over fe's outputs (fwd.q, k, v, erase, write must be fe's)."""
+    a = FrontendChunkFwdArgs()
+    a.fe, a.fwd = fe, fwd
+    return a
+
+
+def run_frontend_chunk_fwd(args: FrontendChunkFwdArgs) -> None:
+    check(lib().dn_frontend_chunk_fwd(ctypes.byref(args), stream_handle()))
 
 
 def wait_give_ups() -> int:

@@ -710,8 +710,10 @@ int dn_step(const dn_step_args* a, hipStream_t stream) {
   return DN_OK;
 }
 
-int dn_frontend(const dn_frontend_args* a, hipStream_t stream) {
-  g_last_error.clear();
+namespace {
+
+// dn_frontend's argument checks (also those of dn_frontend_chunk_fwd's `fe`).
+int check_frontend(const dn_frontend_args* a) {
   if (!a) return fail(DN_ERR_NULL, "args is NULL");
   // conv.rs:88-90 and qkv.rs:397-401
   if (a->sequence < 1) return fail(DN_ERR_SEQUENCE, "sequence length must be at least 1");
@@ -762,8 +764,108 @@ int dn_frontend(const dn_frontend_args* a, hipStream_t stream) {
     return fail(DN_ERR_NULL, "a required tensor pointer is NULL");
   if (a->write_gate == DN_WRITE_CHANNEL && a->write == a->erase)
     return fail(DN_ERR_SHAPE, "per-channel erase and write gates need separate buffers");
+  return DN_OK;
+}
+
+// The front-end's outputs are the chunk forward's inputs, at the same sizes.
+int check_frontend_chunk(const dn_frontend_chunk_fwd_args* a) {
+  if (!a) return fail(DN_ERR_NULL, "args is NULL");
+  if (int rc = check_frontend(&a->fe)) return rc;
+  if (int rc = check_fwd(&a->fwd)) return rc;
+  const dn_frontend_args& fe = a->fe;
+  const dn_chunk_fwd_args& f = a->fwd;
+  if (fe.n_householder != 1)
+    return fail(DN_ERR_UNSUPPORTED,
+                "dn_frontend_chunk_fwd takes n_householder 1 (DeltaProduct folds its micro-steps "
+                "between dn_frontend and dn_chunk_fwd)");
+  const bool ch = fe.write_gate == DN_WRITE_CHANNEL;
+  if (fe.batch != f.batch || fe.sequence != f.sequence || fe.nheads != f.nheads ||
+      fe.head_k_dim != f.head_k_dim || fe.head_v_dim != f.head_v_dim ||
+      f.erase_width != (ch ? f.head_k_dim : 1) || f.write_width != (ch ? f.head_v_dim : 1) ||
+      fe.out_dtype != f.qkv_dtype)
+    return fail(DN_ERR_SHAPE, "the chunk forward's sizes, gate widths and dtype must be the "
+                              "front-end's outputs'");
+  if (f.q != fe.q || f.k != fe.k || f.v != fe.v || f.erase != fe.erase || f.write != fe.write)
+    return fail(DN_ERR_SHAPE, "fwd.q, k, v, erase and write must be fe's outputs");
+  return DN_OK;
+}
+
+// Where the front-end's q/k half runs in the intra kernel's load stage: the
+// two-kernel MFMA forward with per-head gates at head_k_dim 128, a conv of
+// length 4 with the reference's default activations (SiLU in the conv,
+// nothing after it), bf16 throughout, and 16-byte rows.
+bool fe_fusable(const dn_frontend_chunk_fwd_args* a, const Dims& d, int algo) {
+  const dn_frontend_args& fe = a->fe;
+  auto al = [](const void* p, size_t b) { return reinterpret_cast<uintptr_t>(p) % b == 0; };
+  return algo == DN_ALGO_MFMA && !a->fwd.check_finite && d.K == 128 && d.ew == 1 &&
+         d.ww == 1 && d.dw <= 1 && fe.conv_kernel == 4 && fe.conv_activation == DN_ACT_SILU &&
+         fe.qk_activation == DN_ACT_SILU && fe.in_dtype == DN_BF16 &&
+         fe.out_dtype == DN_BF16 && fe.proj_stride % 8 == 0 && al(fe.projected, 16) &&
+         al(fe.conv_weight, 16) && al(fe.q, 16) && al(fe.k, 16);
+}
+
+}  // namespace
+
+int dn_frontend(const dn_frontend_args* a, hipStream_t stream) {
+  g_last_error.clear();
+  if (int rc = check_frontend(a)) return rc;
   hipError_t e = launch_frontend(*a, stream);
   if (e != hipSuccess) return hip_fail(e, "dn_frontend launch");
+  return DN_OK;
+}
+
+size_t dn_frontend_chunk_fwd_workspace_bytes(const dn_frontend_chunk_fwd_args* a) {
+  if (check_frontend_chunk(a)) return 0;
+  return dn_chunk_fwd_workspace_bytes(&a->fwd);
+}
+
+int dn_frontend_chunk_fwd(const dn_frontend_chunk_fwd_args* a, hipStream_t stream) {
+  g_last_error.clear();
+  if (int rc = check_frontend_chunk(a)) return rc;
+  const dn_frontend_args& fe = a->fe;
+  const dn_chunk_fwd_args* f = &a->fwd;
+  Dims d = make_dims(f->batch, f->sequence, f->nheads, f->head_k_dim, f->head_v_dim,
+                     f->erase_width, f->write_width, f->decay_width, f->has_gate, f->chunk_len,
+                     f->scale);
+  const int algo = fwd_algo(f, d);
+  if (algo < 0)
+    return fail(DN_ERR_UNSUPPORTED, "the requested MFMA path does not cover this shape/dtype");
+  if (!fe_fusable(a, run_dims(d, algo), algo)) {
+    // The two calls in turn.
+    if (int rc = dn_frontend(&fe, stream)) return rc;
+    return dn_chunk_fwd(f, stream);
+  }
+  d = run_dims(d, algo);
+  const size_t need = fwd_workspace(d, algo);
+  void* ws = f->workspace;
+  if (ws) {
+    if (f->workspace_bytes < need)
+      return fail(DN_ERR_WORKSPACE, "workspace too small: need " + std::to_string(need) +
+                                        " bytes");
+  } else if (need) {
+    hipError_t e = pool_get(need, &ws, stream);
+    if (e != hipSuccess) return hip_fail(e, "workspace allocation");
+  }
+  // v and the write gates; then q and k in the intra kernel, which reads the
+  // old conv window; then the next window.
+  hipError_t e = launch_frontend(fe, stream, kFrontV | kFrontGates);
+  if (e != hipSuccess) return hip_fail(e, "dn_frontend_chunk_fwd front-end launch");
+  FeParams fp{};
+  fp.proj = static_cast<const uint16_t*>(fe.projected);
+  fp.stride = fe.proj_stride;
+  fp.w = fe.conv_weight;
+  fp.bias = fe.conv_bias;
+  fp.win = static_cast<const uint16_t*>(fe.window_in);
+  fp.conv_dim = int(fe.nheads * (2 * fe.head_k_dim + fe.head_v_dim));
+  fp.l2 = fe.qk_norm == DN_QKNORM_L2;
+  fp.q = static_cast<uint16_t*>(fe.q);
+  fp.k = static_cast<uint16_t*>(fe.k);
+  e = mfma_fwd(d, f->y_dtype, f->q, f->k, f->v, f->erase, f->write,
+               f->has_gate ? f->g : nullptr, f->state_in, f->y, f->state_out, ws, stream, false,
+               &fp);
+  if (e != hipSuccess) return hip_fail(e, "dn_frontend_chunk_fwd launch");
+  e = launch_frontend(fe, stream, kFrontWindow);
+  if (e != hipSuccess) return hip_fail(e, "dn_frontend_chunk_fwd window launch");
   return DN_OK;
 }
 

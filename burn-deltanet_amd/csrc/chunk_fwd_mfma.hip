@@ -35,9 +35,11 @@
 //        32-deep k-step so accumulator tiles serve as MFMA operands in place.
 
 #include <algorithm>
+#include <type_traits>
 #include <map>
 #include <mutex>
 
+#include "activations.hpp"
 #include "dn_common.hpp"
 #include "mfma_scan.hpp"
 #include "mfma_util.hpp"
@@ -64,11 +66,42 @@ struct BwdTiles {
 // ---------------------------------------------------------------------------
 // intra
 // ---------------------------------------------------------------------------
+// Sum over each row of 16 lanes, the result in every lane of the row: the
+// four DPP steps dn_frontend's L2 norm takes (pairs, quads, half rows, rows),
+// in its order, so that a norm formed here equals its output bit for bit.
+__device__ inline float sum16_rows(float x) {
+  auto dpp = [](float v, auto ctrl) -> float {
+    return __int_as_float(
+        __builtin_amdgcn_update_dpp(0, __float_as_int(v), decltype(ctrl)::value, 0xF, 0xF, false));
+  };
+  x += dpp(x, std::integral_constant<int, 0xB1>{});   // quad_perm [1,0,3,2]
+  x += dpp(x, std::integral_constant<int, 0x4E>{});   // quad_perm [2,3,0,1]
+  x += dpp(x, std::integral_constant<int, 0x141>{});  // row_half_mirror
+  x += dpp(x, std::integral_constant<int, 0x140>{});  // row_mirror
+  return x;
+}
+
+// FE (dn_frontend_chunk_fwd): the intra kernel forms q and k itself from the
+// projection, as dn_frontend does (QkvProjection::forward, qkv.rs:386-421):
+// the causal depthwise conv of length 4 over the raw q/k columns, the rows
+// before the sequence from the conv window (ShortConv, conv.rs:85-121), SiLU
+// (the conv's and the q/k activation fused, the reference's default,
+// qkv.rs:223-229), and the L2 norm over the head (norm.rs:83-90). A token row is 16 lanes × 8
+// channels, dn_frontend's layout at head_k_dim 128, with its order of
+// operations, so the values equal its output. They are staged for the scores
+// and written to the q and k tensors, which the scan reads: the projection's
+// q/k columns are read once, where dn_frontend then dn_chunk_fwd write q and
+// k and read them twice. (FeParams: dn_common.hpp.)
+
 // BT (the backward's recompute): the kernel also writes the reverse scan's
 // transposed tiles (Tᵀ hi/lo, attnᵀ, Kc, Qgᵀ, Kgᵀ, e^{G_last}) from the
-// tiles it holds in LDS, as the per-channel kernel does.
-template <int K, bool GATED, bool BT = false>
-__global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int G, BwdTiles bt) {
+// tiles it holds in LDS, as the per-channel kernel does. FE: the front-end's
+// q/k as above (head_k_dim 128; a grid that is a multiple of nheads, so that
+// a workgroup sees one head and keeps its conv weights in LDS).
+// (FE: two workgroups per CU asked of the register allocator.)
+template <int K, bool GATED, bool BT = false, bool FE = false>
+__global__ __launch_bounds__(kThreads, FE ? 2 : 1)
+void mfma_intra_kernel(MfmaParams p, int G, BwdTiles bt, FeParams fe) {
   constexpr int KP = K + 8;                     // padded LDS row (bf16 elements)
   constexpr int KS8 = K / 8;                    // 16-byte segments per key row
   constexpr int NLD = kL * KS8 / kThreads;      // 16-byte loads per lane per tile
@@ -86,6 +119,14 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
   __shared__ float A[kL][kL + 1];  // strict-lower Akk, fp32 (upper blocks never read)
   __shared__ __attribute__((aligned(16))) uint16_t At[kL * (kL + 8)];  // attn, bf16
   __shared__ float gcs[kL], ers[kL];
+  static_assert(!FE || (K == 128 && !BT), "the fused front-end: head_k_dim 128, forward");
+  // FE: thread (s, c8) owns token rows RPT·s … +RPT−1 and channels 8·c8 … +7
+  // of q and k, and holds the raw rows RPT·s − 3 … for its conv taps; the
+  // conv weights and bias of the head's q and k channels sit in LDS.
+  constexpr int RPT = kL * KS8 / kThreads;
+  constexpr int NX = FE ? RPT + 3 : 1;
+  __shared__ __attribute__((aligned(16))) float few[FE ? 2 * K : 1][4];
+  __shared__ float feb[FE ? 2 * K : 1];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   // attn goes out where p.attn is set (the forward; the backward's recompute
@@ -101,11 +142,42 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
   // next chunk's K, Q and gates are loaded into registers while this one
   // is processed.
   uint4 kr[NLD], qr[NLD];
+  uint4 xq[NX], xk[NX];
   float gr = 0.f, er = 0.f;
   auto load = [&](int cid) {
     const int h = cid % p.H, n = (cid / p.H) % p.N, b = cid / (p.H * p.N);
+    if constexpr (FE) {
+      // Rows clamped into the sequence, loaded together; at its start the
+      // three rows before it come from the window's columns 1 … 3.
+      const int s = tid / KS8, c8 = tid % KS8;
+      const int qc = h * K + 8 * c8, kc = (p.H + h) * K + 8 * c8;
+      const uint16_t* pb = fe.proj + size_t(b) * p.S * size_t(fe.stride);
 #pragma unroll
-    for (int m = 0; m < NLD; ++m) {
+      for (int j = 0; j < NX; ++j) {
+        const int tok = min(max(n * kL + RPT * s - 3 + j, 0), p.S - 1);
+        const uint16_t* src = pb + size_t(tok) * size_t(fe.stride);
+        xq[j] = *reinterpret_cast<const uint4*>(src + qc);
+        xk[j] = *reinterpret_cast<const uint4*>(src + kc);
+      }
+      if (n == 0 && s == 0) {
+        const uint16_t* wb = fe.win + size_t(b) * fe.conv_dim * 4;
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+          uint32_t wq[4], wk[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            wq[e] = uint32_t(wb[size_t(qc + 2 * e) * 4 + j + 1]) |
+                    (uint32_t(wb[size_t(qc + 2 * e + 1) * 4 + j + 1]) << 16);
+            wk[e] = uint32_t(wb[size_t(kc + 2 * e) * 4 + j + 1]) |
+                    (uint32_t(wb[size_t(kc + 2 * e + 1) * 4 + j + 1]) << 16);
+          }
+          xq[j] = make_uint4(wq[0], wq[1], wq[2], wq[3]);
+          xk[j] = make_uint4(wk[0], wk[1], wk[2], wk[3]);
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < (FE ? 0 : NLD); ++m) {
       const int idx = tid + kThreads * m, row = idx / KS8, c8 = idx % KS8;
       const int tok = n * kL + row;
       kr[m] = qr[m] = make_uint4(0u, 0u, 0u, 0u);
@@ -122,7 +194,67 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
       er = tok < p.S ? p.erase[row] : 0.f;
     }
   };
+  if constexpr (FE) {
+    const int h = int(blockIdx.x) % p.H;
+    for (int c = tid; c < 2 * K; c += kThreads) {
+      const int ch = c < K ? h * K + c : (p.H + h) * K + (c - K);
+      *reinterpret_cast<float4*>(few[c]) = *reinterpret_cast<const float4*>(fe.w + size_t(ch) * 4);
+      feb[c] = fe.bias ? fe.bias[ch] : 0.f;
+    }
+    __syncthreads();
+  }
   if (int(blockIdx.x) < G) load(blockIdx.x);
+
+  // FE: q or k (g = 0, 1) of this thread's rows from the raw rows x, into the
+  // LDS tile and the output tensor (rows past the sequence end: zero in the
+  // tile, not stored).
+  auto fe_rows = [&](const uint4 (&x)[NX], int g, uint16_t* tile, uint16_t* out, int b, int n,
+                     int h) {
+    const int s = tid / KS8, c8 = tid % KS8;
+    float xv[NX][8];
+#pragma unroll
+    for (int j = 0; j < NX; ++j) {
+      const uint32_t w4[4] = {x[j].x, x[j].y, x[j].z, x[j].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        xv[j][2 * e] = lo_f(w4[e]);
+        xv[j][2 * e + 1] = hi_f(w4[e]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+      float y[8], ss = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int c = g * K + 8 * c8 + i;
+        const float4 w4 = *reinterpret_cast<const float4*>(few[c]);
+        float a = feb[c];
+        a = fmaf(w4.x, xv[r][i], a);
+        a = fmaf(w4.y, xv[r + 1][i], a);
+        a = fmaf(w4.z, xv[r + 2][i], a);
+        a = fmaf(w4.w, xv[r + 3][i], a);
+        // The reference's default activations (SiLU in the conv, nothing
+        // after it; qkv.rs:223-229), fixed at compile time as dn_frontend's
+        // FSILU kernels fix them.
+        a = a * sigmoidf_(a);
+        y[i] = a;
+        ss = fmaf(a, a, ss);
+      }
+      if (fe.l2) {
+        const float inv = rsqrtf(sum16_rows(ss) + 1e-6f);  // norm.rs:83-90
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] *= inv;
+      }
+      const int row = RPT * s + r, tok = n * kL + row;
+      uint4 v = make_uint4(pk_bf16(y[0], y[1]), pk_bf16(y[2], y[3]), pk_bf16(y[4], y[5]),
+                           pk_bf16(y[6], y[7]));
+      if (tok < p.S)
+        *reinterpret_cast<uint4*>(out + ((size_t(b) * p.S + tok) * p.H + h) * K + 8 * c8) = v;
+      else
+        v = make_uint4(0u, 0u, 0u, 0u);
+      *reinterpret_cast<uint4*>(&tile[row * KP + 8 * c8]) = v;
+    }
+  };
 
   // T (hi, lo) and attn of the previous chunk, 16 values of one row per lane:
   // their global stores are issued after the next chunk is staged, so no
@@ -171,11 +303,17 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_kernel(MfmaParams p, int 
   };
 
   for (int cid = blockIdx.x; cid < G; cid += gridDim.x) {
+    if constexpr (FE) {
+      const int h = cid % p.H, n = (cid / p.H) % p.N, b = cid / (p.H * p.N);
+      fe_rows(xk, 1, Ks, fe.k, b, n, h);
+      fe_rows(xq, 0, Qs, fe.q, b, n, h);
+    } else {
 #pragma unroll
-    for (int m = 0; m < NLD; ++m) {
-      const int idx = tid + kThreads * m, row = idx / KS8, c8 = idx % KS8;
-      *reinterpret_cast<uint4*>(&Ks[row * KP + 8 * c8]) = kr[m];
-      *reinterpret_cast<uint4*>(&Qs[row * KP + 8 * c8]) = qr[m];
+      for (int m = 0; m < NLD; ++m) {
+        const int idx = tid + kThreads * m, row = idx / KS8, c8 = idx % KS8;
+        *reinterpret_cast<uint4*>(&Ks[row * KP + 8 * c8]) = kr[m];
+        *reinterpret_cast<uint4*>(&Qs[row * KP + 8 * c8]) = qr[m];
+      }
     }
     // In-chunk cumulative gate and the erase gate, one token per lane.
     if (wave == 0) {
@@ -1224,8 +1362,26 @@ int resident_per_cu(const void* fn, int threads) {
 }
 
 hipError_t launch_intra(const MfmaParams& p, const Dims& d, hipStream_t stream,
-                        const BwdTiles* bt = nullptr) {
+                        const BwdTiles* bt = nullptr, const FeParams* fe = nullptr) {
   const size_t G = size_t(d.B) * d.N * d.H;
+  if (fe) {
+    // The front-end's q/k in the load stage (per-head gates, head_k_dim 128):
+    // a grid that is a multiple of nheads, so that each workgroup keeps one
+    // head's conv weights.
+    ProfScope ps("dn_mfma_intra_fe", stream);
+    const void* fn = p.gated ? reinterpret_cast<const void*>(&mfma_intra_kernel<128, true, false, true>)
+                             : reinterpret_cast<const void*>(&mfma_intra_kernel<128, false, false, true>);
+    const size_t cap = size_t(resident_per_cu(fn, kThreads)) * device_cu_count();
+    const size_t H = size_t(d.H);
+    const size_t grid = std::max(H, std::min(G, cap) / H * H);
+    if (p.gated)
+      hipLaunchKernelGGL((mfma_intra_kernel<128, true, false, true>), dim3(unsigned(grid)),
+                         dim3(kThreads), 0, stream, p, int(G), BwdTiles{}, *fe);
+    else
+      hipLaunchKernelGGL((mfma_intra_kernel<128, false, false, true>), dim3(unsigned(grid)),
+                         dim3(kThreads), 0, stream, p, int(G), BwdTiles{}, *fe);
+    return hipGetLastError();
+  }
   if (pc_path(d)) {
     ProfScope ps(bt ? "dn_mfma_intra_pc_bwd" : "dn_mfma_intra_pc", stream);
     const bool hd = !per_channel(d);
@@ -1260,7 +1416,7 @@ hipError_t launch_intra(const MfmaParams& p, const Dims& d, hipStream_t stream,
     const int grid = int(std::min<size_t>(G, size_t(resident_per_cu(fn, kThreads)) *             \
                                                  device_cu_count()));                            \
     hipLaunchKernelGGL((mfma_intra_kernel<KD, GT, BTV>), dim3(unsigned(grid)), dim3(kThreads),   \
-                       0, stream, p, int(G), bt ? *bt : BwdTiles{});                             \
+                       0, stream, p, int(G), bt ? *bt : BwdTiles{}, FeParams{});                 \
   } while (0)
 #define DN_INTRA_G(KD, BTV)                              \
   do {                                                   \
@@ -1476,11 +1632,11 @@ size_t mfma_fwd_workspace(const Dims& d, bool fused) {
 hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, const void* v,
                     const float* erase, const float* write, const float* g,
                     const float* state_in, void* y, float* state_out, void* ws,
-                    hipStream_t stream, bool fused) {
+                    hipStream_t stream, bool fused, const FeParams* fe) {
   if (fused)
     return fused_fwd(d, y_dtype, q, k, v, erase, write, g, state_in, y, state_out, ws, stream);
   MfmaParams p = make_params(d, q, k, v, erase, write, g, state_in, y, state_out, ws);
-  hipError_t e = launch_intra(p, d, stream);
+  hipError_t e = launch_intra(p, d, stream, nullptr, fe);
   if (e != hipSuccess) return e;
   const int P = seg_parts(d);
   if (P == 1) return launch_scan<false>(p, d, y_dtype == DN_BF16, stream);

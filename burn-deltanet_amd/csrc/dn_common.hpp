@@ -86,8 +86,11 @@ hipError_t launch_step(const dn_step_args& a, float scale, hipStream_t stream);
 constexpr int64_t kRecMaxK = DN_RECURRENT_MAX_K;
 bool recurrent_supported(const dn_recurrent_args& a);
 hipError_t launch_recurrent(const dn_recurrent_args& a, float scale, hipStream_t stream);
-// dn_frontend: the projection front-end (frontend.hip).
-hipError_t launch_frontend(const dn_frontend_args& a, hipStream_t stream);
+// dn_frontend: the projection front-end (frontend.hip). `parts` selects what
+// it writes (launch_frontend: all of it): the q/k units, the v units, the
+// write gates, the next conv window (after every read of the old one).
+enum FrontParts { kFrontQK = 1, kFrontV = 2, kFrontGates = 4, kFrontWindow = 8, kFrontAll = 15 };
+hipError_t launch_frontend(const dn_frontend_args& a, hipStream_t stream, int parts = kFrontAll);
 // dn_out_norm: the per-head (gated) RMSNorm (out_norm.hip).
 hipError_t launch_out_norm(const dn_out_norm_args& a, hipStream_t stream);
 hipError_t launch_unit_lower_inverse(const dn_tri_args& a, hipStream_t stream);
@@ -116,10 +119,25 @@ bool mfma_bwd_supported(const Dims& d, int qkv_dtype);
 // tiles in the workspace, or with `fused` (where fused_fwd_supported holds)
 // the one kernel of chunk_fwd_fused.hip.
 size_t mfma_fwd_workspace(const Dims& d, bool fused = false);
+// The projection front-end's q/k formed in the intra kernel's load stage
+// (dn_frontend_chunk_fwd): the raw projection columns, the conv of length 4
+// with its window and SiLU (the reference's default activations), the L2
+// norm, written to q and k for the scan. Per-head gates, head_k_dim 128,
+// bf16 throughout.
+struct FeParams {
+  const uint16_t* proj;  // [B][S][stride] bf16; q of head h at column h·K, k at (H + h)·K
+  long long stride;      // elements between consecutive tokens' rows
+  const float* w;        // [conv_dim][4] conv weights (tap j weighs x[t − 3 + j])
+  const float* bias;     // [conv_dim] or null
+  const uint16_t* win;   // [B][conv_dim][4] bf16, newest column last
+  int conv_dim;
+  int l2;                // 1: L2 norm over the head (else none)
+  uint16_t *q, *k;       // [B][S][H][K] bf16
+};
 hipError_t mfma_fwd(const Dims& d, int y_dtype, const void* q, const void* k, const void* v,
                     const float* erase, const float* write, const float* g,
                     const float* state_in, void* y, float* state_out, void* ws,
-                    hipStream_t stream, bool fused = false);
+                    hipStream_t stream, bool fused = false, const FeParams* fe = nullptr);
 // The MFMA forward with the output norm applied in the scan's y write
 // (OutNorm::forward, norm.rs:106-144): y receives the normalised output.
 // hipErrorCooperativeLaunchTooLarge, before any launch, when the scan's grid

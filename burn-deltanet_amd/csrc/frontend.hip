@@ -612,7 +612,8 @@ hipError_t launch_gate(const GateParams& g, hipStream_t stream) {
 }
 
 template <class TI, class TO>
-hipError_t frontend_typed(const dn_frontend_args& a, hipStream_t stream) {
+hipError_t frontend_typed(const dn_frontend_args& a, hipStream_t stream, int parts) {
+  const bool do_qk = parts & kFrontQK, do_v = parts & kFrontV;
   const int H = int(a.nheads), dk = int(a.head_k_dim), dv = int(a.head_v_dim);
   const int u = int(a.n_householder), K = int(a.conv_kernel);
   const int key_dim = H * dk, value_dim = H * dv;
@@ -680,20 +681,23 @@ hipError_t frontend_typed(const dn_frontend_args& a, hipStream_t stream) {
   // Conv length 4 reads a channel's weights and window row as one vector.
   p.win_vec = K == 4 && aligned(a.conv_weight, 16) && aligned(a.window_in, 4 * sizeof(TI)) &&
               aligned(a.window_out, 4 * sizeof(TI));
-  p.rows_win = p.S == 1 && p.win_vec && rows_qk && rows_v;
+  p.rows_win = p.S == 1 && p.win_vec && rows_qk && rows_v && do_qk && do_v && (parts & kFrontWindow);
   p.wout = a.window_out;
-  hipError_t e;
+  hipError_t e = hipSuccess;
+  if (!do_qk) p.n[0] = p.n[1] = 0;  // the units of group 2 (v) only, or none
   if (one_launch) {
-    p.n[2] = u * H * (dv / dk);
+    p.n[2] = do_v ? u * H * (dv / dk) : 0;
     p.ch0[2] = vch;
     p.nu[2] = u * H * (dv / dk);
     p.out[2] = a.v;
     p.post_act[2] = v_post;
     p.norm[2] = 0;
-    e = dispatch_heads<TI, TO>(p, true, rows_qk, stream);
+    if (p.n[0] + p.n[1] + p.n[2] > 0) e = dispatch_heads<TI, TO>(p, true, rows_qk, stream);
   } else {
-    e = dispatch_heads<TI, TO>(p, qk_vec, rows_qk, stream);
+    if (do_qk) e = dispatch_heads<TI, TO>(p, qk_vec, rows_qk, stream);
     if (e != hipSuccess) return e;
+  }
+  if (!one_launch && do_v) {
     p.D = dv;
     p.n[0] = u * H;
     p.n[1] = p.n[2] = 0;
@@ -707,43 +711,45 @@ hipError_t frontend_typed(const dn_frontend_args& a, hipStream_t stream) {
   }
   if (e != hipSuccess) return e;
   // Write gates.
-  const float es = a.allow_neg_eigval ? 2.f : 1.f;
-  GateParams g{};
-  g.proj = a.projected;
-  g.stride = a.proj_stride;
-  g.rows = a.batch * a.sequence;
-  if (a.write_gate == DN_WRITE_FIXED) {
-    g.c0 = 0;
-    g.width = u * H;
-    g.scale = es;
-    g.fixed = 1;
-    g.out = a.erase;
-    g.out2 = a.write == a.erase ? nullptr : a.write;
-    e = launch_gate<TI>(g, stream);
-  } else if (a.write_gate == DN_WRITE_SCALAR) {
-    g.c0 = conv_dim;
-    g.width = u * H;
-    g.scale = es;
-    g.out = a.erase;
-    g.out2 = a.write == a.erase ? nullptr : a.write;
-    e = launch_gate<TI>(g, stream);
-  } else {
-    g.c0 = conv_dim;
-    g.width = u * key_dim;
-    g.scale = es;
-    g.out = a.erase;
-    e = launch_gate<TI>(g, stream);
+  if (parts & kFrontGates) {
+    const float es = a.allow_neg_eigval ? 2.f : 1.f;
+    GateParams g{};
+    g.proj = a.projected;
+    g.stride = a.proj_stride;
+    g.rows = a.batch * a.sequence;
+    if (a.write_gate == DN_WRITE_FIXED) {
+      g.c0 = 0;
+      g.width = u * H;
+      g.scale = es;
+      g.fixed = 1;
+      g.out = a.erase;
+      g.out2 = a.write == a.erase ? nullptr : a.write;
+      e = launch_gate<TI>(g, stream);
+    } else if (a.write_gate == DN_WRITE_SCALAR) {
+      g.c0 = conv_dim;
+      g.width = u * H;
+      g.scale = es;
+      g.out = a.erase;
+      g.out2 = a.write == a.erase ? nullptr : a.write;
+      e = launch_gate<TI>(g, stream);
+    } else {
+      g.c0 = conv_dim;
+      g.width = u * key_dim;
+      g.scale = es;
+      g.out = a.erase;
+      e = launch_gate<TI>(g, stream);
+      if (e != hipSuccess) return e;
+      g.c0 = conv_dim + u * key_dim;
+      g.width = u * value_dim;
+      g.scale = 1.f;
+      g.out = a.write;
+      e = launch_gate<TI>(g, stream);
+    }
     if (e != hipSuccess) return e;
-    g.c0 = conv_dim + u * key_dim;
-    g.width = u * value_dim;
-    g.scale = 1.f;
-    g.out = a.write;
-    e = launch_gate<TI>(g, stream);
   }
-  if (e != hipSuccess) return e;
   // The next window, after every read of the old one above (unless the
   // rows kernel wrote it).
-  if (K > 0 && !p.rows_win) {
+  if ((parts & kFrontWindow) && K > 0 && !p.rows_win) {
     p.out[0] = a.window_out;
     const unsigned grid = unsigned((int64_t(p.B) * conv_dim + kFrontThreads - 1) / kFrontThreads);
     hipLaunchKernelGGL(frontend_window_kernel<TI>, dim3(grid), dim3(kFrontThreads), 0, stream, p);
@@ -754,12 +760,12 @@ hipError_t frontend_typed(const dn_frontend_args& a, hipStream_t stream) {
 
 }  // namespace
 
-hipError_t launch_frontend(const dn_frontend_args& a, hipStream_t stream) {
+hipError_t launch_frontend(const dn_frontend_args& a, hipStream_t stream, int parts) {
   const bool in_bf = a.in_dtype == DN_BF16, out_bf = a.out_dtype == DN_BF16;
-  if (in_bf && out_bf) return frontend_typed<bf16, bf16>(a, stream);
-  if (in_bf) return frontend_typed<bf16, float>(a, stream);
-  if (out_bf) return frontend_typed<float, bf16>(a, stream);
-  return frontend_typed<float, float>(a, stream);
+  if (in_bf && out_bf) return frontend_typed<bf16, bf16>(a, stream, parts);
+  if (in_bf) return frontend_typed<bf16, float>(a, stream, parts);
+  if (out_bf) return frontend_typed<float, bf16>(a, stream, parts);
+  return frontend_typed<float, float>(a, stream, parts);
 }
 
 }  // namespace dn

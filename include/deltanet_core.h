@@ -322,6 +322,33 @@ typedef struct {
 int dn_chunk_fwd_out_norm(const dn_chunk_fwd_out_norm_args *args, hipStream_t stream);
 size_t dn_chunk_fwd_out_norm_workspace_bytes(const dn_chunk_fwd_out_norm_args *args);
 
+/* QkvProjection::forward (src/common/qkv.rs:373-449) and then
+ * DeltaChunkBackendExt::delta_chunk_recalculated (chunk_recalculated.rs:115-151)
+ * on its outputs, as every family runs them over a sequence
+ * (gated_deltanet_1.rs:162-177, deltanet.rs:151-165, gated_deltanet_2.rs:213-261).
+ * `fe` as for dn_frontend (n_householder 1); `fwd` as for dn_chunk_fwd, with
+ * fwd.q, k, v, erase and write the front-end's outputs fe.q, k, v, erase and
+ * write (the same pointers), and the sizes, gate widths and q/k/v dtype that
+ * follow from fe. The results, the front-end's outputs and the next conv
+ * window included, are those of dn_frontend followed by dn_chunk_fwd, bit for
+ * bit. Where the chunk forward runs the two-kernel MFMA path with per-head
+ * gates at head_k_dim 128, with a conv of length 4 and SiLU as the conv's and
+ * the q/k activation (the reference's default), a bf16 projection, window and
+ * q/k/v, 16-byte aligned rows and no check_finite, the front-end's q/k
+ * half runs in the chunk forward's load stage: its intra kernel reads the raw
+ * projection columns and the conv window, applies the conv, the activations
+ * and the L2 norm, and writes q and k for the scan, so the projection's q/k
+ * columns are read once and q and k written once, where the two calls write
+ * them and read them twice. Otherwise the call runs the two calls. The
+ * workspace is dn_chunk_fwd's (dn_frontend_chunk_fwd_workspace_bytes). */
+typedef struct {
+  dn_frontend_args fe;
+  dn_chunk_fwd_args fwd;
+} dn_frontend_chunk_fwd_args;
+
+int dn_frontend_chunk_fwd(const dn_frontend_chunk_fwd_args *args, hipStream_t stream);
+size_t dn_frontend_chunk_fwd_workspace_bytes(const dn_frontend_chunk_fwd_args *args);
+
 /* Bounded cross-workgroup waits that gave up on the current device since the
  * library was loaded (synchronises the device). No counterpart in the
  * reference; nonzero means an output of dn_chunk_fwd_out_norm was wrong. */
