@@ -524,8 +524,9 @@ def bench_config2_bwd(torch, pkg, steps, warmup):
 def bench_chunk_lengths(torch, pkg, steps, warmup):
     """Config 2 at other chunk lengths as AUTO serves them (the MFMA kernels'
     64-token chunks: with a per-head forget gate the chunk length orders the
-    roundings only), and the fp32 kernels that shapes outside the MFMA path
-    fall back to, forced (DN_ALGO_GENERIC) at chunk 64."""
+    roundings only), the fp32 kernels that shapes outside the MFMA path
+    fall back to, forced (DN_ALGO_GENERIC) at chunk 64, and config 2 at
+    head_k_dim 256 (the MFMA forward; the generic kernels forced beside it)."""
     B, T, H, K, V = 8, 4096, 16, 128, 256
     dev = torch.device("cuda:0")
     q, k, v, beta, g = gdn_inputs(torch, B, T, H, K, V, 0.05, 20260837, torch.bfloat16, dev)
@@ -534,8 +535,8 @@ def bench_chunk_lengths(torch, pkg, steps, warmup):
     s1 = torch.empty_like(s0)
     abi = pkg.abi
     out = {"workload": "config 2 (B=8 T=4096 H=16 dk=128 dv=256, bf16 q/k/v) at chunk_len 32 "
-                       "and 128 under AUTO, on the generic fp32 kernels at 64, and with "
-                       "per-channel erase/write gates under AUTO"}
+                       "and 128 under AUTO, on the generic fp32 kernels at 64, with "
+                       "per-channel erase/write gates under AUTO, and at head_k_dim 256"}
     for name, L, algo in (("auto_chunk32", 32, 0), ("auto_chunk128", 128, 0),
                           ("forced_generic_chunk64", 64, 1)):
         a = abi.chunk_fwd_args(q, k, v, beta, beta, g, s0, y, s1, L, None, algo=algo)
@@ -564,6 +565,29 @@ def bench_chunk_lengths(torch, pkg, steps, warmup):
         "gates": "erase [.., dk], write [.., dv], per-head forget gate",
         "algo": ALGO_NAMES.get(chosen, chosen), "ms_per_step": round(ms, 3),
         "tokens_per_s": round(B * T / (ms / 1e3), 1), "kernels": kern}
+    del ws, e, w
+    # head_k_dim 256 (config 2 otherwise): the MFMA forward under AUTO, and
+    # the generic fp32 kernels it used to fall back to, forced.
+    K2 = 256
+    q2, k2, v2, beta2, g2 = gdn_inputs(torch, B, T, H, K2, V, 0.05, 20260839, torch.bfloat16, dev)
+    s2 = torch.zeros((B, H, K2, V), dtype=torch.float32, device=dev)
+    s3 = torch.empty_like(s2)
+    wide = {"shape": "B=8 T=4096 H=16 dk=256 dv=256, per-head gates, chunk 64"}
+    for name, algo in (("auto", 0), ("forced_generic", 1)):
+        a = abi.chunk_fwd_args(q2, k2, v2, beta2, beta2, g2, s2, y, s3, 64, None, algo=algo)
+        ws = torch.empty(max(abi.lib().dn_chunk_fwd_workspace_bytes(a), 1), dtype=torch.uint8,
+                         device=dev)
+        a.workspace, a.workspace_bytes = ws.data_ptr(), ws.numel()
+        chosen = abi.lib().dn_chunk_fwd_algo(a)
+        ms, kern = _timed(torch, abi, lambda: abi.run_chunk_fwd(a), steps if algo == 0 else 3,
+                          warmup if algo == 0 else 1)
+        wide[name] = {"algo": ALGO_NAMES.get(chosen, chosen), "ms_per_step": round(ms, 3),
+                      "tokens_per_s": round(B * T / (ms / 1e3), 1), "kernels": kern}
+        del ws
+    # Per token against config 2 (dk = 128) on the same kernels at chunk 32.
+    wide["per_token_cost_vs_config2"] = round(
+        wide["auto"]["ms_per_step"] / out["auto_chunk32"]["ms_per_step"], 3)
+    out["head_k_dim_256"] = wide
     return out
 
 

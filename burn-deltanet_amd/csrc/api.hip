@@ -490,7 +490,8 @@ bool norm_fusable(const dn_chunk_fwd_out_norm_args* a) {
   const bool gate_ok = !a->gate || (a->gate_dtype == a->fwd.y_dtype &&
                                     reinterpret_cast<uintptr_t>(a->gate) % word == 0 &&
                                     a->gate_stride % 4 == 0 && a->gate_stride < (int64_t(1) << 25));
-  return gate_ok && reinterpret_cast<uintptr_t>(a->fwd.y) % word == 0;
+  // The norm-applying scans cover head_k_dim 64 and 128.
+  return gate_ok && reinterpret_cast<uintptr_t>(a->fwd.y) % word == 0 && a->fwd.head_k_dim <= 128;
 }
 
 }  // namespace

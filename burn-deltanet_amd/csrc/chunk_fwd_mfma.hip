@@ -2,8 +2,10 @@
 //
 // Covers the per-head gate shapes of Gated DeltaNet / DeltaNet / DeltaProduct:
 // bf16 q/k/v, head_k_dim ∈ {64, 128}, head_v_dim a multiple of 64,
-// chunk_len 64, erase/write/forget gates of width 1 (or no forget gate).
-// Everything else takes the generic kernels.
+// chunk_len 64, erase/write/forget gates of width 1 (or no forget gate);
+// head_k_dim 256 with head_v_dim a multiple of 128 in the forward. The
+// per-channel kernels below cover the channel-wide gates. Everything else
+// takes the generic kernels.
 //
 // Two kernels on v_mfma_f32_16x16x32_bf16 (64-lane waves):
 //
@@ -1423,7 +1425,10 @@ hipError_t launch_intra(const MfmaParams& p, const Dims& d, hipStream_t stream,
     if (p.gated) DN_INTRA(KD, true, BTV);                \
     else DN_INTRA(KD, false, BTV);                       \
   } while (0)
-    if (d.K == 128) {
+    if (d.K == 256) {
+      if (bt) return hipErrorInvalidValue;  // head_k_dim 256: the forward only
+      DN_INTRA_G(256, false);
+    } else if (d.K == 128) {
       if (bt) DN_INTRA_G(128, true); else DN_INTRA_G(128, false);
     } else {
       if (bt) DN_INTRA_G(64, true); else DN_INTRA_G(64, false);
@@ -1439,6 +1444,9 @@ hipError_t launch_intra(const MfmaParams& p, const Dims& d, hipStream_t stream,
 // (config 4, 64 sequences of dv = 128: 256 two-wave workgroups run its scan
 // 3% faster than 128 four-wave ones).
 int scan_waves(const Dims& d) {
+  // head_k_dim 256: eight waves, whose staging registers (11 per lane) fit
+  // beside the 64 of the state's rows.
+  if (d.K == 256) return 8;
   const int groups = (d.B * d.H + 7) / 8;
   const int cus = device_cu_count();
   if (d.V % 128 == 0 && size_t(groups) * 8 * (d.V / 128) >= size_t(cus)) return 8;
@@ -1536,7 +1544,20 @@ hipError_t launch_scan(const MfmaParams& p, const Dims& d, bool yb, hipStream_t 
   } while (0)
 #define DN_SCAN_W(KD, TY) \
   do { if (waves == 8) DN_SCAN(KD, TY, 8); else if (waves == 4) DN_SCAN(KD, TY, 4); else DN_SCAN(KD, TY, 2); } while (0)
-  if (d.K == 128) {
+  if (d.K == 256) {
+    // head_k_dim 256: per-head gates, the forward only.
+    if constexpr (ST) {
+      return hipErrorInvalidValue;
+    } else {
+      if (pc || waves != 8) return hipErrorInvalidValue;
+      if (yb)
+        hipLaunchKernelGGL((mfma_scan_kernel<256, bf16, 8, false>), dim3(blocks), dim3(512), 0,
+                           stream, p);
+      else
+        hipLaunchKernelGGL((mfma_scan_kernel<256, float, 8, false>), dim3(blocks), dim3(512), 0,
+                           stream, p);
+    }
+  } else if (d.K == 128) {
     if (yb && !ST) DN_SCAN_W(128, bf16); else DN_SCAN_W(128, float);
   } else {
     if (yb && !ST) DN_SCAN_W(64, bf16); else DN_SCAN_W(64, float);
@@ -1610,18 +1631,22 @@ hipError_t launch_scan_norm(const MfmaParams& p, const Dims& d, bool yb, hipStre
 
 bool mfma_fwd_supported(const Dims& d, int qkv_dtype, int y_dtype) {
   (void)y_dtype;
-  if (!(qkv_dtype == DN_BF16 && (d.K == 64 || d.K == 128) && d.V % kBV == 0 && d.L == kL))
-    return false;
+  if (!(qkv_dtype == DN_BF16 && d.V % kBV == 0 && d.L == kL)) return false;
   if (!token_rows_fit_32bit(d)) return false;
+  // head_k_dim 256: per-head (or no) gates, eight-wave scan workgroups of
+  // 128 value columns.
+  if (d.K == 256) return !pc_path(d) && d.ew == 1 && d.ww == 1 && d.dw <= 1 && d.V % 128 == 0;
+  if (d.K != 64 && d.K != 128) return false;
   if (pc_path(d)) return (d.ew == 1 || d.ew == d.K) && (d.ww == 1 || d.ww == d.V);
   return d.ew == 1 && d.ww == 1 && d.dw <= 1;
 }
 
 // The MFMA backward: its chunk-local kernel and scans know the per-head
-// gates and the all-per-channel ones (GDN-2); per-channel erase or write
-// gates beside a per-head forget gate take the generic kernels.
+// gates and the all-per-channel ones (GDN-2), at head_k_dim 64 and 128;
+// per-channel erase or write gates beside a per-head forget gate, and
+// head_k_dim 256, take the generic kernels.
 bool mfma_bwd_supported(const Dims& d, int qkv_dtype) {
-  return mfma_fwd_supported(d, qkv_dtype, DN_BF16) &&
+  return d.K <= 128 && mfma_fwd_supported(d, qkv_dtype, DN_BF16) &&
          (per_channel(d) || (d.ew == 1 && d.ww == 1));
 }
 

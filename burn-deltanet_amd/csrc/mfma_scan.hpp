@@ -110,7 +110,11 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   // round trip through HBM.
   // Double-buffered for per-head gates: the next chunk is staged while this
   // one is consumed, so one barrier per chunk suffices. The per-channel
-  // tiles do not fit twice in LDS: they are staged between two barriers.
+  // tiles, and head_k_dim 256's (88 KB a chunk), do not fit twice in LDS:
+  // they are staged between two barriers. (A head_k_dim 256 variant that
+  // kept the K and [64][64] tiles double-buffered and restaged a single Q
+  // tile after a barrier behind phase 1 measured slower, 487 → 652 µs at
+  // B=8 T=4096 H=16 dv=256: its extra staging registers spill in the loop.)
   // The states mode and the transition pass write no y: they fetch no attn
   // (per-head gates).
   constexpr int NKQ = PC ? 3 : 2;  // K-wide tiles
@@ -122,7 +126,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   constexpr int C16 = BUF / 8;    // 16-byte chunks per chunk's tiles
   static_assert(C16 % NT == 0, "staging assumes whole rounds");
   constexpr int NPF = C16 / NT;   // chunks staged per lane
-  constexpr int NBUF = PC ? 1 : 2;
+  constexpr int NBUF = PC || K > 128 ? 1 : 2;
   __shared__ __attribute__((aligned(16))) uint16_t tiles[NBUF][BUF];
   __shared__ float gxe[NBUF][kL], gwr[NBUF][kL], gys[NBUF][kL], gegl[NBUF];
   // e^{G_last−G} per token (per-head gates), rows of V' for the state update.
@@ -526,7 +530,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   stage(0, 0, NPF);
   __syncthreads();
   for (int n = 0; n < p.N; ++n) {
-    const int cur = PC ? 0 : (n & 1);
+    const int cur = NBUF == 1 ? 0 : (n & 1);
     const int nn = n + 1 < p.N ? n + 1 : n;  // the last chunk prefetches itself again
     const uint16_t* tl = tiles[cur];
     const float egl = PC ? 1.f : gegl[cur];

@@ -54,6 +54,10 @@ CASES = [
     (1, 200, 3, 128, 128, True, 2.0, 0.02, False),
     (1, 128, 2, 128, 64, True, 1.0, 0.02, True),
     (1, 1000, 2, 128, 256, True, 1.0, 0.02, False),
+    # head_k_dim 256 (one 128-column workgroup per head and value block)
+    (1, 300, 2, 256, 256, True, 1.0, 0.02, False),
+    (2, 128, 3, 256, 128, False, 2.0, 0.02, False),
+    (1, 200, 1, 256, 512, True, 1.0, 0.0, False),
 ]
 
 
@@ -78,6 +82,40 @@ def test_mfma_fwd_in_place_state_fp32_y(rng):
     y, s = run_mfma(g_args, y_dtype=torch.float32, in_place=True)
     y0, s0 = O.chunk_fwd(*ref_in, chunk_len=64, dtype=np.float32)
     assert rel_err(y, y0) < TOL and rel_err(s, s0) < TOL
+
+
+def test_mfma_head_k_dim_256_fp32_y_in_place_and_chunk_len(rng):
+    """head_k_dim 256: fp32 y with the state updated in place, and a request
+    for chunk_len 128 served by the 64-token kernels, against the oracle's
+    chunk forward at the requested length; the backward at this width takes
+    the generic kernels under AUTO."""
+    announce("mfma fwd head_k_dim 256: fp32 y in place, chunk_len 128")
+    args = gdn_inputs(rng, 1, 260, 2, 256, 128, True, 1.0, 0.02)
+    g_args = to_gpu(args, torch.bfloat16)
+    ref_in = as_oracle_inputs(g_args)
+    y, s = run_mfma(g_args, y_dtype=torch.float32, in_place=True)
+    y0, s0 = O.chunk_fwd(*ref_in, chunk_len=64, dtype=np.float64)
+    ey, es = rel_err(y, y0), rel_err(s, s0)
+    print(f"  in place: rel err y {ey:.2e} state {es:.2e}", flush=True)
+    assert ey < TOL and es < TOL
+    g_args = to_gpu(args, torch.bfloat16)
+    q, k, v, e, w, g, s_in = g_args
+    yb = torch.empty((1, 260, 2, 128), dtype=torch.bfloat16, device=DEV)
+    s_out = torch.empty_like(s_in)
+    a = pkg.abi.chunk_fwd_args(q, k, v, e, w, g, s_in, yb, s_out, 128, None)
+    assert pkg.abi.lib().dn_chunk_fwd_algo(a) == MFMA
+    pkg.abi.run_chunk_fwd(a)
+    torch.cuda.synchronize()
+    y0, s0 = O.chunk_fwd(*as_oracle_inputs(g_args), chunk_len=128, dtype=np.float64)
+    ey, es = rel_err(np_of(yb), y0), rel_err(np_of(s_out), s0)
+    print(f"  chunk_len 128: rel err y {ey:.2e} state {es:.2e}", flush=True)
+    assert ey < TOL and es < TOL
+    dy = torch.zeros((1, 260, 2, 128), device=DEV)
+    grads = (torch.empty(q.shape, device=DEV), torch.empty(k.shape, device=DEV),
+             torch.empty(v.shape, device=DEV), torch.empty_like(e), torch.empty_like(w),
+             torch.empty_like(g), torch.empty_like(s_in))
+    b = pkg.abi.chunk_bwd_args(dy, None, q, k, v, e, w, g, s_in, grads, 64, None)
+    assert pkg.abi.lib().dn_chunk_bwd_algo(b) == pkg.abi.DN_ALGO_GENERIC
 
 
 def test_mfma_matches_generic_path(rng):
