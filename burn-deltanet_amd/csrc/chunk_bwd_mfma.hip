@@ -1210,9 +1210,10 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
 
 }  // namespace
 
-// head_v_dim 64 or 128 in one pass; a multiple of 128 in passes of 128 columns.
+// head_v_dim 64 or 128 in one pass; above 128 in passes of 128 columns, the
+// last of 64 when head_v_dim is an odd multiple of 64.
 bool mfma_chunk_bwd_supported(const Dims& d, int qkv_dtype) {
-  return mfma_fwd_supported(d, qkv_dtype, DN_BF16) && (d.V == 64 || d.V % 128 == 0);
+  return d.K <= 128 && mfma_fwd_supported(d, qkv_dtype, DN_BF16) && d.V % 64 == 0;
 }
 
 // The fp32 partial sums of the value-summed gradients across the passes:
@@ -1267,8 +1268,9 @@ hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const v
   const size_t G = size_t(d.B) * d.N * d.H;
   const bool pc = d.dw == d.K && d.K > 1;
   const bool f32 = grad_dtype == DN_F32;
-  // One pass for head_v_dim 64 or 128, else passes of 128 value columns.
-  const int vd = d.V <= 128 ? int(d.V) : 128, passes = int(d.V) / vd;
+  // One pass for head_v_dim 64 or 128, else passes of 128 value columns (the
+  // last of 64 when head_v_dim is an odd multiple of 64).
+  const int passes = d.V <= 128 ? 1 : int((d.V + 127) / 128);
   const size_t rows = size_t(d.B) * d.S * d.H;
   p.vs = int(d.V);
   p.pq = partials;
@@ -1286,9 +1288,14 @@ hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const v
 #define DN_CB(KD, VD, PCV, TG)                                                                  \
   hipLaunchKernelGGL((mfma_chunk_bwd_kernel<KD, VD, PCV, TG>), dim3(unsigned(G)), dim3(kNT), 0, \
                      stream, p)
-#define DN_CB_L(KD, TG)                                                                        \
-  hipLaunchKernelGGL((mfma_chunk_bwd_kernel<KD, 128, false, TG, true>), dim3(unsigned(G)),      \
+#define DN_CB_L(KD, VD, TG)                                                                    \
+  hipLaunchKernelGGL((mfma_chunk_bwd_kernel<KD, VD, false, TG, true>), dim3(unsigned(G)),       \
                      dim3(kNT), 0, stream, p)
+#define DN_CB_LV(KD, TG)                           \
+  do {                                             \
+    if (vd == 128) DN_CB_L(KD, 128, TG);           \
+    else DN_CB_L(KD, 64, TG);                      \
+  } while (0)
 #define DN_CB_E(KD, TG)                                                                          \
   hipLaunchKernelGGL((mfma_chunk_bwd_kernel<KD, 128, false, TG, false, true>), dim3(unsigned(G)), \
                      dim3(kNT), 0, stream, p)
@@ -1303,14 +1310,14 @@ hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const v
     else DN_CB_T(KD, VD, false);          \
   } while (0)
   for (int i = 0; i < passes; ++i) {
-    p.voff = vd * i;
+    const int vd = passes == 1 ? int(d.V) : i + 1 < passes || d.V % 128 == 0 ? 128 : 64;
+    p.voff = 128 * i;
     p.pass = passes == 1 ? 0 : i == 0 ? 1 : i + 1 == passes ? 3 : 2;
     if (p.pass == 3 && !pc) {
-      // Several passes imply vd = 128.
       if (d.K == 128) {
-        if (f32) DN_CB_L(128, float); else DN_CB_L(128, bf16);
+        if (f32) DN_CB_LV(128, float); else DN_CB_LV(128, bf16);
       } else {
-        if (f32) DN_CB_L(64, float); else DN_CB_L(64, bf16);
+        if (f32) DN_CB_LV(64, float); else DN_CB_LV(64, bf16);
       }
     } else if ((p.pass == 1 || p.pass == 2) && !pc) {
       if (d.K == 128) {
@@ -1328,6 +1335,7 @@ hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const v
   }
 #undef DN_CB_P
 #undef DN_CB_E
+#undef DN_CB_LV
 #undef DN_CB_L
 #undef DN_CB_T
 #undef DN_CB

@@ -358,6 +358,12 @@ BWD_CASES = [
     (1, 96, 2, 64, 512, "head"),  # two middle passes, each adding to the handed-on sums
     (1, 128, 2, 128, 256, None),
     (1, 256, 2, 128, 256, "head", {"const_keys": True}),
+    # an odd multiple of 64 above 128: passes of 128 columns and a last of 64
+    (1, 128, 2, 128, 192, "head"),
+    (1, 130, 2, 128, 192, (128, 192)),
+    (1, 100, 2, 64, 320, "head"),  # 128, 128 (a middle pass), then 64
+    (1, 96, 2, 128, 192, None),
+    (1, 128, 2, 64, 192, (1, 1)),
 ]
 
 
@@ -463,11 +469,13 @@ def test_mfma_bwd_is_chosen_and_matches_generic(rng):
         assert rel_err(m, gnr) < TOL
 
 
-def test_mfma_chunk_local_backward_runs_in_value_passes(rng):
+@pytest.mark.parametrize("V,gates", [(256, "head"), (192, "head"), (192, (128, 192))])
+def test_mfma_chunk_local_backward_runs_in_value_passes(rng, V, gates):
     """head_v_dim 256 runs the MFMA chunk-local kernel (two 128-column passes
-    under one profiler scope), not the generic one."""
-    announce("mfma bwd, dv 256: kernels")
-    args, dy, ds = bwd_inputs(rng, 1, 128, 2, 128, 256, "head")
+    under one profiler scope), not the generic one; 192 likewise, as a pass of
+    128 columns and one of 64."""
+    announce(f"mfma bwd, dv {V} {gates}: kernels")
+    args, dy, ds = bwd_inputs(rng, 1, 128, 2, 128, V, gates)
     q, k, v, e, w, g, s = to_gpu(args, torch.bfloat16)
     tdy = torch.tensor(dy, dtype=torch.float32, device=DEV).to(torch.bfloat16)
     tds = torch.tensor(ds, dtype=torch.float32, device=DEV)
