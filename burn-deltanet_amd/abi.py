@@ -19,7 +19,7 @@ LIB_PATH = _HERE / "libdeltanet_core.so"
 
 DN_F32, DN_BF16 = 0, 1
 DN_ALGO_AUTO, DN_ALGO_GENERIC, DN_ALGO_MFMA, DN_ALGO_MFMA_FUSED = 0, 1, 2, 3
-RECURRENT_MAX_K = 256  # dn_recurrent's head_k_dim limit (deltanet_core.h)
+RECURRENT_MAX_K = 512  # dn_recurrent's head_k_dim limit (deltanet_core.h)
 DN_ACT_IDENTITY, DN_ACT_SILU, DN_ACT_RELU, DN_ACT_ELU_PLUS_ONE = 0, 1, 2, 3
 DN_QKNORM_NONE, DN_QKNORM_L2, DN_QKNORM_SUM = 0, 1, 2
 DN_WRITE_FIXED, DN_WRITE_SCALAR, DN_WRITE_CHANNEL = 0, 1, 2

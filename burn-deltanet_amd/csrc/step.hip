@@ -287,7 +287,7 @@ __global__ __launch_bounds__(kRowThreads) void step_row_kernel(StepParams p) {
 // 0 included), so rows past K hold zeros throughout and every LDS read of a
 // row is one base register plus an immediate offset.
 template <class TQ, class TY, int RPT, int C>
-__global__ __launch_bounds__(kRowThreads, RPT <= 16 ? 4 : 2) void recurrent_row_kernel(StepParams p) {
+__global__ __launch_bounds__(kRowThreads, RPT <= 16 ? 4 : RPT <= 32 ? 2 : 1) void recurrent_row_kernel(StepParams p) {
   constexpr int W = 64 * C;
   constexpr int KP = kRowWaves * RPT;          // padded rows
   constexpr int TB = 4;                        // tokens per staged block
@@ -494,15 +494,18 @@ hipError_t launch_recurrent_c(const StepParams& p, hipStream_t stream) {
   hipLaunchKernelGGL((recurrent_row_kernel<TQ, TY, RPT, C>), grid, dim3(kRowThreads), 0, stream, p)
   if (p.K <= 64) DN_REC(8);
   else if (p.K <= 128) DN_REC(16);
-  else DN_REC(32);
+  else if (p.K <= 256) DN_REC(32);
+  else if constexpr (C == 1) DN_REC(64);  // above 256 rows: one column a lane
+  else return hipErrorInvalidValue;
 #undef DN_REC
   return hipGetLastError();
 }
 
 template <class TQ, class TY>
 hipError_t launch_recurrent_typed(const StepParams& p, hipStream_t stream) {
-  // Two columns per lane (8-byte state accesses) when the rows allow it.
-  const bool c2 = p.V >= 128 && p.V % 2 == 0 &&
+  // Two columns per lane (8-byte state accesses) when the rows allow it (up
+  // to 256 state rows: 512 would hold 128 registers of state a lane).
+  const bool c2 = p.K <= 256 && p.V >= 128 && p.V % 2 == 0 &&
                   ((reinterpret_cast<uintptr_t>(p.s_in) | reinterpret_cast<uintptr_t>(p.s_out)) %
                    8) == 0;
   return c2 ? launch_recurrent_c<TQ, TY, 2>(p, stream) : launch_recurrent_c<TQ, TY, 1>(p, stream);

@@ -199,9 +199,9 @@ int dn_step(const dn_step_args *args, hipStream_t stream);
  * token to the last (one read and one write of it per call instead of one
  * of each per token). DeltaProduct's decode folds its u Householder
  * micro-steps into a u-token sequence and runs it this way
- * (delta_product.rs:270-305). head_k_dim up to 256; larger returns
+ * (delta_product.rs:270-305). head_k_dim up to 512; larger returns
  * DN_ERR_UNSUPPORTED (delta_step per token covers it). */
-#define DN_RECURRENT_MAX_K 256
+#define DN_RECURRENT_MAX_K 512
 int dn_recurrent(const dn_recurrent_args *args, hipStream_t stream);
 
 /* The projection front-end: everything QkvProjection::forward does after its

@@ -2,7 +2,7 @@
 
 Checked against the oracle's recurrent pass (recurrent.rs:107-142) and against
 the same tokens run as one dn_step per token, across the shapes the kernel
-specialises on: rows per lane (head_k_dim up to 64 / 128 / 256), one or two
+specialises on: rows per lane (head_k_dim up to 64 / 128 / 256 / 512), one or two
 columns per lane (head_v_dim below 128 or odd vs even from 128), every gate
 width, fp32 and bf16 inputs, and a state updated in place. Bars: normwise
 relative error 1e-4 for fp32 inputs, 2e-2 for bf16 inputs (BASELINE.json
@@ -34,6 +34,10 @@ CASES = [
     (1, 5, 1, 1, 1, 1, 1, 1, torch.float32),
     (2, 24, 4, 128, 256, 1, 1, 1, torch.bfloat16),
     (1, 2, 16, 128, 128, 1, 1, 1, torch.bfloat16),
+    # above 256 state rows: 64 rows a lane, one column a lane
+    (1, 9, 2, 384, 160, 384, 1, 384, torch.float32),
+    (2, 6, 2, 512, 128, 1, 128, 1, torch.float32),
+    (1, 8, 2, 512, 256, 1, 1, 1, torch.bfloat16),
 ]
 
 
