@@ -263,17 +263,33 @@ void mfma_intra_kernel(MfmaParams p, int G, BwdTiles bt, FeParams fe) {
   // wait on them lands at the top of the loop.
   uint4 pend[6];
   int pend_cid = -1;
+  // The forward stores them packed (mfma_util.hpp: kTriTrio elements per
+  // chunk-head from p.T on, the blocks above the diagonal band left out);
+  // the backward's recompute (BT) as full [64][64] tiles.
   auto store_pending = [&]() {
     const int row = tid / 4, c0 = 16 * (tid % 4);
-    const size_t off = size_t(pend_cid) * kL * kL + row * kL + c0;
-    uint4* tdst = reinterpret_cast<uint4*>(p.T + off);
-    uint4* ldst = reinterpret_cast<uint4*>(p.Tlo + off);
+    uint16_t *tp, *lp, *ap;
+    if constexpr (BT) {
+      const size_t off = size_t(pend_cid) * kL * kL + row * kL + c0;
+      tp = p.T + off;
+      lp = p.Tlo + off;
+      ap = attn_out ? p.attn + off : nullptr;
+    } else {
+      const int tb = row >> 4, kk = c0 >> 5;
+      if (tb < 2 && kk == 1) return;  // above the band: zero
+      tp = p.T + size_t(pend_cid) * kTriTrio + tril_step(tb, kk) * kTriBlk + (row & 15) * 32 +
+           (c0 & 31);
+      lp = tp + kTriPacked;
+      ap = tp + 2 * kTriPacked;
+    }
+    uint4* tdst = reinterpret_cast<uint4*>(tp);
+    uint4* ldst = reinterpret_cast<uint4*>(lp);
     tdst[0] = pend[0];
     tdst[1] = pend[1];
     ldst[0] = pend[2];
     ldst[1] = pend[3];
     if (attn_out) {
-      uint4* adst = reinterpret_cast<uint4*>(p.attn + off);
+      uint4* adst = reinterpret_cast<uint4*>(ap);
       adst[0] = pend[4];
       adst[1] = pend[5];
     }

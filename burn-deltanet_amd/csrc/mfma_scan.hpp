@@ -124,8 +124,16 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
                 oTl = oT + kL * kL, oAt = oTl + kL * kL, oKc = oAt + kL * kL,
                 BUF = NKQ * kL * K + NLL * kL * kL + (PC ? K * kL : 0);
   constexpr int C16 = BUF / 8;    // 16-byte chunks per chunk's tiles
-  static_assert(C16 % NT == 0, "staging assumes whole rounds");
-  constexpr int NPF = C16 / NT;   // chunks staged per lane
+  // The forward with per-head gates (not the states mode) reads T, T lo and
+  // attn packed, kTriTrio elements per chunk-head from p.T (mfma_util.hpp);
+  // a packed round's last lanes may idle, in whole waves.
+  constexpr bool kCT = !PC && !ST;
+  constexpr int NKQC = NKQ * kL * K / 8;           // 16-byte chunks of the K-wide tiles
+  constexpr int NCT = NLL * kTriPacked / 8;        // of the packed [64][64] tiles
+  static_assert(NKQC % NT == 0 && NCT % 64 == 0, "staging rounds");
+  static_assert(kCT || C16 % NT == 0, "staging assumes whole rounds");
+  constexpr int NRC = kCT ? (NCT + NT - 1) / NT : 1;  // packed rounds
+  constexpr int NPF = kCT ? NKQC / NT + NRC : C16 / NT;  // chunks staged per lane
   constexpr int NBUF = PC || K > 128 ? 1 : 2;
   __shared__ __attribute__((aligned(16))) uint16_t tiles[NBUF][BUF];
   __shared__ float gxe[NBUF][kL], gwr[NBUF][kL], gys[NBUF][kL], gegl[NBUF];
@@ -213,6 +221,10 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
           const uint32_t klast = uint32_t((rl - 1) * HK) + kcol;
           pf[m] = ld16((which ? p.q : p.k) + row0 * K, min(koff + rowc * uint32_t(HK), klast));
         }
+      } else if constexpr (kCT) {
+        const int cc0 = i0 - NKQC;  // the round's first packed chunk
+        if (cc0 + NT <= NCT || tid < NCT - cc0)
+          pf[m] = ld16(p.T + cid * kTriTrio, 8u * uint32_t(cc0 + tid));
       } else if (i0 < (NKQ * kL * K + NLL * kL * kL) / 8) {
         const int ii0 = i0 - NKQ * kL * K / 8;
         const int which = ii0 / (kL * kL / 8);
@@ -251,6 +263,21 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   const int aK0x = K >= 128 ? addr_k(8, 0) : aK0;
   const int aK1x = K >= 128 ? addr_k(8, 1) : aK1;
   const int a60 = tile_at<kL>(r6, perm_pos(8 * c6)), a61 = tile_at<kL>(r6, perm_pos(8 * c6 + 4));
+  // Packed chunk NT·j + tid: tile `which`, block st (rows 16·tril_tb(st) …,
+  // columns 32·tril_kk(st) …), row r and column group cg inside it.
+  int cb0[NRC], cb1[NRC];
+  if constexpr (kCT) {
+#pragma unroll
+    for (int j = 0; j < NRC; ++j) {
+      const int cc = NT * j + tid;
+      const int which = cc / (kTriPacked / 8), ci = cc % (kTriPacked / 8);
+      const int st = ci >> 6, r = (ci >> 2) & 15, cg = ci & 3;
+      const int row = 16 * tril_tb(st) + r, col = 32 * tril_kk(st) + 8 * cg;
+      const int base = which == 0 ? oT : which == 1 ? oTl : oAt;
+      cb0[j] = base + tile_at<kL>(row, perm_pos(col));
+      cb1[j] = base + tile_at<kL>(row, perm_pos(col + 4));
+    }
+  }
   auto stage = [&](int buf, int m0, int m1) {
     uint16_t* tl = tiles[buf];
 #pragma unroll
@@ -265,6 +292,11 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
         const bool flip = K >= 128 && (dr & 8);
         b0 = base + (flip ? aK0x : aK0);
         b1 = base + (flip ? aK1x : aK1);
+      } else if constexpr (kCT) {
+        const int cc0 = i0 - NKQC;
+        if (!(cc0 + NT <= NCT || tid < NCT - cc0)) continue;
+        b0 = cb0[cc0 / NT];
+        b1 = cb1[cc0 / NT];
       } else if (i0 < (NKQ * kL * K + NLL * kL * kL) / 8) {
         const int ii0 = i0 - NKQ * kL * K / 8;
         const int which = ii0 / (kL * kL / 8), dr = (ii0 - which * (kL * kL / 8)) / LC8;

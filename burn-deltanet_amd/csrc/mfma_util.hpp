@@ -107,5 +107,15 @@ __device__ inline uint4 frag_lo(const f32x4& a, const f32x4& b, const uint4& h) 
 constexpr int kTriSteps = 6;
 __host__ __device__ constexpr int tril_tb(int s) { return s < 2 ? s : 2 + ((s - 2) >> 1); }
 __host__ __device__ constexpr int tril_kk(int s) { return s < 2 ? 0 : (s - 2) & 1; }
+__host__ __device__ constexpr int tril_step(int tb, int kk) { return tb < 2 ? tb : 2 * tb - 2 + kk; }
+
+// The forward's T, T lo and attn of a chunk-head in HBM, packed: each
+// lower-triangular 64×64 tile as its six nonzero 16×32 blocks (in step order,
+// row-major inside a block), the three tiles back to back. The two blocks
+// above the diagonal band are never stored or read: a quarter less tile
+// traffic between the intra kernel and the scan.
+constexpr int kTriBlk = 16 * 32;
+constexpr int kTriPacked = kTriSteps * kTriBlk;  // elements per packed tile
+constexpr int kTriTrio = 3 * kTriPacked;         // per chunk-head
 
 }  // namespace dn
