@@ -265,11 +265,12 @@ void mfma_intra_kernel(MfmaParams p, int G, BwdTiles bt, FeParams fe) {
   int pend_cid = -1;
   // The forward stores them packed (mfma_util.hpp: kTriTrio elements per
   // chunk-head from p.T on, the blocks above the diagonal band left out);
-  // the backward's recompute (BT) as full [64][64] tiles.
+  // the backward's recompute (BT) and head_k_dim 256 as full [64][64] tiles
+  // (tri_packed).
   auto store_pending = [&]() {
     const int row = tid / 4, c0 = 16 * (tid % 4);
     uint16_t *tp, *lp, *ap;
-    if constexpr (BT) {
+    if constexpr (!tri_packed(K, BT)) {
       const size_t off = size_t(pend_cid) * kL * kL + row * kL + c0;
       tp = p.T + off;
       lp = p.Tlo + off;

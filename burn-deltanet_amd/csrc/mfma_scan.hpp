@@ -127,7 +127,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   // The forward with per-head gates (not the states mode) reads T, T lo and
   // attn packed, kTriTrio elements per chunk-head from p.T (mfma_util.hpp);
   // a packed round's last lanes may idle, in whole waves.
-  constexpr bool kCT = !PC && !ST;
+  constexpr bool kCT = !PC && tri_packed(K, ST);
   constexpr int NKQC = NKQ * kL * K / 8;           // 16-byte chunks of the K-wide tiles
   constexpr int NCT = NLL * kTriPacked / 8;        // of the packed [64][64] tiles
   static_assert(NKQC % NT == 0 && NCT % 64 == 0, "staging rounds");

@@ -117,5 +117,12 @@ __host__ __device__ constexpr int tril_step(int tb, int kk) { return tb < 2 ? tb
 constexpr int kTriBlk = 16 * 32;
 constexpr int kTriPacked = kTriSteps * kTriBlk;  // elements per packed tile
 constexpr int kTriTrio = 3 * kTriPacked;         // per chunk-head
+// Whether the per-head forward's intra kernel and scan pass the tiles
+// packed: not for the backward's recompute (its transposing reads take full
+// tiles), nor at head_k_dim 256, whose single-buffered scan ran slower on
+// packed tiles (B=8 T=4096 H=16 dv=256: 0.68 → 0.86 ms).
+__host__ __device__ constexpr bool tri_packed(int K, bool backward) {
+  return !backward && K <= 128;
+}
 
 }  // namespace dn
