@@ -611,9 +611,10 @@ int dn_chunk_bwd(const dn_chunk_bwd_args* a, hipStream_t stream) {
   if (int rc = check_bwd(a)) return rc;
   const int algo = bwd_algo(a, bwd_dims(a));
   if (algo < 0)
-    return fail(DN_ERR_UNSUPPORTED, "DN_ALGO_MFMA needs bf16 q/k/v, head_k_dim 64 or 128, "
-                                    "head_v_dim a multiple of 64, and chunk_len 64 with a "
-                                    "per-channel forget gate");
+    return fail(DN_ERR_UNSUPPORTED, "DN_ALGO_MFMA needs bf16 q/k/v, head_k_dim 64 or 128 "
+                                    "(or 256 with per-head gates and head_v_dim a multiple "
+                                    "of 128), head_v_dim a multiple of 64, and chunk_len 64 "
+                                    "with a per-channel forget gate");
   const Dims d = run_dims(bwd_dims(a), algo);
   const size_t need = bwd_workspace(d, algo, a->qkv_dtype);
   void* ws = a->workspace;

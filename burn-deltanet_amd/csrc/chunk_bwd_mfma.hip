@@ -59,6 +59,12 @@ struct CbParams {
   // them by atomics (nothing waits on them); 3: the last, which adds them and
   // stores.
   int vs, voff, pass;
+  // head_k_dim 256 (KA = 2K, per-head gates): each value pass runs as two
+  // launches, one per half of the key channels; phase A contracts over all
+  // KA keys in both and only the first (koff = 0) stores its outputs. rpass:
+  // the pass code (as `pass`) of the sums over key channels (d_g, a width-1
+  // d_erase) across all the launches of a call; `pass` where KA = K.
+  int koff, rpass;
   float *pq, *pk, *pe, *pg, *pw;  // partials of d_q, d_k, d_erase, d_g, width-1 d_write
   // Per-head gates over several passes: each thread's partial sums of dattn
   // and dT (16 fp32 per thread per chunk-head), which the passes before the
@@ -170,15 +176,20 @@ __device__ inline void stage_perm(uint16_t* R, int dst, const uint16_t* src, int
 // product; the score backward (the rest of phase C and phase D's scores) runs
 // once, in the last pass, on the summed dattn and dT. They still store their
 // share of the value-summed gradients (phase B's terms).
-template <int K, int V, bool PC, class TG, bool LASTP = false, bool EARLY = false>
+// KA: the head_k_dim of the tensors; phase A's contractions run over all KA
+// keys and phases B–D over K of them from channel p.koff on (KA = 2K: the
+// key halves of head_k_dim 256, per-head gates).
+template <int K, int V, bool PC, class TG, bool LASTP = false, bool EARLY = false, int KA = K>
 __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   static_assert(!(LASTP && PC), "the per-channel last pass reads its partials at the stores");
+  static_assert(KA == K || (KA == 2 * K && !PC), "key halves: per-head gates");
+  constexpr int KS = KA;  // row stride of q, k, the states and the key-channel outputs
   static_assert(!(EARLY && (PC || LASTP)), "partial score sums: per-head gates, not the last pass");
   constexpr bool F32DY = std::is_same<TG, float>::value;
-  constexpr int TT = kL * kL, TK = kL * K, TV = kL * V;
+  constexpr int TT = kL * kL, TK = kL * K, TKA = kL * KA, TV = kL * V;
   constexpr int OFF_A1 = 4 * TV > 8 * TT ? 4 * TV : 8 * TT;
   constexpr int RBIG = OFF_A1 + 4 * TT;
-  static_assert(5 * TT + (PC ? 3 : 1) * TK <= RBIG, "phase-A operands fit");
+  static_assert(5 * TT + (PC ? 3 : 1) * TKA <= RBIG, "phase-A operands fit");
   static_assert((F32DY ? 6 : 5) * TV <= RBIG, "phase-B operands fit");
   static_assert(4 * TT + 2 * TK <= OFF_A1, "score operands fit");
   constexpr int GP = K + 4;  // fp32 row pitch of the per-channel cumulative gate
@@ -218,8 +229,12 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   auto rowc = [&](int t) { return row_of(min(t, valid - 1)); };
   const size_t o64 = size_t(cid) * kL * kL, oLK = size_t(cid) * kL * K;
   const int VS = p.vs, vo = p.voff;  // row stride and first column of the value axis
-  const float* S0 = p.states + size_t(cid) * K * VS + vo;
-  const float* dSa = p.ds_after + size_t(cid) * K * VS + vo;
+  const float* S0 = p.states + size_t(cid) * KS * VS + vo;
+  const float* dSa = p.ds_after + size_t(cid) * KS * VS + vo;
+  // This launch's first key channel (phases B–D), and whether it stores the
+  // outputs of phase A and accumulates the value-summed dattn and dT.
+  const int koff = KA == K ? 0 : p.koff;
+  const bool store_a = koff == 0;
   const TG* dy = static_cast<const TG*>(p.dy);
   const bool gated = PC || p.gated;
   auto rowi = [&](int ib, int r) { return 16 * ib + 4 * g4 + r; };
@@ -255,8 +270,8 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
     }
   }
 
-  constexpr int NKR = kL * K / 8 / kNT;  // 16-byte chunks per thread of a [64][K] tile
-  static_assert(NKR * kNT * 8 == kL * K, "K-wide staging assumes whole rounds");
+  constexpr int NKR = kL * KA / 8 / kNT;  // 16-byte chunks per thread of a [64][KA] tile
+  static_assert(NKR * kNT * 8 == kL * KA, "K-wide staging assumes whole rounds");
   uint4 tp[5], tk[PC ? 3 : 1][NKR];
   tp[0] = load_perm(p.T + o64, tid);
   tp[1] = load_perm(p.Tlo + o64, tid);
@@ -265,14 +280,14 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   tp[4] = load_perm(p.AtT + o64, tid);
 #pragma unroll
   for (int m = 0; m < NKR; ++m) {
-    const int idx = tid + kNT * m, row = idx / (K / 8), c8 = idx % (K / 8);
+    const int idx = tid + kNT * m, row = idx / (KA / 8), c8 = idx % (KA / 8);
     if constexpr (PC) {
       const size_t o = oLK + size_t(row) * K + 8 * c8;
       tk[0][m] = *reinterpret_cast<const uint4*>(p.Kg + o);
       tk[1][m] = *reinterpret_cast<const uint4*>(p.Kglo + o);
       tk[2][m] = *reinterpret_cast<const uint4*>(p.Kc + o);
     } else {
-      const uint4 x = *reinterpret_cast<const uint4*>(p.k + rowc(row) * K + 8 * c8);
+      const uint4 x = *reinterpret_cast<const uint4*>(p.k + rowc(row) * KS + 8 * c8);
       tk[0][m] = row < valid ? x : make_uint4(0u, 0u, 0u, 0u);
     }
   }
@@ -295,8 +310,8 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   store_perm(R, oAt, tp[4], tid);
 #pragma unroll
   for (int m = 0; m < NKR; ++m) {
-    const int idx = tid + kNT * m, row = idx / (K / 8), c8 = idx % (K / 8);
-    const int at = tile_at<K>(row, 8 * c8);
+    const int idx = tid + kNT * m, row = idx / (KA / 8), c8 = idx % (KA / 8);
+    const int at = tile_at<KA>(row, 8 * c8);
     *reinterpret_cast<uint4*>(&R[oKop + at]) = tk[0][m];
     if constexpr (PC) {
       *reinterpret_cast<uint4*>(&R[oKgl + at]) = tk[1][m];
@@ -307,12 +322,20 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   // ---- phase A's global operands -------------------------------------------
   const bool vwave = wave < V / 16;
   const int col = 16 * wave + r16;  // this lane's value column in phase A
-  float pS[K / 32][8], pD[K / 32][8], vv[4][4], wv[4][4], dyv[2][8];
+  // S₀ and dS for PDEP k-steps at a time: all of them at head_k_dim ≤ 128;
+  // at 256 the first four, each register set reloaded with the k-step four
+  // ahead once its fragments are split.
+  constexpr int KAS = KA / 32, PDEP = KAS > 4 ? 4 : KAS;
+  float pS[PDEP][8], pD[PDEP][8], vv[4][4], wv[4][4], dyv[2][8];
+  auto load_sd = [&](float (&dst)[8], const float* src, int s) {
+#pragma unroll
+    for (int t = 0; t < 8; ++t) dst[t] = src[size_t(32 * s + k8 + t) * VS + col];
+  };
   if (vwave) {
     // S₀ and dS rows 32·s + 8·(lane/16) + t of this lane's column (B operands
     // of kg·S₀ and kc·dS).
 #pragma unroll
-    for (int s = 0; s < K / 32; ++s)
+    for (int s = 0; s < PDEP; ++s)
 #pragma unroll
       for (int t = 0; t < 8; ++t) {
         pS[s][t] = S0[size_t(32 * s + k8 + t) * VS + col];
@@ -384,12 +407,13 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib) X[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < K / 32; ++s) {
+    for (int s = 0; s < KAS; ++s) {
       uint4 sh, sl;
-      split8(pS[s], sh, sl);
+      split8(pS[s % PDEP], sh, sl);
+      if (s + PDEP < KAS) load_sd(pS[s % PDEP], S0, s + PDEP);
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib) {
-        const int at = tile_at<K>(16 * ib + r16, 32 * s + k8);
+        const int at = tile_at<KA>(16 * ib + r16, 32 * s + k8);
         const uint4 a = ld8u(&R[oKop + at]);
         X[ib] = mfma16(a, sh, X[ib]);
         X[ib] = mfma16(a, sl, X[ib]);
@@ -442,12 +466,13 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib) kd[ib] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < K / 32; ++s) {
+      for (int s = 0; s < KAS; ++s) {
         uint4 dh, dl;
-        split8(pD[s], dh, dl);
+        split8(pD[s % PDEP], dh, dl);
+        if (s + PDEP < KAS) load_sd(pD[s % PDEP], dSa, s + PDEP);
 #pragma unroll
         for (int ib = 0; ib < 4; ++ib) {
-          const uint4 a = ld8u(&R[oKc + tile_at<K>(16 * ib + r16, 32 * s + k8)]);
+          const uint4 a = ld8u(&R[oKc + tile_at<KA>(16 * ib + r16, 32 * s + k8)]);
           kd[ib] = mfma16(a, dh, kd[ib]);
           kd[ib] = mfma16(a, dl, kd[ib]);
         }
@@ -482,9 +507,10 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int i = rowi(ib, r);
-        if (i < valid) st(gv, row_of(i) * VS + vo + col, dW[ib][r] * wv[ib][r]);
+        if (store_a && i < valid) st(gv, row_of(i) * VS + vo + col, dW[ib][r] * wv[ib][r]);
         rs[4 * ib + r] = dW[ib][r] * vv[ib][r];
-        if (p.ww != 1 && i < valid) p.dwrite[row_of(i) * VS + vo + col] = rs[4 * ib + r];
+        if (p.ww != 1 && store_a && i < valid)
+          p.dwrite[row_of(i) * VS + vo + col] = rs[4 * ib + r];
       }
     if (p.ww == 1) atomicAdd(&racc[0][red_row], reduce16(rs, lane));
   }
@@ -515,8 +541,8 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   if (kwave) {
 #pragma unroll
     for (int s = 0; s < V / 32; ++s) {
-      const float4* s0r = reinterpret_cast<const float4*>(S0 + size_t(c) * VS + 32 * s + k8);
-      const float4* dsr = reinterpret_cast<const float4*>(dSa + size_t(c) * VS + 32 * s + k8);
+      const float4* s0r = reinterpret_cast<const float4*>(S0 + size_t(koff + c) * VS + 32 * s + k8);
+      const float4* dsr = reinterpret_cast<const float4*>(dSa + size_t(koff + c) * VS + 32 * s + k8);
       *reinterpret_cast<float4*>(bS[s]) = s0r[0];
       *reinterpret_cast<float4*>(bS[s] + 4) = s0r[1];
       *reinterpret_cast<float4*>(bD[s]) = dsr[0];
@@ -630,7 +656,7 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   float* const da = PC || !p.pda ? nullptr : p.pda + (size_t(cid) * kNT + tid) * 16;
   f32x4 pda_r[4];
   if constexpr (!PC) {
-    if (LASTP || (EARLY && p.pass == 2))
+    if (LASTP || (EARLY && p.pass == 2 && store_a))
 #pragma unroll
       for (int j = 0; j < 4; ++j) pda_r[j] = reinterpret_cast<const f32x4*>(da)[j];
   }
@@ -664,13 +690,14 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
       }
   }
   if constexpr (!PC) {
-    if (LASTP || (EARLY && p.pass == 2))
+    if (LASTP || (EARLY && p.pass == 2 && store_a))
 #pragma unroll
       for (int u = 0; u < 2; ++u) dat[u] += pda_r[u];
   }
   if constexpr (EARLY) {
+    if (store_a)
 #pragma unroll
-    for (int u = 0; u < 2; ++u) reinterpret_cast<f32x4*>(da)[u] = dat[u];
+      for (int u = 0; u < 2; ++u) reinterpret_cast<f32x4*>(da)[u] = dat[u];
   }
   // dAqk = tril(dattn) (per-head decay: ⊙ e^{Gᵢ−Gⱼ}, the head mask) as
   // [i][j] and as [j][i] (per-head: times the readout scale).
@@ -725,13 +752,14 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   }
   __syncthreads();
   if constexpr (!PC) {
-    if (LASTP || (EARLY && p.pass == 2))
+    if (LASTP || (EARLY && p.pass == 2 && store_a))
 #pragma unroll
       for (int u = 0; u < 2; ++u) dTt[u] += pda_r[2 + u];
   }
   if constexpr (EARLY) {
+    if (store_a)
 #pragma unroll
-    for (int u = 0; u < 2; ++u) reinterpret_cast<f32x4*>(da)[2 + u] = dTt[u];
+      for (int u = 0; u < 2; ++u) reinterpret_cast<f32x4*>(da)[2 + u] = dTt[u];
   } else {
     // dTᵀ with dT's row index permuted (it is the contraction index of dTᵀ·T);
     // T and Tᵀ staged again.
@@ -832,8 +860,8 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   }
   for (int idx = tid; idx < kL * K / 8; idx += kNT) {
     const int i = idx / (K / 8), c8 = idx % (K / 8);
-    uint4 kv = *reinterpret_cast<const uint4*>(p.k + rowc(i) * K + 8 * c8);
-    uint4 qv = *reinterpret_cast<const uint4*>(p.q + rowc(i) * K + 8 * c8);
+    uint4 kv = *reinterpret_cast<const uint4*>(p.k + rowc(i) * KS + koff + 8 * c8);
+    uint4 qv = *reinterpret_cast<const uint4*>(p.q + rowc(i) * KS + koff + 8 * c8);
     if (i >= valid) kv = qv = make_uint4(0u, 0u, 0u, 0u);
     const uint32_t kw[4] = {kv.x, kv.y, kv.z, kv.w}, qw[4] = {qv.x, qv.y, qv.z, qv.w};
 #pragma unroll
@@ -855,7 +883,7 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
       for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const size_t at = rowc(rowi(ib, r)) * K + c;
+          const size_t at = rowc(rowi(ib, r)) * KS + koff + c;
           pre_q[4 * ib + r] = p.pq[at];
           pre_k[4 * ib + r] = p.pk[at];
         }
@@ -863,8 +891,11 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
     if (wave == 0) {
       const size_t at = rowc(lane);
       if (p.ww == 1) pre_w = p.pw[at];
-      pre_e = p.pe[at];
-      if (gated) pre_g = p.pg[at];
+      // (key halves: the sums over key channels go through st_sum(rpass))
+      if constexpr (KA == K) {
+        pre_e = p.pe[at];
+        if (gated) pre_g = p.pg[at];
+      }
     }
   }
   if (kwave) {
@@ -1088,10 +1119,10 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
           for (int r = 0; r < 4; ++r) {
             const int i = rowi(pb, r);
             const bool ok = i < valid;
-            if (ok) st_sum(p.pass, gq, p.pq, row_of(i) * K + c, dqA[pb][r] * p.scale);
+            if (ok) st_sum(p.pass, gq, p.pq, row_of(i) * KS + koff + c, dqA[pb][r] * p.scale);
             dkA[pb][r] += dkeA[pb][r] * eA[pb][r];
             rde[r] = dkeA[pb][r] * kv[r];
-            if (p.ew != 1 && ok) st_sum(p.pass, p.derase, p.pe, row_of(i) * K + c, rde[r]);
+            if (p.ew != 1 && ok) st_sum(p.pass, p.derase, p.pe, row_of(i) * KS + koff + c, rde[r]);
           }
           if (p.ew == 1) {
             const float tot4 = reduce4(rde, lane);
@@ -1117,7 +1148,7 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int i = rowi(ib, r);
-          if (i < valid) st_sum(p.pass, gk, p.pk, row_of(i) * K + c, dkA[ib][r]);
+          if (i < valid) st_sum(p.pass, gk, p.pk, row_of(i) * KS + koff + c, dkA[ib][r]);
         }
     } else {
       float rde[16];
@@ -1130,7 +1161,7 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
           const int i = rowi(ib, r);
           const bool ok = i < valid;
           if (ok) {
-            const size_t at = row_of(i) * K + c;
+            const size_t at = row_of(i) * KS + koff + c;
             const float vq = dqA[ib][r] * p.scale, vk = dkA[ib][r] + dkeA[ib][r] * er_s[i];
             if constexpr (LASTP) {
               st_pre(p.pass, gq, p.pq, at, vq, pre_q[4 * ib + r]);
@@ -1141,7 +1172,8 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
             }
           }
           rde[4 * ib + r] = dkeA[ib][r] * kv[r];
-          if (p.ew != 1 && ok) st_sum(p.pass, p.derase, p.pe, row_of(i) * K + c, rde[4 * ib + r]);
+          if (p.ew != 1 && ok)
+            st_sum(p.pass, p.derase, p.pe, row_of(i) * KS + koff + c, rde[4 * ib + r]);
         }
       }
       if (p.ew == 1) atomicAdd(&racc[1][red_row], reduce16(rde, lane));
@@ -1174,7 +1206,7 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
         for (int r = 0; r < 4; ++r) {
           const int i = rowi(ib, r);
           if (i < valid)
-            st_sum(p.pass, p.dg, p.pg, row_of(i) * K + c, dgA[ib][r] + after[ib] + carry);
+            st_sum(p.pass, p.dg, p.pg, row_of(i) * KS + koff + c, dgA[ib][r] + after[ib] + carry);
         }
         carry += blk[ib];
       }
@@ -1190,20 +1222,25 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
         if (lane + off < 64) v += t;
       }
       if (lane < valid) {
-        if constexpr (LASTP)
+        if constexpr (LASTP && KA == K)
           st_pre(p.pass, p.dg, p.pg, row_of(lane), v, pre_g);
         else
-          st_sum(p.pass, p.dg, p.pg, row_of(lane), v);
+          st_sum(p.rpass, p.dg, p.pg, row_of(lane), v);
       }
     }
   }
   if (tid < valid) {
     if constexpr (LASTP) {
-      if (p.ww == 1) st_pre(p.pass, p.dwrite, p.pw, row_of(tid), racc[0][tid], pre_w);
-      if (p.ew == 1) st_pre(p.pass, p.derase, p.pe, row_of(tid), racc[1][tid], pre_e);
+      if (p.ww == 1 && store_a) st_pre(p.pass, p.dwrite, p.pw, row_of(tid), racc[0][tid], pre_w);
+      if (p.ew == 1) {
+        if constexpr (KA == K)
+          st_pre(p.pass, p.derase, p.pe, row_of(tid), racc[1][tid], pre_e);
+        else
+          st_sum(p.rpass, p.derase, p.pe, row_of(tid), racc[1][tid]);
+      }
     } else {
-      if (p.ww == 1) st_sum(p.pass, p.dwrite, p.pw, row_of(tid), racc[0][tid]);
-      if (p.ew == 1) st_sum(p.pass, p.derase, p.pe, row_of(tid), racc[1][tid]);
+      if (p.ww == 1 && store_a) st_sum(p.pass, p.dwrite, p.pw, row_of(tid), racc[0][tid]);
+      if (p.ew == 1) st_sum(p.rpass, p.derase, p.pe, row_of(tid), racc[1][tid]);
     }
   }
 }
@@ -1211,21 +1248,25 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
 }  // namespace
 
 // head_v_dim 64 or 128 in one pass; above 128 in passes of 128 columns, the
-// last of 64 when head_v_dim is an odd multiple of 64.
+// last of 64 when head_v_dim is an odd multiple of 64. head_k_dim 256 with
+// per-head gates: each pass as two launches over the halves of the keys.
 bool mfma_chunk_bwd_supported(const Dims& d, int qkv_dtype) {
-  return d.K <= 128 && mfma_fwd_supported(d, qkv_dtype, DN_BF16) && d.V % 64 == 0;
+  if (!(mfma_fwd_supported(d, qkv_dtype, DN_BF16) && d.V % 64 == 0)) return false;
+  if (d.K == 256) return d.dw <= 1 && d.ew == 1 && d.ww == 1;
+  return d.K <= 128;
 }
 
 // The fp32 partial sums of the value-summed gradients across the passes:
 // per (token, head) d_q, d_k (K each), d_erase (ew), d_g (dw) and d_write
-// (1 when its width is 1). None for a single pass.
+// (1 when its width is 1). None for a single pass of a single launch (at
+// head_k_dim 256 the key halves add d_g and d_erase across launches).
 size_t mfma_chunk_bwd_partials(const Dims& d) {
-  if (d.V <= 128) return 0;
+  if (d.V <= 128 && d.K <= 128) return 0;
   const size_t rows = size_t(d.B) * d.S * d.H;
   const bool pc = d.dw == d.K && d.K > 1;
   const size_t G = size_t(d.B) * d.N * d.H;
   return align_up(rows * (2 * d.K + d.ew + d.dw + (d.ww == 1 ? 1 : 0)) * sizeof(float), 256) +
-         (pc ? 0 : G * kNT * 16 * sizeof(float));  // dattn and dT partial sums
+         (pc || d.V <= 128 ? 0 : G * kNT * 16 * sizeof(float));  // dattn and dT partial sums
 }
 
 hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const void* q,
@@ -1279,7 +1320,8 @@ hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const v
   p.pg = p.pe ? p.pe + rows * d.ew : nullptr;
   p.pw = p.pg ? p.pg + rows * d.dw : nullptr;
   p.pda = nullptr;
-  if (partials && !pc) {
+  p.koff = 0;
+  if (partials && !pc && d.V > 128) {
     const size_t head = align_up(rows * (2 * d.K + d.ew + d.dw + (d.ww == 1 ? 1 : 0)) *
                                      sizeof(float), 256);
     p.pda = reinterpret_cast<float*>(reinterpret_cast<char*>(partials) + head);
@@ -1309,10 +1351,48 @@ hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const v
     if (pc) DN_CB_T(KD, VD, true);        \
     else DN_CB_T(KD, VD, false);          \
   } while (0)
+  if (d.K == 256) {
+    // Per value pass, the two key halves; the sums over key channels pass
+    // through the partials across all 2·passes launches (rpass).
+#define DN_CB2(VD, TG, LP, EP)                                                                   \
+  hipLaunchKernelGGL((mfma_chunk_bwd_kernel<128, VD, false, TG, LP, EP, 256>), dim3(unsigned(G)), \
+                     dim3(kNT), 0, stream, p)
+#define DN_CB2_K(VD, LP, EP)                    \
+  do {                                          \
+    if (f32) DN_CB2(VD, float, LP, EP);         \
+    else DN_CB2(VD, bf16, LP, EP);              \
+  } while (0)
+    const int launches = 2 * passes;
+    for (int i = 0; i < passes; ++i) {
+      const int vd = passes == 1 ? int(d.V) : i + 1 < passes || d.V % 128 == 0 ? 128 : 64;
+      p.voff = 128 * i;
+      p.pass = passes == 1 ? 0 : i == 0 ? 1 : i + 1 == passes ? 3 : 2;
+      for (int half = 0; half < 2; ++half) {
+        const int j = 2 * i + half;
+        p.koff = 128 * half;
+        p.rpass = j == 0 ? 1 : j + 1 == launches ? 3 : 2;
+        if (p.pass == 3) {
+          if (vd == 128) DN_CB2_K(128, true, false); else DN_CB2_K(64, true, false);
+        } else if (p.pass != 0) {
+          DN_CB2_K(128, false, true);
+        } else if (vd == 128) {
+          DN_CB2_K(128, false, false);
+        } else {
+          DN_CB2_K(64, false, false);
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+      }
+    }
+#undef DN_CB2_K
+#undef DN_CB2
+    return hipGetLastError();
+  }
   for (int i = 0; i < passes; ++i) {
     const int vd = passes == 1 ? int(d.V) : i + 1 < passes || d.V % 128 == 0 ? 128 : 64;
     p.voff = 128 * i;
     p.pass = passes == 1 ? 0 : i == 0 ? 1 : i + 1 == passes ? 3 : 2;
+    p.rpass = p.pass;
     if (p.pass == 3 && !pc) {
       if (d.K == 128) {
         if (f32) DN_CB_LV(128, float); else DN_CB_LV(128, bf16);

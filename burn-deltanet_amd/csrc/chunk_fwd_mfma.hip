@@ -973,7 +973,8 @@ __global__ __launch_bounds__(256) void seg_carry_kernel(MfmaParams p) {
 // Same layout as the forward scan: one workgroup per (b, h, 16·W value
 // columns), a wave owns 16 columns and all K state rows of dS in fp32 MFMA
 // accumulators; the chunk's tiles (Kc, attnᵀ, Tᵀ hi/lo, Qgᵀ, Kgᵀ) are staged
-// once in double-buffered LDS with the same k-permutation. dS is read as bf16
+// once in double-buffered LDS with the same k-permutation (head_k_dim 256:
+// 120 KB a chunk, single-buffered between two barriers). dS is read as bf16
 // hi + lo parts, dV' likewise for Tᵀ·dV'.
 struct RevParams {
   int B, S, H, V, N;
@@ -998,8 +999,9 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_rev_scan_kernel(RevParams p) 
   constexpr int NPF = C16 / NT;
   constexpr int NK = kL * K / 8;                   // 16-byte chunks of the K-wide tile
   constexpr int N64 = 3 * kL * kL / 8;             // of the three 64×64 tiles
-  __shared__ __attribute__((aligned(16))) uint16_t tiles[2][BUF];
-  __shared__ float gch[2][K];
+  constexpr int NBUF = K > 128 ? 1 : 2;
+  __shared__ __attribute__((aligned(16))) uint16_t tiles[NBUF][BUF];
+  __shared__ float gch[NBUF][K];
 
   const int ntile = p.V / BW;
   const int BH = p.B * p.H;
@@ -1120,7 +1122,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_rev_scan_kernel(RevParams p) 
   __syncthreads();
   for (int it = 0; it < p.N; ++it) {
     const int n = p.N - 1 - it;
-    const int cur = it & 1;
+    const int cur = NBUF == 1 ? 0 : (it & 1);
     const int nn = n > 0 ? n - 1 : n;  // the first chunk prefetches itself again
     const uint16_t* tl = tiles[cur];
     {
@@ -1252,7 +1254,12 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_rev_scan_kernel(RevParams p) 
         dS[rb] = mfma16(ld8(&tl[oKg + at]), as8(zf[kk]), dS[rb]);
       }
     }
-    stage(cur ^ 1);
+    if constexpr (NBUF == 1) {
+      __syncthreads();  // every wave is done with this chunk's tiles
+      stage(0);
+    } else {
+      stage(cur ^ 1);
+    }
     __syncthreads();
   }
   float* dout = p.dstate + size_t(bh) * K * p.V + jl;
@@ -1443,8 +1450,7 @@ hipError_t launch_intra(const MfmaParams& p, const Dims& d, hipStream_t stream,
     else DN_INTRA(KD, false, BTV);                       \
   } while (0)
     if (d.K == 256) {
-      if (bt) return hipErrorInvalidValue;  // head_k_dim 256: the forward only
-      DN_INTRA_G(256, false);
+      if (bt) DN_INTRA_G(256, true); else DN_INTRA_G(256, false);
     } else if (d.K == 128) {
       if (bt) DN_INTRA_G(128, true); else DN_INTRA_G(128, false);
     } else {
@@ -1562,11 +1568,12 @@ hipError_t launch_scan(const MfmaParams& p, const Dims& d, bool yb, hipStream_t 
 #define DN_SCAN_W(KD, TY) \
   do { if (waves == 8) DN_SCAN(KD, TY, 8); else if (waves == 4) DN_SCAN(KD, TY, 4); else DN_SCAN(KD, TY, 2); } while (0)
   if (d.K == 256) {
-    // head_k_dim 256: per-head gates, the forward only.
+    // head_k_dim 256: per-head gates, eight-wave workgroups.
+    if (pc || waves != 8) return hipErrorInvalidValue;
     if constexpr (ST) {
-      return hipErrorInvalidValue;
+      hipLaunchKernelGGL((mfma_scan_kernel<256, float, 8, false, true>), dim3(blocks), dim3(512),
+                         0, stream, p);
     } else {
-      if (pc || waves != 8) return hipErrorInvalidValue;
       if (yb)
         hipLaunchKernelGGL((mfma_scan_kernel<256, bf16, 8, false>), dim3(blocks), dim3(512), 0,
                            stream, p);
@@ -1659,12 +1666,14 @@ bool mfma_fwd_supported(const Dims& d, int qkv_dtype, int y_dtype) {
 }
 
 // The MFMA backward: its chunk-local kernel and scans know the per-head
-// gates and the all-per-channel ones (GDN-2), at head_k_dim 64 and 128;
-// per-channel erase or write gates beside a per-head forget gate, and
-// head_k_dim 256, take the generic kernels.
+// gates and the all-per-channel ones (GDN-2), at head_k_dim 64 and 128, and
+// the per-head gates at head_k_dim 256; per-channel erase or write gates
+// beside a per-head forget gate take the generic kernels.
 bool mfma_bwd_supported(const Dims& d, int qkv_dtype) {
-  return d.K <= 128 && mfma_fwd_supported(d, qkv_dtype, DN_BF16) &&
-         (per_channel(d) || (d.ew == 1 && d.ww == 1));
+  if (!mfma_fwd_supported(d, qkv_dtype, DN_BF16)) return false;
+  // head_k_dim 256: per-head gates (the forward's condition), width-1 gates
+  if (d.K == 256) return true;
+  return d.K <= 128 && (per_channel(d) || (d.ew == 1 && d.ww == 1));
 }
 
 size_t mfma_fwd_workspace(const Dims& d, bool fused) {
@@ -1812,7 +1821,10 @@ hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
   hipLaunchKernelGGL((mfma_rev_scan_kernel<KD, TG, W>), dim3(blocks), dim3(64 * W), 0, side, rp)
 #define DN_REV_W(KD, TG) \
   do { if (waves == 8) DN_REV(KD, TG, 8); else if (waves == 4) DN_REV(KD, TG, 4); else DN_REV(KD, TG, 2); } while (0)
-  if (d.K == 128) {
+  if (d.K == 256) {
+    // eight waves (head_v_dim a multiple of 128)
+    if (grad_dtype == DN_BF16) DN_REV(256, bf16, 8); else DN_REV(256, float, 8);
+  } else if (d.K == 128) {
     if (grad_dtype == DN_BF16) DN_REV_W(128, bf16); else DN_REV_W(128, float);
   } else {
     if (grad_dtype == DN_BF16) DN_REV_W(64, bf16); else DN_REV_W(64, float);

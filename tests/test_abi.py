@@ -307,9 +307,9 @@ def bwd_args(**over):
 def test_head_k_dim_256_forward_runs_mfma():
     """head_k_dim 256 with per-head (or no) gates and head_v_dim a multiple of
     128: the forward runs the MFMA kernels under AUTO (its scan in eight-wave
-    workgroups of 128 value columns); per-channel gates, other value widths,
-    the one-kernel forward and the backward stay on the generic kernels
-    there. No pointer is read."""
+    workgroups of 128 value columns), and so does the backward with per-head
+    gates; per-channel gates, other value widths and the one-kernel forward
+    stay on the generic kernels there. No pointer is read."""
     lib = abi.lib()
     MFMA, GEN = abi.DN_ALGO_MFMA, abi.DN_ALGO_GENERIC
     base = dict(batch=2, sequence=1000, nheads=4, head_k_dim=256, head_v_dim=256,
@@ -324,9 +324,13 @@ def test_head_k_dim_256_forward_runs_mfma():
         assert lib.dn_chunk_fwd_algo(ctypes.byref(a)) == (MFMA if auto == MFMA else -9), over
     a = fwd_args(**base, algo=abi.DN_ALGO_MFMA_FUSED)
     assert lib.dn_chunk_fwd_algo(ctypes.byref(a)) == -9
-    b = bwd_args(head_k_dim=256)
-    assert lib.dn_chunk_bwd_algo(ctypes.byref(b)) == GEN
-    assert lib.dn_chunk_bwd_algo(ctypes.byref(bwd_args(head_k_dim=256, algo=MFMA))) == -9
+    for over, auto in ((dict(), MFMA), (dict(has_gate=0), MFMA), (dict(head_v_dim=512), MFMA),
+                       (dict(head_v_dim=192), GEN), (dict(erase_width=256), GEN),
+                       (dict(decay_width=256), GEN)):
+        b = bwd_args(**{**dict(head_k_dim=256, head_v_dim=256), **over})
+        assert lib.dn_chunk_bwd_algo(ctypes.byref(b)) == auto, over
+        b = bwd_args(**{**dict(head_k_dim=256, head_v_dim=256), **over}, algo=MFMA)
+        assert lib.dn_chunk_bwd_algo(ctypes.byref(b)) == (MFMA if auto == MFMA else -9), over
 
 
 def test_mfma_backward_needs_a_16_byte_aligned_d_y():

@@ -88,7 +88,7 @@ def test_mfma_head_k_dim_256_fp32_y_in_place_and_chunk_len(rng):
     """head_k_dim 256: fp32 y with the state updated in place, and a request
     for chunk_len 128 served by the 64-token kernels, against the oracle's
     chunk forward at the requested length; the backward at this width takes
-    the generic kernels under AUTO."""
+    the MFMA kernels under AUTO."""
     announce("mfma fwd head_k_dim 256: fp32 y in place, chunk_len 128")
     args = gdn_inputs(rng, 1, 260, 2, 256, 128, True, 1.0, 0.02)
     g_args = to_gpu(args, torch.bfloat16)
@@ -115,7 +115,7 @@ def test_mfma_head_k_dim_256_fp32_y_in_place_and_chunk_len(rng):
              torch.empty(v.shape, device=DEV), torch.empty_like(e), torch.empty_like(w),
              torch.empty_like(g), torch.empty_like(s_in))
     b = pkg.abi.chunk_bwd_args(dy, None, q, k, v, e, w, g, s_in, grads, 64, None)
-    assert pkg.abi.lib().dn_chunk_bwd_algo(b) == pkg.abi.DN_ALGO_GENERIC
+    assert pkg.abi.lib().dn_chunk_bwd_algo(b) == MFMA
 
 
 def test_mfma_matches_generic_path(rng):
@@ -364,6 +364,15 @@ BWD_CASES = [
     (1, 100, 2, 64, 320, "head"),  # 128, 128 (a middle pass), then 64
     (1, 96, 2, 128, 192, None),
     (1, 128, 2, 64, 192, (1, 1)),
+    # head_k_dim 256 (per-head gates): each value pass as two launches over
+    # the halves of the key channels, d_g and d_erase summed across them
+    (1, 128, 2, 256, 128, "head"),
+    (1, 200, 2, 256, 128, None),
+    (1, 192, 2, 256, 128, "head", {"beta_scale": 2.0}),
+    (1, 256, 2, 256, 128, "head", {"const_keys": True}),
+    (1, 128, 2, 256, 256, "head"),
+    (1, 130, 2, 256, 256, None),
+    (1, 150, 2, 256, 384, "head"),  # a middle value pass
 ]
 
 
@@ -442,6 +451,22 @@ def test_mfma_bwd_matches_oracle(rng, case, dy_dtype):
         err = rel_err(np_of(a), b)
         print(f"  {name} rel err {err:.2e}", flush=True)
         assert err < TOL, name
+
+
+@pytest.mark.parametrize("V,gates", [(128, "head"), (256, None)])
+def test_mfma_bwd_head_k_dim_256_is_chosen(rng, V, gates):
+    """AUTO runs the MFMA backward at head_k_dim 256 with per-head gates
+    (the generic fp32 kernels before: 103 ms at the config-2 shape)."""
+    announce(f"mfma bwd head_k_dim 256 chosen V={V} gates={gates}")
+    args, dy, ds = bwd_inputs(rng, 1, 128, 2, 256, V, gates)
+    q, k, v, e, w, g, s = to_gpu(args, torch.bfloat16)
+    tdy = torch.tensor(dy, dtype=torch.float32, device=DEV)
+    tds = torch.tensor(ds, dtype=torch.float32, device=DEV)
+    grads = (torch.empty(q.shape, device=DEV), torch.empty(k.shape, device=DEV),
+             torch.empty(v.shape, device=DEV), torch.empty_like(e), torch.empty_like(w),
+             torch.empty_like(g) if g is not None else None, torch.empty_like(s))
+    a = pkg.abi.chunk_bwd_args(tdy, tds, q, k, v, e, w, g, s, grads, 64, None)
+    assert pkg.abi.lib().dn_chunk_bwd_algo(a) == MFMA
 
 
 def test_mfma_bwd_is_chosen_and_matches_generic(rng):
