@@ -410,7 +410,12 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
     for (int s = 0; s < KAS; ++s) {
       uint4 sh, sl;
       split8(pS[s % PDEP], sh, sl);
-      if (s + PDEP < KAS) load_sd(pS[s % PDEP], S0, s + PDEP);
+      if (s + PDEP < KAS) {
+        // (a scheduling barrier: hoisted to the staging, these reloads
+        // spilled the loaded values there, each load waited for in turn)
+        __builtin_amdgcn_sched_barrier(0);
+        load_sd(pS[s % PDEP], S0, s + PDEP);
+      }
 #pragma unroll
       for (int ib = 0; ib < 4; ++ib) {
         const int at = tile_at<KA>(16 * ib + r16, 32 * s + k8);
@@ -469,7 +474,10 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
       for (int s = 0; s < KAS; ++s) {
         uint4 dh, dl;
         split8(pD[s % PDEP], dh, dl);
-        if (s + PDEP < KAS) load_sd(pD[s % PDEP], dSa, s + PDEP);
+        if (s + PDEP < KAS) {
+          __builtin_amdgcn_sched_barrier(0);
+          load_sd(pD[s % PDEP], dSa, s + PDEP);
+        }
 #pragma unroll
         for (int ib = 0; ib < 4; ++ib) {
           const uint4 a = ld8u(&R[oKc + tile_at<KA>(16 * ib + r16, 32 * s + k8)]);
