@@ -493,11 +493,11 @@ def bench_config5(torch, pkg, steps, warmup):
             "roofline_chunk_bwd": cb_roof, "kernels_fwd": fk, "kernels_bwd": bk}
 
 
-def bench_config2_bwd(torch, pkg, steps, warmup, V=256):
+def bench_config2_bwd(torch, pkg, steps, warmup, V=256, K=128):
     """The custom backward (dn_chunk_bwd: combined_backward) at the config-2
-    shape: B=8, T=4096, H=16, dk=128, dv=256 (or V), per-head gates, bf16
-    q/k/v and dO, fp32 state; the gradients of all seven inputs."""
-    B, T, H, K = 8, 4096, 16, 128
+    shape: B=8, T=4096, H=16, dk=128 (or K), dv=256 (or V), per-head gates,
+    bf16 q/k/v and dO, fp32 state; the gradients of all seven inputs."""
+    B, T, H = 8, 4096, 16
     dev = torch.device("cuda:0")
     q, k, v, beta, g = gdn_inputs(torch, B, T, H, K, V, 0.05, 20260834, torch.bfloat16, dev)
     s0 = torch.zeros((B, H, K, V), dtype=torch.float32, device=dev)
@@ -932,6 +932,11 @@ def main():
         b192 = bench_config2_bwd(torch, pkg, args.extra_steps, MIN_WARMUP, V=192)
         extra["config2_backward"]["head_v_dim_192"] = {
             k: b192[k] for k in ("algo", "ms_per_call", "tokens_per_s", "kernels")}
+        # head_k_dim 256: each value pass of the chunk-local kernel as two
+        # launches over the key halves (103 ms on the generic kernels).
+        b256 = bench_config2_bwd(torch, pkg, args.extra_steps, MIN_WARMUP, K=256)
+        extra["config2_backward"]["head_k_dim_256"] = {
+            k: b256[k] for k in ("algo", "ms_per_call", "tokens_per_s", "roofline", "kernels")}
         print(f"[bench] config2_backward {extra['config2_backward']}", file=sys.stderr,
               flush=True)
         torch.cuda.empty_cache()

@@ -1813,7 +1813,10 @@ hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
   hipStream_t side = nullptr;
   if ((e = side_fork(stream, &side)) != hipSuccess) return e;
   RevParams rp{d.B, d.S, d.H, d.V, d.N, dy, dstate_final, ds_after, dstate, bt};
-  const int waves = scan_waves(d);
+  // head_k_dim 256: four-wave workgroups, whose single wave per SIMD has the
+  // register file for its 256 dS rows and the next chunk's 120 KB of tiles
+  // (eight waves spilled: 5.05 against 3.85 ms at B=8 T=4096 H=16 dv=256).
+  const int waves = d.K == 256 ? 4 : scan_waves(d);
   const unsigned blocks = unsigned(((d.B * d.H + 7) / 8) * 8 * (d.V / (16 * waves)));
   {
   ProfScope ps("dn_mfma_rev_scan", side);
@@ -1822,8 +1825,7 @@ hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
 #define DN_REV_W(KD, TG) \
   do { if (waves == 8) DN_REV(KD, TG, 8); else if (waves == 4) DN_REV(KD, TG, 4); else DN_REV(KD, TG, 2); } while (0)
   if (d.K == 256) {
-    // eight waves (head_v_dim a multiple of 128)
-    if (grad_dtype == DN_BF16) DN_REV(256, bf16, 8); else DN_REV(256, float, 8);
+    if (grad_dtype == DN_BF16) DN_REV(256, bf16, 4); else DN_REV(256, float, 4);
   } else if (d.K == 128) {
     if (grad_dtype == DN_BF16) DN_REV_W(128, bf16); else DN_REV_W(128, float);
   } else {
