@@ -646,8 +646,9 @@ int dn_chunk_bwd(const dn_chunk_bwd_args* a, hipStream_t stream) {
     float* states = reinterpret_cast<float*>(base);
     float* ds_after = reinterpret_cast<float*>(base + bwd_state_bytes(d));
     void* mws = base + 2 * bwd_state_bytes(d);
+    const bool g4 = states_g4(d);
     e = mfma_bwd_scans(d, a->grad_dtype, a->d_y, a->d_state_final, a->q, a->k, a->v, a->erase,
-                       a->write, g, a->state_in, states, ds_after, a->d_state, mws, stream);
+                       a->write, g, a->state_in, states, ds_after, a->d_state, mws, stream, g4);
     if (e == hipSuccess)
       e = mfma_chunk_bwd(
           d, a->grad_dtype, a->d_y, a->q, a->k, a->v, a->erase, a->write, g, states, ds_after,
@@ -657,7 +658,7 @@ int dn_chunk_bwd(const dn_chunk_bwd_args* a, hipStream_t stream) {
               ? reinterpret_cast<float*>(static_cast<char*>(mws) +
                                          align_up(mfma_bwd_workspace(d), 256))
               : nullptr,
-          stream);
+          stream, g4);
   } else {
     e = generic_bwd(d, a->qkv_dtype, a->grad_dtype, a->d_y, a->d_state_final, a->q, a->k, a->v,
                     a->erase, a->write, g, a->state_in, a->d_q, a->d_k, a->d_v, a->d_erase,

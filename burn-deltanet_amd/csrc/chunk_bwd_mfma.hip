@@ -184,6 +184,9 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   static_assert(!(LASTP && PC), "the per-channel last pass reads its partials at the stores");
   static_assert(KA == K || (KA == 2 * K && !PC), "key halves: per-head gates");
   constexpr int KS = KA;  // row stride of q, k, the states and the key-channel outputs
+  // The states and state cotangents in row groups of four, [G][K/4][V][4]
+  // (mfma_bwd_scans' g4, at head_k_dim 256), else [G][K][V].
+  constexpr bool G4 = KA == 256;
   static_assert(!(EARLY && (PC || LASTP)), "partial score sums: per-head gates, not the last pass");
   constexpr bool F32DY = std::is_same<TG, float>::value;
   constexpr int TT = kL * kL, TK = kL * K, TKA = kL * KA, TV = kL * V;
@@ -229,8 +232,11 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   auto rowc = [&](int t) { return row_of(min(t, valid - 1)); };
   const size_t o64 = size_t(cid) * kL * kL, oLK = size_t(cid) * kL * K;
   const int VS = p.vs, vo = p.voff;  // row stride and first column of the value axis
-  const float* S0 = p.states + size_t(cid) * KS * VS + vo;
-  const float* dSa = p.ds_after + size_t(cid) * KS * VS + vo;
+  // Row-major: element (row, column) at S0[row·VS + column]; in row groups
+  // of four at S0[(row/4·VS + column)·4 + row%4] (the pass's first column
+  // is then 4·vo floats in).
+  const float* S0 = p.states + size_t(cid) * KS * VS + (G4 ? 4 * vo : vo);
+  const float* dSa = p.ds_after + size_t(cid) * KS * VS + (G4 ? 4 * vo : vo);
   // This launch's first key channel (phases B–D), and whether it stores the
   // outputs of phase A and accumulates the value-summed dattn and dT.
   const int koff = KA == K ? 0 : p.koff;
@@ -328,19 +334,35 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   constexpr int KAS = KA / 32, PDEP = KAS > 4 ? 4 : KAS;
   float pS[PDEP][8], pD[PDEP][8], vv[4][4], wv[4][4], dyv[2][8];
   auto load_sd = [&](float (&dst)[8], const float* src, int s) {
+    if constexpr (G4) {
+      // rows 32s + k8 … +3 and +4 … +7 of column col: two 16-byte loads
+      const float4* b = reinterpret_cast<const float4*>(src) + size_t(8 * s + 2 * g4) * VS + col;
+      const float4 lo = b[0], hi = b[VS];
+      dst[0] = lo.x; dst[1] = lo.y; dst[2] = lo.z; dst[3] = lo.w;
+      dst[4] = hi.x; dst[5] = hi.y; dst[6] = hi.z; dst[7] = hi.w;
+    } else {
 #pragma unroll
-    for (int t = 0; t < 8; ++t) dst[t] = src[size_t(32 * s + k8 + t) * VS + col];
+      for (int t = 0; t < 8; ++t) dst[t] = src[size_t(32 * s + k8 + t) * VS + col];
+    }
   };
   if (vwave) {
     // S₀ and dS rows 32·s + 8·(lane/16) + t of this lane's column (B operands
     // of kg·S₀ and kc·dS).
+    if constexpr (G4) {
 #pragma unroll
-    for (int s = 0; s < PDEP; ++s)
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-        pS[s][t] = S0[size_t(32 * s + k8 + t) * VS + col];
-        pD[s][t] = dSa[size_t(32 * s + k8 + t) * VS + col];
+      for (int s = 0; s < PDEP; ++s) {
+        load_sd(pS[s], S0, s);
+        load_sd(pD[s], dSa, s);
       }
+    } else {
+#pragma unroll
+      for (int s = 0; s < PDEP; ++s)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          pS[s][t] = S0[size_t(32 * s + k8 + t) * VS + col];
+          pD[s][t] = dSa[size_t(32 * s + k8 + t) * VS + col];
+        }
+    }
 #pragma unroll
     for (int ib = 0; ib < 4; ++ib)
 #pragma unroll
@@ -547,14 +569,27 @@ __global__ __launch_bounds__(kNT) void mfma_chunk_bwd_kernel(CbParams p) {
   const int c = 16 * wave + r16;  // this lane's key channel in phases B and D
   float bS[V / 32][8], bD[V / 32][8], eA[4][4];
   if (kwave) {
+    if constexpr (G4) {
+      // row koff + c: element (koff + c)%4 of each column's row group
+      const int row = koff + c;
+      const size_t o = size_t(row >> 2) * VS * 4 + (row & 3);
 #pragma unroll
-    for (int s = 0; s < V / 32; ++s) {
-      const float4* s0r = reinterpret_cast<const float4*>(S0 + size_t(koff + c) * VS + 32 * s + k8);
-      const float4* dsr = reinterpret_cast<const float4*>(dSa + size_t(koff + c) * VS + 32 * s + k8);
-      *reinterpret_cast<float4*>(bS[s]) = s0r[0];
-      *reinterpret_cast<float4*>(bS[s] + 4) = s0r[1];
-      *reinterpret_cast<float4*>(bD[s]) = dsr[0];
-      *reinterpret_cast<float4*>(bD[s] + 4) = dsr[1];
+      for (int s = 0; s < V / 32; ++s)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          bS[s][t] = S0[o + size_t(32 * s + k8 + t) * 4];
+          bD[s][t] = dSa[o + size_t(32 * s + k8 + t) * 4];
+        }
+    } else {
+#pragma unroll
+      for (int s = 0; s < V / 32; ++s) {
+        const float4* s0r = reinterpret_cast<const float4*>(S0 + size_t(koff + c) * VS + 32 * s + k8);
+        const float4* dsr = reinterpret_cast<const float4*>(dSa + size_t(koff + c) * VS + 32 * s + k8);
+        *reinterpret_cast<float4*>(bS[s]) = s0r[0];
+        *reinterpret_cast<float4*>(bS[s] + 4) = s0r[1];
+        *reinterpret_cast<float4*>(bD[s]) = dsr[0];
+        *reinterpret_cast<float4*>(bD[s] + 4) = dsr[1];
+      }
     }
   }
   __syncthreads();
@@ -1281,7 +1316,9 @@ hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const v
                           const void* k, const void* v, const float* erase, const float* write,
                           const float* g, const float* states, const float* ds_after, void* dq,
                           void* dk, void* dv, float* derase, float* dwrite, float* dg,
-                          const MfmaTiles& tiles, float* partials, hipStream_t stream) {
+                          const MfmaTiles& tiles, float* partials, hipStream_t stream, bool g4) {
+  // The chunk-local kernels read the row-group layout exactly at head_k_dim 256.
+  if (g4 != (d.K == 256)) return hipErrorInvalidValue;
   CbParams p;
   p.S = d.S;
   p.H = d.H;

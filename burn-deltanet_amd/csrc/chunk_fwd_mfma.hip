@@ -985,7 +985,8 @@ struct RevParams {
   BwdTiles bt;
 };
 
-template <int K, class TG, int WAVES>
+// G4: ds_after in row groups of four ([G][K/4][V][4], states_g4).
+template <int K, class TG, int WAVES, bool G4 = false>
 __global__ __launch_bounds__(64 * WAVES) void mfma_rev_scan_kernel(RevParams p) {
   constexpr int KK = K / 32;
   constexpr int RBK = K / 16;
@@ -1125,7 +1126,12 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_rev_scan_kernel(RevParams p) 
     const int cur = NBUF == 1 ? 0 : (it & 1);
     const int nn = n > 0 ? n - 1 : n;  // the first chunk prefetches itself again
     const uint16_t* tl = tiles[cur];
-    {
+    if constexpr (G4) {
+      float4* dst = reinterpret_cast<float4*>(p.ds_after + chunk_of(n) * K * p.V) + jl;
+#pragma unroll
+      for (int rb = 0; rb < RBK; ++rb)
+        dst[size_t(4 * rb + q4) * p.V] = make_float4(dS[rb][0], dS[rb][1], dS[rb][2], dS[rb][3]);
+    } else {
       float* dst = p.ds_after + chunk_of(n) * K * p.V + jl;
 #pragma unroll
       for (int rb = 0; rb < RBK; ++rb)
@@ -1522,8 +1528,10 @@ Dims seg_dims(const Dims& d, int P) {
   return s;
 }
 
+// g4 (ST): write the states in row groups of four (states_g4).
 template <bool ST>
-hipError_t launch_scan(const MfmaParams& p, const Dims& d, bool yb, hipStream_t stream) {
+hipError_t launch_scan(const MfmaParams& p, const Dims& d, bool yb, hipStream_t stream,
+                       bool g4 = false) {
   const bool pc = pc_path(d);
   if constexpr (!ST) {
     if (p.seg) {
@@ -1567,6 +1575,20 @@ hipError_t launch_scan(const MfmaParams& p, const Dims& d, bool yb, hipStream_t 
   } while (0)
 #define DN_SCAN_W(KD, TY) \
   do { if (waves == 8) DN_SCAN(KD, TY, 8); else if (waves == 4) DN_SCAN(KD, TY, 4); else DN_SCAN(KD, TY, 2); } while (0)
+  if constexpr (ST) {
+    if (g4) {
+      // Eight-wave workgroups (head_k_dim 64, 128, 256).
+      if (waves != 8 || (pc && d.K == 256)) return hipErrorInvalidValue;
+#define DN_SCAN_G4(KD, PCV)                                                                    \
+  hipLaunchKernelGGL((mfma_scan_kernel<KD, float, 8, PCV, true, 0, 0, true>), dim3(blocks),     \
+                     dim3(512), 0, stream, p)
+      if (d.K == 256) DN_SCAN_G4(256, false);
+      else if (d.K == 128) { if (pc) DN_SCAN_G4(128, true); else DN_SCAN_G4(128, false); }
+      else { if (pc) DN_SCAN_G4(64, true); else DN_SCAN_G4(64, false); }
+#undef DN_SCAN_G4
+      return hipGetLastError();
+    }
+  }
   if (d.K == 256) {
     // head_k_dim 256: per-head gates, eight-wave workgroups.
     if (pc || waves != 8) return hipErrorInvalidValue;
@@ -1790,11 +1812,13 @@ size_t mfma_bwd_workspace(const Dims& d) {
          region(size_t(d.B) * d.H * K * d.V * 4);  // the recompute's final state (unused)
 }
 
+bool states_g4(const Dims& d) { return d.K == 256; }
+
 hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
                           const float* dstate_final, const void* q, const void* k, const void* v,
                           const float* erase, const float* write, const float* g,
                           const float* state_in, float* states, float* ds_after, float* dstate,
-                          void* ws, hipStream_t stream) {
+                          void* ws, hipStream_t stream, bool g4) {
   const size_t G = size_t(d.B) * d.N * d.H, K = size_t(d.K);
   // The forward recompute (states mode) and the reverse scan need nothing
   // from each other: after the intra kernel, the reverse scan and its tiles
@@ -1822,20 +1846,35 @@ hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
   ProfScope ps("dn_mfma_rev_scan", side);
 #define DN_REV(KD, TG, W) \
   hipLaunchKernelGGL((mfma_rev_scan_kernel<KD, TG, W>), dim3(blocks), dim3(64 * W), 0, side, rp)
+#define DN_REV4(KD, TG, W)                                                                     \
+  hipLaunchKernelGGL((mfma_rev_scan_kernel<KD, TG, W, true>), dim3(blocks), dim3(64 * W), 0,  \
+                     side, rp)
 #define DN_REV_W(KD, TG) \
   do { if (waves == 8) DN_REV(KD, TG, 8); else if (waves == 4) DN_REV(KD, TG, 4); else DN_REV(KD, TG, 2); } while (0)
+  if (g4 && waves != 8 && d.K != 256) return hipErrorInvalidValue;
   if (d.K == 256) {
-    if (grad_dtype == DN_BF16) DN_REV(256, bf16, 4); else DN_REV(256, float, 4);
+    if (g4) {
+      if (grad_dtype == DN_BF16) DN_REV4(256, bf16, 4); else DN_REV4(256, float, 4);
+    } else {
+      if (grad_dtype == DN_BF16) DN_REV(256, bf16, 4); else DN_REV(256, float, 4);
+    }
+  } else if (g4) {
+    if (d.K == 128) {
+      if (grad_dtype == DN_BF16) DN_REV4(128, bf16, 8); else DN_REV4(128, float, 8);
+    } else {
+      if (grad_dtype == DN_BF16) DN_REV4(64, bf16, 8); else DN_REV4(64, float, 8);
+    }
   } else if (d.K == 128) {
     if (grad_dtype == DN_BF16) DN_REV_W(128, bf16); else DN_REV_W(128, float);
   } else {
     if (grad_dtype == DN_BF16) DN_REV_W(64, bf16); else DN_REV_W(64, float);
   }
 #undef DN_REV_W
+#undef DN_REV4
 #undef DN_REV
   }
   if ((e = hipGetLastError()) != hipSuccess) return e;
-  if ((e = launch_scan<true>(p, d, false, stream)) != hipSuccess) return e;
+  if ((e = launch_scan<true>(p, d, false, stream, g4)) != hipSuccess) return e;
   return side_join(stream);
 }
 

@@ -930,7 +930,7 @@ hipError_t generic_bwd(const Dims& d, int qkv_dtype, int grad_dtype, const void*
   if (mfma_ws) {
     // Both scans on MFMA; the chunk-local gradients below are unchanged.
     e = mfma_bwd_scans(d, grad_dtype, dy, dstate_final, q, k, v, erase, write, g, state_in,
-                       states, ds_after, dstate, mfma_ws, stream);
+                       states, ds_after, dstate, mfma_ws, stream, false);
     if (e != hipSuccess) return e;
   } else if ((e = generic_bwd_scans(d, grad_dtype, dy, dstate_final, state_in, ws, states,
                                     ds_after, dstate, stream)) != hipSuccess) {

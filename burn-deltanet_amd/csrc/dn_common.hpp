@@ -169,13 +169,22 @@ hipError_t fused_fwd(const Dims& d, int y_dtype, const void* q, const void* k, c
                      hipStream_t stream);
 // The backward's two scans on MFMA (bf16 q/k/v, the shapes mfma_fwd_supported
 // accepts): the states entering each chunk and the state cotangents leaving
-// each chunk, fp32 [G][K][V], plus the initial state's cotangent.
+// each chunk, fp32 [G][K][V], plus the initial state's cotangent. g4: both
+// per-chunk arrays in row groups of four instead, [G][K/4][V][4] (a lane's
+// four accumulator rows of its column are one 16-byte store), which the
+// MFMA chunk-local kernel reads; where states_g4(d) holds, at head_k_dim
+// 256 (B=8 T=4096 H=16 dv=256: states scan 2543 → 692 µs, reverse scan
+// 3846 → 1623 µs, the chunk-local kernel 5.29 → 5.95 ms, whose key-channel
+// phase reads a row as 16-byte-strided words there). At head_k_dim 128 the
+// scans gained 80 µs each at dv = 256 and the chunk-local kernel lost 260;
+// BASELINE config 5's two-wave scans were slower with it.
 size_t mfma_bwd_workspace(const Dims& d);
+bool states_g4(const Dims& d);
 hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
                           const float* dstate_final, const void* q, const void* k, const void* v,
                           const float* erase, const float* write, const float* g,
                           const float* state_in, float* states, float* ds_after, float* dstate,
-                          void* ws, hipStream_t stream);
+                          void* ws, hipStream_t stream, bool g4);
 // The per-chunk tiles mfma_bwd_scans leaves in its workspace: T (hi, lo) and
 // Tᵀ (hi, lo), attnᵀ [G][64][64]; kc = e^{G_last−G}⊙K [G][64][K]; per-channel
 // decay: kg = e⊙e^G⊙K hi, lo [G][64][K]; per-head: the cumulative gate [G][64].
@@ -194,7 +203,7 @@ hipError_t mfma_chunk_bwd(const Dims& d, int grad_dtype, const void* dy, const v
                           const void* k, const void* v, const float* erase, const float* write,
                           const float* g, const float* states, const float* ds_after, void* dq,
                           void* dk, void* dv, float* derase, float* dwrite, float* dg,
-                          const MfmaTiles& tiles, float* partials, hipStream_t stream);
+                          const MfmaTiles& tiles, float* partials, hipStream_t stream, bool g4);
 
 // Per-kernel HIP-event timing (dn_profile_enable): a scope records a start
 // event on construction and a stop event on destruction, on `stream`.

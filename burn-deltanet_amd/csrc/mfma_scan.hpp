@@ -95,7 +95,9 @@ __device__ inline int scan_opaque(int x) {
 // values of chunk n and the gate, and after phase 3 writes the normalised
 // output over them. The last two chunks finish after the loop.
 // NORM: 0 none, 1 OutNorm::Plain, 2 OutNorm::Gated with the gate in y's dtype.
-template <int K, class TY, int WAVES, bool PC, bool ST = false, int SEG = 0, int NORM = 0>
+// G4 (ST): the states in row groups of four ([G][K/4][V][4], states_g4).
+template <int K, class TY, int WAVES, bool PC, bool ST = false, int SEG = 0, int NORM = 0,
+          bool G4 = false>
 __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   static_assert(NORM == 0 || (!ST && SEG != 1), "the output norm applies to y");
   constexpr int KK = K / 32;      // 32-deep k-steps over the key axis
@@ -584,7 +586,13 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
     // flight (its wait is for older loads only).
     if (n >= 3) norm_finish(n - 3);
     if (n >= 1) norm_publish(n - 1);
-    if constexpr (ST) {
+    if constexpr (ST && G4) {
+      // a lane's four rows of its column as one 16-byte store
+      float4* sdst = reinterpret_cast<float4*>(p.states + chunk_of(n) * K * p.V) + jl;
+#pragma unroll
+      for (int rb = 0; rb < RBK; ++rb)
+        sdst[size_t(4 * rb + q4) * p.V] = make_float4(S[rb][0], S[rb][1], S[rb][2], S[rb][3]);
+    } else if constexpr (ST) {
       float* sdst = p.states + chunk_of(n) * K * p.V + jl;
 #pragma unroll
       for (int rb = 0; rb < RBK; ++rb)
