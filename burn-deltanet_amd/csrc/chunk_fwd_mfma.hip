@@ -1837,10 +1837,13 @@ hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
   hipStream_t side = nullptr;
   if ((e = side_fork(stream, &side)) != hipSuccess) return e;
   RevParams rp{d.B, d.S, d.H, d.V, d.N, dy, dstate_final, ds_after, dstate, bt};
-  // head_k_dim 256: four-wave workgroups, whose single wave per SIMD has the
-  // register file for its 256 dS rows and the next chunk's 120 KB of tiles
-  // (eight waves spilled: 5.05 against 3.85 ms at B=8 T=4096 H=16 dv=256).
-  const int waves = d.K == 256 ? 4 : scan_waves(d);
+  // head_k_dim 256: eight waves with ds_after in row groups of four (the
+  // generic kernels' row-major layout: four, whose single wave per SIMD has
+  // the register file for 256 dS rows beside the next chunk's 120 KB of
+  // tiles; eight waves spilled there). At B=8 T=4096 H=16 dv=256: eight
+  // waves row-major 5.05 ms, four 3.85, four in row groups 1.61, eight in
+  // row groups 1.36.
+  const int waves = d.K == 256 && !g4 ? 4 : scan_waves(d);
   const unsigned blocks = unsigned(((d.B * d.H + 7) / 8) * 8 * (d.V / (16 * waves)));
   {
   ProfScope ps("dn_mfma_rev_scan", side);
@@ -1854,7 +1857,7 @@ hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
   if (g4 && waves != 8 && d.K != 256) return hipErrorInvalidValue;
   if (d.K == 256) {
     if (g4) {
-      if (grad_dtype == DN_BF16) DN_REV4(256, bf16, 4); else DN_REV4(256, float, 4);
+      if (grad_dtype == DN_BF16) DN_REV4(256, bf16, 8); else DN_REV4(256, float, 8);
     } else {
       if (grad_dtype == DN_BF16) DN_REV(256, bf16, 4); else DN_REV(256, float, 4);
     }
