@@ -59,9 +59,9 @@ typedef enum {
 
 /* Which kernels run dn_chunk_fwd / dn_chunk_bwd. AUTO picks the MFMA path
  * (DN_ALGO_MFMA) whenever the shape, dtypes and pointers allow it (bf16
- * q/k/v, head_k_dim 64 or 128 with head_v_dim a multiple of 64; for the
- * forward with per-head or no gates also head_k_dim 256 with head_v_dim a
- * multiple of 128): q and k
+ * q/k/v, head_k_dim 64 or 128 with head_v_dim a multiple of 64; with
+ * per-head or no gates also head_k_dim 256 with head_v_dim a multiple of
+ * 128, forward and backward): q and k
  * (and, for the backward, d_y) at 16-byte boundaries, v at a 4-byte one, and
  * nheads·max(head_k_dim, head_v_dim) below 2^23 (the kernels address a
  * chunk's token rows with 32-bit byte offsets). Otherwise AUTO runs the
