@@ -91,7 +91,7 @@ def bench_chunk_fwd(torch, pkg, steps, warmup, algo):
     yb = B * T * H * V * 2              # y, bf16
     gates = 2 * B * T * H * 4           # β and g, fp32
     st = B * H * K * V * 4              # one fp32 state
-    tri = 3 * G * L * L * 2             # T (hi, lo) and attn, bf16
+    tri = 3 * G * 6 * 16 * 32 * 2       # T (hi, lo) and attn, bf16: their six nonzero 16x32 blocks
     gcb = G * L * 4                     # in-chunk cumulative gate, fp32
     # The bytes each kernel moves by its own design (intermediates included),
     # beside the path's algorithmic bytes. (The scan forms (e^{G_last-G} k)^T
@@ -797,7 +797,9 @@ def main():
     ap.add_argument("--profile-pass", action="store_true",
                     help="short run for rocprofv3 --pmc: a 1 GiB copy (calibration), then 2 "
                          "forward, 2 decode, 2 DeltaProduct-decode, 2 front-end and 2 "
-                         "output-norm calls and one config-5 forward + backward; prints no JSON")
+                         "output-norm calls, one config-5 forward + backward, one config-4 "
+                         "forward, one config-2-shape backward at head_k_dim 128 and one at "
+                         "256, block decode and inverse calls; prints no JSON")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -825,6 +827,7 @@ def main():
         bench_config5(torch, pkg, 1, 0)
         bench_config4(torch, pkg, 1, 0)
         bench_config2_bwd(torch, pkg, 1, 0)
+        bench_config2_bwd(torch, pkg, 1, 0, K=256)
         bench_block_decode(torch, pkg, 2, 0)
         bench_unit_lower_inverse(torch, pkg, 2, 0)
         torch.cuda.synchronize()
