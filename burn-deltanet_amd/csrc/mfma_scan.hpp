@@ -117,13 +117,13 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   // kept the K and [64][64] tiles double-buffered and restaged a single Q
   // tile after a barrier behind phase 1 measured slower, 487 → 652 µs at
   // B=8 T=4096 H=16 dv=256: its extra staging registers spill in the loop.)
-  // The states mode and the transition pass write no y: they fetch no attn
-  // (per-head gates).
-  constexpr int NKQ = PC ? 3 : 2;  // K-wide tiles
+  // Without y (the states mode, the transition pass) neither Q (qg) nor attn
+  // is staged: they only form y.
   constexpr bool kYOut = !ST && SEG != 1;              // y is written
-  constexpr int NLL = PC || kYOut ? 3 : 2;             // [64][64] tiles: T, Tlo (, attn)
-  constexpr int oK = 0, oQ = oK + kL * K, oKl = oQ + kL * K, oT = NKQ * kL * K,
-                oTl = oT + kL * kL, oAt = oTl + kL * kL, oKc = oAt + kL * kL,
+  constexpr int NKQ = 1 + (kYOut ? 1 : 0) + (PC ? 1 : 0);  // K-wide tiles: K (, Q) (, kg lo)
+  constexpr int NLL = kYOut ? 3 : 2;                   // [64][64] tiles: T, Tlo (, attn)
+  constexpr int oK = 0, oQ = oK + kL * K, oKl = (kYOut ? 2 : 1) * kL * K, oT = NKQ * kL * K,
+                oTl = oT + kL * kL, oAt = oTl + kL * kL, oKc = oT + NLL * kL * kL,
                 BUF = NKQ * kL * K + NLL * kL * kL + (PC ? K * kL : 0);
   constexpr int C16 = BUF / 8;    // 16-byte chunks per chunk's tiles
   // The forward with per-head gates (not the states mode) reads T, T lo and
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
         if constexpr (PC) {
           // kg, qg and kg lo: written by the intra kernel per chunk-head
           // (zero past the sequence end).
-          const uint16_t* base = which == 0 ? p.Kg : which == 1 ? p.Qg : p.Kglo;
+          const uint16_t* base = which == 0 ? p.Kg : (kYOut && which == 1) ? p.Qg : p.Kglo;
           pf[m] = ld16(base + cid * kL * K + 8 * (i0 - which * (kL * K / 8)), 8u * tid);
         } else {
           // Row tid/(K/8) + rowc, clamped through its (monotonic) offset.
@@ -290,7 +290,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
       if (i0 < NKQ * kL * K / 8) {
         const int which = i0 / (kL * K / 8);
         const int dr = (i0 - which * (kL * K / 8)) / KC8;  // row advance, a multiple of 8
-        const int base = (which == 0 ? oK : which == 1 ? oQ : oKl) + dr * K;
+        const int base = (which == 0 ? oK : (kYOut && which == 1) ? oQ : oKl) + dr * K;
         const bool flip = K >= 128 && (dr & 8);
         b0 = base + (flip ? aK0x : aK0);
         b1 = base + (flip ? aK1x : aK1);
@@ -627,7 +627,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
       auto rd = [&](int st) {
         const int at = tile_at<K>(16 * (st & 3) + r16, 32 * (st >> 2) + k8);
         kf[st % NR] = ld8(&tl[oK + at]);
-        qf[st % NR] = ld8(&tl[oQ + at]);
+        if constexpr (kYOut) qf[st % NR] = ld8(&tl[oQ + at]);
         if constexpr (PC) kl[st % NR] = ld8(&tl[oKl + at]);
       };
 #pragma unroll
@@ -649,7 +649,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
             const int c = step % NR;
             X[tb] = mfma16(kf[c], as8(sh), X[tb]);
             X[tb] = mfma16(kf[c], as8(sl), X[tb]);
-            yt[tb] = mfma16(as8(sh), qf[c], yt[tb]);
+            if constexpr (kYOut) yt[tb] = mfma16(as8(sh), qf[c], yt[tb]);
           }
           if (kk + 1 < KK) {
 #pragma unroll
@@ -675,7 +675,7 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
             X[tb] = mfma16(kf[c], as8(sl), X[tb]);
             // kg carries the fp32 gate factors, so it has a lo part too.
             if constexpr (PC) X[tb] = mfma16(kl[c], as8(sh), X[tb]);
-            yt[tb] = mfma16(as8(sh), qf[c], yt[tb]);
+            if constexpr (kYOut) yt[tb] = mfma16(as8(sh), qf[c], yt[tb]);
           }
         }
       }
