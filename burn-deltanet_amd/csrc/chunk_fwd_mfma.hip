@@ -663,7 +663,8 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p, B
       const size_t go = (size_t(cid) * kL + i) * K + d0i;
       *reinterpret_cast<uint4*>(p.Kg + go) = make_uint4(gh[0], gh[1], gh[2], gh[3]);
       *reinterpret_cast<uint4*>(p.Kglo + go) = make_uint4(gl[0], gl[1], gl[2], gl[3]);
-      *reinterpret_cast<uint4*>(p.Qg + go) = make_uint4(qq[0], qq[1], qq[2], qq[3]);
+      // qg feeds only the forward's y (the backward's scans read Qgᵀ).
+      if constexpr (!BT) *reinterpret_cast<uint4*>(p.Qg + go) = make_uint4(qq[0], qq[1], qq[2], qq[3]);
       if constexpr (BT) {
         // Qgᵀ and Kgᵀ: the four lanes holding rows i0…i0+3 of the same eight
         // channels trade channel-pair words, so that lane q ends with channels
@@ -708,10 +709,11 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p, B
     __syncthreads();
     // Scores of block row rb: wave w ≤ rb forms block (rb, w); a wave past
     // the diagonal writes attn's zero block (rb, w). attn row i, column j:
-    // the 16 lanes of one q4 store 16 consecutive columns.
+    // the 16 lanes of one q4 store 16 consecutive columns. (The backward
+    // writes attnᵀ only: attn feeds the forward's y.)
     {
       const int cb = wave, j = 16 * cb + r16;
-      uint16_t* adst = p.attn + size_t(cid) * kL * kL + size_t(16 * rb + 4 * q4) * kL + j;
+      uint16_t* adst = BT ? nullptr : p.attn + size_t(cid) * kL * kL + size_t(16 * rb + 4 * q4) * kL + j;
       if (cb <= rb) {
         f32x4 acck = {0.f, 0.f, 0.f, 0.f}, accq = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -761,15 +763,17 @@ __global__ __launch_bounds__(kThreads) void mfma_intra_pc_kernel(MfmaParams p, B
           const int i = 16 * rb + 4 * q4 + rr;
           A[i][j] = (j < i) ? acck[rr] : 0.f;
           av[rr] = pk_bf16((j <= i) ? accq[rr] : 0.f, 0.f);
-          adst[rr * kL] = uint16_t(av[rr]);
+          if constexpr (!BT) adst[rr * kL] = uint16_t(av[rr]);
         }
         if constexpr (BT)  // attnᵀ row j, columns 16·rb + 4·q4 … +3
           *reinterpret_cast<uint2*>(bt.AtT + size_t(cid) * kL * kL + size_t(j) * kL + 16 * rb +
                                     4 * q4) =
               make_uint2(av[0] | (av[1] << 16), av[2] | (av[3] << 16));
       } else {
+        if constexpr (!BT) {
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) adst[rr * kL] = 0;
+          for (int rr = 0; rr < 4; ++rr) adst[rr * kL] = 0;
+        }
         if constexpr (BT)
           *reinterpret_cast<uint2*>(bt.AtT + size_t(cid) * kL * kL + size_t(j) * kL + 16 * rb +
                                     4 * q4) = make_uint2(0u, 0u);
@@ -1829,8 +1833,9 @@ hipError_t mfma_bwd_scans(const Dims& d, int grad_dtype, const void* dy,
   float* s_scratch = reinterpret_cast<float*>(reinterpret_cast<char*>(bt.egl) + region(G * K * 4));
   MfmaParams p = make_params(d, q, k, v, erase, write, g, state_in, nullptr, s_scratch, ws);
   p.states = states;
-  // The states mode reads no attn (the intra kernel still forms it for attnᵀ).
-  if (!pc_path(d)) p.attn = nullptr;
+  // The states mode reads neither attn nor qg (the intra kernels form attn for
+  // attnᵀ and write neither).
+  p.attn = nullptr;
   // The intra kernel writes the reverse scan's transposed tiles too.
   hipError_t e = launch_intra(p, d, stream, &bt);
   if (e != hipSuccess) return e;
