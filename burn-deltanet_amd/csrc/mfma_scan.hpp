@@ -112,8 +112,10 @@ __global__ __launch_bounds__(64 * WAVES) void mfma_scan_kernel(MfmaParams p) {
   // round trip through HBM.
   // Double-buffered for per-head gates: the next chunk is staged while this
   // one is consumed, so one barrier per chunk suffices. The per-channel
-  // tiles, and head_k_dim 256's (88 KB a chunk), do not fit twice in LDS:
-  // they are staged between two barriers. (A head_k_dim 256 variant that
+  // tiles with y, and head_k_dim 256's (88 KB a chunk), do not fit twice in
+  // LDS: they are staged between two barriers. (Without y the per-channel
+  // tiles take 64 KB; double-buffered, config 5's two-wave states scan ran
+  // slower, 861 → 1057 µs.) (A head_k_dim 256 variant that
   // kept the K and [64][64] tiles double-buffered and restaged a single Q
   // tile after a barrier behind phase 1 measured slower, 487 → 652 µs at
   // B=8 T=4096 H=16 dv=256: its extra staging registers spill in the loop.)
